@@ -1,0 +1,292 @@
+#!/usr/bin/env python3
+"""Benchmark of the split-K paged GQA decode operator on one MI355X.
+
+A step is one decode call (partition kernel + merge kernel) over one batch of
+synthetic input. Default workload: Llama-3-8B decode geometry (B4, 32 query /
+8 KV heads, head_dim 128, page 16, uniform 4096 context, split 256, FP16 KV,
+FP32 accumulate and output).
+
+Protocol
+* Inputs are resident in HBM before timing. K/V are replicated into enough
+  buffer sets to cover >= 512 MiB and every step uses the next set, so a step
+  cannot be served from the 256 MB Infinity Cache.
+* Correctness gate first: the GPU output is compared with the C FP32 split-K
+  restatement on the same inputs (this is also the CPU-baseline leg); no
+  timing is reported if it fails.
+* Timed region: W untimed warmup steps, then exactly K steps as hipGraph
+  replays (one captured graph per buffer set), bracketed by synchronize and
+  HIP events on the launch stream. Eager launches are timed the same way.
+* Roofline: K launches of the partition kernel alone (captured, replayed) give
+  its average duration; achieved = logical KV bytes / duration.
+* The reference's sampling protocol (30 repetitions x 20 inner calls, runners
+  in randomized order, p50) is reported for both merge kernels.
+
+Prints one JSON line.
+"""
+import argparse
+import hashlib
+import json
+import math
+import os
+import random
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "paged-decode-lab_amd"))
+
+METRIC = "µs/decode call and achieved KV HBM GB/s (% of peak), 1 MI355X"
+PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E, public specification
+ROTATION_BYTES = 512 << 20      # > 2x the 256 MB Infinity Cache
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default="llama3_8b_b4_l4096")
+    p.add_argument("--split-tokens", type=int, default=None)
+    p.add_argument("--merge", choices=["serial", "shared"], default="serial")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="bound on the CPU-baseline sample (0 disables timing, the gate still runs)")
+    p.add_argument("--cpu-threads", type=int, default=None)
+    p.add_argument("--repetitions", type=int, default=30)
+    p.add_argument("--inner", type=int, default=20)
+    p.add_argument("--quiet", action="store_true", help="suppress progress lines on stderr")
+    return p.parse_args()
+
+
+def log(args, message):
+    if not args.quiet:
+        print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def source_digest():
+    h = hashlib.sha256()
+    for rel in ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "include/paged_decode.h"):
+        h.update((REPO / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def recorded_traffic(workload, digest):
+    """HBM bytes per partition launch from committed rocprofv3 --pmc summaries.
+
+    Used only when the summary was taken on the same kernel source (digest).
+    """
+    path = REPO / "profiles" / f"traffic_{workload}.json"
+    if not path.exists():
+        return None
+    record = json.loads(path.read_text())
+    if record.get("source_digest") != digest:
+        return None
+    return record.get("hbm_bytes_per_launch")
+
+
+def time_region(torch, fn, steps):
+    """HIP-event and wall time of `steps` calls of fn on the current stream."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end), (time.perf_counter() - wall) * 1e3
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(each GPU box has one GPU; the operator shards by sequence or KV head with no exchange).",
+              file=sys.stderr)
+        return 2
+    if args.steps <= 0 or args.warmup < 0:
+        print("--steps must be positive and --warmup non-negative", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from paged_decode.metrics import kv_bytes, summarize, unique_token_bytes
+    from paged_decode.runtime import DecodePlan
+    from paged_decode.workload import make_workload
+
+    w = make_workload(args.workload, split_tokens=args.split_tokens)
+    L = w.layout
+    log(args, f"workload {w.name}: {w.description}; split_tokens={w.split_tokens} merge={args.merge}")
+    q_h, k_h, v_h = w.host_tensors()
+    logical = kv_bytes(w.lengths, L.kv_heads, L.head_dim, w.element_size)
+    unique = unique_token_bytes(w.table, w.lengths, L.page_size, L.kv_heads, L.head_dim, w.element_size)
+
+    device = torch.device("cuda", 0)
+    q = torch.from_numpy(q_h).to(device)
+    k0 = torch.from_numpy(k_h).to(device)
+    v0 = torch.from_numpy(v_h).to(device)
+    set_bytes = k0.numel() * k0.element_size() * 2
+    sets = max(1, math.ceil(ROTATION_BYTES / set_bytes))
+    ks = [k0] + [k0.clone() for _ in range(sets - 1)]
+    vs = [v0] + [v0.clone() for _ in range(sets - 1)]
+    log(args, f"{sets} K/V buffer set(s) of {set_bytes / 2**20:.1f} MiB; logical KV bytes/call {logical}")
+
+    plans = {m: DecodePlan(L, w.table, w.lengths, device=device, split_tokens=w.split_tokens, merge=m)
+             for m in ("serial", "shared")}
+    plan = plans[args.merge]
+
+    # --- correctness gate and CPU baseline (the only leg that touches oracle/) ---
+    sys.path.insert(0, str(REPO))
+    from oracle import cpu as cpu_oracle
+
+    threads = args.cpu_threads or min(len(os.sched_getaffinity(0)), 64)
+    log(args, f"gate: C FP32 restatement on {threads} thread(s)")
+    expected = cpu_oracle.decode(q_h, k_h, v_h, w.table, w.lengths, w.split_tokens, threads=threads)
+    gate = {}
+    for name, p in plans.items():
+        for i in (0, sets - 1):
+            got = p.run(q, ks[i], vs[i]).cpu().numpy()
+            err = float(np.max(np.abs(got.astype(np.float64) - expected)))
+            if w.dtype == np.float16:
+                ok = err <= 2e-3
+            else:
+                ok = bool(np.all(np.abs(got - expected) <= 1e-6 + 1e-5 * np.abs(expected)))
+            gate[name] = max(gate.get(name, 0.0), err)
+            if not ok or not np.isfinite(got).all():
+                print(json.dumps({"error": "correctness gate failed", "merge": name, "max_abs": err}))
+                return 1
+    log(args, f"gate passed: max abs error vs CPU {max(gate.values()):.3e}")
+
+    cpu_baseline = None
+    if args.cpu_seconds > 0:
+        calls, start = 0, time.perf_counter()
+        while True:
+            cpu_oracle.decode(q_h, k_h, v_h, w.table, w.lengths, w.split_tokens, threads=threads)
+            calls += 1
+            elapsed = time.perf_counter() - start
+            if elapsed >= args.cpu_seconds or calls >= 100000:
+                break
+        cpu_us = elapsed / calls * 1e6
+        cpu_baseline = {
+            "value": round(logical / (cpu_us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "us_per_call": round(cpu_us, 2),
+            "sample": f"{calls} full decode calls of this workload ({elapsed:.1f} s) with the C FP32 split-K "
+                      f"restatement (oracle/cpu_decode.c, OpenMP, {threads} threads), same host arrays",
+        }
+        log(args, f"CPU baseline: {cpu_us:.1f} us/call")
+
+    # --- warmup, graph capture ---
+    stream = torch.cuda.current_stream()
+    for i in range(args.warmup):
+        plan.run(q, ks[i % sets], vs[i % sets])
+    torch.cuda.synchronize()
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=side):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        return g
+
+    graphs = {m: [capture(lambda p=p, i=i: p.run(q, ks[i], vs[i])) for i in range(sets)]
+              for m, p in plans.items()}
+    for i in range(args.warmup):
+        graphs[args.merge][i % sets].replay()
+
+    # --- timed region: exactly K steps ---
+    graph_ms, graph_wall = time_region(torch, lambda i: graphs[args.merge][i % sets].replay(), args.steps)
+    eager_ms, eager_wall = time_region(torch, lambda i: plan.run(q, ks[i % sets], vs[i % sets]), args.steps)
+    us_graph = graph_ms * 1e3 / args.steps
+    us_eager = eager_ms * 1e3 / args.steps
+    log(args, f"graph {us_graph:.2f} us/call, eager {us_eager:.2f} us/call")
+
+    # --- partition kernel alone (roofline numerator) ---
+    burst = 20
+    partial_graphs = []
+    for i in range(sets):
+        def launches(i=i):
+            for j in range(burst):
+                plan.run_partial(q, ks[(i + j) % sets], vs[(i + j) % sets])
+        partial_graphs.append(capture(launches))
+    partial_graphs[0].replay()
+    reps = max(1, args.steps // burst)
+    partial_ms, _ = time_region(torch, lambda i: partial_graphs[i % sets].replay(), reps)
+    partial_us = partial_ms * 1e3 / (reps * burst)
+    achieved = logical / (partial_us * 1e-6) / 1e9
+
+    # --- reference sampling protocol: p50 over 30 x 20, randomized order ---
+    rng = random.Random(w.seed)
+    samples = {m: ([], []) for m in plans}
+    for _ in range(args.repetitions):
+        order = list(plans)
+        rng.shuffle(order)
+        for m in order:
+            dev, wall = time_region(torch, lambda i, m=m: graphs[m][i % sets].replay(), args.inner)
+            samples[m][0].append(dev / args.inner)
+            samples[m][1].append(wall / args.inner)
+    protocol = {}
+    for m, (dev, wall) in samples.items():
+        s = summarize(dev, wall, L.batch)
+        protocol[m] = {"p50_us": round(s["device_ms_p50"] * 1e3, 3), "p95_us": round(s["device_ms_p95"] * 1e3, 3),
+                       "min_us": round(s["device_ms_min"] * 1e3, 3),
+                       "p50_GBps": round(logical / (s["device_ms_p50"] * 1e-3) / 1e9, 1)}
+
+    digest = source_digest()
+    value = logical / (us_graph * 1e-6) / 1e9
+    record = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(graph_ms / args.steps, 6),
+        "us_per_call": round(us_graph, 3),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "eager_us_per_call": round(us_eager, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if w.dtype == np.float16 else "f32",
+        "accumulate": "f32",
+        "data": "synthetic (seeded N(0,1) q/k/v, shuffled page table)",
+        "config": {
+            "workload": w.name, "batch": L.batch, "query_heads": L.query_heads, "kv_heads": L.kv_heads,
+            "head_dim": L.head_dim, "page_size": L.page_size, "context": int(w.lengths.max()),
+            "split_tokens": w.split_tokens, "splits": plan.splits, "merge": args.merge, "mode": "hipgraph",
+            "kv_buffer_sets": sets, "parallelism": "single GPU",
+        },
+        "kv_bytes_per_call": logical,
+        "unique_kv_bytes_per_call": unique,
+        "workspace_bytes": plan.workspace_bytes,
+        "roofline": {
+            "bound": "hbm", "kernel": "partial_kernel", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": recorded_traffic(w.name, digest), "avg_launch_us": round(partial_us, 3),
+        },
+        "cpu_baseline": cpu_baseline,
+        "protocol_graph_p50": protocol,
+        "gate_max_abs_vs_cpu": {m: float(f"{e:.3e}") for m, e in gate.items()},
+        "wall_ms": {"graph": round(graph_wall, 3), "eager": round(eager_wall, 3)},
+        "source_digest": digest,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(record), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,115 @@
+/*
+ * paged_decode.h -- C ABI of the MI355X (gfx950) split-K paged GQA decode operator.
+ *
+ * One-token attention decode over a paged KV cache:
+ *   q      [batch, query_heads, head_dim]                     float16 or float32
+ *   k, v   [physical_pages, page_size, kv_heads, head_dim]      same dtype as q
+ *   table  [batch, table_width]  int32 physical page of each logical page
+ *   lengths[batch]               int32 live tokens per sequence
+ *   out    [batch, query_heads, head_dim]                     float32
+ * out[b,h] = softmax(K q / sqrt(head_dim)) V over the live tokens of sequence b
+ * through KV head h / (query_heads / kv_heads); an empty sequence gives zeros.
+ * Token t of sequence b is at page table[b, t / page_size], offset
+ * t % page_size. Tokens whose page id is outside [0, physical_pages) are
+ * skipped, never dereferenced.
+ *
+ * Work is cut into `splits` partitions of `split_tokens` tokens; every
+ * partition leaves one max-corrected softmax state per query head in the
+ * caller's workspace, and a merge kernel combines them:
+ *   numerator [batch, query_heads, splits, head_dim]  float32
+ *   stats     [batch, query_heads, splits, 2]         float32 (max, denominator)
+ * The workspace needs no initialisation; every element is written per call.
+ *
+ * All pointers are device pointers. `stream` is a hipStream_t (passed as
+ * void* so FFI layers need no HIP headers); calls are asynchronous on it, never
+ * allocate, never synchronise, and may be captured into a hipGraph. A call is
+ * not reentrant for one workspace: use separate workspaces on concurrent
+ * streams.
+ *
+ * Every function returns PD_OK or a PD_ERR_* code; on error nothing is
+ * launched (except PD_ERR_LAUNCH, reported by the runtime after submission).
+ */
+#ifndef PAGED_DECODE_H
+#define PAGED_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum pd_status {
+    PD_OK = 0,
+    PD_ERR_NULL_POINTER = 1,  /* a required pointer is NULL */
+    PD_ERR_SHAPE = 2,         /* a dimension is outside the supported range */
+    PD_ERR_DTYPE = 3,         /* dtype is not PD_DTYPE_F32 / PD_DTYPE_F16 */
+    PD_ERR_SPLIT = 4,         /* splits / split_tokens outside their range */
+    PD_ERR_MERGE = 5,         /* unknown merge mode or shared-merge bound exceeded */
+    PD_ERR_LAUNCH = 6         /* the HIP runtime rejected a kernel launch */
+};
+
+enum pd_dtype { PD_DTYPE_F32 = 0, PD_DTYPE_F16 = 1 };
+
+/* Merge strategies, numbered as the reference's merge_mode argument. */
+enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
+
+/* Largest partition count the LDS-bounded (shared) merge accepts. */
+#define PD_SHARED_MERGE_MAX_PARTS 4096
+
+/*
+ * Full decode: partition kernel then merge kernel, both on `stream`.
+ * Replaces the native entry `decode(q, k, v, table, lengths, numerator, stats,
+ * out, split_tokens, merge_mode)` of reference
+ * src/paged_decode/csrc/bindings.cpp:3-9 / decode.cu:197-246, with the tensor
+ * shapes passed explicitly. Limits (decode.cu:209-235): 1 <= batch,
+ * query_heads <= 65535; head_dim in {64, 128}; page_size in {16, 32};
+ * query_heads % kv_heads == 0; 1 <= table_width <= 65536; 1 <= splits <= 65535;
+ * 1 <= split_tokens <= 1048576; merge_mode PD_MERGE_SHARED needs
+ * splits <= PD_SHARED_MERGE_MAX_PARTS.
+ */
+int pd_decode(const void* q, const void* k, const void* v, int dtype,
+              const int32_t* table, const int32_t* lengths,
+              float* numerator, float* stats, float* out,
+              int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+              int table_width, int physical_pages, int splits, int split_tokens,
+              int merge_mode, void* stream);
+
+/*
+ * Partition stage only (the first launch of pd_decode): fills numerator and
+ * stats. Replaces the partial_decode launch of reference decode.cu:176-182.
+ */
+int pd_decode_partial(const void* q, const void* k, const void* v, int dtype,
+                      const int32_t* table, const int32_t* lengths,
+                      float* numerator, float* stats,
+                      int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                      int table_width, int physical_pages, int splits, int split_tokens,
+                      void* stream);
+
+/*
+ * Merge stage only (the second launch of pd_decode): combines `splits`
+ * states per (sequence, query head) into out. Replaces the merge_decode /
+ * merge_shared launches of reference decode.cu:183-193.
+ */
+int pd_decode_merge(const float* numerator, const float* stats, float* out,
+                    int batch, int query_heads, int head_dim, int splits,
+                    int merge_mode, void* stream);
+
+/*
+ * Bytes of numerator + stats for a plan; the counterpart of the reference's
+ * DecodePlan.workspace_bytes (src/paged_decode/runtime.py:71-73) for this
+ * workspace layout. Returns 0 for non-positive arguments.
+ */
+size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits);
+
+/* Static description of a status code (never NULL). */
+const char* pd_status_string(int status);
+
+/* ABI version of this header: bumped on any signature change. */
+int pd_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGED_DECODE_H */

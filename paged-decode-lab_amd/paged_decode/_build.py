@@ -1,0 +1,92 @@
+"""Ahead-of-time build of the native libraries, in-tree, for gfx950.
+
+* ``libpaged_decode_hip.so`` -- HIP kernels and the C ABI of
+  ``include/paged_decode.h``, compiled by ``hipcc --offload-arch=gfx950``.
+* ``_C.so`` -- the thin PyTorch extension (host C++ only, compiled by the host
+  compiler against torch's headers) that calls the C ABI.
+
+Sources are compiled as written: nothing here runs torch's hipify step. Run as
+``python -m paged_decode._build`` or through ``__graft_entry__.build()``.
+"""
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+CSRC = PACKAGE / "csrc"
+REPO = PACKAGE.parent.parent
+INCLUDE = REPO / "include"
+HIP_LIBRARY = PACKAGE / "libpaged_decode_hip.so"
+EXTENSION = PACKAGE / "_C.so"
+ARCH = os.environ.get("PAGED_DECODE_ARCH", "gfx950")
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+# -packed-fp32-ops keeps the device compiler from forming v_pk_{add,mul,fma}_f32.
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wall", "-Wno-unused-command-line-argument"]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(str(c) for c in cmd), flush=True)
+    result = subprocess.run([str(c) for c in cmd], capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"command failed ({result.returncode}): {' '.join(str(c) for c in cmd)}\n"
+                           f"{result.stdout}\n{result.stderr}")
+    noise = "is not a recognized feature for this target"
+    for line in result.stderr.splitlines():
+        if verbose and noise not in line:
+            print(line, flush=True)
+
+
+def _atomic_output(path):
+    return path.with_name(path.name + f".tmp{os.getpid()}")
+
+
+def build_hip_library(verbose=False):
+    hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
+    tmp = _atomic_output(HIP_LIBRARY)
+    _run([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-o", tmp, CSRC / "decode.hip"], verbose)
+    os.replace(tmp, HIP_LIBRARY)
+    return HIP_LIBRARY
+
+
+def build_extension(verbose=False):
+    import torch
+    from torch.utils import cpp_extension
+
+    cxx = os.environ.get("CXX", "g++")
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    includes = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], str(ROCM / "include"),
+                str(INCLUDE)]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = _atomic_output(EXTENSION)
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-DTORCH_EXTENSION_NAME=_C", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-I{p}" for p in includes],
+           CSRC / "torch_ext.cpp", "-o", tmp,
+           f"-L{PACKAGE}", "-lpaged_decode_hip", f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch",
+           "-ltorch_cpu", "-ltorch_hip", "-ltorch_python", f"-L{ROCM / 'lib'}", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}", f"-Wl,-rpath,{ROCM / 'lib'}"]
+    _run(cmd, verbose)
+    os.replace(tmp, EXTENSION)
+    return EXTENSION
+
+
+def build(verbose=False):
+    """Compile both libraries; returns their paths."""
+    return build_hip_library(verbose), build_extension(verbose)
+
+
+def built():
+    return HIP_LIBRARY.exists() and EXTENSION.exists()
+
+
+if __name__ == "__main__":
+    for path in build(verbose="-q" not in sys.argv):
+        print(path)

@@ -1,0 +1,48 @@
+"""ctypes binding of the C ABI in ``include/paged_decode.h``.
+
+This is the stub an FFI caller (or a maintainer of the reference wiring its
+``load_extension`` to this library) would write: plain pointers and ints, the
+stream as an opaque pointer. ``PROTOTYPES`` mirrors the header one to one.
+"""
+import ctypes
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parent / "libpaged_decode_hip.so"
+
+PD_OK = 0
+PD_ERR_NULL_POINTER = 1
+PD_ERR_SHAPE = 2
+PD_ERR_DTYPE = 3
+PD_ERR_SPLIT = 4
+PD_ERR_MERGE = 5
+PD_ERR_LAUNCH = 6
+PD_DTYPE_F32 = 0
+PD_DTYPE_F16 = 1
+PD_MERGE_SERIAL = 0
+PD_MERGE_SHARED = 1
+PD_SHARED_MERGE_MAX_PARTS = 4096
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+PROTOTYPES = {
+    "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
+    "pd_decode_partial": (_I, [_P, _P, _P, _I, _P, _P, _P, _P] + [_I] * 9 + [_P]),
+    "pd_decode_merge": (_I, [_P, _P, _P] + [_I] * 5 + [_P]),
+    "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
+    "pd_status_string": (ctypes.c_char_p, [_I]),
+    "pd_abi_version": (_I, []),
+}
+
+
+def load(path=LIBRARY):
+    """Load the library and attach the prototypes (raises OSError if absent)."""
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+def status_string(lib, status):
+    return lib.pd_status_string(status).decode()

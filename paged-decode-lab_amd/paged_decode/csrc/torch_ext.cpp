@@ -1,0 +1,145 @@
+// Thin PyTorch-ROCm extension over the C ABI in include/paged_decode.h.
+//
+// Exposes `decode(q, k, v, table, lengths, numerator, stats, out, split_tokens,
+// merge_mode)` with the argument list of reference
+// src/paged_decode/csrc/bindings.cpp:3-9, and repeats the tensor checks of
+// reference decode.cu:201-237 (as TORCH_CHECK -> RuntimeError) for this
+// operator's workspace layout: numerator [B, Hq, splits, D] and
+// stats [B, Hq, splits, 2], one state per partition. Launches go to the current
+// torch stream of q's device, so calls follow torch stream semantics and can be
+// captured by torch.cuda.CUDAGraph (hipGraph). Nothing is allocated here.
+
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <cstdint>
+
+#include "paged_decode.h"
+
+namespace {
+
+void check_status(int status) {
+    TORCH_CHECK(status == PD_OK, "paged_decode: ", pd_status_string(status), " (status ", status, ")");
+}
+
+hipStream_t current_stream(const torch::Tensor& like) {
+    return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(like.get_device()).stream();
+}
+
+int dtype_code(const torch::Tensor& q) {
+    return q.scalar_type() == at::kHalf ? PD_DTYPE_F16 : PD_DTYPE_F32;
+}
+
+struct Shape {
+    int64_t batch, heads, dim, kv_heads, page_size, pages, width, splits;
+};
+
+Shape check_inputs(const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
+                   const torch::Tensor& table, const torch::Tensor& lengths,
+                   const torch::Tensor& numerator, const torch::Tensor& stats, int64_t split_tokens) {
+    for (const auto& t : {q, k, v, table, lengths, numerator, stats}) {
+        TORCH_CHECK(t.is_cuda() && t.is_contiguous(), "all tensors must be contiguous GPU tensors");
+        TORCH_CHECK(t.device() == q.device(), "device mismatch");
+    }
+    TORCH_CHECK(q.dim() == 3 && k.dim() == 4 && v.sizes() == k.sizes(), "expected q[B,H,D], k/v[P,T,KV,D]");
+    Shape s{q.size(0), q.size(1), q.size(2), 0, 0, 0, 0, 0};
+    TORCH_CHECK(s.batch > 0 && s.batch <= 65535 && s.heads > 0 && s.heads <= 65535,
+                "batch and head count must be in [1,65535]");
+    TORCH_CHECK(s.dim == 64 || s.dim == 128, "supported head dimensions: 64,128");
+    TORCH_CHECK(k.size(0) > 0 && k.size(1) > 0 && k.size(2) > 0 && k.size(3) == s.dim &&
+                    s.heads % k.size(2) == 0 && k.size(0) <= INT32_MAX && (k.size(1) == 16 || k.size(1) == 32),
+                "invalid cache shape");
+    s.pages = k.size(0);
+    s.page_size = k.size(1);
+    s.kv_heads = k.size(2);
+    TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(), "q/k/v dtype mismatch");
+    TORCH_CHECK(q.scalar_type() == at::kHalf || q.scalar_type() == at::kFloat,
+                "supported input dtypes: float16,float32");
+    TORCH_CHECK(table.dim() == 2 && table.size(0) == s.batch && table.size(1) > 0 && table.size(1) <= 65536 &&
+                    lengths.dim() == 1 && lengths.size(0) == s.batch,
+                "metadata shape mismatch");
+    TORCH_CHECK(table.scalar_type() == at::kInt && lengths.scalar_type() == at::kInt, "metadata must be int32");
+    s.width = table.size(1);
+    TORCH_CHECK(numerator.dim() == 4 && numerator.size(0) == s.batch && numerator.size(1) == s.heads &&
+                    numerator.size(2) > 0 && numerator.size(3) == s.dim,
+                "invalid numerator workspace");
+    s.splits = numerator.size(2);
+    TORCH_CHECK(s.splits <= 65535 && split_tokens > 0 && split_tokens <= 1048576, "invalid split configuration");
+    TORCH_CHECK(stats.dim() == 4 && stats.size(0) == s.batch && stats.size(1) == s.heads &&
+                    stats.size(2) == s.splits && stats.size(3) == 2,
+                "invalid stats workspace");
+    TORCH_CHECK(numerator.scalar_type() == at::kFloat && stats.scalar_type() == at::kFloat,
+                "workspaces must be float32");
+    return s;
+}
+
+void check_output(const torch::Tensor& q, const torch::Tensor& out, int64_t merge_mode, int64_t splits) {
+    TORCH_CHECK(out.is_cuda() && out.is_contiguous() && out.device() == q.device(),
+                "output must be a contiguous tensor on the input device");
+    TORCH_CHECK(out.sizes() == q.sizes(), "invalid output shape");
+    TORCH_CHECK(out.scalar_type() == at::kFloat, "output must be float32");
+    TORCH_CHECK(merge_mode == PD_MERGE_SERIAL || (merge_mode == PD_MERGE_SHARED && splits <= PD_SHARED_MERGE_MAX_PARTS),
+                "shared merge requires at most 4096 partial states");
+}
+
+}  // namespace
+
+void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
+            torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t split_tokens,
+            int64_t merge_mode) {
+    const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
+    check_output(q, out, merge_mode, s.splits);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    check_status(pd_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype_code(q), table.data_ptr<int32_t>(),
+                           lengths.data_ptr<int32_t>(), numerator.data_ptr<float>(), stats.data_ptr<float>(),
+                           out.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
+                           static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
+                           static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
+                           static_cast<int>(split_tokens), static_cast<int>(merge_mode), current_stream(q)));
+}
+
+// Partition stage alone (first launch of decode); used to time that kernel.
+void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
+             torch::Tensor numerator, torch::Tensor stats, int64_t split_tokens) {
+    const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
+    check_status(pd_decode_partial(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype_code(q), table.data_ptr<int32_t>(),
+        lengths.data_ptr<int32_t>(), numerator.data_ptr<float>(), stats.data_ptr<float>(),
+        static_cast<int>(s.batch), static_cast<int>(s.heads), static_cast<int>(s.kv_heads),
+        static_cast<int>(s.dim), static_cast<int>(s.page_size), static_cast<int>(s.width),
+        static_cast<int>(s.pages), static_cast<int>(s.splits), static_cast<int>(split_tokens), current_stream(q)));
+}
+
+// Merge stage alone (second launch of decode).
+void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t merge_mode) {
+    for (const auto& t : {numerator, stats, out}) {
+        TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.device() == out.device(),
+                    "all tensors must be contiguous GPU tensors on one device");
+        TORCH_CHECK(t.scalar_type() == at::kFloat, "workspaces/output must be float32");
+    }
+    TORCH_CHECK(numerator.dim() == 4 && stats.dim() == 4 && out.dim() == 3, "invalid workspace shapes");
+    TORCH_CHECK(stats.size(0) == numerator.size(0) && stats.size(1) == numerator.size(1) &&
+                    stats.size(2) == numerator.size(2) && stats.size(3) == 2 && out.size(0) == numerator.size(0) &&
+                    out.size(1) == numerator.size(1) && out.size(2) == numerator.size(3),
+                "workspace/output shape mismatch");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
+    check_status(pd_decode_merge(numerator.data_ptr<float>(), stats.data_ptr<float>(), out.data_ptr<float>(),
+                                 static_cast<int>(numerator.size(0)), static_cast<int>(numerator.size(1)),
+                                 static_cast<int>(numerator.size(3)), static_cast<int>(numerator.size(2)),
+                                 static_cast<int>(merge_mode), current_stream(out)));
+}
+
+PYBIND11_MODULE(_C, m) {
+    m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
+    m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)");
+    m.def("partial", &partial, "Partition stage only");
+    m.def("merge", &merge, "Merge stage only");
+    m.def("workspace_bytes", [](int64_t b, int64_t h, int64_t d, int64_t s) {
+        return static_cast<int64_t>(pd_workspace_bytes(static_cast<int>(b), static_cast<int>(h),
+                                                       static_cast<int>(d), static_cast<int>(s)));
+    });
+    m.def("abi_version", &pd_abi_version);
+}

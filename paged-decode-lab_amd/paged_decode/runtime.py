@@ -1,0 +1,133 @@
+"""Validated, allocation-free replay API over the gfx950 decode kernels.
+
+``DecodePlan`` keeps the constructor, attributes, validation order, exception
+types and borrowed-output contract of reference
+``src/paged_decode/runtime.py:23-90``. Underneath, ``run`` makes one call into
+the ``_C`` PyTorch extension, which launches the HIP kernels of
+``libpaged_decode_hip.so`` on the current stream. There is no CPU or eager
+fallback: if the native libraries cannot be loaded, plan construction fails.
+"""
+from functools import lru_cache
+import importlib
+import math
+
+import torch
+
+from .layout import Layout, validate_metadata
+
+# One (m, l, n[D]) state per partition and query head: the LDS-bounded merge
+# holds one float per partition.
+_SHARED_MERGE_MAX_PARTS = 4096
+# Observable fallback rule of the reference (runtime.py:54): its workspace had
+# four states per partition, so "shared" becomes "serial_fallback" above
+# 1024 partitions. Kept so merge_implementation reports the same value.
+_REFERENCE_STATES_PER_SPLIT = 4
+
+
+@lru_cache(maxsize=1)
+def load_extension():
+    """Load the prebuilt extension; build it in-tree first if it is missing.
+
+    Never called on import: plan construction is where native code is first
+    touched (reference ``runtime.py:9-20``), so compilation and loading stay
+    out of timed regions and graph capture.
+    """
+    from . import _build
+
+    if not _build.built():
+        _build.build()
+    try:
+        return importlib.import_module(f"{__package__}._C")
+    except ImportError as exc:  # pragma: no cover - exercised only on broken installs
+        raise RuntimeError(f"paged_decode native extension failed to load: {exc}") from exc
+
+
+class DecodePlan:
+    """Static metadata + reusable workspace for one decode shape.
+
+    table/lengths are CPU integer arrays and are copied during construction.
+    KV contents and q can change between runs; metadata requires a new plan.
+    The output is borrowed storage, overwritten by the next run. A plan may be
+    used on one stream at a time; use distinct plans for concurrent streams.
+    Device metadata and workspace attributes are internal and must not be edited.
+    """
+
+    def __init__(self, layout: Layout, table, lengths, *, device="cuda", split_tokens=256, merge="serial"):
+        if merge not in ("serial", "shared"):
+            raise ValueError("merge must be 'serial' or 'shared'")
+        if layout.head_dim not in (64, 128):
+            raise ValueError("head_dim must be 64 or 128")
+        if layout.page_size not in (16, 32):
+            raise ValueError("page_size must be 16 or 32")
+        if layout.batch > 65535 or layout.query_heads > 65535:
+            raise ValueError("batch/head count exceeds grid limits")
+        if isinstance(split_tokens, bool) or not isinstance(split_tokens, int) or not 1 <= split_tokens <= 1048576:
+            raise ValueError("split_tokens must be an integer in [1,1048576]")
+        table, lengths = validate_metadata(layout, table, lengths)
+        if table.shape[1] > 65536:
+            raise ValueError("page table width must not exceed 65536")
+        self.max_context = int(lengths.max(initial=0))
+        if self.max_context > 1048576:
+            raise ValueError("this implementation supports at most 1M context tokens")
+        self.splits = max(1, math.ceil(self.max_context / split_tokens))
+        if self.splits > 65535:
+            raise ValueError("too many context splits")
+        self.layout, self.split_tokens = layout, split_tokens
+        self.merge = merge
+        if merge == "shared":
+            fits = self.splits * _REFERENCE_STATES_PER_SPLIT <= _SHARED_MERGE_MAX_PARTS
+            self.merge_implementation = "shared" if fits else "serial_fallback"
+        else:
+            self.merge_implementation = "serial"
+        self._merge_mode = int(self.merge_implementation == "shared")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("DecodePlan requires a GPU (torch 'cuda') device")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self._table_cpu, self._lengths_cpu = table, lengths
+        self._table = torch.tensor(table, device=self.device)
+        self._lengths = torch.tensor(lengths, device=self.device)
+        shape = (layout.batch, layout.query_heads, self.splits)
+        self._numerator = torch.empty((*shape, layout.head_dim), device=self.device, dtype=torch.float32)
+        self._stats = torch.empty((*shape, 2), device=self.device, dtype=torch.float32)
+        self._out = torch.empty((layout.batch, layout.query_heads, layout.head_dim),
+                                dtype=torch.float32, device=self.device)
+        self._extension = load_extension()
+
+    @property
+    def workspace_bytes(self):
+        """Bytes of the partition-state workspace (numerator + stats)."""
+        return sum(t.numel() * t.element_size() for t in (self._numerator, self._stats))
+
+    def _check(self, q, k, v):
+        layout = self.layout
+        expected_q = (layout.batch, layout.query_heads, layout.head_dim)
+        expected_k = (layout.physical_pages, layout.page_size, layout.kv_heads, layout.head_dim)
+        if tuple(q.shape) != expected_q or tuple(k.shape) != expected_k or tuple(v.shape) != expected_k:
+            raise ValueError("input shape does not match plan")
+        if q.dtype not in (torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+            raise TypeError("q/k/v must share float16 or float32 dtype")
+        for tensor in (q, k, v):
+            if tensor.device != self.device or not tensor.is_contiguous():
+                raise ValueError("inputs must be contiguous on the plan device")
+            if tensor.requires_grad:
+                raise ValueError("inference only: detach tensors requiring gradients")
+
+    def run(self, q, k, v):
+        """Decode one token per sequence; returns the borrowed FP32 [B, Hq, D] output."""
+        self._check(q, k, v)
+        self._extension.decode(q, k, v, self._table, self._lengths, self._numerator, self._stats,
+                               self._out, self.split_tokens, self._merge_mode)
+        return self._out
+
+    def run_partial(self, q, k, v):
+        """Partition stage only (fills the workspace); for stage timing."""
+        self._check(q, k, v)
+        self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
+                                self.split_tokens)
+
+    def run_merge(self):
+        """Merge stage only, from the current workspace; returns the borrowed output."""
+        self._extension.merge(self._numerator, self._stats, self._out, self._merge_mode)
+        return self._out

@@ -1,0 +1,144 @@
+"""Host-side boundary checks that need no GPU.
+
+* DecodePlan constructor validation (reference runtime.py:33-60): every check
+  that precedes the device check raises the reference's exception type.
+* The C-ABI library loads, exports every function include/paged_decode.h
+  declares, and rejects invalid arguments with the documented status codes
+  before touching the GPU.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from paged_decode import cabi
+from paged_decode.layout import Layout
+from paged_decode.runtime import DecodePlan
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "paged_decode.h"
+
+
+def plan_args():
+    return Layout(1, 8, 2, 64, 16, 8), np.arange(8, dtype=np.int32)[None], np.array([127])
+
+
+@pytest.mark.parametrize("kwargs,exc", [
+    (dict(merge="fast"), ValueError),
+    (dict(split_tokens=0), ValueError),
+    (dict(split_tokens=True), ValueError),
+    (dict(split_tokens=2.0), ValueError),
+    (dict(split_tokens=np.int64(4)), ValueError),
+    (dict(split_tokens=1048577), ValueError),
+    (dict(device="cpu"), ValueError),
+])
+def test_plan_rejects_bad_arguments(kwargs, exc):
+    layout, table, lengths = plan_args()
+    with pytest.raises(exc):
+        DecodePlan(layout, table, lengths, **kwargs)
+
+
+@pytest.mark.parametrize("layout", [Layout(1, 8, 2, 96, 16, 8), Layout(1, 8, 2, 64, 8, 8),
+                                    Layout(65536, 8, 2, 64, 16, 8), Layout(1, 65536 * 2, 2, 64, 16, 8)])
+def test_plan_rejects_unsupported_layouts(layout):
+    with pytest.raises(ValueError):
+        DecodePlan(layout, np.zeros((layout.batch, 8), dtype=np.int32), np.zeros(layout.batch, dtype=np.int32))
+
+
+def test_plan_rejects_bad_metadata_and_limits():
+    layout = Layout(1, 8, 2, 64, 16, 8)
+    with pytest.raises(ValueError):
+        DecodePlan(layout, np.array([[0, 9]]), np.array([20]))            # live page out of range
+    with pytest.raises(TypeError):
+        DecodePlan(layout, np.array([[0., 1.]]), np.array([20]))
+    wide = Layout(1, 8, 2, 64, 16, 65537)
+    with pytest.raises(ValueError):
+        DecodePlan(wide, np.zeros((1, 65537), dtype=np.int32), np.array([1]))  # width > 65536
+    long = Layout(1, 8, 2, 64, 32, 40000)
+    with pytest.raises(ValueError):
+        DecodePlan(long, np.arange(40000, dtype=np.int32)[None], np.array([1048577]))  # > 1M tokens
+    with pytest.raises(ValueError):
+        DecodePlan(long, np.arange(40000, dtype=np.int32)[None], np.array([70000]), split_tokens=1)
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(pd_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert header_functions() == sorted(cabi.PROTOTYPES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = cabi.load()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.pd_abi_version() == 1
+    assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4 * 32 * 16 * 130 * 4
+    assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
+    assert "success" in cabi.status_string(lib, cabi.PD_OK)
+    assert cabi.status_string(lib, 99) == "unknown status"
+
+
+def test_extension_exports_reference_entry():
+    from paged_decode.runtime import load_extension
+
+    ext = load_extension()
+    for name in ("decode", "partial", "merge", "workspace_bytes", "abi_version"):
+        assert hasattr(ext, name)
+    assert ext.workspace_bytes(4, 32, 128, 16) == 4 * 32 * 16 * 130 * 4
+
+
+def fake(n=1):
+    """Distinct non-null host addresses; validation rejects before any use."""
+    buf = (ctypes.c_char * (64 * n))()
+    return [ctypes.addressof(buf) + 64 * i for i in range(n)], buf
+
+
+BASE = dict(dtype=1, batch=4, query_heads=32, kv_heads=8, head_dim=128, page_size=16, table_width=256,
+            physical_pages=1024, splits=16, split_tokens=256, merge_mode=0)
+
+
+def call_decode(lib, ptrs, **over):
+    a = {**BASE, **over}
+    return lib.pd_decode(ptrs[0], ptrs[1], ptrs[2], a["dtype"], ptrs[3], ptrs[4], ptrs[5], ptrs[6], ptrs[7],
+                         a["batch"], a["query_heads"], a["kv_heads"], a["head_dim"], a["page_size"],
+                         a["table_width"], a["physical_pages"], a["splits"], a["split_tokens"],
+                         a["merge_mode"], None)
+
+
+@pytest.mark.parametrize("over,status", [
+    (dict(dtype=2), cabi.PD_ERR_DTYPE),
+    (dict(batch=0), cabi.PD_ERR_SHAPE),
+    (dict(batch=65536), cabi.PD_ERR_SHAPE),
+    (dict(query_heads=30), cabi.PD_ERR_SHAPE),
+    (dict(head_dim=96), cabi.PD_ERR_SHAPE),
+    (dict(page_size=8), cabi.PD_ERR_SHAPE),
+    (dict(table_width=65537), cabi.PD_ERR_SHAPE),
+    (dict(physical_pages=0), cabi.PD_ERR_SHAPE),
+    (dict(splits=0), cabi.PD_ERR_SPLIT),
+    (dict(splits=65536), cabi.PD_ERR_SPLIT),
+    (dict(split_tokens=0), cabi.PD_ERR_SPLIT),
+    (dict(split_tokens=(1 << 20) + 1), cabi.PD_ERR_SPLIT),
+    (dict(merge_mode=2), cabi.PD_ERR_MERGE),
+    (dict(merge_mode=1, splits=4097), cabi.PD_ERR_MERGE),
+])
+def test_c_abi_rejects_invalid_arguments(over, status):
+    lib = cabi.load()
+    ptrs, _keep = fake(8)
+    assert call_decode(lib, ptrs, **over) == status
+
+
+def test_c_abi_rejects_null_pointers():
+    lib = cabi.load()
+    ptrs, _keep = fake(8)
+    for i in range(8):
+        broken = list(ptrs)
+        broken[i] = None
+        assert call_decode(lib, broken) == cabi.PD_ERR_NULL_POINTER
+    assert lib.pd_decode_merge(None, ptrs[1], ptrs[2], 4, 32, 128, 16, 0, None) == cabi.PD_ERR_NULL_POINTER
+    assert lib.pd_decode_merge(ptrs[0], ptrs[1], ptrs[2], 4, 32, 128, 16, 7, None) == cabi.PD_ERR_MERGE
+    assert lib.pd_decode_partial(ptrs[0], ptrs[1], ptrs[2], 1, ptrs[3], ptrs[4], ptrs[5], ptrs[6],
+                                 4, 32, 8, 128, 16, 256, 1024, 0, 256, None) == cabi.PD_ERR_SPLIT
