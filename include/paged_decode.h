@@ -56,6 +56,8 @@ enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
 
 /* Largest partition count the LDS-bounded (shared) merge accepts. */
 #define PD_SHARED_MERGE_MAX_PARTS 4096
+/* Largest partition count the fused LDS-bounded merge accepts. */
+#define PD_FUSED_SHARED_MAX_PARTS 1024
 
 /*
  * Full decode: partition kernel then merge kernel, both on `stream`.
@@ -74,6 +76,24 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype,
               int batch, int query_heads, int kv_heads, int head_dim, int page_size,
               int table_width, int physical_pages, int splits, int split_tokens,
               int merge_mode, void* stream);
+
+/*
+ * Full decode in ONE launch: the partition kernel's last workgroup per
+ * (sequence, KV head) row runs the merge (serial or LDS-bounded, as
+ * merge_mode says) on that row's states. Same result contract as pd_decode;
+ * no reference counterpart beyond decode() itself (decode.cu:197-246), of which
+ * it is a faster schedule.
+ * `counters` is int32[batch * query_heads] of device memory, all zero before
+ * the first call; every call leaves it all zero again, so it needs no reset
+ * between calls or graph replays. Shared merge needs
+ * splits <= PD_FUSED_SHARED_MAX_PARTS.
+ */
+int pd_decode_fused(const void* q, const void* k, const void* v, int dtype,
+                    const int32_t* table, const int32_t* lengths,
+                    float* numerator, float* stats, int32_t* counters, float* out,
+                    int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                    int table_width, int physical_pages, int splits, int split_tokens,
+                    int merge_mode, void* stream);
 
 /*
  * Partition stage only (the first launch of pd_decode): fills numerator and
@@ -105,7 +125,7 @@ size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits);
 /* Static description of a status code (never NULL). */
 const char* pd_status_string(int status);
 
-/* ABI version of this header: bumped on any signature change. */
+/* ABI version of this header: bumped on any signature change (2: pd_decode_fused). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

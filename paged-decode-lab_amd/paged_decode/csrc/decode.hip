@@ -1,23 +1,29 @@
 // Split-K paged GQA decode attention for gfx950 (AMD Instinct MI355X).
 //
-// Implements the C ABI declared in include/paged_decode.h. Two launches per
-// decode call, both on the caller's stream:
+// Implements the C ABI declared in include/paged_decode.h. pd_decode makes two
+// launches per call, both on the caller's stream:
 //
-//  1. partial_kernel: one 256-thread workgroup per (partition, KV head [,
+//  1. partial_kernel: one workgroup of NW waves per (partition, KV head [,
 //     head tile], sequence). Each K/V row is loaded from HBM exactly once and
-//     used by every query head of the GQA group, held in registers. The four
-//     waves take contiguous quarters of the partition; inside a wave, a 16-byte
-//     load covers TPL consecutive tokens (lanes [r*LPT, (r+1)*LPT) hold token
-//     r's row), loads are double-buffered chunk by chunk, q.k is reduced with
-//     DPP row operations, and each token row r keeps its own online-softmax
-//     stream. Streams are combined within the wave by lane shuffles and across
-//     waves through LDS, leaving one (m, l, n[D]) state per query head and
-//     partition. Scores are kept in log2 units (scale * log2 e) and
-//     exponentiated with v_exp_f32.
+//     used by every query head of the GQA group, held in registers. The waves
+//     take contiguous shares of the partition; inside a wave, a 16-byte load
+//     covers TPL consecutive tokens (lanes [r*LPT, (r+1)*LPT) hold token r's
+//     row), chunks of NL loads stream through PD + 1 register buffers in fully
+//     unrolled blocks (PD chunks in flight), q.k is reduced with DPP row
+//     operations, page ids come from a lane-indexed window via v_readlane
+//     (requested at kernel start, in parallel with the length), and each token row r
+//     keeps its own online-softmax stream. Streams are combined within the
+//     wave by lane shuffles and across waves through LDS, leaving one
+//     (m, l, n[D]) state per query head and partition. Scores are kept in log2
+//     units (scale * log2 e) and exponentiated with v_exp_f32.
 //  2. merge_serial_kernel or merge_shared_kernel: max-corrected combination of
 //     the partition states of one (sequence, query head) row, one lane per
 //     output dimension; the shared variant computes each partition's weight
 //     once into LDS and is bounded to PD_SHARED_MERGE_MAX_PARTS partitions.
+//
+// pd_decode_fused runs the same merge algebra (serial or LDS-weighted) inside
+// the partition kernel: the last workgroup to finish a row, detected with a
+// device-scope arrival counter, combines that row's states. One launch per call.
 //
 // Semantics follow reference src/paged_decode/csrc/decode.cu:26-168 (online
 // softmax and merge algebra, empty rows -> 0, l > 0 merge guard, page-id guard)
@@ -25,6 +31,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cfloat>
 #include <cstdint>
 
@@ -33,8 +40,6 @@
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kPartialWaves = 4;
-constexpr int kPartialThreads = kWave * kPartialWaves;
 constexpr float kNoToken = -FLT_MAX;  // running max before any live token
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -101,6 +106,13 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Partition states (max, denominator) are float pairs. Merge loops are
+// branch-free and unrolled so the loads of kMergeUnroll states are in flight
+// together; a data-dependent branch per state would chain their latencies.
+constexpr int kMergeUnroll = 8;
+
+__device__ __forceinline__ float2 load_state(const float2* st, int j) { return st[j]; }
+
 // ---------------------------------------------------------------------------
 // Element types. A lane moves 16 bytes per load: 8 halves or 4 floats.
 template <typename T>
@@ -150,6 +162,13 @@ struct Elem<float> {
 // ---------------------------------------------------------------------------
 // Partition kernel.
 
+// Fused-merge modes of the partition kernel (PartialParams::fuse).
+enum FuseMode { kFuseNone = 0, kFuseSerial = 1, kFuseShared = 2 };
+
+// A chunk's scores may exceed the running max by up to 2^kRescaleSlack before
+// the accumulators are rescaled; weights then stay <= 2^8, far from overflow.
+constexpr float kRescaleSlack = 8.0f;
+
 struct PartialParams {
     const void* q;
     const void* k;
@@ -158,6 +177,8 @@ struct PartialParams {
     const int32_t* lengths;
     float* numerator;  // [B, Hq, splits, D]
     float* stats;      // [B, Hq, splits, 2]
+    float* out;        // [B, Hq, D], written by the fused merge
+    int32_t* counters; // [B * Hkv * head_tiles] arrival counters, zero between calls
     int query_heads;
     int group;       // query heads per KV head
     int head_tiles;  // ceil(group / GT)
@@ -166,6 +187,7 @@ struct PartialParams {
     int physical_pages;
     int splits;
     int split_tokens;
+    int fuse;              // FuseMode
     uint32_t token_bytes;  // bytes between consecutive tokens of a page (kv_heads * D * elem)
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) / sqrt(D)
@@ -178,11 +200,20 @@ struct Chunk {
     uint32_t live;  // bit i: group i addresses a live page inside the wave's range
 };
 
+// Floats of dynamic LDS the partition kernel needs: the per-wave states of the
+// workgroup combine, or (fused LDS-bounded merge) one weight per head tile and
+// partition, whichever is larger; the two uses never overlap in time.
+template <int D, int GT, int NW>
+constexpr int wave_state_floats() { return NW * GT * (D + 2); }
+
 // T: element type; D: head dim; GT: query heads per tile (the GQA group, padded
-// to a power of two, or a slice of it); NL: 16-byte loads per chunk per lane.
-template <typename T, int D, int GT, int NL>
-__global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialParams p) {
+// to a power of two, or a slice of it); NL: 16-byte loads of K (and of V) per
+// lane per chunk; NW: waves per workgroup; PD: chunks in flight ahead of the
+// one being consumed; NC: chunks per straight-line block.
+template <typename T, int D, int GT, int NL, int NW, int PD, int NC>
+__global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams p) {
     using E = Elem<T>;
+    constexpr int kThreads = kWave * NW;
     constexpr int EPL = E::kPerLoad;  // elements per lane per load
     constexpr int LPT = D / EPL;      // lanes per token row
     constexpr int TPL = kWave / LPT;  // tokens per load
@@ -190,7 +221,9 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
     static_assert(TPL >= 2 && TPL <= 8 && (TPL & (TPL - 1)) == 0, "unsupported row split");
     static_assert(NL <= 32, "live mask is 32 bits");
 
-    __shared__ float wave_state[kPartialWaves][GT][D + 2];
+    extern __shared__ float smem[];
+    float (*wave_state)[GT][D + 2] = reinterpret_cast<float (*)[GT][D + 2]>(smem);  // [NW][GT][D+2]
+    __shared__ int is_last;
 
     const int split = blockIdx.x;
     const int kv_head = blockIdx.y / p.head_tiles;
@@ -202,14 +235,24 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
     const int col = lane % LPT;
 
     // Partition [tb, te) of sequence b; the end is clamped to the table capacity
-    // (decode.cu:42-44). Quarters are cut on TPL multiples.
+    // (decode.cu:42-44). Wave shares are contiguous and cut on TPL multiples.
     const int page_size = 1 << p.page_shift;
     const int capacity = p.table_width << p.page_shift;
-    const int len = max(0, min(p.lengths[b], capacity));
+    const int32_t* pages = p.table + static_cast<int64_t>(b) * p.table_width;
+    // The page-id window (lane i holds the id of logical page window + i) is
+    // requested before the sequence length is known, in parallel with it: it
+    // starts at this wave's first page for a full-length partition, which is
+    // exact for every partition but a sequence's last (re-aimed below).
     const int64_t first = static_cast<int64_t>(split) * p.split_tokens;
+    const int per_full = ((p.split_tokens + NW - 1) / NW + TPL - 1) / TPL * TPL;
+    int window = static_cast<int>(min<int64_t>(first + static_cast<int64_t>(wave) * per_full, capacity - 1)) >>
+                 p.page_shift;
+    int window_ids = pages[min(window + lane, p.table_width - 1)];
+
+    const int len = max(0, min(p.lengths[b], capacity));
     const int tb = static_cast<int>(min<int64_t>(first, len));
     const int te = static_cast<int>(min<int64_t>(first + p.split_tokens, len));
-    int per = (te - tb + kPartialWaves - 1) / kPartialWaves;
+    int per = (te - tb + NW - 1) / NW;
     per = (per + TPL - 1) / TPL * TPL;
     const int wb = min(tb + wave * per, te);
     const int we = min(wb + per, te);
@@ -235,16 +278,20 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
         for (int j = 0; j < EPL; ++j) acc[g][j] = 0.0f;
     }
 
-    const int32_t* pages = p.table + static_cast<int64_t>(b) * p.table_width;
     const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(kv_head) * D * sizeof(T);
     const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(kv_head) * D * sizeof(T);
     // Groups with no live token are redirected to this sequence's q row: always
     // mapped, finite, and the same line for every lane.
     const char* park = reinterpret_cast<const char*>(q_base);
     const uint32_t lane_bytes = static_cast<uint32_t>(col) * 16u;
+    int rb = wb, re = wb;  // token range of the current window segment
 
     // Issue the 2*NL loads of the chunk whose first aligned group starts at c0.
-    auto issue = [&](Chunk<NL>& ch, int c0) {
+    // Page ids come from `window_ids` (lane i holds the id of logical page
+    // window + i) through v_readlane, so no scalar load sits on the issue path.
+    // Lanes whose token lies outside the wave's range read a token inside it
+    // (same page), so every value that reaches the FMAs is live data.
+    auto issue = [&](Chunk<NL>& ch, int c0, int window_ids, int window) {
         const char* kp[NL];
         const char* vp[NL];
         uint32_t off[NL];
@@ -252,12 +299,13 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int g = c0 + i * TPL;  // wave-uniform, multiple of TPL
-            int lo = max(g, wb);
-            int hi = min(g + TPL, we) - 1;
-            if (lo > hi) lo = hi = we - 1;
+            int lo = max(g, rb);
+            int hi = min(g + TPL, re) - 1;
+            if (lo > hi) lo = hi = re - 1;
             // All tokens of [lo, hi] share one page because TPL divides page_size.
-            const int page = pages[lo >> p.page_shift];
-            const bool ok = g < we && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
+            const int slot = min(max((lo >> p.page_shift) - window, 0), kWave - 1);
+            const int page = __builtin_amdgcn_readlane(window_ids, slot);
+            const bool ok = g < re && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
             live |= static_cast<uint32_t>(ok) << i;
             const int t = min(max(g + row, lo), hi);
             const uint64_t page_off = static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
@@ -276,7 +324,9 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // Fold one chunk into the per-row online-softmax state.
+    // Fold one chunk into the per-row online-softmax state. The running max is
+    // raised (and the accumulators rescaled) only when a chunk's max exceeds it
+    // by more than kRescaleSlack, a wave-uniform and rare branch.
     auto consume = [&](const Chunk<NL>& ch, int c0) {
         float s[NL][GT];
 #pragma unroll
@@ -284,30 +334,43 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
             const int t = c0 + i * TPL + row;
             // Bitwise '&' keeps this branch-free (a '&&' on the uniform bit
             // becomes a scalar branch per load).
-            const bool valid = (((ch.live >> i) & 1u) != 0u) & (t >= wb) & (t < we);
+            const bool valid = (((ch.live >> i) & 1u) != 0u) & (t >= rb) & (t < re);
 #pragma unroll
             for (int g = 0; g < GT; ++g) {
                 const float d = group_sum<LPT>(E::dot(qv[g], ch.k[i]));
-                s[i][g] = valid ? d * p.scale_log2 : -INFINITY;
+                s[i][g] = valid ? d : -INFINITY;
+            }
+        }
+        float chunk_max[GT];
+        bool grow = false;
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            float cm = s[0][g];
+#pragma unroll
+            for (int i = 1; i < NL; ++i) cm = fmaxf(cm, s[i][g]);
+            chunk_max[g] = cm * p.scale_log2;
+            grow |= chunk_max[g] > m[g] + kRescaleSlack;
+        }
+        if (__any(grow)) {
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                const float m_new = fmaxf(m[g], chunk_max[g]);
+                const float alpha = fast_exp2(m[g] - m_new);  // 0 after kNoToken, else <= 1
+                m[g] = m_new;
+                l[g] *= alpha;
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) acc[g][j] *= alpha;
             }
         }
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
-            float chunk_max = s[0][g];
-#pragma unroll
-            for (int i = 1; i < NL; ++i) chunk_max = fmaxf(chunk_max, s[i][g]);
-            const float m_new = fmaxf(m[g], chunk_max);
-            const float alpha = fast_exp2(m[g] - m_new);  // 1 while no token seen, 0 after the first
-            m[g] = m_new;
-            float sum = l[g] * alpha;
+            float sum = l[g];
 #pragma unroll
             for (int i = 0; i < NL; ++i) {
-                s[i][g] = fast_exp2(s[i][g] - m_new);  // exp2(-inf) = 0 for masked tokens
+                s[i][g] = fast_exp2(fmaf(s[i][g], p.scale_log2, -m[g]));  // 0 for masked tokens
                 sum += s[i][g];
             }
             l[g] = sum;
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) acc[g][j] *= alpha;
         }
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
@@ -320,28 +383,30 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
         }
     };
 
-    if (wb < we) {
-        const int g0 = wb & ~(TPL - 1);
-        const int chunks = (we - g0 + CT - 1) / CT;
-        Chunk<NL> a, c;
-        issue(a, g0);
-        // Ping-pong: the next chunk's loads are in flight while this one is
-        // consumed. The steady loop and the tail issue unconditionally inside
-        // straight-line blocks whose contents differ, so the wait counters
-        // only ever cover the buffer being consumed.
-        int n = 0;
-        for (; n + 2 < chunks; n += 2) {
-            issue(c, g0 + (n + 1) * CT);
-            consume(a, g0 + n * CT);
-            issue(a, g0 + (n + 2) * CT);
-            consume(c, g0 + (n + 1) * CT);
+    // The wave's range is walked in segments of at most 64 pages (one window of
+    // page ids); partitions up to 63 pages per wave take a single segment.
+    for (rb = wb; rb < we; rb = re) {
+        if ((rb >> p.page_shift) != window) {
+            window = rb >> p.page_shift;
+            window_ids = pages[min(window + lane, p.table_width - 1)];
         }
-        if (n + 1 < chunks) {
-            issue(c, g0 + (n + 1) * CT);
-            consume(a, g0 + n * CT);
-            consume(c, g0 + (n + 1) * CT);
-        } else {
-            consume(a, g0 + n * CT);
+        re = min(we, (window + kWave) << p.page_shift);
+        // Blocks of NC chunks run as fully unrolled straight-line code with PD
+        // chunks in flight ahead of the one being consumed; the PD + 1 buffers
+        // rotate by compile-time index, so no register holding a pending load
+        // is ever copied and every wait covers exactly one chunk. (Loads kept
+        // in flight across a loop back-edge make the compiler wait for all of
+        // them.) The pipeline fills and drains once per block.
+        for (int s = rb & ~(TPL - 1); s < re; s += NC * CT) {
+            Chunk<NL> buf[PD + 1];
+#pragma unroll
+            for (int n = 0; n < PD; ++n) issue(buf[n], s + n * CT, window_ids, window);
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                if (s + n * CT >= re) break;
+                if (n + PD < NC) issue(buf[(n + PD) % (PD + 1)], s + (n + PD) * CT, window_ids, window);
+                consume(buf[n % (PD + 1)], s + n * CT);
+            }
         }
     }
 
@@ -378,18 +443,18 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
     }
     __syncthreads();
 
-    // Combine the four waves; one partition state per query head.
-    for (int idx = threadIdx.x; idx < GT * D; idx += kPartialThreads) {
+    // Combine the waves; one partition state per query head.
+    for (int idx = threadIdx.x; idx < GT * D; idx += kThreads) {
         const int g = idx / D;
         const int d = idx - g * D;
         if (g >= heads_here) break;
         float mx = kNoToken;
 #pragma unroll
-        for (int w = 0; w < kPartialWaves; ++w)
+        for (int w = 0; w < NW; ++w)
             if (wave_state[w][g][D + 1] > 0.0f) mx = fmaxf(mx, wave_state[w][g][D]);
         float num = 0.0f, den = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kPartialWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float lw = wave_state[w][g][D + 1];
             if (lw > 0.0f) {
                 const float f = fast_exp2(wave_state[w][g][D] - mx);
@@ -404,31 +469,114 @@ __global__ void __launch_bounds__(kPartialThreads) partial_kernel(const PartialP
             p.stats[part * 2 + 1] = den;
         }
     }
+    if (p.fuse == kFuseNone) return;
+
+    // Fused merge: the last workgroup to finish a (sequence, KV head, tile) row
+    // combines that row's partition states. Release: every thread's stores are
+    // made device-visible before the arrival is counted.
+    __threadfence();
+    __syncthreads();
+    const int64_t row_id = static_cast<int64_t>(b) * gridDim.y + blockIdx.y;
+    if (threadIdx.x == 0) is_last = atomicAdd(&p.counters[row_id], 1) == p.splits - 1;
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();  // acquire: observe the other workgroups' states
+    const float2* st_base = reinterpret_cast<const float2*>(p.stats);
+    if (p.fuse == kFuseShared) {
+        // LDS-bounded: one weight per (head, partition), computed once by the
+        // wave that owns the head.
+        float* weight = smem;                         // [GT][splits]; wave states are dead now
+        float* row_den = smem + GT * p.splits;        // [GT]
+        for (int g = wave; g < heads_here; g += NW) {
+            const float2* st = st_base + (q_row + g) * p.splits;
+            float mx = kNoToken;
+            for (int j = lane; j < p.splits; j += kWave) {
+                const float2 s = load_state(st, j);
+                mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
+            }
+            mx = wave_max(mx);
+            float den = 0.0f;
+            for (int j = lane; j < p.splits; j += kWave) {
+                const float2 s = load_state(st, j);
+                const float f = s.y > 0.0f ? fast_exp2(s.x - mx) : 0.0f;
+                weight[g * p.splits + j] = f;
+                den = fmaf(f, s.y, den);
+            }
+            den = wave_sum(den);
+            if (lane == 0) row_den[g] = den;
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < heads_here * D; idx += kThreads) {
+            const int g = idx / D;
+            const int d = idx - g * D;
+            const float* num = p.numerator + (q_row + g) * p.splits * D + d;
+            const float* w = weight + g * p.splits;
+            float acc_d = 0.0f;
+#pragma unroll kMergeUnroll
+            for (int j = 0; j < p.splits; ++j) {
+                const float n = num[static_cast<int64_t>(j) * D];
+                acc_d = w[j] > 0.0f ? fmaf(w[j], n, acc_d) : acc_d;
+            }
+            const float den = row_den[g];
+            p.out[(q_row + g) * D + d] = den > 0.0f ? acc_d / den : 0.0f;
+        }
+    } else {
+        // Serial: every lane scans the row's states itself.
+        for (int idx = threadIdx.x; idx < heads_here * D; idx += kThreads) {
+            const int g = idx / D;
+            const int d = idx - g * D;
+            const float2* st = st_base + (q_row + g) * p.splits;
+            float mx = kNoToken;
+#pragma unroll kMergeUnroll
+            for (int j = 0; j < p.splits; ++j) {
+                const float2 s = load_state(st, j);
+                mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
+            }
+            const float* num = p.numerator + (q_row + g) * p.splits * D + d;
+            float den = 0.0f, acc_d = 0.0f;
+#pragma unroll kMergeUnroll
+            for (int j = 0; j < p.splits; ++j) {
+                const float2 s = load_state(st, j);
+                const float n = num[static_cast<int64_t>(j) * D];
+                const bool live = s.y > 0.0f;
+                const float f = live ? fast_exp2(s.x - mx) : 0.0f;
+                den = live ? fmaf(f, s.y, den) : den;
+                acc_d = live ? fmaf(f, n, acc_d) : acc_d;
+            }
+            p.out[(q_row + g) * D + d] = den > 0.0f ? acc_d / den : 0.0f;
+        }
+    }
+    if (threadIdx.x == 0) p.counters[row_id] = 0;  // ready for the next call
 }
 
 // ---------------------------------------------------------------------------
 // Merge kernels: one workgroup per (sequence, query head) row, one lane per
 // output dimension. A state with l == 0 is the identity (decode.cu:94-107).
 
+// Serial: every lane scans all partition states itself (no LDS).
 template <int D>
 __global__ void __launch_bounds__(D) merge_serial_kernel(const float* __restrict__ numerator,
                                                          const float* __restrict__ stats,
                                                          float* __restrict__ out, int parts) {
     const int64_t row = blockIdx.x;
     const int d = threadIdx.x;
-    const float* st = stats + row * parts * 2;
+    const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
     float mx = kNoToken;
-    for (int j = 0; j < parts; ++j)
-        if (st[2 * j + 1] > 0.0f) mx = fmaxf(mx, st[2 * j]);
+#pragma unroll kMergeUnroll
+    for (int j = 0; j < parts; ++j) {
+        const float2 s = load_state(st, j);
+        mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
+    }
     const float* num = numerator + row * parts * D + d;
     float den = 0.0f, acc = 0.0f;
+#pragma unroll kMergeUnroll
     for (int j = 0; j < parts; ++j) {
-        const float lj = st[2 * j + 1];
-        if (lj > 0.0f) {
-            const float f = fast_exp2(st[2 * j] - mx);
-            den = fmaf(f, lj, den);
-            acc = fmaf(f, num[static_cast<int64_t>(j) * D], acc);
-        }
+        const float2 s = load_state(st, j);
+        const float n = num[static_cast<int64_t>(j) * D];
+        const bool live = s.y > 0.0f;
+        const float f = live ? fast_exp2(s.x - mx) : 0.0f;
+        den = live ? fmaf(f, s.y, den) : den;
+        acc = live ? fmaf(f, n, acc) : acc;
     }
     out[row * D + d] = den > 0.0f ? acc / den : 0.0f;
 }
@@ -444,11 +592,13 @@ __global__ void __launch_bounds__(D) merge_shared_kernel(const float* __restrict
     const int d = threadIdx.x;
     const int lane = d % kWave;
     const int wave = d / kWave;
-    const float* st = stats + row * parts * 2;
+    const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
 
     float mx = kNoToken;
-    for (int j = d; j < parts; j += D)
-        if (st[2 * j + 1] > 0.0f) mx = fmaxf(mx, st[2 * j]);
+    for (int j = d; j < parts; j += D) {
+        const float2 s = load_state(st, j);
+        mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
+    }
     mx = wave_max(mx);
     if (lane == 0) scratch[0][wave] = mx;
     __syncthreads();
@@ -458,10 +608,10 @@ __global__ void __launch_bounds__(D) merge_shared_kernel(const float* __restrict
 
     float den = 0.0f;
     for (int j = d; j < parts; j += D) {
-        const float lj = st[2 * j + 1];
-        const float f = lj > 0.0f ? fast_exp2(st[2 * j] - mx) : 0.0f;
+        const float2 s = load_state(st, j);
+        const float f = s.y > 0.0f ? fast_exp2(s.x - mx) : 0.0f;
         weight[j] = f;
-        den = fmaf(f, lj, den);
+        den = fmaf(f, s.y, den);
     }
     den = wave_sum(den);
     if (lane == 0) scratch[1][wave] = den;
@@ -472,7 +622,13 @@ __global__ void __launch_bounds__(D) merge_shared_kernel(const float* __restrict
 
     const float* num = numerator + row * parts * D + d;
     float acc = 0.0f;
-    for (int j = 0; j < parts; ++j) acc = fmaf(weight[j], num[static_cast<int64_t>(j) * D], acc);
+#pragma unroll kMergeUnroll
+    for (int j = 0; j < parts; ++j) {
+        // A state with weight 0 (empty partition) contributes nothing, whatever
+        // its numerator holds.
+        const float n = num[static_cast<int64_t>(j) * D];
+        acc = weight[j] > 0.0f ? fmaf(weight[j], n, acc) : acc;
+    }
     out[row * D + d] = den > 0.0f ? acc / den : 0.0f;
 }
 
@@ -496,37 +652,56 @@ int check_common(const void* q, const void* k, const void* v, int dtype, const i
 
 int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LAUNCH; }
 
+// Waves per partition workgroup and 16-byte loads of K (and of V) per lane per
+// chunk, chunks in flight ahead of the one being consumed, and chunks per
+// straight-line block.
+#ifndef PD_PARTIAL_WAVES
+#define PD_PARTIAL_WAVES 4
+#endif
+#ifndef PD_CHUNK_LOADS
+#define PD_CHUNK_LOADS 1
+#endif
+#ifndef PD_PREFETCH
+#define PD_PREFETCH 4
+#endif
+#ifndef PD_BLOCK_CHUNKS
+#define PD_BLOCK_CHUNKS 16
+#endif
+
 template <typename T, int D, int GT>
 int launch_partial(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    constexpr int NL = GT >= 8 ? 4 : 8;
+    constexpr int NW = PD_PARTIAL_WAVES;
+    constexpr int NL = PD_CHUNK_LOADS;
+    constexpr int PD = PD_PREFETCH;
+    constexpr int NC = PD_BLOCK_CHUNKS;
+    size_t floats = static_cast<size_t>(wave_state_floats<D, GT, NW>());
+    if (prm.fuse == kFuseShared) floats = std::max(floats, static_cast<size_t>(GT) * (prm.splits + 1));
     const dim3 grid(prm.splits, kv_heads * prm.head_tiles, batch);
-    hipLaunchKernelGGL((partial_kernel<T, D, GT, NL>), grid, dim3(kPartialThreads), 0, stream, prm);
+    hipLaunchKernelGGL((partial_kernel<T, D, GT, NL, NW, PD, NC>), grid, dim3(kWave * NW), floats * sizeof(float),
+                       stream, prm);
     return launch_status();
 }
 
+// Head tile: the GQA group padded to 1, 2, 4 or 8 query heads; larger groups
+// are cut into tiles of 8 (one workgroup per tile).
+int head_tile(int group) { return group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8; }
+
 template <typename T, int D>
 int dispatch_group(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    const int group = prm.group;
-    if (group == 1) {
-        prm.head_tiles = 1;
-        return launch_partial<T, D, 1>(prm, batch, kv_heads, stream);
+    const int gt = head_tile(prm.group);
+    prm.head_tiles = (prm.group + gt - 1) / gt;
+    switch (gt) {
+        case 1: return launch_partial<T, D, 1>(prm, batch, kv_heads, stream);
+        case 2: return launch_partial<T, D, 2>(prm, batch, kv_heads, stream);
+        case 4: return launch_partial<T, D, 4>(prm, batch, kv_heads, stream);
+        default: return launch_partial<T, D, 8>(prm, batch, kv_heads, stream);
     }
-    if (group == 2) {
-        prm.head_tiles = 1;
-        return launch_partial<T, D, 2>(prm, batch, kv_heads, stream);
-    }
-    if (group <= 4) {
-        prm.head_tiles = 1;
-        return launch_partial<T, D, 4>(prm, batch, kv_heads, stream);
-    }
-    prm.head_tiles = (group + 7) / 8;
-    return launch_partial<T, D, 8>(prm, batch, kv_heads, stream);
 }
 
 int run_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-                const int32_t* lengths, float* numerator, float* stats, int batch, int query_heads,
-                int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
-                int splits, int split_tokens, hipStream_t stream) {
+                const int32_t* lengths, float* numerator, float* stats, float* out, int32_t* counters,
+                int fuse, int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                int table_width, int physical_pages, int splits, int split_tokens, hipStream_t stream) {
     const size_t elem = dtype == PD_DTYPE_F16 ? 2 : 4;
     PartialParams prm{};
     prm.q = q;
@@ -536,6 +711,9 @@ int run_partial(const void* q, const void* k, const void* v, int dtype, const in
     prm.lengths = lengths;
     prm.numerator = numerator;
     prm.stats = stats;
+    prm.out = out;
+    prm.counters = counters;
+    prm.fuse = fuse;
     prm.query_heads = query_heads;
     prm.group = query_heads / kv_heads;
     prm.page_shift = page_size == 16 ? 4 : 5;
@@ -597,9 +775,9 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, co
                                     kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                                     split_tokens);
     if (status != PD_OK) return status;
-    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch, query_heads, kv_heads,
-                       head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                       static_cast<hipStream_t>(stream));
+    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, nullptr, nullptr, kFuseNone, batch,
+                       query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                       split_tokens, static_cast<hipStream_t>(stream));
 }
 
 int pd_decode_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads,
@@ -621,10 +799,30 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
         status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch, query_heads, kv_heads,
-                         head_dim, page_size, table_width, physical_pages, splits, split_tokens, s);
+    status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, nullptr, nullptr, kFuseNone, batch,
+                         query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                         split_tokens, s);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode, s);
+}
+
+int pd_decode_fused(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
+                    const int32_t* lengths, float* numerator, float* stats, int32_t* counters, float* out,
+                    int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
+                    int physical_pages, int splits, int split_tokens, int merge_mode, void* stream) {
+    int status = check_common(q, k, v, dtype, table, lengths, numerator, stats, batch, query_heads,
+                              kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                              split_tokens);
+    if (status == PD_OK)
+        status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
+    if (status == PD_OK && !counters) status = PD_ERR_NULL_POINTER;
+    if (status == PD_OK && merge_mode == PD_MERGE_SHARED && splits > PD_FUSED_SHARED_MAX_PARTS)
+        status = PD_ERR_MERGE;
+    if (status != PD_OK) return status;
+    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, out, counters,
+                       merge_mode == PD_MERGE_SHARED ? kFuseShared : kFuseSerial, batch, query_heads,
+                       kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
+                       static_cast<hipStream_t>(stream));
 }
 
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {
@@ -645,6 +843,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 1; }
+int pd_abi_version(void) { return 2; }
 
 }  // extern "C"
