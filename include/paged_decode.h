@@ -13,11 +13,12 @@
  * t % page_size. Tokens whose page id is outside [0, physical_pages) are
  * skipped, never dereferenced.
  *
- * Work is cut into `splits` partitions of `split_tokens` tokens; every
- * partition leaves one max-corrected softmax state per query head in the
- * caller's workspace, and a merge kernel combines them:
- *   numerator [batch, query_heads, splits, head_dim]  float32
- *   stats     [batch, query_heads, splits, 2]         float32 (max, denominator)
+ * Work is cut into `splits` partitions of `split_tokens` tokens, each cut into
+ * four contiguous quarters; every quarter leaves one max-corrected softmax
+ * state per query head in the caller's workspace, and a merge combines them:
+ *   numerator [batch, query_heads, 4 * splits, head_dim]  float32
+ *   stats     [batch, query_heads, 4 * splits, 2]         float32 (max, denominator)
+ * (state 4 * split + quarter; the reference's workspace shape, decode.cu:223-231).
  * The workspace needs no initialisation; every element is written per call.
  *
  * All pointers are device pointers. `stream` is a hipStream_t (passed as
@@ -54,10 +55,8 @@ enum pd_dtype { PD_DTYPE_F32 = 0, PD_DTYPE_F16 = 1 };
 /* Merge strategies, numbered as the reference's merge_mode argument. */
 enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
 
-/* Largest partition count the LDS-bounded (shared) merge accepts. */
+/* Largest state count (4 * splits) the LDS-bounded (shared) merge accepts. */
 #define PD_SHARED_MERGE_MAX_PARTS 4096
-/* Largest partition count the fused LDS-bounded merge accepts. */
-#define PD_FUSED_SHARED_MAX_PARTS 1024
 
 /*
  * Full decode: partition kernel then merge kernel, both on `stream`.
@@ -68,7 +67,7 @@ enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
  * query_heads <= 65535; head_dim in {64, 128}; page_size in {16, 32};
  * query_heads % kv_heads == 0; 1 <= table_width <= 65536; 1 <= splits <= 65535;
  * 1 <= split_tokens <= 1048576; merge_mode PD_MERGE_SHARED needs
- * splits <= PD_SHARED_MERGE_MAX_PARTS.
+ * 4 * splits <= PD_SHARED_MERGE_MAX_PARTS.
  */
 int pd_decode(const void* q, const void* k, const void* v, int dtype,
               const int32_t* table, const int32_t* lengths,
@@ -85,8 +84,9 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype,
  * it is a faster schedule.
  * `counters` is int32[batch * query_heads] of device memory, all zero before
  * the first call; every call leaves it all zero again, so it needs no reset
- * between calls or graph replays. Shared merge needs
- * splits <= PD_FUSED_SHARED_MAX_PARTS.
+ * between calls or graph replays. When the LDS-bounded merge of a row's
+ * states does not fit beside the partition kernel it runs as its own kernel
+ * (two launches, same algorithm).
  */
 int pd_decode_fused(const void* q, const void* k, const void* v, int dtype,
                     const int32_t* table, const int32_t* lengths,
@@ -107,7 +107,7 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype,
                       void* stream);
 
 /*
- * Merge stage only (the second launch of pd_decode): combines `splits`
+ * Merge stage only (the second launch of pd_decode): combines the 4 * splits
  * states per (sequence, query head) into out. Replaces the merge_decode /
  * merge_shared launches of reference decode.cu:183-193.
  */
@@ -116,16 +116,18 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out,
                     int merge_mode, void* stream);
 
 /*
- * Bytes of numerator + stats for a plan; the counterpart of the reference's
- * DecodePlan.workspace_bytes (src/paged_decode/runtime.py:71-73) for this
- * workspace layout. Returns 0 for non-positive arguments.
+ * Bytes of numerator + stats for a plan: batch * query_heads * 4 * splits *
+ * (head_dim + 2) * 4, the reference's DecodePlan.workspace_bytes
+ * (src/paged_decode/runtime.py:71-73, docs/DESIGN.md:69-76). Returns 0 for
+ * non-positive arguments.
  */
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits);
 
 /* Static description of a status code (never NULL). */
 const char* pd_status_string(int status);
 
-/* ABI version of this header: bumped on any signature change (2: pd_decode_fused). */
+/* ABI version of this header: bumped on any signature or layout change
+ * (2: pd_decode_fused; 3: four states per partition). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

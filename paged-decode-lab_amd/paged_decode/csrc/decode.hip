@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <cstdint>
+#include <type_traits>
 
 #include "paged_decode.h"
 
@@ -160,10 +161,20 @@ struct Elem<float> {
 };
 
 // ---------------------------------------------------------------------------
-// Partition kernel.
+// Partition kernels.
+//
+// Both kernels cut every partition of split_tokens tokens into kQuarters
+// contiguous quarters and give each quarter of each KV head (and head tile) to
+// one wave, which leaves its own max-corrected state per query head in the
+// workspace: numerator [B, Hq, 4 * splits, D] and stats [B, Hq, 4 * splits, 2],
+// state index 4 * split + quarter. Waves never combine with each other, so the
+// kernels have no workgroup barrier on the hot path.
 
-// Fused-merge modes of the partition kernel (PartialParams::fuse).
+// Fused-merge modes (PartialParams::fuse).
 enum FuseMode { kFuseNone = 0, kFuseSerial = 1, kFuseShared = 2 };
+
+// States per partition (quarters of the partition).
+constexpr int kQuarters = 4;
 
 // A chunk's scores may exceed the running max by up to 2^kRescaleSlack before
 // the accumulators are rescaled; weights then stay <= 2^8, far from overflow.
@@ -175,14 +186,17 @@ struct PartialParams {
     const void* v;
     const int32_t* table;
     const int32_t* lengths;
-    float* numerator;  // [B, Hq, splits, D]
-    float* stats;      // [B, Hq, splits, 2]
-    float* out;        // [B, Hq, D], written by the fused merge
-    int32_t* counters; // [B * Hkv * head_tiles] arrival counters, zero between calls
+    float* numerator;   // [B, Hq, 4 * splits, D]
+    float* stats;       // [B, Hq, 4 * splits, 2]
+    float* out;         // [B, Hq, D], written by the fused merge
+    int32_t* counters;  // [B * gridDim.y] arrival counters, zero between calls
     int query_heads;
-    int group;       // query heads per KV head
-    int head_tiles;  // ceil(group / GT)
-    int page_shift;  // log2(page_size)
+    int group;          // query heads per KV head
+    int head_tiles;     // ceil(group / GT)
+    int heads_per_wg;   // KV heads per workgroup (hw)
+    int tiles_per_wg;   // head tiles per workgroup (tw)
+    int quarters_per_wg;  // partition quarters per workgroup (qw)
+    int page_shift;     // log2(page_size)
     int table_width;
     int physical_pages;
     int splits;
@@ -193,118 +207,158 @@ struct PartialParams {
     float scale_log2;      // log2(e) / sqrt(D)
 };
 
-template <int NL>
-struct Chunk {
-    u32x4 k[NL];
-    u32x4 v[NL];
-    uint32_t live;  // bit i: group i addresses a live page inside the wave's range
+// Which KV head, head tile and token range a wave owns. Workgroup x covers
+// quarter group (blockIdx.x % (4 / qw)) of partition blockIdx.x / (4 / qw);
+// workgroup y covers KV heads [hg * hw, hg * hw + hw) and head tiles
+// [tg * tw, tg * tw + tw); the wave index splits into (head, tile, quarter).
+struct WaveWork {
+    int split, quarter, kv_head, tile, wb, we;
+    int64_t q_row;   // first query-head row of the tile
+    int heads_here;  // live query heads in the tile
 };
 
-// Floats of dynamic LDS the partition kernel needs: the per-wave states of the
-// workgroup combine, or (fused LDS-bounded merge) one weight per head tile and
-// partition, whichever is larger; the two uses never overlap in time.
-template <int D, int GT, int NW>
-constexpr int wave_state_floats() { return NW * GT * (D + 2); }
+template <int GT, int ALIGN>
+__device__ __forceinline__ WaveWork wave_work(const PartialParams& p, int wave) {
+    WaveWork w;
+    const int qw = p.quarters_per_wg;
+    const int groups = kQuarters / qw;
+    const int qq = wave % qw;
+    const int tt = (wave / qw) % p.tiles_per_wg;
+    const int hh = wave / (qw * p.tiles_per_wg);
+    const int tile_groups = p.head_tiles / p.tiles_per_wg;
+    w.split = blockIdx.x / groups;
+    w.quarter = (blockIdx.x - w.split * groups) * qw + qq;
+    w.kv_head = (blockIdx.y / tile_groups) * p.heads_per_wg + hh;
+    w.tile = (blockIdx.y % tile_groups) * p.tiles_per_wg + tt;
+    const int b = blockIdx.z;
+    const int capacity = p.table_width << p.page_shift;
+    const int len = max(0, min(p.lengths[b], capacity));  // decode.cu:42-44
+    const int64_t first = static_cast<int64_t>(w.split) * p.split_tokens;
+    const int tb = static_cast<int>(min<int64_t>(first, len));
+    const int te = static_cast<int>(min<int64_t>(first + p.split_tokens, len));
+    int per = (te - tb + kQuarters - 1) / kQuarters;
+    per = (per + ALIGN - 1) / ALIGN * ALIGN;
+    w.wb = min(tb + w.quarter * per, te);
+    w.we = min(w.wb + per, te);
+    const int member0 = w.tile * GT;
+    w.heads_here = max(0, min(GT, p.group - member0));
+    w.q_row = static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(w.kv_head) * p.group + member0;
+    return w;
+}
 
-// T: element type; D: head dim; GT: query heads per tile (the GQA group, padded
-// to a power of two, or a slice of it); NL: 16-byte loads of K (and of V) per
-// lane per chunk; NW: waves per workgroup; PD: chunks in flight ahead of the
-// one being consumed; NC: chunks per straight-line block.
-template <typename T, int D, int GT, int NL, int NW, int PD, int NC>
-__global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams p) {
+// The first logical page a wave will read if its partition is full length:
+// lets the page-id window be requested before the sequence length arrives.
+template <int ALIGN>
+__device__ __forceinline__ int speculative_page(const PartialParams& p, int wave) {
+    const int qw = p.quarters_per_wg;
+    const int groups = kQuarters / qw;
+    const int split = blockIdx.x / groups;
+    const int quarter = (blockIdx.x - split * groups) * qw + wave % qw;
+    const int per_full = ((p.split_tokens + kQuarters - 1) / kQuarters + ALIGN - 1) / ALIGN * ALIGN;
+    const int capacity = p.table_width << p.page_shift;
+    const int64_t start = static_cast<int64_t>(split) * p.split_tokens + static_cast<int64_t>(quarter) * per_full;
+    return static_cast<int>(min<int64_t>(start, capacity - 1)) >> p.page_shift;
+}
+
+// Stores one wave's state for its GT heads. acc[g][e] lives in the row layout
+// (lanes [r*LPT, (r+1)*LPT) = token row r, dims col*EPL .. col*EPL+EPL-1) and
+// has already been summed over rows into the lanes of row 0; m and l for head g
+// are in lane g.
+template <int D, int GT, int EPL, int LPT>
+__device__ __forceinline__ void store_wave_state(const PartialParams& p, const WaveWork& w, int lane,
+                                                 const float (&acc)[GT][EPL], float m, float l) {
+    const int parts = kQuarters * p.splits;
+    const int part = w.split * kQuarters + w.quarter;
+    if (lane < LPT) {
+        const int col = lane;
+#pragma unroll
+        for (int g = 0; g < GT; ++g) {
+            if (g < w.heads_here) {
+                f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + g) * parts + part) * D + col * EPL);
+#pragma unroll
+                for (int e = 0; e < EPL; e += 4) dst[e / 4] = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
+            }
+        }
+    }
+    if (lane < w.heads_here) {
+        float2* st = reinterpret_cast<float2*>(p.stats) + (w.q_row + lane) * parts + part;
+        *st = make_float2(l > 0.0f ? m : kNoToken, l);
+    }
+}
+
+template <int D, int GT>
+__device__ void fused_merge_tail(const PartialParams& p, float* smem);
+
+// ---------------------------------------------------------------------------
+// FP32 (and generic) partition kernel, VALU only.
+//
+// Lanes [r*LPT, (r+1)*LPT) hold token r of a TPL-token load (16 bytes each);
+// q.k is a per-lane partial dot reduced over the LPT lanes of the row with DPP;
+// every token row keeps its own online-softmax stream, combined across rows at
+// the end of the wave. Chunks of NL loads stream through PD + 1 register
+// buffers in fully unrolled blocks of NC chunks.
+template <typename T, int D, int GT, int NL, int PD, int NC>
+__global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams p) {
     using E = Elem<T>;
-    constexpr int kThreads = kWave * NW;
-    constexpr int EPL = E::kPerLoad;  // elements per lane per load
-    constexpr int LPT = D / EPL;      // lanes per token row
-    constexpr int TPL = kWave / LPT;  // tokens per load
-    constexpr int CT = NL * TPL;      // tokens per chunk per wave
+    constexpr int EPL = E::kPerLoad;
+    constexpr int LPT = D / EPL;
+    constexpr int TPL = kWave / LPT;
+    constexpr int CT = NL * TPL;
     static_assert(TPL >= 2 && TPL <= 8 && (TPL & (TPL - 1)) == 0, "unsupported row split");
-    static_assert(NL <= 32, "live mask is 32 bits");
+
+    struct Chunk {
+        u32x4 k[NL];
+        u32x4 v[NL];
+        uint32_t live;
+    };
 
     extern __shared__ float smem[];
-    float (*wave_state)[GT][D + 2] = reinterpret_cast<float (*)[GT][D + 2]>(smem);  // [NW][GT][D+2]
-    __shared__ int is_last;
-
-    const int split = blockIdx.x;
-    const int kv_head = blockIdx.y / p.head_tiles;
-    const int tile = blockIdx.y - kv_head * p.head_tiles;
-    const int b = blockIdx.z;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
     const int row = lane / LPT;
     const int col = lane % LPT;
-
-    // Partition [tb, te) of sequence b; the end is clamped to the table capacity
-    // (decode.cu:42-44). Wave shares are contiguous and cut on TPL multiples.
     const int page_size = 1 << p.page_shift;
-    const int capacity = p.table_width << p.page_shift;
-    const int32_t* pages = p.table + static_cast<int64_t>(b) * p.table_width;
-    // The page-id window (lane i holds the id of logical page window + i) is
-    // requested before the sequence length is known, in parallel with it: it
-    // starts at this wave's first page for a full-length partition, which is
-    // exact for every partition but a sequence's last (re-aimed below).
-    const int64_t first = static_cast<int64_t>(split) * p.split_tokens;
-    const int per_full = ((p.split_tokens + NW - 1) / NW + TPL - 1) / TPL * TPL;
-    int window = static_cast<int>(min<int64_t>(first + static_cast<int64_t>(wave) * per_full, capacity - 1)) >>
-                 p.page_shift;
+    const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
+    int window = speculative_page<TPL>(p, wave);
     int window_ids = pages[min(window + lane, p.table_width - 1)];
-
-    const int len = max(0, min(p.lengths[b], capacity));
-    const int tb = static_cast<int>(min<int64_t>(first, len));
-    const int te = static_cast<int>(min<int64_t>(first + p.split_tokens, len));
-    int per = (te - tb + NW - 1) / NW;
-    per = (per + TPL - 1) / TPL * TPL;
-    const int wb = min(tb + wave * per, te);
-    const int we = min(wb + per, te);
-
-    const int member0 = tile * GT;  // first GQA member handled here
-    const int heads_here = min(GT, p.group - member0);
-    const int64_t q_row = static_cast<int64_t>(b) * p.query_heads + kv_head * p.group + member0;
-    const T* q_base = static_cast<const T*>(p.q) + q_row * D;
+    const WaveWork w = wave_work<GT, TPL>(p, wave);
+    const T* q_base = static_cast<const T*>(p.q) + w.q_row * D;
 
     u32x4 qv[GT];
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
         qv[g] = u32x4{0u, 0u, 0u, 0u};
-        if (g < heads_here) qv[g] = *reinterpret_cast<const u32x4*>(q_base + g * D + col * EPL);
+        if (g < w.heads_here) qv[g] = *reinterpret_cast<const u32x4*>(q_base + g * D + col * EPL);
     }
-
     float m[GT], l[GT], acc[GT][EPL];
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
         m[g] = kNoToken;
         l[g] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) acc[g][j] = 0.0f;
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
     }
-
-    const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(kv_head) * D * sizeof(T);
-    const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(kv_head) * D * sizeof(T);
-    // Groups with no live token are redirected to this sequence's q row: always
+    const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(w.kv_head) * D * sizeof(T);
+    const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(w.kv_head) * D * sizeof(T);
+    // Groups with no live token are redirected to this tile's q row: always
     // mapped, finite, and the same line for every lane.
     const char* park = reinterpret_cast<const char*>(q_base);
     const uint32_t lane_bytes = static_cast<uint32_t>(col) * 16u;
-    int rb = wb, re = wb;  // token range of the current window segment
+    int rb = w.wb, re = w.wb;
 
-    // Issue the 2*NL loads of the chunk whose first aligned group starts at c0.
-    // Page ids come from `window_ids` (lane i holds the id of logical page
-    // window + i) through v_readlane, so no scalar load sits on the issue path.
-    // Lanes whose token lies outside the wave's range read a token inside it
-    // (same page), so every value that reaches the FMAs is live data.
-    auto issue = [&](Chunk<NL>& ch, int c0, int window_ids, int window) {
+    auto issue = [&](Chunk& ch, int c0, int ids, int win) {
         const char* kp[NL];
         const char* vp[NL];
         uint32_t off[NL];
         uint32_t live = 0;
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const int g = c0 + i * TPL;  // wave-uniform, multiple of TPL
+            const int g = c0 + i * TPL;
             int lo = max(g, rb);
             int hi = min(g + TPL, re) - 1;
             if (lo > hi) lo = hi = re - 1;
-            // All tokens of [lo, hi] share one page because TPL divides page_size.
-            const int slot = min(max((lo >> p.page_shift) - window, 0), kWave - 1);
-            const int page = __builtin_amdgcn_readlane(window_ids, slot);
+            const int slot = min(max((lo >> p.page_shift) - win, 0), kWave - 1);
+            const int page = __builtin_amdgcn_readlane(ids, slot);
             const bool ok = g < re && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
             live |= static_cast<uint32_t>(ok) << i;
             const int t = min(max(g + row, lo), hi);
@@ -318,22 +372,14 @@ __global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams
         for (int i = 0; i < NL; ++i) ch.k[i] = *reinterpret_cast<const u32x4*>(kp[i] + off[i]);
 #pragma unroll
         for (int i = 0; i < NL; ++i) ch.v[i] = *reinterpret_cast<const u32x4*>(vp[i] + off[i]);
-        // Keep the whole chunk's loads ahead of the following consume; left
-        // alone, the scheduler sinks them into it to save registers and the
-        // prefetch distance collapses.
         __builtin_amdgcn_sched_barrier(0);
     };
 
-    // Fold one chunk into the per-row online-softmax state. The running max is
-    // raised (and the accumulators rescaled) only when a chunk's max exceeds it
-    // by more than kRescaleSlack, a wave-uniform and rare branch.
-    auto consume = [&](const Chunk<NL>& ch, int c0) {
+    auto consume = [&](const Chunk& ch, int c0) {
         float s[NL][GT];
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int t = c0 + i * TPL + row;
-            // Bitwise '&' keeps this branch-free (a '&&' on the uniform bit
-            // becomes a scalar branch per load).
             const bool valid = (((ch.live >> i) & 1u) != 0u) & (t >= rb) & (t < re);
 #pragma unroll
             for (int g = 0; g < GT; ++g) {
@@ -355,11 +401,11 @@ __global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams
 #pragma unroll
             for (int g = 0; g < GT; ++g) {
                 const float m_new = fmaxf(m[g], chunk_max[g]);
-                const float alpha = fast_exp2(m[g] - m_new);  // 0 after kNoToken, else <= 1
+                const float alpha = fast_exp2(m[g] - m_new);
                 m[g] = m_new;
                 l[g] *= alpha;
 #pragma unroll
-                for (int j = 0; j < EPL; ++j) acc[g][j] *= alpha;
+                for (int e = 0; e < EPL; ++e) acc[g][e] *= alpha;
             }
         }
 #pragma unroll
@@ -367,7 +413,7 @@ __global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams
             float sum = l[g];
 #pragma unroll
             for (int i = 0; i < NL; ++i) {
-                s[i][g] = fast_exp2(fmaf(s[i][g], p.scale_log2, -m[g]));  // 0 for masked tokens
+                s[i][g] = fast_exp2(fmaf(s[i][g], p.scale_log2, -m[g]));
                 sum += s[i][g];
             }
             l[g] = sum;
@@ -379,38 +425,30 @@ __global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams
 #pragma unroll
             for (int g = 0; g < GT; ++g)
 #pragma unroll
-                for (int j = 0; j < EPL; ++j) acc[g][j] = fmaf(s[i][g], vf[j], acc[g][j]);
+                for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(s[i][g], vf[e], acc[g][e]);
         }
     };
 
-    // The wave's range is walked in segments of at most 64 pages (one window of
-    // page ids); partitions up to 63 pages per wave take a single segment.
-    for (rb = wb; rb < we; rb = re) {
+    for (rb = w.wb; rb < w.we; rb = re) {
         if ((rb >> p.page_shift) != window) {
             window = rb >> p.page_shift;
             window_ids = pages[min(window + lane, p.table_width - 1)];
         }
-        re = min(we, (window + kWave) << p.page_shift);
-        // Blocks of NC chunks run as fully unrolled straight-line code with PD
-        // chunks in flight ahead of the one being consumed; the PD + 1 buffers
-        // rotate by compile-time index, so no register holding a pending load
-        // is ever copied and every wait covers exactly one chunk. (Loads kept
-        // in flight across a loop back-edge make the compiler wait for all of
-        // them.) The pipeline fills and drains once per block.
-        for (int s = rb & ~(TPL - 1); s < re; s += NC * CT) {
-            Chunk<NL> buf[PD + 1];
+        re = min(w.we, (window + kWave) << p.page_shift);
+        for (int s0 = rb & ~(TPL - 1); s0 < re; s0 += NC * CT) {
+            Chunk buf[PD + 1];
 #pragma unroll
-            for (int n = 0; n < PD; ++n) issue(buf[n], s + n * CT, window_ids, window);
+            for (int n = 0; n < PD; ++n) issue(buf[n], s0 + n * CT, window_ids, window);
 #pragma unroll
             for (int n = 0; n < NC; ++n) {
-                if (s + n * CT >= re) break;
-                if (n + PD < NC) issue(buf[(n + PD) % (PD + 1)], s + (n + PD) * CT, window_ids, window);
-                consume(buf[n % (PD + 1)], s + n * CT);
+                if (s0 + n * CT >= re) break;
+                if (n + PD < NC) issue(buf[(n + PD) % (PD + 1)], s0 + (n + PD) * CT, window_ids, window);
+                consume(buf[n % (PD + 1)], s0 + n * CT);
             }
         }
     }
 
-    // Combine the TPL token-row streams of this wave (lanes LPT, 2*LPT, ... apart).
+    // Combine the TPL token-row streams (lanes LPT, 2*LPT, ... apart).
 #pragma unroll
     for (int g = 0; g < GT; ++g) {
         float mw = m[g];
@@ -421,132 +459,360 @@ __global__ void __launch_bounds__(kWave * NW) partial_kernel(const PartialParams
 #pragma unroll
         for (int x = LPT; x < kWave; x <<= 1) lw += __shfl_xor(lw, x);
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            float a = acc[g][j] * f;
+        for (int e = 0; e < EPL; ++e) {
+            float a = acc[g][e] * f;
 #pragma unroll
             for (int x = LPT; x < kWave; x <<= 1) a += __shfl_xor(a, x);
-            acc[g][j] = a;
+            acc[g][e] = a;
         }
         m[g] = mw;
         l[g] = lw;
     }
-    if (lane < LPT) {
+    // Lane g needs head g's (m, l): every lane holds every head's values.
+    float m_lane = m[0], l_lane = l[0];
+#pragma unroll
+    for (int g = 1; g < GT; ++g) {
+        m_lane = lane == g ? m[g] : m_lane;
+        l_lane = lane == g ? l[g] : l_lane;
+    }
+    store_wave_state<D, GT, EPL, LPT>(p, w, lane, acc, m_lane, l_lane);
+    if (p.fuse != kFuseNone) fused_merge_tail<D, GT>(p, smem);
+}
+
+// ---------------------------------------------------------------------------
+// FP16 partition kernel with q.K^T on the matrix cores.
+//
+// A 16-token tile is scored with D/32 v_mfma_f32_16x16x32_f16: K in the A
+// layout (lane l: token l % 16 of the tile; k-step s covers dims
+// [32 s, 32 s + 32), 8 of them per lane group l / 16, so a load reads 64
+// contiguous bytes of 16 rows), q in the B layout (lane l: query head l % 16,
+// zero past the tile). Lane l then holds head l % 16 for tokens
+// 4 * (l / 16) + 0..3, so each (token, head) score lives in one lane and the
+// softmax bookkeeping costs a few instructions per tile. Weights go through a
+// 16 x GT LDS tile to the P.V step, which stays on the VALU in the row layout
+// (lanes [r*LPT, (r+1)*LPT) hold token r's V row) as mixed-precision FMAs. One
+// running max per head is shared by the whole wave, so its token rows simply
+// add up at the end.
+constexpr int kTileTokens = 16;
+
+template <int D, int GT>
+constexpr int rows_in_lds() {  // rows kept apart in LDS for the final row sum (1 = summed in registers)
+    constexpr int TPL = kWave / (D / 8);
+    return 8 * TPL * GT * D * 4 <= 64 * 1024 ? TPL : 1;
+}
+
+template <int D, int GT>
+constexpr size_t mfma_state_floats() {  // dynamic LDS floats per wave for the row sum
+    return rows_in_lds<D, GT>() > 1 ? static_cast<size_t>(rows_in_lds<D, GT>()) * GT * D : 0;
+}
+
+template <int D, int GT, int PD, int NC>
+__global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
+    using E = Elem<_Float16>;
+    constexpr int EPL = 8;                 // halves per 16-byte lane load
+    constexpr int LPT = D / EPL;           // lanes per token row (V layout)
+    constexpr int TPL = kWave / LPT;       // tokens per V load
+    constexpr int VI = kTileTokens / TPL;  // V loads per tile
+    constexpr int KS = D / 32;             // MFMA k-steps (K loads) per tile
+    constexpr int R = rows_in_lds<D, GT>();
+    static_assert(GT <= 8, "P.V accumulators are sized for at most 8 heads");
+
+    struct Tile {
+        f16x8 k[KS];
+        u32x4 v[VI];
+        uint32_t live;
+    };
+
+    extern __shared__ float smem[];
+    __shared__ float ptile[8][kTileTokens * GT];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int row = lane / LPT;
+    const int col = lane % LPT;
+    const int kt = lane % 16;
+    const int kg = lane / 16;
+    const int page_size = 1 << p.page_shift;
+    const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
+    int window = speculative_page<kTileTokens>(p, wave);
+    int window_ids = pages[min(window + lane, p.table_width - 1)];
+    const WaveWork w = wave_work<GT, kTileTokens>(p, wave);
+    const _Float16* q_base = static_cast<const _Float16*>(p.q) + w.q_row * D;
+
+    f16x8 qb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        u32x4 x = u32x4{0u, 0u, 0u, 0u};
+        if (kt < w.heads_here) x = *reinterpret_cast<const u32x4*>(q_base + kt * D + 32 * s + 8 * kg);
+        qb[s] = __builtin_bit_cast(f16x8, x);
+    }
+
+    float m_head = kNoToken;  // running max (log2 units) of head kt, equal in all lane groups
+    float l_part = 0.0f;      // this lane's share of head kt's denominator
+    float acc[GT][EPL];
+#pragma unroll
+    for (int g = 0; g < GT; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+
+    const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(w.kv_head) * D * 2;
+    const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(w.kv_head) * D * 2;
+    const char* park = reinterpret_cast<const char*>(q_base);
+    const uint32_t k_lane_bytes = static_cast<uint32_t>(kg) * 16u;
+    const uint32_t v_lane_bytes = static_cast<uint32_t>(col) * 16u;
+    float* pt = ptile[wave];
+    int rb = w.wb, re = w.wb;
+
+    auto issue = [&](Tile& tl, int t0, int ids, int win) {
+        int lo = max(t0, rb);
+        int hi = min(t0 + kTileTokens, re) - 1;
+        if (lo > hi) lo = hi = re - 1;
+        const int slot = min(max((lo >> p.page_shift) - win, 0), kWave - 1);
+        const int page = __builtin_amdgcn_readlane(ids, slot);
+        const bool ok = t0 < re && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
+        tl.live = ok;
+        const uint64_t page_off = static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
+        const char* kp = ok ? k_head + page_off : park;
+        const char* vp = ok ? v_head + page_off : park;
+        const int tk = min(max(t0 + kt, lo), hi);
+        const uint32_t koff =
+            ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            tl.k[s] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(kp + koff + 64 * s));
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int tv = min(max(t0 + i * TPL + row, lo), hi);
+            const uint32_t voff =
+                ok ? static_cast<uint32_t>(tv & (page_size - 1)) * p.token_bytes + v_lane_bytes : v_lane_bytes;
+            tl.v[i] = *reinterpret_cast<const u32x4*>(vp + voff);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    auto consume = [&](const Tile& tl, int t0) {
+        f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(tl.k[s], qb[s], sc, 0, 0, 0);
+        float x[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = t0 + 4 * kg + i;
+            const bool valid = (tl.live != 0u) & (t >= rb) & (t < re);
+            x[i] = valid ? sc[i] : -INFINITY;
+            mx = fmaxf(mx, x[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float tile_max = mx * p.scale_log2;
+        if (__any((kt < GT) & (tile_max > m_head + kRescaleSlack))) {
+            const float m_new = fmaxf(m_head, tile_max);
+            const float alpha = fast_exp2(m_head - m_new);
+            m_head = m_new;
+            l_part *= alpha;
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                // Lane g (first lane group) holds head g's factor.
+                const float ag = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), g));
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[g][e] *= ag;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float wgt = fast_exp2(fmaf(x[i], p.scale_log2, -m_head));
+            l_part += wgt;
+            if (kt < GT) pt[(4 * kg + i) * GT + kt] = wgt;
+        }
+        // P.V in the row layout; the wave's own LDS tile needs no barrier.
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            float wv[GT];
+#pragma unroll
+            for (int g = 0; g < GT; ++g) wv[g] = pt[(i * TPL + row) * GT + g];
+            float vf[EPL];
+            E::widen(tl.v[i], vf);
+#pragma unroll
+            for (int g = 0; g < GT; ++g)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(wv[g], vf[e], acc[g][e]);
+        }
+    };
+
+    for (rb = w.wb; rb < w.we; rb = re) {
+        if ((rb >> p.page_shift) != window) {
+            window = rb >> p.page_shift;
+            window_ids = pages[min(window + lane, p.table_width - 1)];
+        }
+        re = min(w.we, (window + kWave) << p.page_shift);
+        for (int s0 = rb & ~(kTileTokens - 1); s0 < re; s0 += NC * kTileTokens) {
+            Tile buf[PD + 1];
+#pragma unroll
+            for (int n = 0; n < PD; ++n) issue(buf[n], s0 + n * kTileTokens, window_ids, window);
+#pragma unroll
+            for (int n = 0; n < NC; ++n) {
+                if (s0 + n * kTileTokens >= re) break;
+                if (n + PD < NC) issue(buf[(n + PD) % (PD + 1)], s0 + (n + PD) * kTileTokens, window_ids, window);
+                consume(buf[n % (PD + 1)], s0 + n * kTileTokens);
+            }
+        }
+    }
+
+    // Sum the wave's token rows (they share one max per head): through this
+    // wave's LDS slice when it fits, else with lane shuffles; then lanes of
+    // row 0 hold the sums. The denominator is summed over the four lane groups
+    // of the MFMA layout.
+    if constexpr (R > 1) {
+        float* rows = smem + static_cast<size_t>(wave) * R * GT * D;  // [R][GT][D]
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
+            f32x4* dst = reinterpret_cast<f32x4*>(rows + (row * GT + g) * D + col * EPL);
+            dst[0] = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+            dst[1] = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+        }
+        if (lane < LPT) {
 #pragma unroll
-            for (int j = 0; j < EPL; ++j) wave_state[wave][g][col * EPL + j] = acc[g][j];
-            if (lane == 0) {
-                wave_state[wave][g][D] = m[g];
-                wave_state[wave][g][D + 1] = l[g];
+            for (int g = 0; g < GT; ++g) {
+                f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const f32x4* src = reinterpret_cast<const f32x4*>(rows + (r * GT + g) * D + col * EPL);
+                    s0 += src[0];
+                    s1 += src[1];
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[g][e] = s0[e];
+                    acc[g][e + 4] = s1[e];
+                }
             }
         }
-    }
-    __syncthreads();
-
-    // Combine the waves; one partition state per query head.
-    for (int idx = threadIdx.x; idx < GT * D; idx += kThreads) {
-        const int g = idx / D;
-        const int d = idx - g * D;
-        if (g >= heads_here) break;
-        float mx = kNoToken;
+    } else {
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
-            if (wave_state[w][g][D + 1] > 0.0f) mx = fmaxf(mx, wave_state[w][g][D]);
-        float num = 0.0f, den = 0.0f;
+        for (int g = 0; g < GT; ++g)
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float lw = wave_state[w][g][D + 1];
-            if (lw > 0.0f) {
-                const float f = fast_exp2(wave_state[w][g][D] - mx);
-                den = fmaf(f, lw, den);
-                num = fmaf(f, wave_state[w][g][d], num);
+            for (int e = 0; e < EPL; ++e) {
+                float a = acc[g][e];
+#pragma unroll
+                for (int x = LPT; x < kWave; x <<= 1) a += __shfl_xor(a, x);
+                acc[g][e] = a;
             }
-        }
-        const int64_t part = (q_row + g) * p.splits + split;
-        p.numerator[part * D + d] = num;
-        if (d == 0) {
-            p.stats[part * 2] = mx;
-            p.stats[part * 2 + 1] = den;
-        }
     }
-    if (p.fuse == kFuseNone) return;
+    float l_head = l_part;
+    l_head += __shfl_xor(l_head, 16);
+    l_head += __shfl_xor(l_head, 32);
+    store_wave_state<D, GT, EPL, LPT>(p, w, lane, acc, m_head, l_head);
+    if (p.fuse != kFuseNone) fused_merge_tail<D, GT>(p, smem);
+}
 
-    // Fused merge: the last workgroup to finish a (sequence, KV head, tile) row
-    // combines that row's partition states. Release: every thread's stores are
-    // made device-visible before the arrival is counted.
+// ---------------------------------------------------------------------------
+// Fused merge: the last workgroup to finish a (sequence, workgroup row) combines
+// the states of every query head that row covers (hw KV heads x tw tiles x GT
+// members) into `out`, then resets the row's counter for the next call.
+// Release: every thread's stores are made device-visible before the arrival is
+// counted; acquire: the last workgroup observes all of them.
+template <int D, int GT>
+__device__ void fused_merge_tail(const PartialParams& p, float* smem) {
+    __shared__ int is_last;
+    const int threads = blockDim.x;
+    const int waves = threads / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x % kWave;
     __threadfence();
     __syncthreads();
-    const int64_t row_id = static_cast<int64_t>(b) * gridDim.y + blockIdx.y;
-    if (threadIdx.x == 0) is_last = atomicAdd(&p.counters[row_id], 1) == p.splits - 1;
+    const int64_t row_id = static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y;
+    if (threadIdx.x == 0) is_last = atomicAdd(&p.counters[row_id], 1) == static_cast<int>(gridDim.x) - 1;
     __syncthreads();
     if (!is_last) return;
-    __threadfence();  // acquire: observe the other workgroups' states
+    __threadfence();
+    const int parts = kQuarters * p.splits;
     const float2* st_base = reinterpret_cast<const float2*>(p.stats);
+    const int hw = p.heads_per_wg, tw = p.tiles_per_wg;
+    const int tile_groups = p.head_tiles / tw;
+    const int kv0 = (blockIdx.y / tile_groups) * hw;
+    const int tile0 = (blockIdx.y % tile_groups) * tw;
+    const int local_heads = hw * tw * GT;
+    const int64_t b_row = static_cast<int64_t>(blockIdx.z) * p.query_heads;
+    // Query-head row of local head lh, or -1 past the GQA group.
+    auto head_row = [&](int lh) -> int64_t {
+        const int kv = kv0 + lh / (tw * GT);
+        const int member = (tile0 + (lh / GT) % tw) * GT + lh % GT;
+        return member < p.group ? b_row + static_cast<int64_t>(kv) * p.group + member : -1;
+    };
     if (p.fuse == kFuseShared) {
-        // LDS-bounded: one weight per (head, partition), computed once by the
-        // wave that owns the head.
-        float* weight = smem;                         // [GT][splits]; wave states are dead now
-        float* row_den = smem + GT * p.splits;        // [GT]
-        for (int g = wave; g < heads_here; g += NW) {
-            const float2* st = st_base + (q_row + g) * p.splits;
+        float* weight = smem;                          // [local_heads][parts]
+        float* den_lds = smem + local_heads * parts;   // [local_heads]
+        for (int lh = wave; lh < local_heads; lh += waves) {
+            const int64_t qr = head_row(lh);
+            if (qr < 0) continue;
+            const float2* st = st_base + qr * parts;
             float mx = kNoToken;
-            for (int j = lane; j < p.splits; j += kWave) {
+            for (int j = lane; j < parts; j += kWave) {
                 const float2 s = load_state(st, j);
                 mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
             }
             mx = wave_max(mx);
             float den = 0.0f;
-            for (int j = lane; j < p.splits; j += kWave) {
+            for (int j = lane; j < parts; j += kWave) {
                 const float2 s = load_state(st, j);
                 const float f = s.y > 0.0f ? fast_exp2(s.x - mx) : 0.0f;
-                weight[g * p.splits + j] = f;
+                weight[lh * parts + j] = f;
                 den = fmaf(f, s.y, den);
             }
             den = wave_sum(den);
-            if (lane == 0) row_den[g] = den;
+            if (lane == 0) den_lds[lh] = den;
         }
         __syncthreads();
-        for (int idx = threadIdx.x; idx < heads_here * D; idx += kThreads) {
-            const int g = idx / D;
-            const int d = idx - g * D;
-            const float* num = p.numerator + (q_row + g) * p.splits * D + d;
-            const float* w = weight + g * p.splits;
-            float acc_d = 0.0f;
+        for (int idx = threadIdx.x; idx < local_heads * D; idx += threads) {
+            const int lh = idx / D;
+            const int d = idx - lh * D;
+            const int64_t qr = head_row(lh);
+            if (qr < 0) continue;
+            const float* num = p.numerator + qr * parts * D + d;
+            const float* w = weight + lh * parts;
+            float acc = 0.0f;
 #pragma unroll kMergeUnroll
-            for (int j = 0; j < p.splits; ++j) {
+            for (int j = 0; j < parts; ++j) {
                 const float n = num[static_cast<int64_t>(j) * D];
-                acc_d = w[j] > 0.0f ? fmaf(w[j], n, acc_d) : acc_d;
+                acc = w[j] > 0.0f ? fmaf(w[j], n, acc) : acc;
             }
-            const float den = row_den[g];
-            p.out[(q_row + g) * D + d] = den > 0.0f ? acc_d / den : 0.0f;
+            const float den = den_lds[lh];
+            p.out[qr * D + d] = den > 0.0f ? acc / den : 0.0f;
         }
     } else {
-        // Serial: every lane scans the row's states itself.
-        for (int idx = threadIdx.x; idx < heads_here * D; idx += kThreads) {
-            const int g = idx / D;
-            const int d = idx - g * D;
-            const float2* st = st_base + (q_row + g) * p.splits;
+        for (int idx = threadIdx.x; idx < local_heads * D; idx += threads) {
+            const int lh = idx / D;
+            const int d = idx - lh * D;
+            const int64_t qr = head_row(lh);
+            if (qr < 0) continue;
+            const float2* st = st_base + qr * parts;
             float mx = kNoToken;
 #pragma unroll kMergeUnroll
-            for (int j = 0; j < p.splits; ++j) {
+            for (int j = 0; j < parts; ++j) {
                 const float2 s = load_state(st, j);
                 mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
             }
-            const float* num = p.numerator + (q_row + g) * p.splits * D + d;
-            float den = 0.0f, acc_d = 0.0f;
+            const float* num = p.numerator + qr * parts * D + d;
+            float den = 0.0f, acc = 0.0f;
 #pragma unroll kMergeUnroll
-            for (int j = 0; j < p.splits; ++j) {
+            for (int j = 0; j < parts; ++j) {
                 const float2 s = load_state(st, j);
                 const float n = num[static_cast<int64_t>(j) * D];
                 const bool live = s.y > 0.0f;
                 const float f = live ? fast_exp2(s.x - mx) : 0.0f;
                 den = live ? fmaf(f, s.y, den) : den;
-                acc_d = live ? fmaf(f, n, acc_d) : acc_d;
+                acc = live ? fmaf(f, n, acc) : acc;
             }
-            p.out[(q_row + g) * D + d] = den > 0.0f ? acc_d / den : 0.0f;
+            p.out[qr * D + d] = den > 0.0f ? acc / den : 0.0f;
         }
     }
     if (threadIdx.x == 0) p.counters[row_id] = 0;  // ready for the next call
+}
+
+// Floats of dynamic LDS the fused LDS-bounded merge needs.
+__host__ __device__ inline size_t fused_shared_floats(int local_heads, int splits) {
+    return static_cast<size_t>(local_heads) * (kQuarters * static_cast<size_t>(splits) + 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -652,12 +918,11 @@ int check_common(const void* q, const void* k, const void* v, int dtype, const i
 
 int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LAUNCH; }
 
-// Waves per partition workgroup and 16-byte loads of K (and of V) per lane per
-// chunk, chunks in flight ahead of the one being consumed, and chunks per
-// straight-line block.
-#ifndef PD_PARTIAL_WAVES
-#define PD_PARTIAL_WAVES 4
-#endif
+// LDS the fused LDS-bounded merge may use beside the partition kernel.
+constexpr size_t kFusedSharedLdsBytes = 48 * 1024;
+
+// FP32 kernel: 16-byte loads of K (and of V) per lane per chunk, chunks in
+// flight ahead of the one being consumed, chunks per straight-line block.
 #ifndef PD_CHUNK_LOADS
 #define PD_CHUNK_LOADS 1
 #endif
@@ -667,35 +932,76 @@ int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LA
 #ifndef PD_BLOCK_CHUNKS
 #define PD_BLOCK_CHUNKS 16
 #endif
+// FP16 kernel (MFMA scoring): 16-token tiles in flight ahead of the one being
+// consumed, and tiles per straight-line block.
+#ifndef PD_MFMA_PREFETCH
+#define PD_MFMA_PREFETCH 1
+#endif
+#ifndef PD_MFMA_BLOCK
+#define PD_MFMA_BLOCK 8
+#endif
+
+// Largest divisor of n not above cap.
+int largest_divisor(int n, int cap) {
+    for (int d = std::min(n, cap); d > 1; --d)
+        if (n % d == 0) return d;
+    return 1;
+}
+
+// Workgroup shape: up to 8 KV heads of the same tokens per workgroup (their
+// slices of a token row are then read together, which the memory system
+// serves best), all head tiles of those heads, and as many partition quarters
+// as fill 8 waves.
+void choose_workgroup(PartialParams& prm, int kv_heads) {
+    prm.heads_per_wg = largest_divisor(kv_heads, 8);
+    prm.tiles_per_wg = largest_divisor(prm.head_tiles, 8 / prm.heads_per_wg);
+    const int hw_tw = prm.heads_per_wg * prm.tiles_per_wg;
+    prm.quarters_per_wg = hw_tw <= 2 ? 4 : hw_tw <= 4 ? 2 : 1;
+}
 
 template <typename T, int D, int GT>
 int launch_partial(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    constexpr int NW = PD_PARTIAL_WAVES;
-    constexpr int NL = PD_CHUNK_LOADS;
-    constexpr int PD = PD_PREFETCH;
-    constexpr int NC = PD_BLOCK_CHUNKS;
-    size_t floats = static_cast<size_t>(wave_state_floats<D, GT, NW>());
-    if (prm.fuse == kFuseShared) floats = std::max(floats, static_cast<size_t>(GT) * (prm.splits + 1));
-    const dim3 grid(prm.splits, kv_heads * prm.head_tiles, batch);
-    hipLaunchKernelGGL((partial_kernel<T, D, GT, NL, NW, PD, NC>), grid, dim3(kWave * NW), floats * sizeof(float),
-                       stream, prm);
+    const int waves = prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
+    size_t floats = std::is_same_v<T, _Float16> ? static_cast<size_t>(waves) * mfma_state_floats<D, GT>() : 0;
+    if (prm.fuse == kFuseShared)
+        floats = std::max(floats, fused_shared_floats(prm.heads_per_wg * prm.tiles_per_wg * GT, prm.splits));
+    const dim3 grid(prm.splits * (kQuarters / prm.quarters_per_wg),
+                    (kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg), batch);
+    if constexpr (std::is_same_v<T, _Float16>) {
+        hipLaunchKernelGGL((partial_mfma_kernel<D, GT, PD_MFMA_PREFETCH, PD_MFMA_BLOCK>), grid, dim3(kWave * waves),
+                           floats * sizeof(float), stream, prm);
+    } else {
+        hipLaunchKernelGGL((partial_kernel<T, D, GT, PD_CHUNK_LOADS, PD_PREFETCH, PD_BLOCK_CHUNKS>), grid,
+                           dim3(kWave * waves), floats * sizeof(float), stream, prm);
+    }
     return launch_status();
 }
 
 // Head tile: the GQA group padded to 1, 2, 4 or 8 query heads; larger groups
-// are cut into tiles of 8 (one workgroup per tile).
+// are cut into tiles of 8.
 int head_tile(int group) { return group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8; }
 
 template <typename T, int D>
 int dispatch_group(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const int gt = head_tile(prm.group);
     prm.head_tiles = (prm.group + gt - 1) / gt;
+    choose_workgroup(prm, kv_heads);
     switch (gt) {
         case 1: return launch_partial<T, D, 1>(prm, batch, kv_heads, stream);
         case 2: return launch_partial<T, D, 2>(prm, batch, kv_heads, stream);
         case 4: return launch_partial<T, D, 4>(prm, batch, kv_heads, stream);
         default: return launch_partial<T, D, 8>(prm, batch, kv_heads, stream);
     }
+}
+
+// LDS the fused LDS-bounded merge would need for these shapes (in floats).
+size_t fused_shared_need(int query_heads, int kv_heads, int splits) {
+    PartialParams prm{};
+    prm.group = query_heads / kv_heads;
+    const int gt = head_tile(prm.group);
+    prm.head_tiles = (prm.group + gt - 1) / gt;
+    choose_workgroup(prm, kv_heads);
+    return fused_shared_floats(prm.heads_per_wg * prm.tiles_per_wg * gt, splits);
 }
 
 int run_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -752,15 +1058,16 @@ int check_merge(const float* numerator, const float* stats, const float* out, in
     if (head_dim != 64 && head_dim != 128) return PD_ERR_SHAPE;
     if (splits < 1 || splits > 65535) return PD_ERR_SPLIT;
     if (merge_mode != PD_MERGE_SERIAL && merge_mode != PD_MERGE_SHARED) return PD_ERR_MERGE;
-    if (merge_mode == PD_MERGE_SHARED && splits > PD_SHARED_MERGE_MAX_PARTS) return PD_ERR_MERGE;
+    if (merge_mode == PD_MERGE_SHARED && kQuarters * splits > PD_SHARED_MERGE_MAX_PARTS) return PD_ERR_MERGE;
     return PD_OK;
 }
 
 int run_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads,
               int head_dim, int splits, int merge_mode, hipStream_t stream) {
     const int rows = batch * query_heads;
-    return head_dim == 64 ? launch_merge<64>(numerator, stats, out, rows, splits, merge_mode, stream)
-                          : launch_merge<128>(numerator, stats, out, rows, splits, merge_mode, stream);
+    const int parts = kQuarters * splits;
+    return head_dim == 64 ? launch_merge<64>(numerator, stats, out, rows, parts, merge_mode, stream)
+                          : launch_merge<128>(numerator, stats, out, rows, parts, merge_mode, stream);
 }
 
 }  // namespace
@@ -816,18 +1123,26 @@ int pd_decode_fused(const void* q, const void* k, const void* v, int dtype, cons
     if (status == PD_OK)
         status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
     if (status == PD_OK && !counters) status = PD_ERR_NULL_POINTER;
-    if (status == PD_OK && merge_mode == PD_MERGE_SHARED && splits > PD_FUSED_SHARED_MAX_PARTS)
-        status = PD_ERR_MERGE;
     if (status != PD_OK) return status;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (merge_mode == PD_MERGE_SHARED &&
+        fused_shared_need(query_heads, kv_heads, splits) * sizeof(float) > kFusedSharedLdsBytes) {
+        // The LDS-bounded merge of this many states does not fit beside the
+        // partition kernel; run it as its own kernel (same algorithm).
+        status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, nullptr, nullptr, kFuseNone,
+                             batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
+                             splits, split_tokens, s);
+        if (status != PD_OK) return status;
+        return run_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode, s);
+    }
     return run_partial(q, k, v, dtype, table, lengths, numerator, stats, out, counters,
                        merge_mode == PD_MERGE_SHARED ? kFuseShared : kFuseSerial, batch, query_heads,
-                       kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                       static_cast<hipStream_t>(stream));
+                       kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens, s);
 }
 
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {
     if (batch <= 0 || query_heads <= 0 || head_dim <= 0 || splits <= 0) return 0;
-    return static_cast<size_t>(batch) * query_heads * splits * (head_dim + 2) * sizeof(float);
+    return static_cast<size_t>(batch) * query_heads * kQuarters * splits * (head_dim + 2) * sizeof(float);
 }
 
 const char* pd_status_string(int status) {
@@ -837,12 +1152,12 @@ const char* pd_status_string(int status) {
         case PD_ERR_SHAPE: return "a dimension is outside the supported range";
         case PD_ERR_DTYPE: return "unsupported dtype (float16 or float32 expected)";
         case PD_ERR_SPLIT: return "invalid split configuration";
-        case PD_ERR_MERGE: return "unknown merge mode or shared merge requires at most 4096 partial states";
+        case PD_ERR_MERGE: return "unknown merge mode or shared merge requires at most 4096 partial states (4 per split)";
         case PD_ERR_LAUNCH: return "kernel launch failed";
         default: return "unknown status";
     }
 }
 
-int pd_abi_version(void) { return 2; }
+int pd_abi_version(void) { return 3; }
 
 }  // extern "C"

@@ -3,9 +3,9 @@
 // Exposes `decode(q, k, v, table, lengths, numerator, stats, out, split_tokens,
 // merge_mode)` with the argument list of reference
 // src/paged_decode/csrc/bindings.cpp:3-9, and repeats the tensor checks of
-// reference decode.cu:201-237 (as TORCH_CHECK -> RuntimeError) for this
-// operator's workspace layout: numerator [B, Hq, splits, D] and
-// stats [B, Hq, splits, 2], one state per partition. Launches go to the current
+// reference decode.cu:201-237 (as TORCH_CHECK -> RuntimeError), including
+// the reference's workspace layout: numerator [B, Hq, 4 * splits, D] and
+// stats [B, Hq, 4 * splits, 2], four states per partition. Launches go to the current
 // torch stream of q's device, so calls follow torch stream semantics and can be
 // captured by torch.cuda.CUDAGraph (hipGraph). Nothing is allocated here.
 
@@ -63,12 +63,12 @@ Shape check_inputs(const torch::Tensor& q, const torch::Tensor& k, const torch::
     TORCH_CHECK(table.scalar_type() == at::kInt && lengths.scalar_type() == at::kInt, "metadata must be int32");
     s.width = table.size(1);
     TORCH_CHECK(numerator.dim() == 4 && numerator.size(0) == s.batch && numerator.size(1) == s.heads &&
-                    numerator.size(2) > 0 && numerator.size(3) == s.dim,
+                    numerator.size(2) > 0 && numerator.size(2) % 4 == 0 && numerator.size(3) == s.dim,
                 "invalid numerator workspace");
-    s.splits = numerator.size(2);
+    s.splits = numerator.size(2) / 4;
     TORCH_CHECK(s.splits <= 65535 && split_tokens > 0 && split_tokens <= 1048576, "invalid split configuration");
     TORCH_CHECK(stats.dim() == 4 && stats.size(0) == s.batch && stats.size(1) == s.heads &&
-                    stats.size(2) == s.splits && stats.size(3) == 2,
+                    stats.size(2) == numerator.size(2) && stats.size(3) == 2,
                 "invalid stats workspace");
     TORCH_CHECK(numerator.scalar_type() == at::kFloat && stats.scalar_type() == at::kFloat,
                 "workspaces must be float32");
@@ -80,7 +80,8 @@ void check_output(const torch::Tensor& q, const torch::Tensor& out, int64_t merg
                 "output must be a contiguous tensor on the input device");
     TORCH_CHECK(out.sizes() == q.sizes(), "invalid output shape");
     TORCH_CHECK(out.scalar_type() == at::kFloat, "output must be float32");
-    TORCH_CHECK(merge_mode == PD_MERGE_SERIAL || (merge_mode == PD_MERGE_SHARED && splits <= PD_SHARED_MERGE_MAX_PARTS),
+    TORCH_CHECK(merge_mode == PD_MERGE_SERIAL ||
+                    (merge_mode == PD_MERGE_SHARED && 4 * splits <= PD_SHARED_MERGE_MAX_PARTS),
                 "shared merge requires at most 4096 partial states");
 }
 
@@ -122,13 +123,14 @@ void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int6
     }
     TORCH_CHECK(numerator.dim() == 4 && stats.dim() == 4 && out.dim() == 3, "invalid workspace shapes");
     TORCH_CHECK(stats.size(0) == numerator.size(0) && stats.size(1) == numerator.size(1) &&
-                    stats.size(2) == numerator.size(2) && stats.size(3) == 2 && out.size(0) == numerator.size(0) &&
-                    out.size(1) == numerator.size(1) && out.size(2) == numerator.size(3),
+                    stats.size(2) == numerator.size(2) && numerator.size(2) % 4 == 0 && stats.size(3) == 2 &&
+                    out.size(0) == numerator.size(0) && out.size(1) == numerator.size(1) &&
+                    out.size(2) == numerator.size(3),
                 "workspace/output shape mismatch");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     check_status(pd_decode_merge(numerator.data_ptr<float>(), stats.data_ptr<float>(), out.data_ptr<float>(),
                                  static_cast<int>(numerator.size(0)), static_cast<int>(numerator.size(1)),
-                                 static_cast<int>(numerator.size(3)), static_cast<int>(numerator.size(2)),
+                                 static_cast<int>(numerator.size(3)), static_cast<int>(numerator.size(2) / 4),
                                  static_cast<int>(merge_mode), current_stream(out)));
 }
 

@@ -15,13 +15,12 @@ import torch
 
 from .layout import Layout, validate_metadata
 
-# One (m, l, n[D]) state per partition and query head: the LDS-bounded merge
-# holds one float per partition.
+# Four (m, l, n[D]) states per partition (one per quarter) and query head, as
+# in the reference's workspace (runtime.py:64-68). The LDS-bounded merge holds
+# one float per state, so "shared" becomes "serial_fallback" above 4096 states
+# (runtime.py:54).
+_STATES_PER_SPLIT = 4
 _SHARED_MERGE_MAX_PARTS = 4096
-# Observable fallback rule of the reference (runtime.py:54): its workspace had
-# four states per partition, so "shared" becomes "serial_fallback" above
-# 1024 partitions. Kept so merge_implementation reports the same value.
-_REFERENCE_STATES_PER_SPLIT = 4
 
 
 @lru_cache(maxsize=1)
@@ -75,7 +74,7 @@ class DecodePlan:
         self.layout, self.split_tokens = layout, split_tokens
         self.merge = merge
         if merge == "shared":
-            fits = self.splits * _REFERENCE_STATES_PER_SPLIT <= _SHARED_MERGE_MAX_PARTS
+            fits = self.splits * _STATES_PER_SPLIT <= _SHARED_MERGE_MAX_PARTS
             self.merge_implementation = "shared" if fits else "serial_fallback"
         else:
             self.merge_implementation = "serial"
@@ -88,7 +87,7 @@ class DecodePlan:
         self._table_cpu, self._lengths_cpu = table, lengths
         self._table = torch.tensor(table, device=self.device)
         self._lengths = torch.tensor(lengths, device=self.device)
-        shape = (layout.batch, layout.query_heads, self.splits)
+        shape = (layout.batch, layout.query_heads, self.splits * _STATES_PER_SPLIT)
         self._numerator = torch.empty((*shape, layout.head_dim), device=self.device, dtype=torch.float32)
         self._stats = torch.empty((*shape, 2), device=self.device, dtype=torch.float32)
         self._out = torch.empty((layout.batch, layout.query_heads, layout.head_dim),

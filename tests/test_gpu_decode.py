@@ -278,8 +278,8 @@ def test_device_page_guard_skips_invalid_ids():
     d_table = torch.from_numpy(table).cuda()
     d_lengths = torch.from_numpy(lengths).cuda()
     splits = 4
-    numerator = torch.empty((2, 8, splits, 128), device="cuda")
-    stats = torch.empty((2, 8, splits, 2), device="cuda")
+    numerator = torch.empty((2, 8, 4 * splits, 128), device="cuda")  # four states per partition
+    stats = torch.empty((2, 8, 4 * splits, 2), device="cuda")
     out = torch.empty((2, 8, 128), device="cuda")
     announce("device page guard")
     status = lib.pd_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F32, d_table.data_ptr(),

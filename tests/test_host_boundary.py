@@ -75,8 +75,8 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 1
-    assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4 * 32 * 16 * 130 * 4
+    assert lib.pd_abi_version() == 3
+    assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
     assert cabi.status_string(lib, 99) == "unknown status"
@@ -88,7 +88,7 @@ def test_extension_exports_reference_entry():
     ext = load_extension()
     for name in ("decode", "partial", "merge", "workspace_bytes", "abi_version"):
         assert hasattr(ext, name)
-    assert ext.workspace_bytes(4, 32, 128, 16) == 4 * 32 * 16 * 130 * 4
+    assert ext.workspace_bytes(4, 32, 128, 16) == 4_259_840
 
 
 def fake(n=1):
@@ -123,7 +123,7 @@ def call_decode(lib, ptrs, **over):
     (dict(split_tokens=0), cabi.PD_ERR_SPLIT),
     (dict(split_tokens=(1 << 20) + 1), cabi.PD_ERR_SPLIT),
     (dict(merge_mode=2), cabi.PD_ERR_MERGE),
-    (dict(merge_mode=1, splits=4097), cabi.PD_ERR_MERGE),
+    (dict(merge_mode=1, splits=1025), cabi.PD_ERR_MERGE),
 ])
 def test_c_abi_rejects_invalid_arguments(over, status):
     lib = cabi.load()
