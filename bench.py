@@ -19,12 +19,16 @@ Protocol
 * Roofline: K launches of the partition kernel alone (captured, replayed) give
   its average duration; achieved = logical KV bytes / duration.
 * The reference's sampling protocol (30 repetitions x 20 inner calls, runners
-  in randomized order, p50) is reported for both merge kernels.
+  in randomized order, p50) is reported for both merge kernels, eager and
+  hipGraph, cold (rotated K/V sets) and warm (one set, cache-resident).
+* A stream-copy probe (out-of-place negation of 512 MiB, read + write)
+  confirms the HBM peak the roofline is priced against.
+* CPU baseline: the C FP32 split-K restatement on all host cores available to
+  the process and on one core, each over a bounded sample of full calls.
 
 Prints one JSON line.
 """
 import argparse
-import hashlib
 import json
 import math
 import os
@@ -40,6 +44,7 @@ sys.path.insert(0, str(REPO / "paged-decode-lab_amd"))
 METRIC = "µs/decode call and achieved KV HBM GB/s (% of peak), 1 MI355X"
 PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E, public specification
 ROTATION_BYTES = 512 << 20      # > 2x the 256 MB Infinity Cache
+PROBE_BYTES = 512 << 20         # stream-copy probe: bytes read (and written) per pass
 
 
 def parse_args():
@@ -64,11 +69,14 @@ def log(args, message):
         print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
-def source_digest():
-    h = hashlib.sha256()
-    for rel in ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "include/paged_decode.h"):
-        h.update((REPO / rel).read_bytes())
-    return h.hexdigest()[:16]
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def recorded_traffic(workload, digest):
@@ -119,6 +127,7 @@ def main():
         return 2
     from paged_decode.metrics import kv_bytes, summarize, unique_token_bytes
     from paged_decode.runtime import DecodePlan
+    from paged_decode.traffic import partition_kernel_name, source_digest
     from paged_decode.workload import make_workload
 
     w = make_workload(args.workload, split_tokens=args.split_tokens)
@@ -164,23 +173,29 @@ def main():
                 return 1
     log(args, f"gate passed: max abs error vs CPU {max(gate.values()):.3e}")
 
-    cpu_baseline = None
-    if args.cpu_seconds > 0:
+    def cpu_leg(n_threads):
         calls, start = 0, time.perf_counter()
         while True:
-            cpu_oracle.decode(q_h, k_h, v_h, w.table, w.lengths, w.split_tokens, threads=threads)
+            cpu_oracle.decode(q_h, k_h, v_h, w.table, w.lengths, w.split_tokens, threads=n_threads)
             calls += 1
             elapsed = time.perf_counter() - start
             if elapsed >= args.cpu_seconds or calls >= 100000:
-                break
-        cpu_us = elapsed / calls * 1e6
+                return elapsed / calls * 1e6, calls, elapsed
+
+    cpu_baseline = None
+    if args.cpu_seconds > 0:
+        cpu_us, calls, elapsed = cpu_leg(threads)
+        one_us, one_calls, one_elapsed = cpu_leg(1)
         cpu_baseline = {
             "value": round(logical / (cpu_us * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port", "us_per_call": round(cpu_us, 2),
             "sample": f"{calls} full decode calls of this workload ({elapsed:.1f} s) with the C FP32 split-K "
                       f"restatement (oracle/cpu_decode.c, OpenMP, {threads} threads), same host arrays",
+            "one_core": {"value": round(logical / (one_us * 1e-6) / 1e9, 3), "us_per_call": round(one_us, 2),
+                         "sample": f"{one_calls} full calls ({one_elapsed:.1f} s), 1 thread"},
+            "cpu": cpu_model(),
         }
-        log(args, f"CPU baseline: {cpu_us:.1f} us/call")
+        log(args, f"CPU baseline: {cpu_us:.1f} us/call on {threads} threads, {one_us:.1f} us/call on 1")
 
     # --- warmup, graph capture ---
     stream = torch.cuda.current_stream()
@@ -228,21 +243,36 @@ def main():
     achieved = logical / (partial_us * 1e-6) / 1e9
 
     # --- reference sampling protocol: p50 over 30 x 20, randomized order ---
+    # Runners: {serial, shared} x {graph, eager}, cold (rotated sets); graph warm (set 0 only).
+    runners = {}
+    for m, p in plans.items():
+        runners[f"{m}/graph"] = lambda i, m=m: graphs[m][i % sets].replay()
+        runners[f"{m}/eager"] = lambda i, p=p: p.run(q, ks[i % sets], vs[i % sets])
+        runners[f"{m}/graph_warm"] = lambda i, m=m: graphs[m][0].replay()
     rng = random.Random(w.seed)
-    samples = {m: ([], []) for m in plans}
+    samples = {name: ([], []) for name in runners}
     for _ in range(args.repetitions):
-        order = list(plans)
+        order = list(runners)
         rng.shuffle(order)
-        for m in order:
-            dev, wall = time_region(torch, lambda i, m=m: graphs[m][i % sets].replay(), args.inner)
-            samples[m][0].append(dev / args.inner)
-            samples[m][1].append(wall / args.inner)
+        for name in order:
+            dev, wall = time_region(torch, runners[name], args.inner)
+            samples[name][0].append(dev / args.inner)
+            samples[name][1].append(wall / args.inner)
     protocol = {}
-    for m, (dev, wall) in samples.items():
+    for name, (dev, wall) in samples.items():
         s = summarize(dev, wall, L.batch)
-        protocol[m] = {"p50_us": round(s["device_ms_p50"] * 1e3, 3), "p95_us": round(s["device_ms_p95"] * 1e3, 3),
-                       "min_us": round(s["device_ms_min"] * 1e3, 3),
-                       "p50_GBps": round(logical / (s["device_ms_p50"] * 1e-3) / 1e9, 1)}
+        protocol[name] = {"p50_us": round(s["device_ms_p50"] * 1e3, 3), "p95_us": round(s["device_ms_p95"] * 1e3, 3),
+                          "min_us": round(s["device_ms_min"] * 1e3, 3),
+                          "p50_GBps": round(logical / (s["device_ms_p50"] * 1e-3) / 1e9, 1)}
+
+    # --- stream-copy probe of the HBM peak ---
+    src = torch.randn(PROBE_BYTES // 4, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    probe_ms, _ = time_region(torch, lambda i: torch.neg(src, out=dst), 20)
+    probe_gbps = 2 * PROBE_BYTES / (probe_ms * 1e-3 / 20) / 1e9
+    del src, dst
 
     digest = source_digest()
     value = logical / (us_graph * 1e-6) / 1e9
@@ -273,12 +303,13 @@ def main():
         "unique_kv_bytes_per_call": unique,
         "workspace_bytes": plan.workspace_bytes,
         "roofline": {
-            "bound": "hbm", "kernel": "partial_kernel", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+            "bound": "hbm", "kernel": partition_kernel_name(w.dtype == np.float16), "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": recorded_traffic(w.name, digest), "avg_launch_us": round(partial_us, 3),
         },
         "cpu_baseline": cpu_baseline,
-        "protocol_graph_p50": protocol,
+        "protocol_p50": protocol,
+        "stream_copy_probe_GBps": round(probe_gbps, 1),
         "gate_max_abs_vs_cpu": {m: float(f"{e:.3e}") for m, e in gate.items()},
         "wall_ms": {"graph": round(graph_wall, 3), "eager": round(eager_wall, 3)},
         "source_digest": digest,

@@ -16,7 +16,7 @@
 //     wave by lane shuffles and across waves through LDS, leaving one
 //     (m, l, n[D]) state per query head and partition. Scores are kept in log2
 //     units (scale * log2 e) and exponentiated with v_exp_f32.
-//  2. merge_serial_kernel or merge_shared_kernel: max-corrected combination of
+//  2. merge_kernel<D, serial | shared weights>: max-corrected combination of
 //     the partition states of one (sequence, query head) row, one lane per
 //     output dimension; the shared variant computes each partition's weight
 //     once into LDS and is bounded to PD_SHARED_MERGE_MAX_PARTS partitions.
@@ -107,12 +107,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Partition states (max, denominator) are float pairs. Merge loops are
-// branch-free and unrolled so the loads of kMergeUnroll states are in flight
-// together; a data-dependent branch per state would chain their latencies.
+// Merge loops are branch-free and unrolled so the loads of kMergeUnroll states
+// are in flight together; a data-dependent branch per state would chain their
+// latencies.
 constexpr int kMergeUnroll = 8;
 
-__device__ __forceinline__ float2 load_state(const float2* st, int j) { return st[j]; }
+// State j of a row, read as one 8-byte load. Callers clamp j into the row and
+// mask the result, so loads are unconditional and issue back to back.
+__device__ __forceinline__ float2 read_state(const float2* st, int j) {
+    return __builtin_bit_cast(float2, reinterpret_cast<const uint64_t*>(st)[j]);
+}
 
 // ---------------------------------------------------------------------------
 // Element types. A lane moves 16 bytes per load: 8 halves or 4 floats.
@@ -749,13 +753,13 @@ __device__ void fused_merge_tail(const PartialParams& p, float* smem) {
             const float2* st = st_base + qr * parts;
             float mx = kNoToken;
             for (int j = lane; j < parts; j += kWave) {
-                const float2 s = load_state(st, j);
+                const float2 s = read_state(st, j);
                 mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
             }
             mx = wave_max(mx);
             float den = 0.0f;
             for (int j = lane; j < parts; j += kWave) {
-                const float2 s = load_state(st, j);
+                const float2 s = read_state(st, j);
                 const float f = s.y > 0.0f ? fast_exp2(s.x - mx) : 0.0f;
                 weight[lh * parts + j] = f;
                 den = fmaf(f, s.y, den);
@@ -790,14 +794,14 @@ __device__ void fused_merge_tail(const PartialParams& p, float* smem) {
             float mx = kNoToken;
 #pragma unroll kMergeUnroll
             for (int j = 0; j < parts; ++j) {
-                const float2 s = load_state(st, j);
+                const float2 s = read_state(st, j);
                 mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
             }
             const float* num = p.numerator + qr * parts * D + d;
             float den = 0.0f, acc = 0.0f;
 #pragma unroll kMergeUnroll
             for (int j = 0; j < parts; ++j) {
-                const float2 s = load_state(st, j);
+                const float2 s = read_state(st, j);
                 const float n = num[static_cast<int64_t>(j) * D];
                 const bool live = s.y > 0.0f;
                 const float f = live ? fast_exp2(s.x - mx) : 0.0f;
@@ -819,83 +823,138 @@ __host__ __device__ inline size_t fused_shared_floats(int local_heads, int split
 // Merge kernels: one workgroup per (sequence, query head) row, one lane per
 // output dimension. A state with l == 0 is the identity (decode.cu:94-107).
 
-// Serial: every lane scans all partition states itself (no LDS).
-template <int D>
-__global__ void __launch_bounds__(D) merge_serial_kernel(const float* __restrict__ numerator,
-                                                         const float* __restrict__ stats,
-                                                         float* __restrict__ out, int parts) {
-    const int64_t row = blockIdx.x;
-    const int d = threadIdx.x;
-    const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
-    float mx = kNoToken;
-#pragma unroll kMergeUnroll
-    for (int j = 0; j < parts; ++j) {
-        const float2 s = load_state(st, j);
-        mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
-    }
-    const float* num = numerator + row * parts * D + d;
-    float den = 0.0f, acc = 0.0f;
-#pragma unroll kMergeUnroll
-    for (int j = 0; j < parts; ++j) {
-        const float2 s = load_state(st, j);
-        const float n = num[static_cast<int64_t>(j) * D];
-        const bool live = s.y > 0.0f;
-        const float f = live ? fast_exp2(s.x - mx) : 0.0f;
-        den = live ? fmaf(f, s.y, den) : den;
-        acc = live ? fmaf(f, n, acc) : acc;
-    }
-    out[row * D + d] = den > 0.0f ? acc / den : 0.0f;
-}
+// One 256-lane workgroup per row. Lane t owns the 16-byte column t % TPR of the
+// states j == t / TPR (mod PG), so a row's numerator loads are spread over the
+// whole workgroup and issued together (kMergeBatch per lane per round), while
+// the weights are formed; the PG column sums then meet in LDS.
+//   serial: every wave scans all states itself for the max and the denominator
+//           (lanes share the scan, reduced with DPP), and each lane recomputes
+//           the weight of its own states; no weight storage.
+//   shared: the workgroup forms each state's weight once, into LDS
+//           (4 bytes per state, hence the 4096-state bound).
+constexpr int kMergeThreads = 256;
+constexpr int kMergeBatch = 16;
+constexpr int kStatsUnroll = 4;
 
-template <int D>
-__global__ void __launch_bounds__(D) merge_shared_kernel(const float* __restrict__ numerator,
-                                                         const float* __restrict__ stats,
-                                                         float* __restrict__ out, int parts) {
-    extern __shared__ float weight[];  // [parts]
-    constexpr int kWaves = D / kWave;
+template <int D, bool kSharedWeights>
+__global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __restrict__ numerator,
+                                                              const float* __restrict__ stats,
+                                                              float* __restrict__ out, int parts) {
+    constexpr int TPR = D / 4;               // lanes per state row
+    constexpr int PG = kMergeThreads / TPR;  // state groups
+    constexpr int NB = kMergeBatch;
+    constexpr int kWaves = kMergeThreads / kWave;
+    constexpr int kScan = kSharedWeights ? kMergeThreads : kWave;  // lanes sharing the state scan
+    extern __shared__ float weight[];        // [parts], shared variant only
+    __shared__ f32x4 column_sum[PG][TPR];
     __shared__ float scratch[2][kWaves];
-    const int64_t row = blockIdx.x;
-    const int d = threadIdx.x;
-    const int lane = d % kWave;
-    const int wave = d / kWave;
+    const int64_t row = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;  // b * Hq + h
+    const int t = threadIdx.x;
+    const int lane = t % kWave;
+    const int wave = t / kWave;
+    const int col = t % TPR;
+    const int pg = t / TPR;
+    const int scan0 = kSharedWeights ? t : lane;
+    const int last = parts - 1;
     const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
+    const f32x4* num = reinterpret_cast<const f32x4*>(numerator + row * parts * D) + col;
 
+    f32x4 buf[NB];
+    float2 own[NB];
+    auto load_batch = [&](int base) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int j = min(base + pg + k * PG, last);
+            buf[k] = num[static_cast<int64_t>(j) * TPR];
+            if constexpr (!kSharedWeights) own[k] = read_state(st, j);
+        }
+    };
+    // The first batch of numerator rows is in flight while the weights form.
+    load_batch(0);
+
+    // Row maximum over live states (l > 0). The first scan round stays in
+    // registers for the denominator pass.
     float mx = kNoToken;
-    for (int j = d; j < parts; j += D) {
-        const float2 s = load_state(st, j);
-        mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
+    float2 first[kStatsUnroll];
+    for (int base = 0; base < parts; base += kStatsUnroll * kScan) {
+        float2 s[kStatsUnroll];
+#pragma unroll
+        for (int i = 0; i < kStatsUnroll; ++i) s[i] = read_state(st, min(base + scan0 + i * kScan, last));
+        if (base == 0) {
+#pragma unroll
+            for (int i = 0; i < kStatsUnroll; ++i) first[i] = s[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kStatsUnroll; ++i) {
+            const bool live = (base + scan0 + i * kScan < parts) & (s[i].y > 0.0f);
+            mx = live ? fmaxf(mx, s[i].x) : mx;
+        }
     }
     mx = wave_max(mx);
-    if (lane == 0) scratch[0][wave] = mx;
-    __syncthreads();
-    mx = scratch[0][0];
+    if constexpr (kSharedWeights) {
+        if (lane == 0) scratch[0][wave] = mx;
+        __syncthreads();
+        mx = scratch[0][0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, scratch[0][w]);
+        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, scratch[0][w]);
+    }
 
+    // Denominator (and, shared variant, every state's weight in LDS).
     float den = 0.0f;
-    for (int j = d; j < parts; j += D) {
-        const float2 s = load_state(st, j);
-        const float f = s.y > 0.0f ? fast_exp2(s.x - mx) : 0.0f;
-        weight[j] = f;
-        den = fmaf(f, s.y, den);
+    for (int base = 0; base < parts; base += kStatsUnroll * kScan) {
+        float2 s[kStatsUnroll];
+#pragma unroll
+        for (int i = 0; i < kStatsUnroll; ++i)
+            s[i] = base == 0 ? first[i] : read_state(st, min(base + scan0 + i * kScan, last));
+#pragma unroll
+        for (int i = 0; i < kStatsUnroll; ++i) {
+            const int j = base + scan0 + i * kScan;
+            const bool live = (j < parts) & (s[i].y > 0.0f);
+            const float f = live ? fast_exp2(s[i].x - mx) : 0.0f;
+            if constexpr (kSharedWeights) {
+                if (j < parts) weight[j] = f;
+            }
+            den = fmaf(f, live ? s[i].y : 0.0f, den);
+        }
     }
     den = wave_sum(den);
-    if (lane == 0) scratch[1][wave] = den;
-    __syncthreads();
-    den = scratch[1][0];
+    if constexpr (kSharedWeights) {
+        if (lane == 0) scratch[1][wave] = den;
+        __syncthreads();  // also publishes weight[]
+        den = scratch[1][0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) den += scratch[1][w];
-
-    const float* num = numerator + row * parts * D + d;
-    float acc = 0.0f;
-#pragma unroll kMergeUnroll
-    for (int j = 0; j < parts; ++j) {
-        // A state with weight 0 (empty partition) contributes nothing, whatever
-        // its numerator holds.
-        const float n = num[static_cast<int64_t>(j) * D];
-        acc = weight[j] > 0.0f ? fmaf(weight[j], n, acc) : acc;
+        for (int w = 1; w < kWaves; ++w) den += scratch[1][w];
     }
-    out[row * D + d] = den > 0.0f ? acc / den : 0.0f;
+
+    // Weighted column sums; a state of weight 0 (empty partition, or a clamped
+    // duplicate past the row) contributes nothing, whatever its numerator holds.
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = 0;;) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int j = base + pg + k * PG;
+            float f;
+            if constexpr (kSharedWeights) {
+                f = weight[min(j, last)];
+            } else {
+                f = own[k].y > 0.0f ? fast_exp2(own[k].x - mx) : 0.0f;
+            }
+            f = j < parts ? f : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = f > 0.0f ? fmaf(f, buf[k][e], acc[e]) : acc[e];
+        }
+        base += NB * PG;
+        if (base >= parts) break;
+        load_batch(base);
+    }
+    column_sum[pg][col] = acc;
+    __syncthreads();
+    if (t < D) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int g = 0; g < PG; ++g) sum += reinterpret_cast<const float*>(column_sum[g])[t];
+        out[row * D + t] = den > 0.0f ? sum / den : 0.0f;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1039,13 +1098,14 @@ int run_partial(const void* q, const void* k, const void* v, int dtype, const in
 }
 
 template <int D>
-int launch_merge(const float* numerator, const float* stats, float* out, int rows, int parts,
+int launch_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads, int parts,
                  int merge_mode, hipStream_t stream) {
+    const dim3 grid(query_heads, batch);
     if (merge_mode == PD_MERGE_SHARED) {
-        hipLaunchKernelGGL((merge_shared_kernel<D>), dim3(rows), dim3(D), parts * sizeof(float), stream,
+        hipLaunchKernelGGL((merge_kernel<D, true>), grid, dim3(kMergeThreads), parts * sizeof(float), stream,
                            numerator, stats, out, parts);
     } else {
-        hipLaunchKernelGGL((merge_serial_kernel<D>), dim3(rows), dim3(D), 0, stream, numerator, stats,
+        hipLaunchKernelGGL((merge_kernel<D, false>), grid, dim3(kMergeThreads), 0, stream, numerator, stats,
                            out, parts);
     }
     return launch_status();
@@ -1064,10 +1124,9 @@ int check_merge(const float* numerator, const float* stats, const float* out, in
 
 int run_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads,
               int head_dim, int splits, int merge_mode, hipStream_t stream) {
-    const int rows = batch * query_heads;
     const int parts = kQuarters * splits;
-    return head_dim == 64 ? launch_merge<64>(numerator, stats, out, rows, parts, merge_mode, stream)
-                          : launch_merge<128>(numerator, stats, out, rows, parts, merge_mode, stream);
+    return head_dim == 64 ? launch_merge<64>(numerator, stats, out, batch, query_heads, parts, merge_mode, stream)
+                          : launch_merge<128>(numerator, stats, out, batch, query_heads, parts, merge_mode, stream);
 }
 
 }  // namespace

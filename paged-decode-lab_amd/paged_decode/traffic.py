@@ -1,0 +1,165 @@
+"""HBM bytes per partition launch, from two ``rocprofv3 --pmc`` passes.
+
+``run`` is the program the counter passes profile: it builds a DecodePlan for a
+named workload, replicates K/V into buffer sets covering >= 512 MiB (so no
+launch is served from the 256 MB Infinity Cache), launches the partition kernel
+``--launches`` times round-robin over the sets, then runs a plain elementwise
+copy (``torch.neg`` of a float32 tensor, out of place) of a known size. The
+copy calibrates the counters: FETCH_SIZE and WRITE_SIZE are reported in KiB
+per dispatch, and the copy's true traffic is its tensor size read plus the same
+size written, so ``scale = true bytes / counter bytes`` for each counter.
+
+``summarize FETCH_DIR WRITE_DIR`` reads the counter CSVs of the two passes and
+writes ``profiles/traffic_<workload>.json`` with the scaled read and write
+bytes per partition launch, the algorithmic KV bytes next to them, and the
+digest of the kernel source the counters were taken on.
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT/fetch -- \\
+        python3 paged-decode-lab_amd/paged_decode/traffic.py run
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -- \\
+        python3 paged-decode-lab_amd/paged_decode/traffic.py run
+    python3 paged-decode-lab_amd/paged_decode/traffic.py summarize OUT/fetch OUT/write
+"""
+import argparse
+import csv
+import hashlib
+import json
+import math
+import sys
+from pathlib import Path
+
+PACKAGE_ROOT = Path(__file__).resolve().parent.parent
+REPO = PACKAGE_ROOT.parent
+ROTATION_BYTES = 512 << 20
+COPY_BYTES = 256 << 20
+SOURCES = ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "include/paged_decode.h")
+
+
+def source_digest():
+    """Short digest of the kernel source and its header."""
+    h = hashlib.sha256()
+    for rel in SOURCES:
+        h.update((REPO / rel).read_bytes())
+    return h.hexdigest()[:16]
+
+
+def partition_kernel_name(dtype_is_half):
+    return "partial_mfma_kernel" if dtype_is_half else "partial_kernel"
+
+
+def run(args):
+    import numpy as np
+    import torch
+
+    from paged_decode.runtime import DecodePlan
+    from paged_decode.workload import make_workload
+
+    w = make_workload(args.workload)
+    q_h, k_h, v_h = w.host_tensors()
+    dev = torch.device("cuda", 0)
+    q = torch.from_numpy(q_h).to(dev)
+    k0, v0 = torch.from_numpy(k_h).to(dev), torch.from_numpy(v_h).to(dev)
+    sets = max(1, math.ceil(ROTATION_BYTES / (2 * k0.numel() * k0.element_size())))
+    ks = [k0] + [k0.clone() for _ in range(sets - 1)]
+    vs = [v0] + [v0.clone() for _ in range(sets - 1)]
+    plan = DecodePlan(w.layout, w.table, w.lengths, device=dev, split_tokens=w.split_tokens)
+    print(f"[traffic] {w.name}: {args.launches} partition launches over {sets} K/V sets", flush=True)
+    for i in range(args.launches):
+        plan.run_partial(q, ks[i % sets], vs[i % sets])
+    torch.cuda.synchronize()
+    src = torch.randn(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.copies):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(f"[traffic] {args.copies} calibration copies of {COPY_BYTES} bytes; half={w.dtype == np.float16}",
+          flush=True)
+
+
+def read_counter(directory, counter):
+    """{kernel name: [values per dispatch]} for one counter from rocprofv3 CSVs."""
+    per_kernel = {}
+    files = sorted(Path(directory).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    for path in files:
+        with open(path, newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                per_kernel.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return per_kernel
+
+
+def pick(per_kernel, needle):
+    names = [n for n in per_kernel if needle in n]
+    if len(names) != 1:
+        raise SystemExit(f"expected one kernel matching {needle!r}, found {names}")
+    values = per_kernel[names[0]]
+    return names[0], values
+
+
+def summarize(args):
+    from paged_decode.metrics import kv_bytes
+    from paged_decode.workload import make_workload
+    import numpy as np
+
+    w = make_workload(args.workload)
+    logical = kv_bytes(w.lengths, w.layout.kv_heads, w.layout.head_dim, w.element_size)
+    kernel = partition_kernel_name(w.dtype == np.float16)
+    record = {"workload": w.name, "kernel": kernel, "algorithmic_bytes_per_launch": logical}
+    total = 0.0
+    for counter, directory, key in (("FETCH_SIZE", args.fetch_dir, "read"), ("WRITE_SIZE", args.write_dir, "write")):
+        per_kernel = read_counter(directory, counter)
+        name, values = pick(per_kernel, kernel + "<")
+        _, copies = pick(per_kernel, "neg_kernel")
+        copy_kib = sum(copies) / len(copies)
+        scale = COPY_BYTES / (copy_kib * 1024.0)
+        kib = sum(values) / len(values)
+        scaled = kib * 1024.0 * scale
+        total += scaled
+        record[f"{counter.lower()}_kib_per_launch"] = round(kib, 1)
+        record[f"{counter.lower()}_copy_kib"] = round(copy_kib, 1)
+        record[f"{counter.lower()}_scale"] = round(scale, 4)
+        record[f"hbm_{key}_bytes_per_launch"] = round(scaled)
+        record[f"{counter.lower()}_launches"] = len(values)
+        record["kernel_symbol"] = name
+    record["hbm_bytes_per_launch"] = round(total)
+    record["traffic_over_algorithmic"] = round(total / logical, 4)
+    record["copy_bytes"] = COPY_BYTES
+    record["source_digest"] = source_digest()
+    record["commands"] = [
+        "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -- "
+        f"python3 paged-decode-lab_amd/paged_decode/traffic.py run --workload {w.name}",
+        "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -- "
+        f"python3 paged-decode-lab_amd/paged_decode/traffic.py run --workload {w.name}",
+        f"python3 paged-decode-lab_amd/paged_decode/traffic.py summarize gpurun_out/pmc_fetch gpurun_out/pmc_write "
+        f"--workload {w.name}",
+    ]
+    out = REPO / "profiles" / f"traffic_{w.name}.json"
+    out.parent.mkdir(exist_ok=True)
+    out.write_text(json.dumps(record, indent=2) + "\n")
+    print(json.dumps(record, indent=2))
+
+
+def main(argv=None):
+    # Run as a script, this file's directory leads sys.path; the package root must instead.
+    here = str(Path(__file__).resolve().parent)
+    sys.path[:] = [x for x in sys.path if Path(x or ".").resolve() != Path(here)]
+    sys.path.insert(0, str(PACKAGE_ROOT))
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = p.add_subparsers(dest="cmd", required=True)
+    r = sub.add_parser("run")
+    r.add_argument("--workload", default="llama3_8b_b4_l4096")
+    r.add_argument("--launches", type=int, default=24)
+    r.add_argument("--copies", type=int, default=4)
+    s = sub.add_parser("summarize")
+    s.add_argument("fetch_dir")
+    s.add_argument("write_dir")
+    s.add_argument("--workload", default="llama3_8b_b4_l4096")
+    args = p.parse_args(argv)
+    return run(args) if args.cmd == "run" else summarize(args)
+
+
+if __name__ == "__main__":
+    sys.exit(main())
