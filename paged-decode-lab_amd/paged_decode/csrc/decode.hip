@@ -107,6 +107,84 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// gfx950 v_permlane32_swap / v_permlane16_swap on float pairs. For (a, b):
+//   swap32: lanes 0-31 get (a[l], a[l+32]), lanes 32-63 get (b[l-32], b[l]);
+//   swap16: even 16-lane rows get (a[l], a[l+16]), odd rows (b[l-16], b[l]).
+// The pair's sum is a + partner's a in the lower half (even rows) and
+// b + partner's b in the upper half (odd rows): one reduce-scatter step.
+// The builtins return a two-element vector; its elements are copied into
+// scalars before the bit cast (a bit cast of a vector-element lvalue reads
+// element 0 with this compiler).
+struct FloatPair {
+    float first, second;
+};
+
+__device__ __forceinline__ FloatPair permlane32_swap(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b),
+                                                    false, false);
+    const unsigned first = r[0], second = r[1];
+    return {__builtin_bit_cast(float, first), __builtin_bit_cast(float, second)};
+}
+
+__device__ __forceinline__ FloatPair permlane16_swap(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, a), __builtin_bit_cast(unsigned, b),
+                                                    false, false);
+    const unsigned first = r[0], second = r[1];
+    return {__builtin_bit_cast(float, first), __builtin_bit_cast(float, second)};
+}
+
+__device__ __forceinline__ float swap32_sum(float a, float b) {
+    const FloatPair r = permlane32_swap(a, b);
+    return r.first + r.second;
+}
+
+__device__ __forceinline__ float swap16_sum(float a, float b) {
+    const FloatPair r = permlane16_swap(a, b);
+    return r.first + r.second;
+}
+
+// Max / sum over lanes l, l ^ 16, l ^ 32, l ^ 48, result in every lane.
+__device__ __forceinline__ float max_over_lane_groups(float x) {
+    const FloatPair r = permlane32_swap(x, x);
+    x = fmaxf(r.first, r.second);
+    const FloatPair s = permlane16_swap(x, x);
+    return fmaxf(s.first, s.second);
+}
+
+__device__ __forceinline__ float sum_over_lane_groups(float x) {
+    x = swap32_sum(x, x);
+    return swap16_sum(x, x);
+}
+
+constexpr int kDppRowRotate8 = 0x128;  // row_ror:8, lane l reads lane l ^ 8 of its 16-lane row
+
+// Sums v over the wave's R token rows (lanes [r * 64 / R, (r + 1) * 64 / R))
+// and scatters the result: the lanes of row r end with elements
+// [r * N / R, (r + 1) * N / R) of v, summed over all rows. Halving steps over
+// lane bits 5, 4 (swaps) and 3 (DPP), most significant first.
+template <int N, int R>
+__device__ __forceinline__ void row_reduce_scatter(const float (&v)[N], float (&out)[N / R], int lane) {
+    static_assert(R == 4 || R == 8, "four or eight token rows per wave");
+    float h1[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) h1[i] = swap32_sum(v[i], v[i + N / 2]);
+    float h2[N / 4];
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) h2[i] = swap16_sum(h1[i], h1[i + N / 4]);
+    if constexpr (R == 4) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) out[i] = h2[i];
+    } else {
+        const bool upper = (lane & 8) != 0;
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) {
+            const float mine = upper ? h2[i + N / 8] : h2[i];
+            const float send = upper ? h2[i] : h2[i + N / 8];
+            out[i] = mine + dpp_move<kDppRowRotate8>(send);
+        }
+    }
+}
+
 // Merge loops are branch-free and unrolled so the loads of kMergeUnroll states
 // are in flight together; a data-dependent branch per state would chain their
 // latencies.
@@ -281,6 +359,37 @@ __device__ __forceinline__ void store_wave_state(const PartialParams& p, const W
                 f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + g) * parts + part) * D + col * EPL);
 #pragma unroll
                 for (int e = 0; e < EPL; e += 4) dst[e / 4] = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
+            }
+        }
+    }
+    if (lane < w.heads_here) {
+        float2* st = reinterpret_cast<float2*>(p.stats) + (w.q_row + lane) * parts + part;
+        *st = make_float2(l > 0.0f ? m : kNoToken, l);
+    }
+}
+
+// Stores a wave's state when lane (row, col) holds elements
+// [row * CNT, (row + 1) * CNT) of column col's flattened (head, element) array;
+// m and l for head g are in lane g.
+template <int D, int GT, int EPL, int CNT>
+__device__ __forceinline__ void store_scattered_state(const PartialParams& p, const WaveWork& w, int lane, int row,
+                                                      int col, const float (&v)[CNT], float m, float l) {
+    const int parts = kQuarters * p.splits;
+    const int part = w.split * kQuarters + w.quarter;
+    constexpr int kStore = CNT < 4 ? CNT : 4;  // floats per store
+#pragma unroll
+    for (int i = 0; i < CNT; i += kStore) {
+        const int flat = row * CNT + i;
+        const int g = flat / EPL;
+        const int e = flat % EPL;
+        if (g < w.heads_here) {
+            float* dst = p.numerator + ((w.q_row + g) * parts + part) * D + col * EPL + e;
+            if constexpr (kStore == 4) {
+                *reinterpret_cast<f32x4*>(dst) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+            } else if constexpr (kStore == 2) {
+                *reinterpret_cast<float2*>(dst) = make_float2(v[i], v[i + 1]);
+            } else {
+                *dst = v[i];
             }
         }
     }
@@ -499,17 +608,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 // add up at the end.
 constexpr int kTileTokens = 16;
 
-template <int D, int GT>
-constexpr int rows_in_lds() {  // rows kept apart in LDS for the final row sum (1 = summed in registers)
-    constexpr int TPL = kWave / (D / 8);
-    return 8 * TPL * GT * D * 4 <= 64 * 1024 ? TPL : 1;
-}
-
-template <int D, int GT>
-constexpr size_t mfma_state_floats() {  // dynamic LDS floats per wave for the row sum
-    return rows_in_lds<D, GT>() > 1 ? static_cast<size_t>(rows_in_lds<D, GT>()) * GT * D : 0;
-}
-
 template <int D, int GT, int PD, int NC>
 __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
     using E = Elem<_Float16>;
@@ -518,7 +616,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     constexpr int TPL = kWave / LPT;       // tokens per V load
     constexpr int VI = kTileTokens / TPL;  // V loads per tile
     constexpr int KS = D / 32;             // MFMA k-steps (K loads) per tile
-    constexpr int R = rows_in_lds<D, GT>();
     static_assert(GT <= 8, "P.V accumulators are sized for at most 8 heads");
 
     struct Tile {
@@ -607,9 +704,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
             x[i] = valid ? sc[i] : -INFINITY;
             mx = fmaxf(mx, x[i]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float tile_max = mx * p.scale_log2;
+        const float tile_max = max_over_lane_groups(mx) * p.scale_log2;
         if (__any((kt < GT) & (tile_max > m_head + kRescaleSlack))) {
             const float m_new = fmaxf(m_head, tile_max);
             const float alpha = fast_exp2(m_head - m_new);
@@ -663,50 +758,21 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         }
     }
 
-    // Sum the wave's token rows (they share one max per head): through this
-    // wave's LDS slice when it fits, else with lane shuffles; then lanes of
-    // row 0 hold the sums. The denominator is summed over the four lane groups
-    // of the MFMA layout.
-    if constexpr (R > 1) {
-        float* rows = smem + static_cast<size_t>(wave) * R * GT * D;  // [R][GT][D]
+    // Sum the wave's token rows (they share one max per head) with a
+    // reduce-scatter in registers: lane (row r, column c) ends with elements
+    // [r * CNT, (r + 1) * CNT) of the (head, element) array of column c. The
+    // denominator is summed over the four lane groups of the MFMA layout.
+    constexpr int N = GT * EPL;
+    constexpr int CNT = N / TPL;
+    float flat[N];
 #pragma unroll
-        for (int g = 0; g < GT; ++g) {
-            f32x4* dst = reinterpret_cast<f32x4*>(rows + (row * GT + g) * D + col * EPL);
-            dst[0] = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
-            dst[1] = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
-        }
-        if (lane < LPT) {
+    for (int g = 0; g < GT; ++g)
 #pragma unroll
-            for (int g = 0; g < GT; ++g) {
-                f32x4 s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const f32x4* src = reinterpret_cast<const f32x4*>(rows + (r * GT + g) * D + col * EPL);
-                    s0 += src[0];
-                    s1 += src[1];
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    acc[g][e] = s0[e];
-                    acc[g][e + 4] = s1[e];
-                }
-            }
-        }
-    } else {
-#pragma unroll
-        for (int g = 0; g < GT; ++g)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                float a = acc[g][e];
-#pragma unroll
-                for (int x = LPT; x < kWave; x <<= 1) a += __shfl_xor(a, x);
-                acc[g][e] = a;
-            }
-    }
-    float l_head = l_part;
-    l_head += __shfl_xor(l_head, 16);
-    l_head += __shfl_xor(l_head, 32);
-    store_wave_state<D, GT, EPL, LPT>(p, w, lane, acc, m_head, l_head);
+        for (int e = 0; e < EPL; ++e) flat[g * EPL + e] = acc[g][e];
+    float mine[CNT];
+    row_reduce_scatter<N, TPL>(flat, mine, lane);
+    const float l_head = sum_over_lane_groups(l_part);
+    store_scattered_state<D, GT, EPL, CNT>(p, w, lane, row, col, mine, m_head, l_head);
     if (p.fuse != kFuseNone) fused_merge_tail<D, GT>(p, smem);
 }
 
@@ -999,6 +1065,10 @@ constexpr size_t kFusedSharedLdsBytes = 48 * 1024;
 #ifndef PD_MFMA_BLOCK
 #define PD_MFMA_BLOCK 8
 #endif
+// KV heads per partition workgroup, at most.
+#ifndef PD_WG_HEADS
+#define PD_WG_HEADS 8
+#endif
 
 // Largest divisor of n not above cap.
 int largest_divisor(int n, int cap) {
@@ -1012,7 +1082,7 @@ int largest_divisor(int n, int cap) {
 // serves best), all head tiles of those heads, and as many partition quarters
 // as fill 8 waves.
 void choose_workgroup(PartialParams& prm, int kv_heads) {
-    prm.heads_per_wg = largest_divisor(kv_heads, 8);
+    prm.heads_per_wg = largest_divisor(kv_heads, PD_WG_HEADS);
     prm.tiles_per_wg = largest_divisor(prm.head_tiles, 8 / prm.heads_per_wg);
     const int hw_tw = prm.heads_per_wg * prm.tiles_per_wg;
     prm.quarters_per_wg = hw_tw <= 2 ? 4 : hw_tw <= 4 ? 2 : 1;
@@ -1021,7 +1091,7 @@ void choose_workgroup(PartialParams& prm, int kv_heads) {
 template <typename T, int D, int GT>
 int launch_partial(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const int waves = prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
-    size_t floats = std::is_same_v<T, _Float16> ? static_cast<size_t>(waves) * mfma_state_floats<D, GT>() : 0;
+    size_t floats = 0;
     if (prm.fuse == kFuseShared)
         floats = std::max(floats, fused_shared_floats(prm.heads_per_wg * prm.tiles_per_wg * GT, prm.splits));
     const dim3 grid(prm.splits * (kQuarters / prm.quarters_per_wg),
