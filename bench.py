@@ -13,11 +13,14 @@ Protocol
 * Correctness gate first: the GPU output is compared with the C FP32 split-K
   restatement on the same inputs (this is also the CPU-baseline leg); no
   timing is reported if it fails.
-* Timed region: W untimed warmup steps, then exactly K steps as hipGraph
-  replays (one captured graph per buffer set), bracketed by synchronize and
-  HIP events on the launch stream. Eager launches are timed the same way.
-* Roofline: K launches of the partition kernel alone (captured, replayed) give
-  its average duration; achieved = logical KV bytes / duration.
+* Timed region: W untimed warmup steps, then exactly K steps: the K decode
+  calls captured back to back in one hipGraph (call i reads K/V set i mod
+  sets) and replayed once, bracketed by synchronize and HIP events on the
+  launch stream. value = logical KV bytes per call / device time per call.
+  K eager (Python-level) calls are timed the same way and reported beside it.
+* Roofline: K back-to-back launches of the partition kernel alone (one
+  captured graph) give its average launch duration; achieved = logical KV
+  bytes / duration.
 * The reference's sampling protocol (30 repetitions x 20 inner calls, runners
   in randomized order, p50) is reported for both merge kernels, eager and
   hipGraph, cold (rotated K/V sets) and warm (one set, cache-resident).
@@ -67,6 +70,12 @@ def parse_args():
 def log(args, message):
     if not args.quiet:
         print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def device_label(torch):
+    props = torch.cuda.get_device_properties(0)
+    arch = getattr(props, "gcnArchName", "")
+    return f"{props.name or 'AMD GPU'} ({arch}, {props.multi_processor_count} CUs)"
 
 
 def cpu_model():
@@ -218,29 +227,36 @@ def main():
 
     graphs = {m: [capture(lambda p=p, i=i: p.run(q, ks[i], vs[i])) for i in range(sets)]
               for m, p in plans.items()}
-    for i in range(args.warmup):
-        graphs[args.merge][i % sets].replay()
 
     # --- timed region: exactly K steps ---
-    graph_ms, graph_wall = time_region(torch, lambda i: graphs[args.merge][i % sets].replay(), args.steps)
+    # The K decode calls are captured back to back in one graph (call i reads
+    # K/V set i mod sets) and replayed once: device time per call with no host
+    # launch cost in between. Eager: K Python-level calls, host included.
+    def steps_graph(fn, count):
+        def body():
+            for i in range(count):
+                fn(i)
+        g = capture(body)
+        for _ in range(max(1, args.warmup // count)):
+            g.replay()
+        return g
+
+    step_graph = steps_graph(lambda i: plan.run(q, ks[i % sets], vs[i % sets]), args.steps)
+    graph_ms, graph_wall = time_region(torch, lambda i: step_graph.replay(), 1)
+    for i in range(args.warmup):
+        plan.run(q, ks[i % sets], vs[i % sets])
     eager_ms, eager_wall = time_region(torch, lambda i: plan.run(q, ks[i % sets], vs[i % sets]), args.steps)
     us_graph = graph_ms * 1e3 / args.steps
     us_eager = eager_ms * 1e3 / args.steps
-    log(args, f"graph {us_graph:.2f} us/call, eager {us_eager:.2f} us/call")
+    log(args, f"graph of {args.steps} calls: {us_graph:.2f} us/call; eager {us_eager:.2f} us/call")
+    del step_graph
 
-    # --- partition kernel alone (roofline numerator) ---
-    burst = 20
-    partial_graphs = []
-    for i in range(sets):
-        def launches(i=i):
-            for j in range(burst):
-                plan.run_partial(q, ks[(i + j) % sets], vs[(i + j) % sets])
-        partial_graphs.append(capture(launches))
-    partial_graphs[0].replay()
-    reps = max(1, args.steps // burst)
-    partial_ms, _ = time_region(torch, lambda i: partial_graphs[i % sets].replay(), reps)
-    partial_us = partial_ms * 1e3 / (reps * burst)
+    # --- partition kernel alone (roofline numerator): K launches back to back ---
+    partial_graph = steps_graph(lambda i: plan.run_partial(q, ks[i % sets], vs[i % sets]), args.steps)
+    partial_ms, _ = time_region(torch, lambda i: partial_graph.replay(), 1)
+    partial_us = partial_ms * 1e3 / args.steps
     achieved = logical / (partial_us * 1e-6) / 1e9
+    del partial_graph
 
     # --- reference sampling protocol: p50 over 30 x 20, randomized order ---
     # Runners: {serial, shared} x {graph, eager}, cold (rotated sets); graph warm (set 0 only).
@@ -296,7 +312,7 @@ def main():
         "config": {
             "workload": w.name, "batch": L.batch, "query_heads": L.query_heads, "kv_heads": L.kv_heads,
             "head_dim": L.head_dim, "page_size": L.page_size, "context": int(w.lengths.max()),
-            "split_tokens": w.split_tokens, "splits": plan.splits, "merge": args.merge, "mode": "hipgraph",
+            "split_tokens": w.split_tokens, "splits": plan.splits, "merge": args.merge, "mode": "hipgraph, K calls per replay",
             "kv_buffer_sets": sets, "parallelism": "single GPU",
         },
         "kv_bytes_per_call": logical,
@@ -313,7 +329,7 @@ def main():
         "gate_max_abs_vs_cpu": {m: float(f"{e:.3e}") for m, e in gate.items()},
         "wall_ms": {"graph": round(graph_wall, 3), "eager": round(eager_wall, 3)},
         "source_digest": digest,
-        "device": torch.cuda.get_device_name(0),
+        "device": device_label(torch),
     }
     print(json.dumps(record), flush=True)
     return 0

@@ -1058,12 +1058,15 @@ constexpr size_t kFusedSharedLdsBytes = 48 * 1024;
 #define PD_BLOCK_CHUNKS 16
 #endif
 // FP16 kernel (MFMA scoring): 16-token tiles in flight ahead of the one being
-// consumed, and tiles per straight-line block.
+// consumed, and tiles per straight-line block. Short blocks keep the kernel's
+// code small: with 8 waves per CU running through cold straight-line code,
+// instruction fetch is on the critical path (two-tile blocks measured 1 us
+// faster per Llama-3-8B-shape call than eight-tile blocks, same loads).
 #ifndef PD_MFMA_PREFETCH
 #define PD_MFMA_PREFETCH 1
 #endif
 #ifndef PD_MFMA_BLOCK
-#define PD_MFMA_BLOCK 8
+#define PD_MFMA_BLOCK 2
 #endif
 // KV heads per partition workgroup, at most.
 #ifndef PD_WG_HEADS
