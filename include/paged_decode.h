@@ -77,25 +77,6 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype,
               int merge_mode, void* stream);
 
 /*
- * Full decode in ONE launch: the partition kernel's last workgroup per
- * (sequence, KV head) row runs the merge (serial or LDS-bounded, as
- * merge_mode says) on that row's states. Same result contract as pd_decode;
- * no reference counterpart beyond decode() itself (decode.cu:197-246), of which
- * it is a faster schedule.
- * `counters` is int32[batch * query_heads] of device memory, all zero before
- * the first call; every call leaves it all zero again, so it needs no reset
- * between calls or graph replays. When the LDS-bounded merge of a row's
- * states does not fit beside the partition kernel it runs as its own kernel
- * (two launches, same algorithm).
- */
-int pd_decode_fused(const void* q, const void* k, const void* v, int dtype,
-                    const int32_t* table, const int32_t* lengths,
-                    float* numerator, float* stats, int32_t* counters, float* out,
-                    int batch, int query_heads, int kv_heads, int head_dim, int page_size,
-                    int table_width, int physical_pages, int splits, int split_tokens,
-                    int merge_mode, void* stream);
-
-/*
  * Partition stage only (the first launch of pd_decode): fills numerator and
  * stats. Replaces the partial_decode launch of reference decode.cu:176-182.
  */
@@ -127,7 +108,7 @@ size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits);
 const char* pd_status_string(int status);
 
 /* ABI version of this header: bumped on any signature or layout change
- * (2: pd_decode_fused; 3: four states per partition). */
+ * (3: four states per partition; 4: single-launch entry withdrawn). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

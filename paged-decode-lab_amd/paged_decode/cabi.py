@@ -26,7 +26,6 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 PROTOTYPES = {
     "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
-    "pd_decode_fused": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
     "pd_decode_partial": (_I, [_P, _P, _P, _I, _P, _P, _P, _P] + [_I] * 9 + [_P]),
     "pd_decode_merge": (_I, [_P, _P, _P] + [_I] * 5 + [_P]),
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),

@@ -3,31 +3,41 @@
 // Implements the C ABI declared in include/paged_decode.h. pd_decode makes two
 // launches per call, both on the caller's stream:
 //
-//  1. partial_kernel: one workgroup of NW waves per (partition, KV head [,
-//     head tile], sequence). Each K/V row is loaded from HBM exactly once and
-//     used by every query head of the GQA group, held in registers. The waves
-//     take contiguous shares of the partition; inside a wave, a 16-byte load
-//     covers TPL consecutive tokens (lanes [r*LPT, (r+1)*LPT) hold token r's
-//     row), chunks of NL loads stream through PD + 1 register buffers in fully
-//     unrolled blocks (PD chunks in flight), q.k is reduced with DPP row
-//     operations, page ids come from a lane-indexed window via v_readlane
-//     (requested at kernel start, in parallel with the length), and each token row r
-//     keeps its own online-softmax stream. Streams are combined within the
-//     wave by lane shuffles and across waves through LDS, leaving one
-//     (m, l, n[D]) state per query head and partition. Scores are kept in log2
-//     units (scale * log2 e) and exponentiated with v_exp_f32.
+//  1. Partition kernel. Each partition of split_tokens tokens is cut into four
+//     quarters, and each (quarter, KV head, head tile) is one wave's work: it
+//     reads that KV head's K and V rows of the quarter from HBM exactly once,
+//     uses them for every query head of the tile (the GQA group, padded to
+//     GT = 1/2/4/8 heads), and stores one (m, l, n[D]) state per query head in
+//     slot 4 * partition + quarter of the workspace. A workgroup gathers up to
+//     eight KV heads of the same tokens (their head slices of a token row are
+//     then read together) plus enough quarters to make eight waves. Waves
+//     never synchronise with each other.
+//       partial_mfma_kernel (FP16): 16-token tiles; q.K^T on the matrix
+//       cores (v_mfma_f32_16x16x32_f16, K rows as the A operand, the query
+//       heads as B), online softmax with one running max per head and lazy
+//       rescaling (accumulators are rescaled only when a tile's max exceeds
+//       the running max by 2^8), P.V as mixed-precision FMAs on the vector ALU
+//       with P in FP32, then a register reduce-scatter of the token rows
+//       (v_permlane32/16_swap, DPP) so each lane stores its own slice.
+//       partial_kernel (FP32): the same decomposition on the vector ALU;
+//       q.k is reduced over each token row's lanes with DPP, every token row
+//       keeps its own online-softmax stream, and the rows' streams are
+//       combined with lane shuffles before the store.
+//     Page ids come from a 64-entry, lane-indexed window read once per wave
+//     and indexed with v_readlane; loads stream through a short register
+//     pipeline in fully unrolled blocks. Scores are kept in log2 units
+//     (scale * log2 e) and exponentiated with v_exp_f32.
 //  2. merge_kernel<D, serial | shared weights>: max-corrected combination of
-//     the partition states of one (sequence, query head) row, one lane per
-//     output dimension; the shared variant computes each partition's weight
-//     once into LDS and is bounded to PD_SHARED_MERGE_MAX_PARTS partitions.
-//
-// pd_decode_fused runs the same merge algebra (serial or LDS-weighted) inside
-// the partition kernel: the last workgroup to finish a row, detected with a
-// device-scope arrival counter, combines that row's states. One launch per call.
+//     the 4 * splits states of each (sequence, query head) row, with the row's
+//     state loads spread over a 256-lane workgroup. The serial variant has
+//     every wave recompute the maximum and the denominator; the shared variant
+//     forms each state's weight once in LDS and is bounded to
+//     PD_SHARED_MERGE_MAX_PARTS states.
 //
 // Semantics follow reference src/paged_decode/csrc/decode.cu:26-168 (online
 // softmax and merge algebra, empty rows -> 0, l > 0 merge guard, page-id guard)
-// and docs/DESIGN.md:5-65; the decomposition and data paths are this file's own.
+// and docs/DESIGN.md:5-76 (workspace of 4 * S states); the decomposition and
+// data paths are this file's own.
 
 #include <hip/hip_runtime.h>
 
@@ -252,8 +262,6 @@ struct Elem<float> {
 // state index 4 * split + quarter. Waves never combine with each other, so the
 // kernels have no workgroup barrier on the hot path.
 
-// Fused-merge modes (PartialParams::fuse).
-enum FuseMode { kFuseNone = 0, kFuseSerial = 1, kFuseShared = 2 };
 
 // States per partition (quarters of the partition).
 constexpr int kQuarters = 4;
@@ -270,8 +278,6 @@ struct PartialParams {
     const int32_t* lengths;
     float* numerator;   // [B, Hq, 4 * splits, D]
     float* stats;       // [B, Hq, 4 * splits, 2]
-    float* out;         // [B, Hq, D], written by the fused merge
-    int32_t* counters;  // [B * gridDim.y] arrival counters, zero between calls
     int query_heads;
     int group;          // query heads per KV head
     int head_tiles;     // ceil(group / GT)
@@ -283,7 +289,6 @@ struct PartialParams {
     int physical_pages;
     int splits;
     int split_tokens;
-    int fuse;              // FuseMode
     uint32_t token_bytes;  // bytes between consecutive tokens of a page (kv_heads * D * elem)
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) / sqrt(D)
@@ -399,8 +404,6 @@ __device__ __forceinline__ void store_scattered_state(const PartialParams& p, co
     }
 }
 
-template <int D, int GT>
-__device__ void fused_merge_tail(const PartialParams& p, float* smem);
 
 // ---------------------------------------------------------------------------
 // FP32 (and generic) partition kernel, VALU only.
@@ -425,7 +428,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
         uint32_t live;
     };
 
-    extern __shared__ float smem[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
     const int row = lane / LPT;
@@ -589,7 +591,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
         l_lane = lane == g ? l[g] : l_lane;
     }
     store_wave_state<D, GT, EPL, LPT>(p, w, lane, acc, m_lane, l_lane);
-    if (p.fuse != kFuseNone) fused_merge_tail<D, GT>(p, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -624,7 +625,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         uint32_t live;
     };
 
-    extern __shared__ float smem[];
     __shared__ float ptile[8][kTileTokens * GT];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -773,116 +773,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     row_reduce_scatter<N, TPL>(flat, mine, lane);
     const float l_head = sum_over_lane_groups(l_part);
     store_scattered_state<D, GT, EPL, CNT>(p, w, lane, row, col, mine, m_head, l_head);
-    if (p.fuse != kFuseNone) fused_merge_tail<D, GT>(p, smem);
-}
-
-// ---------------------------------------------------------------------------
-// Fused merge: the last workgroup to finish a (sequence, workgroup row) combines
-// the states of every query head that row covers (hw KV heads x tw tiles x GT
-// members) into `out`, then resets the row's counter for the next call.
-// Release: every thread's stores are made device-visible before the arrival is
-// counted; acquire: the last workgroup observes all of them.
-template <int D, int GT>
-__device__ void fused_merge_tail(const PartialParams& p, float* smem) {
-    __shared__ int is_last;
-    const int threads = blockDim.x;
-    const int waves = threads / kWave;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x % kWave;
-    __threadfence();
-    __syncthreads();
-    const int64_t row_id = static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y;
-    if (threadIdx.x == 0) is_last = atomicAdd(&p.counters[row_id], 1) == static_cast<int>(gridDim.x) - 1;
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    const int parts = kQuarters * p.splits;
-    const float2* st_base = reinterpret_cast<const float2*>(p.stats);
-    const int hw = p.heads_per_wg, tw = p.tiles_per_wg;
-    const int tile_groups = p.head_tiles / tw;
-    const int kv0 = (blockIdx.y / tile_groups) * hw;
-    const int tile0 = (blockIdx.y % tile_groups) * tw;
-    const int local_heads = hw * tw * GT;
-    const int64_t b_row = static_cast<int64_t>(blockIdx.z) * p.query_heads;
-    // Query-head row of local head lh, or -1 past the GQA group.
-    auto head_row = [&](int lh) -> int64_t {
-        const int kv = kv0 + lh / (tw * GT);
-        const int member = (tile0 + (lh / GT) % tw) * GT + lh % GT;
-        return member < p.group ? b_row + static_cast<int64_t>(kv) * p.group + member : -1;
-    };
-    if (p.fuse == kFuseShared) {
-        float* weight = smem;                          // [local_heads][parts]
-        float* den_lds = smem + local_heads * parts;   // [local_heads]
-        for (int lh = wave; lh < local_heads; lh += waves) {
-            const int64_t qr = head_row(lh);
-            if (qr < 0) continue;
-            const float2* st = st_base + qr * parts;
-            float mx = kNoToken;
-            for (int j = lane; j < parts; j += kWave) {
-                const float2 s = read_state(st, j);
-                mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
-            }
-            mx = wave_max(mx);
-            float den = 0.0f;
-            for (int j = lane; j < parts; j += kWave) {
-                const float2 s = read_state(st, j);
-                const float f = s.y > 0.0f ? fast_exp2(s.x - mx) : 0.0f;
-                weight[lh * parts + j] = f;
-                den = fmaf(f, s.y, den);
-            }
-            den = wave_sum(den);
-            if (lane == 0) den_lds[lh] = den;
-        }
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < local_heads * D; idx += threads) {
-            const int lh = idx / D;
-            const int d = idx - lh * D;
-            const int64_t qr = head_row(lh);
-            if (qr < 0) continue;
-            const float* num = p.numerator + qr * parts * D + d;
-            const float* w = weight + lh * parts;
-            float acc = 0.0f;
-#pragma unroll kMergeUnroll
-            for (int j = 0; j < parts; ++j) {
-                const float n = num[static_cast<int64_t>(j) * D];
-                acc = w[j] > 0.0f ? fmaf(w[j], n, acc) : acc;
-            }
-            const float den = den_lds[lh];
-            p.out[qr * D + d] = den > 0.0f ? acc / den : 0.0f;
-        }
-    } else {
-        for (int idx = threadIdx.x; idx < local_heads * D; idx += threads) {
-            const int lh = idx / D;
-            const int d = idx - lh * D;
-            const int64_t qr = head_row(lh);
-            if (qr < 0) continue;
-            const float2* st = st_base + qr * parts;
-            float mx = kNoToken;
-#pragma unroll kMergeUnroll
-            for (int j = 0; j < parts; ++j) {
-                const float2 s = read_state(st, j);
-                mx = s.y > 0.0f ? fmaxf(mx, s.x) : mx;
-            }
-            const float* num = p.numerator + qr * parts * D + d;
-            float den = 0.0f, acc = 0.0f;
-#pragma unroll kMergeUnroll
-            for (int j = 0; j < parts; ++j) {
-                const float2 s = read_state(st, j);
-                const float n = num[static_cast<int64_t>(j) * D];
-                const bool live = s.y > 0.0f;
-                const float f = live ? fast_exp2(s.x - mx) : 0.0f;
-                den = live ? fmaf(f, s.y, den) : den;
-                acc = live ? fmaf(f, n, acc) : acc;
-            }
-            p.out[qr * D + d] = den > 0.0f ? acc / den : 0.0f;
-        }
-    }
-    if (threadIdx.x == 0) p.counters[row_id] = 0;  // ready for the next call
-}
-
-// Floats of dynamic LDS the fused LDS-bounded merge needs.
-__host__ __device__ inline size_t fused_shared_floats(int local_heads, int splits) {
-    return static_cast<size_t>(local_heads) * (kQuarters * static_cast<size_t>(splits) + 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1043,9 +933,6 @@ int check_common(const void* q, const void* k, const void* v, int dtype, const i
 
 int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LAUNCH; }
 
-// LDS the fused LDS-bounded merge may use beside the partition kernel.
-constexpr size_t kFusedSharedLdsBytes = 48 * 1024;
-
 // FP32 kernel: 16-byte loads of K (and of V) per lane per chunk, chunks in
 // flight ahead of the one being consumed, chunks per straight-line block.
 #ifndef PD_CHUNK_LOADS
@@ -1094,17 +981,14 @@ void choose_workgroup(PartialParams& prm, int kv_heads) {
 template <typename T, int D, int GT>
 int launch_partial(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const int waves = prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
-    size_t floats = 0;
-    if (prm.fuse == kFuseShared)
-        floats = std::max(floats, fused_shared_floats(prm.heads_per_wg * prm.tiles_per_wg * GT, prm.splits));
     const dim3 grid(prm.splits * (kQuarters / prm.quarters_per_wg),
                     (kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg), batch);
     if constexpr (std::is_same_v<T, _Float16>) {
         hipLaunchKernelGGL((partial_mfma_kernel<D, GT, PD_MFMA_PREFETCH, PD_MFMA_BLOCK>), grid, dim3(kWave * waves),
-                           floats * sizeof(float), stream, prm);
+                           0, stream, prm);
     } else {
         hipLaunchKernelGGL((partial_kernel<T, D, GT, PD_CHUNK_LOADS, PD_PREFETCH, PD_BLOCK_CHUNKS>), grid,
-                           dim3(kWave * waves), floats * sizeof(float), stream, prm);
+                           dim3(kWave * waves), 0, stream, prm);
     }
     return launch_status();
 }
@@ -1126,19 +1010,8 @@ int dispatch_group(PartialParams& prm, int batch, int kv_heads, hipStream_t stre
     }
 }
 
-// LDS the fused LDS-bounded merge would need for these shapes (in floats).
-size_t fused_shared_need(int query_heads, int kv_heads, int splits) {
-    PartialParams prm{};
-    prm.group = query_heads / kv_heads;
-    const int gt = head_tile(prm.group);
-    prm.head_tiles = (prm.group + gt - 1) / gt;
-    choose_workgroup(prm, kv_heads);
-    return fused_shared_floats(prm.heads_per_wg * prm.tiles_per_wg * gt, splits);
-}
-
 int run_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-                const int32_t* lengths, float* numerator, float* stats, float* out, int32_t* counters,
-                int fuse, int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                const int32_t* lengths, float* numerator, float* stats, int batch, int query_heads, int kv_heads, int head_dim, int page_size,
                 int table_width, int physical_pages, int splits, int split_tokens, hipStream_t stream) {
     const size_t elem = dtype == PD_DTYPE_F16 ? 2 : 4;
     PartialParams prm{};
@@ -1149,9 +1022,6 @@ int run_partial(const void* q, const void* k, const void* v, int dtype, const in
     prm.lengths = lengths;
     prm.numerator = numerator;
     prm.stats = stats;
-    prm.out = out;
-    prm.counters = counters;
-    prm.fuse = fuse;
     prm.query_heads = query_heads;
     prm.group = query_heads / kv_heads;
     prm.page_shift = page_size == 16 ? 4 : 5;
@@ -1214,7 +1084,7 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, co
                                     kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                                     split_tokens);
     if (status != PD_OK) return status;
-    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, nullptr, nullptr, kFuseNone, batch,
+    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch,
                        query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                        split_tokens, static_cast<hipStream_t>(stream));
 }
@@ -1238,38 +1108,11 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
         status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, nullptr, nullptr, kFuseNone, batch,
+    status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                          split_tokens, s);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode, s);
-}
-
-int pd_decode_fused(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-                    const int32_t* lengths, float* numerator, float* stats, int32_t* counters, float* out,
-                    int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                    int physical_pages, int splits, int split_tokens, int merge_mode, void* stream) {
-    int status = check_common(q, k, v, dtype, table, lengths, numerator, stats, batch, query_heads,
-                              kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                              split_tokens);
-    if (status == PD_OK)
-        status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
-    if (status == PD_OK && !counters) status = PD_ERR_NULL_POINTER;
-    if (status != PD_OK) return status;
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    if (merge_mode == PD_MERGE_SHARED &&
-        fused_shared_need(query_heads, kv_heads, splits) * sizeof(float) > kFusedSharedLdsBytes) {
-        // The LDS-bounded merge of this many states does not fit beside the
-        // partition kernel; run it as its own kernel (same algorithm).
-        status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, nullptr, nullptr, kFuseNone,
-                             batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
-                             splits, split_tokens, s);
-        if (status != PD_OK) return status;
-        return run_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode, s);
-    }
-    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, out, counters,
-                       merge_mode == PD_MERGE_SHARED ? kFuseShared : kFuseSerial, batch, query_heads,
-                       kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens, s);
 }
 
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {
@@ -1290,6 +1133,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 3; }
+int pd_abi_version(void) { return 4; }
 
 }  // extern "C"
