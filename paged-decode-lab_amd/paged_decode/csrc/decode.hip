@@ -789,7 +789,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 //   shared: the workgroup forms each state's weight once, into LDS
 //           (4 bytes per state, hence the 4096-state bound).
 constexpr int kMergeThreads = 256;
-constexpr int kMergeBatch = 16;
+constexpr int kMergeBatch = 8;
 constexpr int kStatsUnroll = 4;
 
 template <int D, bool kSharedWeights>
@@ -815,14 +815,20 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
     const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
     const f32x4* num = reinterpret_cast<const f32x4*>(numerator + row * parts * D) + col;
 
+    // Rounds of PG states present from `base` on (uniform): loads past the row
+    // are skipped as whole instructions, so small rows issue only what they use.
+    auto rounds_from = [&](int base) { return min(NB, (parts - base + PG - 1) / PG); };
     f32x4 buf[NB];
     float2 own[NB];
     auto load_batch = [&](int base) {
+        const int rounds = rounds_from(base);
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
-            const int j = min(base + pg + k * PG, last);
-            buf[k] = num[static_cast<int64_t>(j) * TPR];
-            if constexpr (!kSharedWeights) own[k] = read_state(st, j);
+            if (k < rounds) {
+                const int j = min(base + pg + k * PG, last);
+                buf[k] = num[static_cast<int64_t>(j) * TPR];
+                if constexpr (!kSharedWeights) own[k] = read_state(st, j);
+            }
         }
     };
     // The first batch of numerator rows is in flight while the weights form.
@@ -834,8 +840,10 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
     float2 first[kStatsUnroll];
     for (int base = 0; base < parts; base += kStatsUnroll * kScan) {
         float2 s[kStatsUnroll];
+        const int present = (parts - base + kScan - 1) / kScan;  // uniform
 #pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i) s[i] = read_state(st, min(base + scan0 + i * kScan, last));
+        for (int i = 0; i < kStatsUnroll; ++i)
+            s[i] = i < present ? read_state(st, min(base + scan0 + i * kScan, last)) : make_float2(kNoToken, 0.0f);
         if (base == 0) {
 #pragma unroll
             for (int i = 0; i < kStatsUnroll; ++i) first[i] = s[i];
@@ -859,9 +867,12 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
     float den = 0.0f;
     for (int base = 0; base < parts; base += kStatsUnroll * kScan) {
         float2 s[kStatsUnroll];
+        const int present = (parts - base + kScan - 1) / kScan;
 #pragma unroll
         for (int i = 0; i < kStatsUnroll; ++i)
-            s[i] = base == 0 ? first[i] : read_state(st, min(base + scan0 + i * kScan, last));
+            s[i] = base == 0 ? first[i]
+                             : (i < present ? read_state(st, min(base + scan0 + i * kScan, last))
+                                            : make_float2(kNoToken, 0.0f));
 #pragma unroll
         for (int i = 0; i < kStatsUnroll; ++i) {
             const int j = base + scan0 + i * kScan;
@@ -886,18 +897,21 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
     // duplicate past the row) contributes nothing, whatever its numerator holds.
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int base = 0;;) {
+        const int rounds = rounds_from(base);
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
-            const int j = base + pg + k * PG;
-            float f;
-            if constexpr (kSharedWeights) {
-                f = weight[min(j, last)];
-            } else {
-                f = own[k].y > 0.0f ? fast_exp2(own[k].x - mx) : 0.0f;
-            }
-            f = j < parts ? f : 0.0f;
+            if (k < rounds) {
+                const int j = base + pg + k * PG;
+                float f;
+                if constexpr (kSharedWeights) {
+                    f = weight[min(j, last)];
+                } else {
+                    f = own[k].y > 0.0f ? fast_exp2(own[k].x - mx) : 0.0f;
+                }
+                f = j < parts ? f : 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = f > 0.0f ? fmaf(f, buf[k][e], acc[e]) : acc[e];
+                for (int e = 0; e < 4; ++e) acc[e] = f > 0.0f ? fmaf(f, buf[k][e], acc[e]) : acc[e];
+            }
         }
         base += NB * PG;
         if (base >= parts) break;
