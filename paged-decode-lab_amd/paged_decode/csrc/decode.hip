@@ -58,6 +58,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 // Note: reinterpret whole vectors (bit_cast of a u32x4 to f16x8 / f32x4), never
 // a single element: clang 22 lowers __builtin_bit_cast of a vector-element
 // lvalue to a read of element 0.
@@ -594,45 +596,74 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 }
 
 // ---------------------------------------------------------------------------
-// FP16 partition kernel with q.K^T on the matrix cores.
+// FP16 partition kernel: q.K^T and P.V both on the matrix cores.
 //
 // A 16-token tile is scored with D/32 v_mfma_f32_16x16x32_f16: K in the A
-// layout (lane l: token l % 16 of the tile; k-step s covers dims
-// [32 s, 32 s + 32), 8 of them per lane group l / 16, so a load reads 64
-// contiguous bytes of 16 rows), q in the B layout (lane l: query head l % 16,
-// zero past the tile). Lane l then holds head l % 16 for tokens
-// 4 * (l / 16) + 0..3, so each (token, head) score lives in one lane and the
-// softmax bookkeeping costs a few instructions per tile. Weights go through a
-// 16 x GT LDS tile to the P.V step, which stays on the VALU in the row layout
-// (lanes [r*LPT, (r+1)*LPT) hold token r's V row) as mixed-precision FMAs. One
-// running max per head is shared by the whole wave, so its token rows simply
-// add up at the end.
+// layout (lane l loads 64 contiguous bytes, dims [32 s + 8 (l / 16), +8) of
+// k-step s, of tile token sigma(l % 16)), q in the B layout (lane l: query
+// head l % 16, zero past the group). With sigma(r) = r / 4 + 4 (r % 4) the
+// result leaves lane l with head n = l % 16 and tokens g, g + 4, g + 8, g + 12
+// of the tile (g = l / 16): exactly the A operand of v_mfma_f32_16x16x16_f16
+// for P (row = head, k = 4 g + e <-> token g + 4 e), so the weights never
+// leave their lanes. V is loaded in the row layout -- load e covers tokens
+// 4 e .. 4 e + 3, lanes [16 r, 16 r + 16) token 4 e + r, VH consecutive halves
+// per lane -- so lane (g, n) holds tokens g + 4 e of dims n VH .. n VH + VH - 1,
+// and half j of its four V loads is the B operand of MFMA block j (column n
+// <-> dim n VH + j). P is split into FP16 high and low parts (two MFMAs per
+// block), which keeps the weights exact to about 2^-22 relative. Each
+// (head, dim) sum then lives in exactly one lane: lane (g, n) ends with heads
+// 4 g .. 4 g + 3 of dims n VH .. n VH + VH - 1, stored directly. One running
+// max per head is shared by the wave, with lazy rescaling as in the FP32
+// kernel.
 constexpr int kTileTokens = 16;
+
+// Tile token loaded by K lane row r (see above).
+__device__ __forceinline__ int k_token_of_row(int r) { return (r >> 2) + 4 * (r & 3); }
+
+template <int VH>
+struct VLoad;
+template <>
+struct VLoad<8> {
+    using type = u32x4;  // 8 halves: head_dim 128
+};
+template <>
+struct VLoad<4> {
+    using type = u32x2;  // 4 halves: head_dim 64
+};
+
+// Half j of each of the four V loads, packed as an MFMA operand (k = load index).
+template <int VH>
+__device__ __forceinline__ f16x4 v_operand(const typename VLoad<VH>::type (&v)[4], int j) {
+    const uint32_t d0 = v[0][j / 2], d1 = v[1][j / 2], d2 = v[2][j / 2], d3 = v[3][j / 2];
+    uint32_t lo, hi;
+    if (j % 2 == 0) {
+        lo = (d0 & 0xFFFFu) | (d1 << 16);
+        hi = (d2 & 0xFFFFu) | (d3 << 16);
+    } else {
+        lo = (d0 >> 16) | (d1 & 0xFFFF0000u);
+        hi = (d2 >> 16) | (d3 & 0xFFFF0000u);
+    }
+    return __builtin_bit_cast(f16x4, u32x2{lo, hi});
+}
 
 template <int D, int GT, int PD, int NC>
 __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
-    using E = Elem<_Float16>;
-    constexpr int EPL = 8;                 // halves per 16-byte lane load
-    constexpr int LPT = D / EPL;           // lanes per token row (V layout)
-    constexpr int TPL = kWave / LPT;       // tokens per V load
-    constexpr int VI = kTileTokens / TPL;  // V loads per tile
-    constexpr int KS = D / 32;             // MFMA k-steps (K loads) per tile
-    static_assert(GT <= 8, "P.V accumulators are sized for at most 8 heads");
+    constexpr int KS = D / 32;             // q.K^T k-steps (K loads) per tile
+    constexpr int VH = D / 16;             // V halves per lane per load = P.V MFMA blocks
+    constexpr int VI = 4;                  // V loads per tile
+    static_assert(GT <= 16, "one MFMA column block holds at most 16 query heads");
+    using VL = typename VLoad<VH>::type;
 
     struct Tile {
         f16x8 k[KS];
-        u32x4 v[VI];
+        VL v[VI];
         uint32_t live;
     };
 
-    __shared__ float ptile[8][kTileTokens * GT];
-
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
-    const int row = lane / LPT;
-    const int col = lane % LPT;
-    const int kt = lane % 16;
-    const int kg = lane / 16;
+    const int n = lane % 16;  // head (q.K^T, P) / column (P.V)
+    const int g = lane / 16;  // lane group: tokens g + 4 e
     const int page_size = 1 << p.page_shift;
     const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
     int window = speculative_page<kTileTokens>(p, wave);
@@ -644,24 +675,22 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         u32x4 x = u32x4{0u, 0u, 0u, 0u};
-        if (kt < w.heads_here) x = *reinterpret_cast<const u32x4*>(q_base + kt * D + 32 * s + 8 * kg);
+        if (n < w.heads_here) x = *reinterpret_cast<const u32x4*>(q_base + n * D + 32 * s + 8 * g);
         qb[s] = __builtin_bit_cast(f16x8, x);
     }
 
-    float m_head = kNoToken;  // running max (log2 units) of head kt, equal in all lane groups
-    float l_part = 0.0f;      // this lane's share of head kt's denominator
-    float acc[GT][EPL];
+    float m_head = kNoToken;  // running max (log2 units) of head n, equal in all lane groups
+    float l_part = 0.0f;      // this lane's share of head n's denominator
+    f32x4 acc[VH];            // acc[j][i]: head 4 g + i, dim n VH + j
 #pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] = 0.0f;
+    for (int j = 0; j < VH; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(w.kv_head) * D * 2;
     const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(w.kv_head) * D * 2;
     const char* park = reinterpret_cast<const char*>(q_base);
-    const uint32_t k_lane_bytes = static_cast<uint32_t>(kg) * 16u;
-    const uint32_t v_lane_bytes = static_cast<uint32_t>(col) * 16u;
-    float* pt = ptile[wave];
+    const uint32_t k_lane_bytes = static_cast<uint32_t>(g) * 16u;
+    const uint32_t v_lane_bytes = static_cast<uint32_t>(n) * VH * 2u;
+    const int k_row_token = k_token_of_row(n);
     int rb = w.wb, re = w.wb;
 
     auto issue = [&](Tile& tl, int t0, int ids, int win) {
@@ -675,18 +704,18 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         const uint64_t page_off = static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
         const char* kp = ok ? k_head + page_off : park;
         const char* vp = ok ? v_head + page_off : park;
-        const int tk = min(max(t0 + kt, lo), hi);
+        const int tk = min(max(t0 + k_row_token, lo), hi);
         const uint32_t koff =
             ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
 #pragma unroll
         for (int s = 0; s < KS; ++s)
             tl.k[s] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(kp + koff + 64 * s));
 #pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            const int tv = min(max(t0 + i * TPL + row, lo), hi);
+        for (int e = 0; e < VI; ++e) {
+            const int tv = min(max(t0 + 4 * e + g, lo), hi);
             const uint32_t voff =
                 ok ? static_cast<uint32_t>(tv & (page_size - 1)) * p.token_bytes + v_lane_bytes : v_lane_bytes;
-            tl.v[i] = *reinterpret_cast<const u32x4*>(vp + voff);
+            tl.v[e] = *reinterpret_cast<const VL*>(vp + voff);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -698,45 +727,43 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         float x[4];
         float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = t0 + 4 * kg + i;
+        for (int e = 0; e < 4; ++e) {
+            const int t = t0 + g + 4 * e;
             const bool valid = (tl.live != 0u) & (t >= rb) & (t < re);
-            x[i] = valid ? sc[i] : -INFINITY;
-            mx = fmaxf(mx, x[i]);
+            x[e] = valid ? sc[e] : -INFINITY;
+            mx = fmaxf(mx, x[e]);
         }
         const float tile_max = max_over_lane_groups(mx) * p.scale_log2;
-        if (__any((kt < GT) & (tile_max > m_head + kRescaleSlack))) {
+        if (__any((n < GT) & (tile_max > m_head + kRescaleSlack))) {
             const float m_new = fmaxf(m_head, tile_max);
             const float alpha = fast_exp2(m_head - m_new);
             m_head = m_new;
             l_part *= alpha;
+            // acc[.][i] belongs to head 4 g + i, whose factor lives in lane 4 g + i.
 #pragma unroll
-            for (int g = 0; g < GT; ++g) {
-                // Lane g (first lane group) holds head g's factor.
-                const float ag = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), g));
+            for (int i = 0; i < 4; ++i) {
+                const float a = __shfl(alpha, 4 * g + i);
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[g][e] *= ag;
+                for (int j = 0; j < VH; ++j) acc[j][i] *= a;
             }
         }
+        float wt[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float wgt = fast_exp2(fmaf(x[i], p.scale_log2, -m_head));
-            l_part += wgt;
-            if (kt < GT) pt[(4 * kg + i) * GT + kt] = wgt;
+        for (int e = 0; e < 4; ++e) {
+            wt[e] = fast_exp2(fmaf(x[e], p.scale_log2, -m_head));
+            l_part += wt[e];
         }
-        // P.V in the row layout; the wave's own LDS tile needs no barrier.
+        f16x4 p_hi, p_lo;
 #pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            float wv[GT];
-#pragma unroll
-            for (int g = 0; g < GT; ++g) wv[g] = pt[(i * TPL + row) * GT + g];
-            float vf[EPL];
-            E::widen(tl.v[i], vf);
-#pragma unroll
-            for (int g = 0; g < GT; ++g)
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(wv[g], vf[e], acc[g][e]);
+        for (int e = 0; e < 4; ++e) {
+            const _Float16 h = static_cast<_Float16>(wt[e]);
+            p_hi[e] = h;
+            p_lo[e] = static_cast<_Float16>(wt[e] - static_cast<float>(h));
         }
+#pragma unroll
+        for (int j = 0; j < VH; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(p_hi, v_operand<VH>(tl.v, j), acc[j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < VH; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(p_lo, v_operand<VH>(tl.v, j), acc[j], 0, 0, 0);
     };
 
     for (rb = w.wb; rb < w.we; rb = re) {
@@ -748,31 +775,34 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         for (int s0 = rb & ~(kTileTokens - 1); s0 < re; s0 += NC * kTileTokens) {
             Tile buf[PD + 1];
 #pragma unroll
-            for (int n = 0; n < PD; ++n) issue(buf[n], s0 + n * kTileTokens, window_ids, window);
+            for (int n0 = 0; n0 < PD; ++n0) issue(buf[n0], s0 + n0 * kTileTokens, window_ids, window);
 #pragma unroll
-            for (int n = 0; n < NC; ++n) {
-                if (s0 + n * kTileTokens >= re) break;
-                if (n + PD < NC) issue(buf[(n + PD) % (PD + 1)], s0 + (n + PD) * kTileTokens, window_ids, window);
-                consume(buf[n % (PD + 1)], s0 + n * kTileTokens);
+            for (int c = 0; c < NC; ++c) {
+                if (s0 + c * kTileTokens >= re) break;
+                if (c + PD < NC) issue(buf[(c + PD) % (PD + 1)], s0 + (c + PD) * kTileTokens, window_ids, window);
+                consume(buf[c % (PD + 1)], s0 + c * kTileTokens);
             }
         }
     }
 
-    // Sum the wave's token rows (they share one max per head) with a
-    // reduce-scatter in registers: lane (row r, column c) ends with elements
-    // [r * CNT, (r + 1) * CNT) of the (head, element) array of column c. The
-    // denominator is summed over the four lane groups of the MFMA layout.
-    constexpr int N = GT * EPL;
-    constexpr int CNT = N / TPL;
-    float flat[N];
-#pragma unroll
-    for (int g = 0; g < GT; ++g)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) flat[g * EPL + e] = acc[g][e];
-    float mine[CNT];
-    row_reduce_scatter<N, TPL>(flat, mine, lane);
+    // Lane (g, n) holds heads 4 g + i of dims n VH .. n VH + VH - 1; the
+    // denominator of head n is summed over the four lane groups.
     const float l_head = sum_over_lane_groups(l_part);
-    store_scattered_state<D, GT, EPL, CNT>(p, w, lane, row, col, mine, m_head, l_head);
+    const int parts = kQuarters * p.splits;
+    const int part = w.split * kQuarters + w.quarter;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int h = 4 * g + i;
+        if (h < w.heads_here) {
+            f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + h) * parts + part) * D + n * VH);
+#pragma unroll
+            for (int j = 0; j < VH; j += 4) dst[j / 4] = f32x4{acc[j][i], acc[j + 1][i], acc[j + 2][i], acc[j + 3][i]};
+        }
+    }
+    if (lane < w.heads_here) {
+        float2* st = reinterpret_cast<float2*>(p.stats) + (w.q_row + lane) * parts + part;
+        *st = make_float2(l_head > 0.0f ? m_head : kNoToken, l_head);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1007,20 +1037,30 @@ int launch_partial(const PartialParams& prm, int batch, int kv_heads, hipStream_
     return launch_status();
 }
 
-// Head tile: the GQA group padded to 1, 2, 4 or 8 query heads; larger groups
-// are cut into tiles of 8.
-int head_tile(int group) { return group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8; }
+// Head tile: the GQA group padded to a power of two up to kMaxTile query heads
+// (16 for the FP16 kernel, whose MFMA column block holds 16 heads; 8 for the
+// FP32 kernel, whose accumulators grow with the tile); larger groups are cut
+// into tiles of kMaxTile.
+int head_tile(int group, int max_tile) {
+    int gt = 1;
+    while (gt < group && gt < max_tile) gt *= 2;
+    return gt;
+}
 
 template <typename T, int D>
 int dispatch_group(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    const int gt = head_tile(prm.group);
+    constexpr bool kHalf = std::is_same_v<T, _Float16>;
+    const int gt = head_tile(prm.group, kHalf ? 16 : 8);
     prm.head_tiles = (prm.group + gt - 1) / gt;
     choose_workgroup(prm, kv_heads);
     switch (gt) {
         case 1: return launch_partial<T, D, 1>(prm, batch, kv_heads, stream);
         case 2: return launch_partial<T, D, 2>(prm, batch, kv_heads, stream);
         case 4: return launch_partial<T, D, 4>(prm, batch, kv_heads, stream);
-        default: return launch_partial<T, D, 8>(prm, batch, kv_heads, stream);
+        case 8: return launch_partial<T, D, 8>(prm, batch, kv_heads, stream);
+        default:
+            if constexpr (kHalf) return launch_partial<T, D, 16>(prm, batch, kv_heads, stream);
+            return PD_ERR_SHAPE;
     }
 }
 
