@@ -957,6 +957,85 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
     }
 }
 
+// Small rows: one wave per (sequence, query head) row, four rows per
+// workgroup, no barriers. Lane l owns column l % TPR of the states
+// j == l / TPR (mod PGW) and lane j (< parts) reads state j's (m, l) for the
+// row maximum and denominator, reduced with DPP. The shared variant forms each
+// state's weight once, in lane j, and broadcasts it with a cross-lane read;
+// the serial variant has every lane recompute the weights it uses. The PGW
+// column sums meet through permlane swaps. Used when a row's states fit in
+// kMergeWaveBatch loads per lane (at most 64 states).
+constexpr int kMergeWaveBatch = 8;
+constexpr int kMergeRowsPerGroup = 4;
+
+template <int D>
+constexpr int merge_wave_max_parts() { return kMergeWaveBatch * (kWave / (D / 4)); }
+
+template <int D, bool kSharedWeights>
+__global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
+    const float* __restrict__ numerator, const float* __restrict__ stats, float* __restrict__ out, int parts,
+    int query_heads) {
+    constexpr int TPR = D / 4;        // lanes per state row
+    constexpr int PGW = kWave / TPR;  // state groups per wave (2 or 4)
+    constexpr int NB = kMergeWaveBatch;
+    static_assert(merge_wave_max_parts<D>() <= kWave, "one state per lane for the statistics");
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int h = blockIdx.x * kMergeRowsPerGroup + wave;
+    if (h >= query_heads) return;  // whole wave; nothing below synchronises across waves
+    const int64_t row = static_cast<int64_t>(blockIdx.y) * query_heads + h;
+    const int col = lane % TPR;
+    const int pg = lane / TPR;
+    const int last = parts - 1;
+    const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
+    const f32x4* num = reinterpret_cast<const f32x4*>(numerator + row * parts * D) + col;
+    const int rounds = (parts + PGW - 1) / PGW;  // uniform, <= NB
+
+    f32x4 buf[NB];
+    float2 own[NB];
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        if (k < rounds) {
+            const int j = min(pg + k * PGW, last);
+            buf[k] = num[static_cast<int64_t>(j) * TPR];
+            if constexpr (!kSharedWeights) own[k] = read_state(st, j);
+        }
+    }
+    const float2 mine = read_state(st, min(lane, last));
+    const bool live = (lane < parts) & (mine.y > 0.0f);
+    const float mx = wave_max(live ? mine.x : kNoToken);
+    const float f = live ? fast_exp2(mine.x - mx) : 0.0f;  // weight of state `lane`
+    const float den = wave_sum(f * (live ? mine.y : 0.0f));
+
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        if (k < rounds) {
+            const int j = pg + k * PGW;
+            float wj;
+            if constexpr (kSharedWeights) {
+                wj = __shfl(f, min(j, last));
+            } else {
+                wj = own[k].y > 0.0f ? fast_exp2(own[k].x - mx) : 0.0f;
+            }
+            wj = j < parts ? wj : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = wj > 0.0f ? fmaf(wj, buf[k][e], acc[e]) : acc[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if constexpr (PGW == 4) acc[e] = sum_over_lane_groups(acc[e]);
+        else acc[e] = swap32_sum(acc[e], acc[e]);
+    }
+    if (pg == 0) {
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = den > 0.0f ? acc[e] / den : 0.0f;
+        *reinterpret_cast<f32x4*>(out + row * D + col * 4) = o;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 
@@ -988,13 +1067,14 @@ int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LA
 #ifndef PD_BLOCK_CHUNKS
 #define PD_BLOCK_CHUNKS 16
 #endif
-// FP16 kernel (MFMA scoring): 16-token tiles in flight ahead of the one being
-// consumed, and tiles per straight-line block. Short blocks keep the kernel's
+// FP16 kernel (MFMA): 16-token tiles issued ahead of the one being consumed,
+// and tiles per straight-line block (with 2 and 2, each block's two tiles are
+// requested together and consumed in order). Short blocks keep the kernel's
 // code small: with 8 waves per CU running through cold straight-line code,
 // instruction fetch is on the critical path (two-tile blocks measured 1 us
 // faster per Llama-3-8B-shape call than eight-tile blocks, same loads).
 #ifndef PD_MFMA_PREFETCH
-#define PD_MFMA_PREFETCH 1
+#define PD_MFMA_PREFETCH 2
 #endif
 #ifndef PD_MFMA_BLOCK
 #define PD_MFMA_BLOCK 2
@@ -1097,8 +1177,20 @@ int run_partial(const void* q, const void* k, const void* v, int dtype, const in
 template <int D>
 int launch_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads, int parts,
                  int merge_mode, hipStream_t stream) {
+    const bool shared = merge_mode == PD_MERGE_SHARED;
+    if (parts <= merge_wave_max_parts<D>()) {
+        const dim3 grid((query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
+        if (shared) {
+            hipLaunchKernelGGL((merge_rows_kernel<D, true>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream,
+                               numerator, stats, out, parts, query_heads);
+        } else {
+            hipLaunchKernelGGL((merge_rows_kernel<D, false>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream,
+                               numerator, stats, out, parts, query_heads);
+        }
+        return launch_status();
+    }
     const dim3 grid(query_heads, batch);
-    if (merge_mode == PD_MERGE_SHARED) {
+    if (shared) {
         hipLaunchKernelGGL((merge_kernel<D, true>), grid, dim3(kMergeThreads), parts * sizeof(float), stream,
                            numerator, stats, out, parts);
     } else {
