@@ -19,7 +19,11 @@
  *   numerator [batch, query_heads, 4 * splits, head_dim]  float32
  *   stats     [batch, query_heads, 4 * splits, 2]         float32 (max, denominator)
  * (state 4 * split + quarter; the reference's workspace shape, decode.cu:223-231).
- * The workspace needs no initialisation; every element is written per call.
+ * Only partitions that hold at least one token of their sequence are written
+ * (partitions 0 .. ceil(len_b / split_tokens) - 1 of row b, len_b clamped to
+ * table_width * page_size) and only those are read by the merge, so the
+ * workspace needs no initialisation and a batch with ragged lengths neither
+ * writes nor reads states past each sequence's end.
  *
  * All pointers are device pointers. `stream` is a hipStream_t (passed as
  * void* so FFI layers need no HIP headers); calls are asynchronous on it, never
@@ -88,12 +92,15 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype,
                       void* stream);
 
 /*
- * Merge stage only (the second launch of pd_decode): combines the 4 * splits
- * states per (sequence, query head) into out. Replaces the merge_decode /
- * merge_shared launches of reference decode.cu:183-193.
+ * Merge stage only (the second launch of pd_decode): combines the live states
+ * of each (sequence, query head) row -- 4 * ceil(len_b / split_tokens) of the
+ * 4 * splits allocated -- into out. Replaces the merge_decode / merge_shared
+ * launches of reference decode.cu:183-193. lengths, page_size, table_width and
+ * split_tokens are the values the partition stage was called with.
  */
 int pd_decode_merge(const float* numerator, const float* stats, float* out,
-                    int batch, int query_heads, int head_dim, int splits,
+                    const int32_t* lengths, int batch, int query_heads, int head_dim,
+                    int page_size, int table_width, int splits, int split_tokens,
                     int merge_mode, void* stream);
 
 /*
@@ -108,7 +115,9 @@ size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits);
 const char* pd_status_string(int status);
 
 /* ABI version of this header: bumped on any signature or layout change
- * (3: four states per partition; 4: single-launch entry withdrawn). */
+ * (3: four states per partition; 4: single-launch entry withdrawn;
+ * 5: states past a sequence's end are neither written nor read, so
+ * pd_decode_merge takes the lengths). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

@@ -304,6 +304,7 @@ struct WaveWork {
     int split, quarter, kv_head, tile, wb, we;
     int64_t q_row;   // first query-head row of the tile
     int heads_here;  // live query heads in the tile
+    bool dead;       // the partition starts at or past the sequence end: no state is written
 };
 
 template <int GT, int ALIGN>
@@ -323,6 +324,7 @@ __device__ __forceinline__ WaveWork wave_work(const PartialParams& p, int wave) 
     const int capacity = p.table_width << p.page_shift;
     const int len = max(0, min(p.lengths[b], capacity));  // decode.cu:42-44
     const int64_t first = static_cast<int64_t>(w.split) * p.split_tokens;
+    w.dead = first >= len;
     const int tb = static_cast<int>(min<int64_t>(first, len));
     const int te = static_cast<int>(min<int64_t>(first + p.split_tokens, len));
     int per = (te - tb + kQuarters - 1) / kQuarters;
@@ -439,6 +441,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
     int window = speculative_page<TPL>(p, wave);
     int window_ids = pages[min(window + lane, p.table_width - 1)];
     const WaveWork w = wave_work<GT, TPL>(p, wave);
+    if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
     const T* q_base = static_cast<const T*>(p.q) + w.q_row * D;
 
     u32x4 qv[GT];
@@ -669,6 +672,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     int window = speculative_page<kTileTokens>(p, wave);
     int window_ids = pages[min(window + lane, p.table_width - 1)];
     const WaveWork w = wave_work<GT, kTileTokens>(p, wave);
+    if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
     const _Float16* q_base = static_cast<const _Float16*>(p.q) + w.q_row * D;
 
     f16x8 qb[KS];
@@ -822,19 +826,41 @@ constexpr int kMergeThreads = 256;
 constexpr int kMergeBatch = 8;
 constexpr int kStatsUnroll = 4;
 
+// States of row b that the partition kernel wrote: four per partition up to
+// the last one holding a token of the sequence (none for an empty sequence).
+// Partitions past the end are never written and never read.
+__device__ __forceinline__ int live_parts(const int32_t* lengths, int b, int split_tokens, int capacity,
+                                          int parts) {
+    const int len = max(0, min(lengths[b], capacity));  // decode.cu:42-44
+    const int64_t live = (static_cast<int64_t>(len) + split_tokens - 1) / split_tokens;
+    return static_cast<int>(min<int64_t>(kQuarters * live, parts));
+}
+
+struct MergeParams {
+    const float* numerator;  // [B, Hq, parts, D]
+    const float* stats;      // [B, Hq, parts, 2]
+    float* out;              // [B, Hq, D]
+    const int32_t* lengths;  // [B]
+    int parts;               // allocated states per row (4 * splits)
+    int query_heads;
+    int split_tokens;
+    int capacity;            // table_width * page_size
+};
+
 template <int D, bool kSharedWeights>
-__global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __restrict__ numerator,
-                                                              const float* __restrict__ stats,
-                                                              float* __restrict__ out, int parts) {
+__global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams mp) {
     constexpr int TPR = D / 4;               // lanes per state row
     constexpr int PG = kMergeThreads / TPR;  // state groups
     constexpr int NB = kMergeBatch;
     constexpr int kWaves = kMergeThreads / kWave;
     constexpr int kScan = kSharedWeights ? kMergeThreads : kWave;  // lanes sharing the state scan
+    constexpr int kScanRound = kStatsUnroll * kScan;
     extern __shared__ float weight[];        // [parts], shared variant only
     __shared__ f32x4 column_sum[PG][TPR];
     __shared__ float scratch[2][kWaves];
-    const int64_t row = static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x;  // b * Hq + h
+    const int b = blockIdx.y;
+    const int64_t row = static_cast<int64_t>(b) * gridDim.x + blockIdx.x;  // b * Hq + h
+    const int parts = mp.parts;
     const int t = threadIdx.x;
     const int lane = t % kWave;
     const int wave = t / kWave;
@@ -842,16 +868,19 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
     const int pg = t / TPR;
     const int scan0 = kSharedWeights ? t : lane;
     const int last = parts - 1;
-    const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(numerator + row * parts * D) + col;
+    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * parts;
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D) + col;
+    // The live count arrives with the first loads, which are issued for the
+    // allocated row and masked afterwards, so it adds no round trip.
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
 
-    // Rounds of PG states present from `base` on (uniform): loads past the row
-    // are skipped as whole instructions, so small rows issue only what they use.
-    auto rounds_from = [&](int base) { return min(NB, (parts - base + PG - 1) / PG); };
+    // Rounds of PG states from `base` on, up to `limit` (uniform): loads past
+    // it are skipped as whole instructions.
+    auto rounds_from = [&](int base, int limit) { return min(NB, (limit - base + PG - 1) / PG); };
     f32x4 buf[NB];
     float2 own[NB];
-    auto load_batch = [&](int base) {
-        const int rounds = rounds_from(base);
+    auto load_batch = [&](int base, int limit) {
+        const int rounds = rounds_from(base, limit);
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             if (k < rounds) {
@@ -861,27 +890,27 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
             }
         }
     };
-    // The first batch of numerator rows is in flight while the weights form.
-    load_batch(0);
+    load_batch(0, parts);
 
-    // Row maximum over live states (l > 0). The first scan round stays in
-    // registers for the denominator pass.
-    float mx = kNoToken;
+    // Row maximum over live states (index < live and l > 0). The first scan
+    // round is issued at once and kept for the denominator pass.
     float2 first[kStatsUnroll];
-    for (int base = 0; base < parts; base += kStatsUnroll * kScan) {
-        float2 s[kStatsUnroll];
-        const int present = (parts - base + kScan - 1) / kScan;  // uniform
 #pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i)
-            s[i] = i < present ? read_state(st, min(base + scan0 + i * kScan, last)) : make_float2(kNoToken, 0.0f);
-        if (base == 0) {
+    for (int i = 0; i < kStatsUnroll; ++i) first[i] = read_state(st, min(scan0 + i * kScan, last));
+    float mx = kNoToken;
 #pragma unroll
-            for (int i = 0; i < kStatsUnroll; ++i) first[i] = s[i];
-        }
+    for (int i = 0; i < kStatsUnroll; ++i) {
+        const bool ok = (scan0 + i * kScan < live) & (first[i].y > 0.0f);
+        mx = ok ? fmaxf(mx, first[i].x) : mx;
+    }
+    for (int base = kScanRound; base < live; base += kScanRound) {
+        float2 sv[kStatsUnroll];
+#pragma unroll
+        for (int i = 0; i < kStatsUnroll; ++i) sv[i] = read_state(st, min(base + scan0 + i * kScan, last));
 #pragma unroll
         for (int i = 0; i < kStatsUnroll; ++i) {
-            const bool live = (base + scan0 + i * kScan < parts) & (s[i].y > 0.0f);
-            mx = live ? fmaxf(mx, s[i].x) : mx;
+            const bool ok = (base + scan0 + i * kScan < live) & (sv[i].y > 0.0f);
+            mx = ok ? fmaxf(mx, sv[i].x) : mx;
         }
     }
     mx = wave_max(mx);
@@ -893,26 +922,26 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
         for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, scratch[0][w]);
     }
 
-    // Denominator (and, shared variant, every state's weight in LDS).
+    // Denominator (and, shared variant, every live state's weight in LDS).
     float den = 0.0f;
-    for (int base = 0; base < parts; base += kStatsUnroll * kScan) {
-        float2 s[kStatsUnroll];
-        const int present = (parts - base + kScan - 1) / kScan;
-#pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i)
-            s[i] = base == 0 ? first[i]
-                             : (i < present ? read_state(st, min(base + scan0 + i * kScan, last))
-                                            : make_float2(kNoToken, 0.0f));
+    auto accumulate_den = [&](const float2 (&sv)[kStatsUnroll], int base) {
 #pragma unroll
         for (int i = 0; i < kStatsUnroll; ++i) {
             const int j = base + scan0 + i * kScan;
-            const bool live = (j < parts) & (s[i].y > 0.0f);
-            const float f = live ? fast_exp2(s[i].x - mx) : 0.0f;
+            const bool ok = (j < live) & (sv[i].y > 0.0f);
+            const float f = ok ? fast_exp2(sv[i].x - mx) : 0.0f;
             if constexpr (kSharedWeights) {
-                if (j < parts) weight[j] = f;
+                if (j < live) weight[j] = f;
             }
-            den = fmaf(f, live ? s[i].y : 0.0f, den);
+            den = fmaf(f, ok ? sv[i].y : 0.0f, den);
         }
+    };
+    accumulate_den(first, 0);
+    for (int base = kScanRound; base < live; base += kScanRound) {
+        float2 sv[kStatsUnroll];
+#pragma unroll
+        for (int i = 0; i < kStatsUnroll; ++i) sv[i] = read_state(st, min(base + scan0 + i * kScan, last));
+        accumulate_den(sv, base);
     }
     den = wave_sum(den);
     if constexpr (kSharedWeights) {
@@ -923,29 +952,29 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
         for (int w = 1; w < kWaves; ++w) den += scratch[1][w];
     }
 
-    // Weighted column sums; a state of weight 0 (empty partition, or a clamped
-    // duplicate past the row) contributes nothing, whatever its numerator holds.
+    // Weighted column sums; a state of weight 0 (empty partition, clamped
+    // duplicate, or past the live count) contributes nothing, whatever its
+    // numerator holds.
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int base = 0;;) {
-        const int rounds = rounds_from(base);
+        const int rounds = rounds_from(base, base == 0 ? parts : live);
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             if (k < rounds) {
                 const int j = base + pg + k * PG;
                 float f;
                 if constexpr (kSharedWeights) {
-                    f = weight[min(j, last)];
+                    f = j < live ? weight[j] : 0.0f;
                 } else {
-                    f = own[k].y > 0.0f ? fast_exp2(own[k].x - mx) : 0.0f;
+                    f = (j < live) & (own[k].y > 0.0f) ? fast_exp2(own[k].x - mx) : 0.0f;
                 }
-                f = j < parts ? f : 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[e] = f > 0.0f ? fmaf(f, buf[k][e], acc[e]) : acc[e];
             }
         }
         base += NB * PG;
-        if (base >= parts) break;
-        load_batch(base);
+        if (base >= live) break;
+        load_batch(base, live);
     }
     column_sum[pg][col] = acc;
     __syncthreads();
@@ -953,18 +982,19 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const float* __res
         float sum = 0.0f;
 #pragma unroll
         for (int g = 0; g < PG; ++g) sum += reinterpret_cast<const float*>(column_sum[g])[t];
-        out[row * D + t] = den > 0.0f ? sum / den : 0.0f;
+        mp.out[row * D + t] = den > 0.0f ? sum / den : 0.0f;
     }
 }
 
 // Small rows: one wave per (sequence, query head) row, four rows per
 // workgroup, no barriers. Lane l owns column l % TPR of the states
-// j == l / TPR (mod PGW) and lane j (< parts) reads state j's (m, l) for the
-// row maximum and denominator, reduced with DPP. The shared variant forms each
+// j == l / TPR (mod PGW) and lane j reads state j's (m, l) for the row
+// maximum and denominator, reduced with DPP. The shared variant forms each
 // state's weight once, in lane j, and broadcasts it with a cross-lane read;
 // the serial variant has every lane recompute the weights it uses. The PGW
-// column sums meet through permlane swaps. Used when a row's states fit in
-// kMergeWaveBatch loads per lane (at most 64 states).
+// column sums meet through permlane swaps. Used when a row's allocated states
+// fit in kMergeWaveBatch loads per lane (at most 64 states); all loads are
+// issued at once and masked with the live count.
 constexpr int kMergeWaveBatch = 8;
 constexpr int kMergeRowsPerGroup = 4;
 
@@ -972,9 +1002,7 @@ template <int D>
 constexpr int merge_wave_max_parts() { return kMergeWaveBatch * (kWave / (D / 4)); }
 
 template <int D, bool kSharedWeights>
-__global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
-    const float* __restrict__ numerator, const float* __restrict__ stats, float* __restrict__ out, int parts,
-    int query_heads) {
+__global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(const MergeParams mp) {
     constexpr int TPR = D / 4;        // lanes per state row
     constexpr int PGW = kWave / TPR;  // state groups per wave (2 or 4)
     constexpr int NB = kMergeWaveBatch;
@@ -982,14 +1010,17 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     const int h = blockIdx.x * kMergeRowsPerGroup + wave;
-    if (h >= query_heads) return;  // whole wave; nothing below synchronises across waves
-    const int64_t row = static_cast<int64_t>(blockIdx.y) * query_heads + h;
+    if (h >= mp.query_heads) return;  // whole wave; nothing below synchronises across waves
+    const int b = blockIdx.y;
+    const int64_t row = static_cast<int64_t>(b) * mp.query_heads + h;
+    const int parts = mp.parts;
     const int col = lane % TPR;
     const int pg = lane / TPR;
     const int last = parts - 1;
-    const float2* st = reinterpret_cast<const float2*>(stats) + row * parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(numerator + row * parts * D) + col;
+    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * parts;
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D) + col;
     const int rounds = (parts + PGW - 1) / PGW;  // uniform, <= NB
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
 
     f32x4 buf[NB];
     float2 own[NB];
@@ -1002,10 +1033,10 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
         }
     }
     const float2 mine = read_state(st, min(lane, last));
-    const bool live = (lane < parts) & (mine.y > 0.0f);
-    const float mx = wave_max(live ? mine.x : kNoToken);
-    const float f = live ? fast_exp2(mine.x - mx) : 0.0f;  // weight of state `lane`
-    const float den = wave_sum(f * (live ? mine.y : 0.0f));
+    const bool ok = (lane < live) & (mine.y > 0.0f);
+    const float mx = wave_max(ok ? mine.x : kNoToken);
+    const float f = ok ? fast_exp2(mine.x - mx) : 0.0f;  // weight of state `lane`
+    const float den = wave_sum(f * (ok ? mine.y : 0.0f));
 
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1014,11 +1045,11 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
             const int j = pg + k * PGW;
             float wj;
             if constexpr (kSharedWeights) {
-                wj = __shfl(f, min(j, last));
+                wj = __shfl(f, min(j, kWave - 1));
             } else {
                 wj = own[k].y > 0.0f ? fast_exp2(own[k].x - mx) : 0.0f;
             }
-            wj = j < parts ? wj : 0.0f;
+            wj = j < live ? wj : 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[e] = wj > 0.0f ? fmaf(wj, buf[k][e], acc[e]) : acc[e];
         }
@@ -1032,7 +1063,7 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
         f32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = den > 0.0f ? acc[e] / den : 0.0f;
-        *reinterpret_cast<f32x4*>(out + row * D + col * 4) = o;
+        *reinterpret_cast<f32x4*>(mp.out + row * D + col * 4) = o;
     }
 }
 
@@ -1175,47 +1206,54 @@ int run_partial(const void* q, const void* k, const void* v, int dtype, const in
 }
 
 template <int D>
-int launch_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads, int parts,
-                 int merge_mode, hipStream_t stream) {
+int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t stream) {
     const bool shared = merge_mode == PD_MERGE_SHARED;
-    if (parts <= merge_wave_max_parts<D>()) {
-        const dim3 grid((query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
+    if (mp.parts <= merge_wave_max_parts<D>()) {
+        const dim3 grid((mp.query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
         if (shared) {
-            hipLaunchKernelGGL((merge_rows_kernel<D, true>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream,
-                               numerator, stats, out, parts, query_heads);
+            hipLaunchKernelGGL((merge_rows_kernel<D, true>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream, mp);
         } else {
-            hipLaunchKernelGGL((merge_rows_kernel<D, false>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream,
-                               numerator, stats, out, parts, query_heads);
+            hipLaunchKernelGGL((merge_rows_kernel<D, false>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream, mp);
         }
         return launch_status();
     }
-    const dim3 grid(query_heads, batch);
+    const dim3 grid(mp.query_heads, batch);
     if (shared) {
-        hipLaunchKernelGGL((merge_kernel<D, true>), grid, dim3(kMergeThreads), parts * sizeof(float), stream,
-                           numerator, stats, out, parts);
+        hipLaunchKernelGGL((merge_kernel<D, true>), grid, dim3(kMergeThreads), mp.parts * sizeof(float), stream, mp);
     } else {
-        hipLaunchKernelGGL((merge_kernel<D, false>), grid, dim3(kMergeThreads), 0, stream, numerator, stats,
-                           out, parts);
+        hipLaunchKernelGGL((merge_kernel<D, false>), grid, dim3(kMergeThreads), 0, stream, mp);
     }
     return launch_status();
 }
 
-int check_merge(const float* numerator, const float* stats, const float* out, int batch,
-                int query_heads, int head_dim, int splits, int merge_mode) {
-    if (!numerator || !stats || !out) return PD_ERR_NULL_POINTER;
+int check_merge(const float* numerator, const float* stats, const float* out, const int32_t* lengths, int batch,
+                int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
+                int merge_mode) {
+    if (!numerator || !stats || !out || !lengths) return PD_ERR_NULL_POINTER;
     if (batch < 1 || batch > 65535 || query_heads < 1 || query_heads > 65535) return PD_ERR_SHAPE;
     if (head_dim != 64 && head_dim != 128) return PD_ERR_SHAPE;
-    if (splits < 1 || splits > 65535) return PD_ERR_SPLIT;
+    if (page_size != 16 && page_size != 32) return PD_ERR_SHAPE;
+    if (table_width < 1 || table_width > 65536) return PD_ERR_SHAPE;
+    if (splits < 1 || splits > 65535 || split_tokens < 1 || split_tokens > (1 << 20)) return PD_ERR_SPLIT;
     if (merge_mode != PD_MERGE_SERIAL && merge_mode != PD_MERGE_SHARED) return PD_ERR_MERGE;
     if (merge_mode == PD_MERGE_SHARED && kQuarters * splits > PD_SHARED_MERGE_MAX_PARTS) return PD_ERR_MERGE;
     return PD_OK;
 }
 
-int run_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads,
-              int head_dim, int splits, int merge_mode, hipStream_t stream) {
-    const int parts = kQuarters * splits;
-    return head_dim == 64 ? launch_merge<64>(numerator, stats, out, batch, query_heads, parts, merge_mode, stream)
-                          : launch_merge<128>(numerator, stats, out, batch, query_heads, parts, merge_mode, stream);
+int run_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
+              int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
+              int merge_mode, hipStream_t stream) {
+    MergeParams mp{};
+    mp.numerator = numerator;
+    mp.stats = stats;
+    mp.out = out;
+    mp.lengths = lengths;
+    mp.parts = kQuarters * splits;
+    mp.query_heads = query_heads;
+    mp.split_tokens = split_tokens;
+    mp.capacity = table_width * page_size;
+    return head_dim == 64 ? launch_merge<64>(mp, batch, merge_mode, stream)
+                          : launch_merge<128>(mp, batch, merge_mode, stream);
 }
 
 }  // namespace
@@ -1235,12 +1273,14 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, co
                        split_tokens, static_cast<hipStream_t>(stream));
 }
 
-int pd_decode_merge(const float* numerator, const float* stats, float* out, int batch, int query_heads,
-                    int head_dim, int splits, int merge_mode, void* stream) {
-    const int status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
+int pd_decode_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
+                    int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
+                    int merge_mode, void* stream) {
+    const int status = check_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size,
+                                   table_width, splits, split_tokens, merge_mode);
     if (status != PD_OK) return status;
-    return run_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode,
-                     static_cast<hipStream_t>(stream));
+    return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
+                     split_tokens, merge_mode, static_cast<hipStream_t>(stream));
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -1251,14 +1291,16 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
                               kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                               split_tokens);
     if (status == PD_OK)
-        status = check_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode);
+        status = check_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width,
+                             splits, split_tokens, merge_mode);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                          split_tokens, s);
     if (status != PD_OK) return status;
-    return run_merge(numerator, stats, out, batch, query_heads, head_dim, splits, merge_mode, s);
+    return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
+                     split_tokens, merge_mode, s);
 }
 
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {
@@ -1279,6 +1321,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 4; }
+int pd_abi_version(void) { return 5; }
 
 }  // extern "C"

@@ -114,13 +114,17 @@ void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor ta
         static_cast<int>(s.pages), static_cast<int>(s.splits), static_cast<int>(split_tokens), current_stream(q)));
 }
 
-// Merge stage alone (second launch of decode).
-void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t merge_mode) {
-    for (const auto& t : {numerator, stats, out}) {
+// Merge stage alone (second launch of decode); lengths, page_size,
+// table_width and split_tokens are those of the partition stage.
+void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, torch::Tensor lengths, int64_t page_size,
+           int64_t table_width, int64_t split_tokens, int64_t merge_mode) {
+    for (const auto& t : {numerator, stats, out, lengths}) {
         TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.device() == out.device(),
                     "all tensors must be contiguous GPU tensors on one device");
-        TORCH_CHECK(t.scalar_type() == at::kFloat, "workspaces/output must be float32");
     }
+    for (const auto& t : {numerator, stats, out}) TORCH_CHECK(t.scalar_type() == at::kFloat, "workspaces/output must be float32");
+    TORCH_CHECK(lengths.scalar_type() == at::kInt && lengths.dim() == 1 && lengths.size(0) == out.size(0),
+                "lengths must be int32 [batch]");
     TORCH_CHECK(numerator.dim() == 4 && stats.dim() == 4 && out.dim() == 3, "invalid workspace shapes");
     TORCH_CHECK(stats.size(0) == numerator.size(0) && stats.size(1) == numerator.size(1) &&
                     stats.size(2) == numerator.size(2) && numerator.size(2) % 4 == 0 && stats.size(3) == 2 &&
@@ -129,8 +133,10 @@ void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int6
                 "workspace/output shape mismatch");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     check_status(pd_decode_merge(numerator.data_ptr<float>(), stats.data_ptr<float>(), out.data_ptr<float>(),
-                                 static_cast<int>(numerator.size(0)), static_cast<int>(numerator.size(1)),
-                                 static_cast<int>(numerator.size(3)), static_cast<int>(numerator.size(2) / 4),
+                                 lengths.data_ptr<int32_t>(), static_cast<int>(numerator.size(0)),
+                                 static_cast<int>(numerator.size(1)), static_cast<int>(numerator.size(3)),
+                                 static_cast<int>(page_size), static_cast<int>(table_width),
+                                 static_cast<int>(numerator.size(2) / 4), static_cast<int>(split_tokens),
                                  static_cast<int>(merge_mode), current_stream(out)));
 }
 

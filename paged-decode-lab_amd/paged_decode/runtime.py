@@ -45,13 +45,17 @@ class DecodePlan:
     """Static metadata + reusable workspace for one decode shape.
 
     table/lengths are CPU integer arrays and are copied during construction.
-    KV contents and q can change between runs; metadata requires a new plan.
+    KV contents and q can change between runs. New metadata of the same shape
+    whose longest sequence fits the reserved context (``max_context``, by
+    default the longest initial sequence) is loaded in place with ``refresh``;
+    anything else requires a new plan.
     The output is borrowed storage, overwritten by the next run. A plan may be
     used on one stream at a time; use distinct plans for concurrent streams.
     Device metadata and workspace attributes are internal and must not be edited.
     """
 
-    def __init__(self, layout: Layout, table, lengths, *, device="cuda", split_tokens=256, merge="serial"):
+    def __init__(self, layout: Layout, table, lengths, *, device="cuda", split_tokens=256, merge="serial",
+                 max_context=None):
         if merge not in ("serial", "shared"):
             raise ValueError("merge must be 'serial' or 'shared'")
         if layout.head_dim not in (64, 128):
@@ -66,9 +70,18 @@ class DecodePlan:
         if table.shape[1] > 65536:
             raise ValueError("page table width must not exceed 65536")
         self.max_context = int(lengths.max(initial=0))
-        if self.max_context > 1048576:
+        if max_context is None:
+            capacity = self.max_context
+        else:
+            if isinstance(max_context, bool) or not isinstance(max_context, int):
+                raise ValueError("max_context must be an integer")
+            if not self.max_context <= max_context <= table.shape[1] * layout.page_size:
+                raise ValueError("max_context must cover the current lengths and fit the page table")
+            capacity = max_context
+        if capacity > 1048576:
             raise ValueError("this implementation supports at most 1M context tokens")
-        self.splits = max(1, math.ceil(self.max_context / split_tokens))
+        self.context_capacity = capacity
+        self.splits = max(1, math.ceil(capacity / split_tokens))
         if self.splits > 65535:
             raise ValueError("too many context splits")
         self.layout, self.split_tokens = layout, split_tokens
@@ -93,6 +106,28 @@ class DecodePlan:
         self._out = torch.empty((layout.batch, layout.query_heads, layout.head_dim),
                                 dtype=torch.float32, device=self.device)
         self._extension = load_extension()
+
+    def refresh(self, table, lengths):
+        """Replace the page table and lengths in place, without reallocating.
+
+        The new metadata is validated like the constructor's, must keep the
+        table's shape, and its longest sequence must fit the plan's reserved
+        context (``max_context`` at construction, else the first lengths).
+        Partitions, workspace and device pointers are unchanged, so graphs
+        captured from ``run`` stay valid and see the new metadata. The copy is
+        ordered on the current stream: call it on the stream the plan runs on,
+        outside graph capture.
+        """
+        table, lengths = validate_metadata(self.layout, table, lengths)
+        if tuple(table.shape) != tuple(self._table.shape):
+            raise ValueError("refresh must keep the page table shape")
+        longest = int(lengths.max(initial=0))
+        if longest > self.context_capacity:
+            raise ValueError("lengths exceed the plan's reserved context; build a plan with a larger max_context")
+        self._table.copy_(torch.from_numpy(table))
+        self._lengths.copy_(torch.from_numpy(lengths))
+        self._table_cpu, self._lengths_cpu = table, lengths
+        self.max_context = longest
 
     @property
     def workspace_bytes(self):
@@ -128,5 +163,7 @@ class DecodePlan:
 
     def run_merge(self):
         """Merge stage only, from the current workspace; returns the borrowed output."""
-        self._extension.merge(self._numerator, self._stats, self._out, self._merge_mode)
+        layout = self.layout
+        self._extension.merge(self._numerator, self._stats, self._out, self._lengths, layout.page_size,
+                              self._table.shape[1], self.split_tokens, self._merge_mode)
         return self._out

@@ -204,19 +204,83 @@ def test_golden_fixtures(golden_dir):
             assert_parity(plan.run(tq, tk, tv).cpu().numpy(), fixtures[f"{name}/out"], q.dtype)
 
 
-def test_workspace_and_output_fully_written():
-    """initcheck analogue: NaN-poisoned workspace and output are overwritten."""
+def test_nan_poisoned_workspace_live_states_written_dead_states_untouched():
+    """initcheck analogue on a ragged batch with an empty sequence.
+
+    Every state the merge reads -- partitions up to each sequence's end -- is
+    written by the call; states past the end are never written (they keep the
+    NaN poison) and never read (the output is finite and matches the oracle).
+    """
     w = make_workload("ragged_shared_b16")
     layout = w.layout
     q, k, v = (torch.from_numpy(x).cuda() for x in w.host_tensors())
-    plan = DecodePlan(layout, w.table, w.lengths, split_tokens=w.split_tokens)
-    for t in (plan._numerator, plan._stats, plan._out):
-        t.fill_(float("nan"))
-    announce("nan-poison ragged_shared_b16")
-    out = plan.run(q, k, v)
+    for merge in ("serial", "shared"):
+        plan = DecodePlan(layout, w.table, w.lengths, split_tokens=w.split_tokens, merge=merge)
+        for t in (plan._numerator, plan._stats, plan._out):
+            t.fill_(float("nan"))
+        announce(f"nan-poison ragged_shared_b16 merge={merge}")
+        out = plan.run(q, k, v)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        assert_parity(out.cpu().numpy(), oracle(q, k, v, w.table, w.lengths), torch.float16)
+        num, st = plan._numerator.cpu().numpy(), plan._stats.cpu().numpy()
+        for b, length in enumerate(w.lengths):
+            live = 4 * -(-int(length) // w.split_tokens)
+            assert np.isfinite(num[b, :, :live]).all() and np.isfinite(st[b, :, :live]).all()
+            assert np.isnan(num[b, :, live:]).all() and np.isnan(st[b, :, live:]).all()
+        assert (w.lengths == 0).any()
+
+
+@pytest.mark.parametrize("merge", ["serial", "shared"])
+def test_refresh_loads_new_metadata_in_place(merge):
+    """refresh(): new table and lengths, same buffers; graphs replay the new metadata."""
+    layout = Layout(3, 16, 4, 128, 16, 3 * 64)
+    rng = np.random.default_rng(11)
+    q, k, v = make_tensors(layout, seed=11)
+    table = rng.permutation(3 * 64).reshape(3, 64).astype(np.int32)
+    lengths = np.array([1000, 17, 512], dtype=np.int32)
+    plan = DecodePlan(layout, table, lengths, split_tokens=128, merge=merge, max_context=1024)
+    assert plan.splits == 8 and plan.context_capacity == 1024 and plan.max_context == 1000
+    announce(f"refresh merge={merge}")
+    assert_parity(plan.run(q, k, v).cpu().numpy(), oracle(q, k, v, table, lengths), torch.float16)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            captured = plan.run(q, k, v)
+    torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    assert torch.isfinite(out).all()
-    assert not torch.isnan(plan._numerator).any() and not torch.isnan(plan._stats).any()
+    buffers = (plan._table.data_ptr(), plan._lengths.data_ptr(), plan._numerator.data_ptr())
+    for new_lengths in ([1024, 0, 3], [0, 0, 0], [129, 1024, 700]):
+        new_table = rng.permutation(3 * 64).reshape(3, 64).astype(np.int32)
+        new_lengths = np.array(new_lengths, dtype=np.int32)
+        plan.refresh(new_table, new_lengths)
+        assert (plan._table.data_ptr(), plan._lengths.data_ptr(), plan._numerator.data_ptr()) == buffers
+        assert plan.max_context == int(new_lengths.max())
+        expected = oracle(q, k, v, new_table, new_lengths)
+        eager = plan.run(q, k, v).clone()
+        assert_parity(eager.cpu().numpy(), expected, torch.float16)
+        captured.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(captured, eager, rtol=0, atol=0)
+
+
+def test_refresh_rejects_what_does_not_fit():
+    layout = Layout(2, 8, 2, 64, 16, 16)
+    table = np.arange(16, dtype=np.int32).reshape(2, 8)
+    plan = DecodePlan(layout, table, np.array([100, 60], dtype=np.int32), split_tokens=32)
+    with pytest.raises(ValueError):
+        plan.refresh(table, np.array([101, 0], dtype=np.int32))      # beyond the reserved context
+    with pytest.raises(ValueError):
+        plan.refresh(table[:, :4], np.array([10, 0], dtype=np.int32))  # table shape changed
+    with pytest.raises(ValueError):
+        plan.refresh(np.full((2, 8), 99, dtype=np.int32), np.array([10, 0], dtype=np.int32))  # live page out of range
+    with pytest.raises(TypeError):
+        plan.refresh(table.astype(np.float32), np.array([10, 0], dtype=np.int32))
+    plan.refresh(table, np.array([100, 100], dtype=np.int32))
+    assert plan.max_context == 100
 
 
 def test_repeated_runs_are_bitwise_identical():

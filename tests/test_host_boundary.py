@@ -39,6 +39,13 @@ def test_plan_rejects_bad_arguments(kwargs, exc):
         DecodePlan(layout, table, lengths, **kwargs)
 
 
+@pytest.mark.parametrize("max_context", [True, 1.0, 126, 129, -1])
+def test_plan_rejects_bad_context_reservation(max_context):
+    layout, table, lengths = plan_args()       # lengths [127], table capacity 8 * 16 = 128 tokens
+    with pytest.raises(ValueError):
+        DecodePlan(layout, table, lengths, max_context=max_context)
+
+
 @pytest.mark.parametrize("layout", [Layout(1, 8, 2, 96, 16, 8), Layout(1, 8, 2, 64, 8, 8),
                                     Layout(65536, 8, 2, 64, 16, 8), Layout(1, 65536 * 2, 2, 64, 16, 8)])
 def test_plan_rejects_unsupported_layouts(layout):
@@ -75,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 4
+    assert lib.pd_abi_version() == 5
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -138,7 +145,19 @@ def test_c_abi_rejects_null_pointers():
         broken = list(ptrs)
         broken[i] = None
         assert call_decode(lib, broken) == cabi.PD_ERR_NULL_POINTER
-    assert lib.pd_decode_merge(None, ptrs[1], ptrs[2], 4, 32, 128, 16, 0, None) == cabi.PD_ERR_NULL_POINTER
-    assert lib.pd_decode_merge(ptrs[0], ptrs[1], ptrs[2], 4, 32, 128, 16, 7, None) == cabi.PD_ERR_MERGE
+    merge_args = dict(batch=4, query_heads=32, head_dim=128, page_size=16, table_width=256, splits=16,
+                      split_tokens=256)
+
+    def call_merge(num, st, out, lengths, merge_mode=0, **over):
+        a = {**merge_args, **over}
+        return lib.pd_decode_merge(num, st, out, lengths, a["batch"], a["query_heads"], a["head_dim"],
+                                   a["page_size"], a["table_width"], a["splits"], a["split_tokens"], merge_mode,
+                                   None)
+
+    assert call_merge(None, ptrs[1], ptrs[2], ptrs[3]) == cabi.PD_ERR_NULL_POINTER
+    assert call_merge(ptrs[0], ptrs[1], ptrs[2], None) == cabi.PD_ERR_NULL_POINTER
+    assert call_merge(ptrs[0], ptrs[1], ptrs[2], ptrs[3], merge_mode=7) == cabi.PD_ERR_MERGE
+    assert call_merge(ptrs[0], ptrs[1], ptrs[2], ptrs[3], page_size=8) == cabi.PD_ERR_SHAPE
+    assert call_merge(ptrs[0], ptrs[1], ptrs[2], ptrs[3], split_tokens=0) == cabi.PD_ERR_SPLIT
     assert lib.pd_decode_partial(ptrs[0], ptrs[1], ptrs[2], 1, ptrs[3], ptrs[4], ptrs[5], ptrs[6],
                                  4, 32, 8, 128, 16, 256, 1024, 0, 256, None) == cabi.PD_ERR_SPLIT
