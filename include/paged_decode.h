@@ -104,6 +104,39 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out,
                     int merge_mode, void* stream);
 
 /*
+ * Paged KV-cache append, the write step before decode. Writes `tokens` new
+ * tokens per sequence: k_new, v_new are [batch, tokens, kv_heads, head_dim]
+ * (same dtype as the cache), and token j of sequence b goes to logical
+ * position positions[b] + j, i.e. page table[b, pos / page_size], slot
+ * pos % page_size of k_cache / v_cache [physical_pages, page_size, kv_heads,
+ * head_dim] -- the decode's own addressing (reference docs/DESIGN.md:10-13).
+ * Tokens whose position is negative or at/after table_width * page_size, or
+ * whose page id is outside [0, physical_pages), are skipped. Pages shared by
+ * several sequences are written as mapped: copy-on-write is the caller's.
+ * No counterpart in the reference, which leaves cache writes to its caller
+ * (docs/DESIGN.md:11-13).
+ */
+int pd_append_kv(const void* k_new, const void* v_new, int dtype,
+                 const int32_t* table, const int32_t* positions,
+                 void* k_cache, void* v_cache,
+                 int batch, int tokens, int kv_heads, int head_dim, int page_size,
+                 int table_width, int physical_pages, void* stream);
+
+/*
+ * As pd_append_kv with positions[b] = lengths[b], all or nothing per
+ * sequence, and lengths advanced on the device: sequence b is written only if
+ * all of its `tokens` positions map to valid cache rows, and then lengths[b]
+ * grows by `tokens`; otherwise its cache rows and length are left unchanged.
+ * An append followed by pd_decode on the same lengths needs no host round
+ * trip, so a decode step can be captured in a hipGraph and replayed.
+ */
+int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype,
+                         const int32_t* table, int32_t* lengths,
+                         void* k_cache, void* v_cache,
+                         int batch, int tokens, int kv_heads, int head_dim, int page_size,
+                         int table_width, int physical_pages, void* stream);
+
+/*
  * Bytes of numerator + stats for a plan: batch * query_heads * 4 * splits *
  * (head_dim + 2) * 4, the reference's DecodePlan.workspace_bytes
  * (src/paged_decode/runtime.py:71-73, docs/DESIGN.md:69-76). Returns 0 for
@@ -117,7 +150,7 @@ const char* pd_status_string(int status);
 /* ABI version of this header: bumped on any signature or layout change
  * (3: four states per partition; 4: single-launch entry withdrawn;
  * 5: states past a sequence's end are neither written nor read, so
- * pd_decode_merge takes the lengths). */
+ * pd_decode_merge takes the lengths; 6: KV-cache append). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

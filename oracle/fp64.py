@@ -18,6 +18,9 @@ Pinned by (``tests/test_oracle.py``):
   reference ``tests/test_oracle.py:8-63``).
 * ``gather_tokens`` -- addressing pinned by the relabelling and shared-page
   checks above and by a direct index check on a hand-built cache.
+* ``scatter_tokens`` / ``append_advance`` -- the inverse of ``gather_tokens``:
+  pinned by round trips (scatter then gather returns the written rows, rows
+  not written are untouched) and by the skip rules on hand-built tables.
 """
 import math
 
@@ -137,3 +140,48 @@ def streaming_attention(q, k, v, table, lengths, split_tokens=256, lanes=4):
                                                   values[start + lane:stop:lanes]))
             out[b, h] = merge_partials(states)
     return out
+
+
+def scatter_tokens(cache, table, positions, new):
+    """Cache after writing ``new[b, j]`` at logical position ``positions[b] + j``.
+
+    Restates the decode's addressing (reference ``docs/DESIGN.md:10-13``) in the
+    write direction: page ``table[b, pos // T]``, slot ``pos % T``. Positions
+    outside ``[0, W * T)`` and page ids outside ``[0, P)`` are skipped. Works on
+    a copy; exact (no arithmetic on values).
+    """
+    out = cache.copy()
+    pages, page_size = cache.shape[0], cache.shape[1]
+    table = np.asarray(table)
+    capacity = table.shape[1] * page_size
+    for b in range(new.shape[0]):
+        for j in range(new.shape[1]):
+            pos = int(positions[b]) + j
+            if not 0 <= pos < capacity:
+                continue
+            page = int(table[b, pos // page_size])
+            if not 0 <= page < pages:
+                continue
+            out[page, pos % page_size] = new[b, j]
+    return out
+
+
+def append_advance(cache, table, lengths, new):
+    """All-or-nothing append at the current lengths; returns (cache, lengths)."""
+    pages, page_size = cache.shape[0], cache.shape[1]
+    table = np.asarray(table)
+    capacity = table.shape[1] * page_size
+    out, grown = cache.copy(), np.array(lengths, dtype=np.int64).copy()
+    for b in range(new.shape[0]):
+        base = int(lengths[b])
+        rows = []
+        for j in range(new.shape[1]):
+            pos = base + j
+            page = int(table[b, pos // page_size]) if 0 <= pos < capacity else -1
+            rows.append(None if not 0 <= page < pages else (page, pos % page_size))
+        if any(r is None for r in rows):
+            continue
+        for j, (page, slot) in enumerate(rows):
+            out[page, slot] = new[b, j]
+        grown[b] = base + new.shape[1]
+    return out, grown.astype(np.int32)

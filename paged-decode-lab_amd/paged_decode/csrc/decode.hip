@@ -1068,6 +1068,78 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Paged KV-cache append: the write step before decode. Token j of sequence b
+// goes to logical position pos_b + j: page table[b, (pos_b + j) / T], slot
+// (pos_b + j) % T, where one token row (all KV heads) is row_bytes contiguous
+// bytes in both the new-token tensors [B, tokens, Hkv, D] and the cache
+// [P, T, Hkv, D], so a token is a straight 16-byte-per-lane copy of its K row
+// and its V row. Same addressing as the gather (reference docs/DESIGN.md:10-13).
+
+struct AppendParams {
+    const char* k_new;
+    const char* v_new;
+    const int32_t* table;
+    const int32_t* positions;  // explicit variant: first position per sequence
+    int32_t* lengths;          // advance variant: positions in, advanced lengths out
+    char* k_cache;
+    char* v_cache;
+    int tokens;
+    int table_width;
+    int page_shift;
+    int physical_pages;
+    uint32_t row_bytes;        // kv_heads * head_dim * element size
+};
+
+// Physical row of logical position pos, or -1 if pos is outside the table's
+// capacity or its page id is outside [0, physical_pages).
+__device__ __forceinline__ int64_t cache_row(const AppendParams& a, const int32_t* pages, int64_t pos) {
+    const int64_t capacity = static_cast<int64_t>(a.table_width) << a.page_shift;
+    if (pos < 0 || pos >= capacity) return -1;
+    const int page = pages[pos >> a.page_shift];
+    if (static_cast<uint32_t>(page) >= static_cast<uint32_t>(a.physical_pages)) return -1;
+    return (static_cast<int64_t>(page) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+}
+
+__device__ __forceinline__ void copy_token_row(const AppendParams& a, int64_t src_row, int64_t dst_row) {
+    const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new + src_row * a.row_bytes);
+    const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new + src_row * a.row_bytes);
+    u32x4* kd = reinterpret_cast<u32x4*>(a.k_cache + dst_row * a.row_bytes);
+    u32x4* vd = reinterpret_cast<u32x4*>(a.v_cache + dst_row * a.row_bytes);
+    const uint32_t chunks = a.row_bytes / 16u;
+    for (uint32_t c = threadIdx.x; c < chunks; c += blockDim.x) {
+        kd[c] = ks[c];
+        vd[c] = vs[c];
+    }
+}
+
+// Explicit positions: workgroup (j, b) writes token j of sequence b; tokens
+// that do not map to a valid cache row are skipped.
+__global__ void __launch_bounds__(256) append_kv_kernel(const AppendParams a) {
+    const int j = blockIdx.x;
+    const int b = blockIdx.y;
+    const int32_t* pages = a.table + static_cast<int64_t>(b) * a.table_width;
+    const int64_t dst = cache_row(a, pages, static_cast<int64_t>(a.positions[b]) + j);
+    if (dst < 0) return;
+    copy_token_row(a, static_cast<int64_t>(b) * a.tokens + j, dst);
+}
+
+// Positions from lengths, all or nothing per sequence: workgroup b writes its
+// `tokens` tokens at lengths[b] .. lengths[b] + tokens - 1 only if every one of
+// them maps to a valid cache row, then advances lengths[b]; otherwise the
+// sequence and its length are left unchanged.
+__global__ void __launch_bounds__(256) append_kv_advance_kernel(const AppendParams a) {
+    const int b = blockIdx.x;
+    const int32_t* pages = a.table + static_cast<int64_t>(b) * a.table_width;
+    const int64_t base = a.lengths[b];
+    bool fits = true;
+    for (int j = 0; j < a.tokens; ++j) fits &= cache_row(a, pages, base + j) >= 0;  // uniform
+    if (!fits) return;
+    for (int j = 0; j < a.tokens; ++j) copy_token_row(a, static_cast<int64_t>(b) * a.tokens + j, cache_row(a, pages, base + j));
+    __syncthreads();  // every thread has read lengths[b] before it changes
+    if (threadIdx.x == 0) a.lengths[b] = static_cast<int32_t>(base + a.tokens);
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 
 int check_common(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -1256,6 +1328,36 @@ int run_merge(const float* numerator, const float* stats, float* out, const int3
                           : launch_merge<128>(mp, batch, merge_mode, stream);
 }
 
+int check_append(const void* k_new, const void* v_new, int dtype, const int32_t* table, const int32_t* positions,
+                 const void* k_cache, const void* v_cache, int batch, int tokens, int kv_heads, int head_dim,
+                 int page_size, int table_width, int physical_pages) {
+    if (!k_new || !v_new || !table || !positions || !k_cache || !v_cache) return PD_ERR_NULL_POINTER;
+    if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_F16) return PD_ERR_DTYPE;
+    if (batch < 1 || batch > 65535 || tokens < 1 || tokens > 65535 || kv_heads < 1 || kv_heads > 65535)
+        return PD_ERR_SHAPE;
+    if (head_dim != 64 && head_dim != 128) return PD_ERR_SHAPE;
+    if (page_size != 16 && page_size != 32) return PD_ERR_SHAPE;
+    if (table_width < 1 || table_width > 65536 || physical_pages < 1) return PD_ERR_SHAPE;
+    return PD_OK;
+}
+
+AppendParams append_params(const void* k_new, const void* v_new, int dtype, const int32_t* table, void* k_cache,
+                           void* v_cache, int tokens, int kv_heads, int head_dim, int page_size, int table_width,
+                           int physical_pages) {
+    AppendParams a{};
+    a.k_new = static_cast<const char*>(k_new);
+    a.v_new = static_cast<const char*>(v_new);
+    a.table = table;
+    a.k_cache = static_cast<char*>(k_cache);
+    a.v_cache = static_cast<char*>(v_cache);
+    a.tokens = tokens;
+    a.table_width = table_width;
+    a.page_shift = page_size == 16 ? 4 : 5;
+    a.physical_pages = physical_pages;
+    a.row_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * (dtype == PD_DTYPE_F16 ? 2 : 4));
+    return a;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1303,6 +1405,32 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
                      split_tokens, merge_mode, s);
 }
 
+int pd_append_kv(const void* k_new, const void* v_new, int dtype, const int32_t* table, const int32_t* positions,
+                 void* k_cache, void* v_cache, int batch, int tokens, int kv_heads, int head_dim, int page_size,
+                 int table_width, int physical_pages, void* stream) {
+    const int status = check_append(k_new, v_new, dtype, table, positions, k_cache, v_cache, batch, tokens, kv_heads,
+                                     head_dim, page_size, table_width, physical_pages);
+    if (status != PD_OK) return status;
+    AppendParams a = append_params(k_new, v_new, dtype, table, k_cache, v_cache, tokens, kv_heads, head_dim,
+                                   page_size, table_width, physical_pages);
+    a.positions = positions;
+    hipLaunchKernelGGL(append_kv_kernel, dim3(tokens, batch), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    return launch_status();
+}
+
+int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype, const int32_t* table, int32_t* lengths,
+                         void* k_cache, void* v_cache, int batch, int tokens, int kv_heads, int head_dim,
+                         int page_size, int table_width, int physical_pages, void* stream) {
+    const int status = check_append(k_new, v_new, dtype, table, lengths, k_cache, v_cache, batch, tokens, kv_heads,
+                                     head_dim, page_size, table_width, physical_pages);
+    if (status != PD_OK) return status;
+    AppendParams a = append_params(k_new, v_new, dtype, table, k_cache, v_cache, tokens, kv_heads, head_dim,
+                                   page_size, table_width, physical_pages);
+    a.lengths = lengths;
+    hipLaunchKernelGGL(append_kv_advance_kernel, dim3(batch), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+    return launch_status();
+}
+
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {
     if (batch <= 0 || query_heads <= 0 || head_dim <= 0 || splits <= 0) return 0;
     return static_cast<size_t>(batch) * query_heads * kQuarters * splits * (head_dim + 2) * sizeof(float);
@@ -1321,6 +1449,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 5; }
+int pd_abi_version(void) { return 6; }
 
 }  // extern "C"

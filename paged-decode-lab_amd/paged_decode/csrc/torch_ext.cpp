@@ -140,11 +140,52 @@ void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, torc
                                  static_cast<int>(merge_mode), current_stream(out)));
 }
 
+// KV-cache append: k_new/v_new [B, tokens, Hkv, D] into k_cache/v_cache
+// [P, T, Hkv, D] at positions[b] + j (advance = false) or at lengths[b] + j with
+// lengths advanced on the device (advance = true, all or nothing per sequence).
+void append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor table, torch::Tensor positions,
+               torch::Tensor k_cache, torch::Tensor v_cache, bool advance) {
+    for (const auto& t : {k_new, v_new, table, positions, k_cache, v_cache}) {
+        TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.device() == k_cache.device(),
+                    "all tensors must be contiguous GPU tensors on one device");
+    }
+    TORCH_CHECK(k_cache.dim() == 4 && v_cache.sizes() == k_cache.sizes(), "expected k/v cache [P,T,KV,D]");
+    TORCH_CHECK(k_new.dim() == 4 && v_new.sizes() == k_new.sizes() && k_new.size(2) == k_cache.size(2) &&
+                    k_new.size(3) == k_cache.size(3),
+                "expected k_new/v_new [B,tokens,KV,D] matching the cache");
+    TORCH_CHECK(k_new.scalar_type() == k_cache.scalar_type() && v_new.scalar_type() == k_cache.scalar_type() &&
+                    v_cache.scalar_type() == k_cache.scalar_type(),
+                "new tokens and cache must share one dtype");
+    TORCH_CHECK(k_cache.scalar_type() == at::kHalf || k_cache.scalar_type() == at::kFloat,
+                "supported cache dtypes: float16,float32");
+    TORCH_CHECK(table.dim() == 2 && table.size(0) == k_new.size(0) && positions.dim() == 1 &&
+                    positions.size(0) == k_new.size(0),
+                "metadata shape mismatch");
+    TORCH_CHECK(table.scalar_type() == at::kInt && positions.scalar_type() == at::kInt, "metadata must be int32");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(k_cache.device());
+    const int dtype = dtype_code(k_cache);
+    const int b = static_cast<int>(k_new.size(0)), tokens = static_cast<int>(k_new.size(1));
+    const int kv = static_cast<int>(k_cache.size(2)), d = static_cast<int>(k_cache.size(3));
+    const int page = static_cast<int>(k_cache.size(1)), width = static_cast<int>(table.size(1));
+    const int pages = static_cast<int>(k_cache.size(0));
+    hipStream_t stream = current_stream(k_cache);
+    if (advance) {
+        check_status(pd_append_kv_advance(k_new.data_ptr(), v_new.data_ptr(), dtype, table.data_ptr<int32_t>(),
+                                          positions.data_ptr<int32_t>(), k_cache.data_ptr(), v_cache.data_ptr(), b,
+                                          tokens, kv, d, page, width, pages, stream));
+    } else {
+        check_status(pd_append_kv(k_new.data_ptr(), v_new.data_ptr(), dtype, table.data_ptr<int32_t>(),
+                                  positions.data_ptr<int32_t>(), k_cache.data_ptr(), v_cache.data_ptr(), b, tokens,
+                                  kv, d, page, width, pages, stream));
+    }
+}
+
 PYBIND11_MODULE(_C, m) {
     m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)");
     m.def("partial", &partial, "Partition stage only");
     m.def("merge", &merge, "Merge stage only");
+    m.def("append_kv", &append_kv, "Paged KV-cache append");
     m.def("workspace_bytes", [](int64_t b, int64_t h, int64_t d, int64_t s) {
         return static_cast<int64_t>(pd_workspace_bytes(static_cast<int>(b), static_cast<int>(h),
                                                        static_cast<int>(d), static_cast<int>(s)));

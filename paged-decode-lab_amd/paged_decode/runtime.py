@@ -129,6 +129,25 @@ class DecodePlan:
         self._table_cpu, self._lengths_cpu = table, lengths
         self.max_context = longest
 
+    def append(self, k_cache, v_cache, k_new, v_new):
+        """Append new tokens at the plan's current lengths and advance them on the device.
+
+        ``k_new``/``v_new`` are ``[B, Hkv, D]`` (one token per sequence) or
+        ``[B, tokens, Hkv, D]``; the cache tensors are those later passed to
+        ``run``. A sequence is written only if all of its new positions fall on
+        valid pages of the plan's table within ``context_capacity``; otherwise
+        it and its length are unchanged. No host synchronisation: an append and
+        a ``run`` can be captured together in one graph. ``max_context`` keeps
+        the value of the last host-side metadata (construction or ``refresh``).
+        """
+        layout = self.layout
+        expected_k = (layout.physical_pages, layout.page_size, layout.kv_heads, layout.head_dim)
+        k_new, v_new = _token_batch(k_new, v_new, layout)
+        _check_cache(k_cache, v_cache, k_new, v_new, expected_k, self.device)
+        if k_new.shape[1] > self.context_capacity:
+            raise ValueError("more new tokens than the plan's reserved context")
+        self._extension.append_kv(k_new, v_new, self._table, self._lengths, k_cache, v_cache, True)
+
     @property
     def workspace_bytes(self):
         """Bytes of the partition-state workspace (numerator + stats)."""
@@ -167,3 +186,44 @@ class DecodePlan:
         self._extension.merge(self._numerator, self._stats, self._out, self._lengths, layout.page_size,
                               self._table.shape[1], self.split_tokens, self._merge_mode)
         return self._out
+
+
+def _token_batch(k_new, v_new, layout):
+    """Accept [B, Hkv, D] (one token) or [B, tokens, Hkv, D]; returns 4-d views."""
+    if k_new.dim() == 3:
+        k_new, v_new = k_new.unsqueeze(1), v_new.unsqueeze(1)
+    if k_new.dim() != 4 or tuple(k_new.shape) != tuple(v_new.shape) or k_new.shape[0] != layout.batch or \
+            tuple(k_new.shape[2:]) != (layout.kv_heads, layout.head_dim) or k_new.shape[1] < 1:
+        raise ValueError("new tokens must be [B, Hkv, D] or [B, tokens, Hkv, D] matching the layout")
+    return k_new, v_new
+
+
+def _check_cache(k_cache, v_cache, k_new, v_new, expected_k, device):
+    if tuple(k_cache.shape) != expected_k or tuple(v_cache.shape) != expected_k:
+        raise ValueError("cache shape does not match the layout")
+    if k_cache.dtype not in (torch.float16, torch.float32) or any(
+            t.dtype != k_cache.dtype for t in (v_cache, k_new, v_new)):
+        raise TypeError("cache and new tokens must share float16 or float32 dtype")
+    for tensor in (k_cache, v_cache, k_new, v_new):
+        if tensor.device != device or not tensor.is_contiguous():
+            raise ValueError("cache and new tokens must be contiguous on the plan device")
+
+
+def append_kv(layout: Layout, k_cache, v_cache, table, positions, k_new, v_new):
+    """Write new tokens into a paged KV cache at explicit positions.
+
+    ``table`` ``[B, W]`` and ``positions`` ``[B]`` are int32 device tensors;
+    token ``j`` of sequence ``b`` goes to logical position
+    ``positions[b] + j`` (page ``table[b, pos // T]``, slot ``pos % T``).
+    Tokens outside the table's capacity or on page ids outside
+    ``[0, physical_pages)`` are skipped. Runs on the current stream.
+    """
+    expected_k = (layout.physical_pages, layout.page_size, layout.kv_heads, layout.head_dim)
+    k_new, v_new = _token_batch(k_new, v_new, layout)
+    _check_cache(k_cache, v_cache, k_new, v_new, expected_k, k_cache.device)
+    for t in (table, positions):
+        if t.device != k_cache.device or t.dtype != torch.int32 or not t.is_contiguous():
+            raise TypeError("table and positions must be contiguous int32 tensors on the cache device")
+    if table.dim() != 2 or table.shape[0] != layout.batch or tuple(positions.shape) != (layout.batch,):
+        raise ValueError("table must be [B, W] and positions [B]")
+    load_extension().append_kv(k_new, v_new, table, positions, k_cache, v_cache, False)

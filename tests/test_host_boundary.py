@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 5
+    assert lib.pd_abi_version() == 6
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -161,3 +161,26 @@ def test_c_abi_rejects_null_pointers():
     assert call_merge(ptrs[0], ptrs[1], ptrs[2], ptrs[3], split_tokens=0) == cabi.PD_ERR_SPLIT
     assert lib.pd_decode_partial(ptrs[0], ptrs[1], ptrs[2], 1, ptrs[3], ptrs[4], ptrs[5], ptrs[6],
                                  4, 32, 8, 128, 16, 256, 1024, 0, 256, None) == cabi.PD_ERR_SPLIT
+
+
+def test_append_entries_reject_invalid_arguments():
+    lib = cabi.load()
+    ptrs, _keep = fake(8)
+    base = dict(dtype=1, batch=4, tokens=1, kv_heads=8, head_dim=128, page_size=16, table_width=256,
+                physical_pages=1024)
+
+    def call(fn, ptr_over=None, **over):
+        a = {**base, **over}
+        p = list(ptrs)
+        for i, value in (ptr_over or {}).items():
+            p[i] = value
+        return fn(p[0], p[1], a["dtype"], p[2], p[3], p[4], p[5], a["batch"], a["tokens"], a["kv_heads"],
+                  a["head_dim"], a["page_size"], a["table_width"], a["physical_pages"], None)
+
+    for fn in (lib.pd_append_kv, lib.pd_append_kv_advance):
+        for i in range(6):
+            assert call(fn, {i: None}) == cabi.PD_ERR_NULL_POINTER
+        assert call(fn, dtype=5) == cabi.PD_ERR_DTYPE
+        for over in (dict(batch=0), dict(tokens=0), dict(head_dim=96), dict(page_size=8), dict(table_width=0),
+                     dict(physical_pages=0)):
+            assert call(fn, **over) == cabi.PD_ERR_SHAPE

@@ -169,3 +169,43 @@ def test_oracle_is_not_imported_by_the_product_package():
         text = path.read_text()
         assert "from oracle" not in text and "import oracle" not in text, path
     assert "oracle.fp64" in sys.modules  # only this test module imported it
+
+
+def test_scatter_then_gather_round_trip():
+    """Writing tokens and reading them back through the same table returns them."""
+    rng = np.random.default_rng(21)
+    pages, page_size, kv, dim = 12, 4, 2, 8
+    cache = rng.standard_normal((pages, page_size, kv, dim))
+    table = rng.permutation(pages).reshape(3, 4).astype(np.int32)
+    new = rng.standard_normal((3, 5, kv, dim))
+    positions = np.array([0, 3, 11], dtype=np.int32)
+    out = fp64.scatter_tokens(cache, table, positions, new)
+    for b in range(3):
+        stop = min(positions[b] + 5, 16)
+        got = np.stack([fp64.gather_tokens(out, table[b], stop, h)[positions[b]:] for h in range(kv)], axis=1)
+        np.testing.assert_array_equal(got, new[b, :stop - positions[b]])
+    written = {(int(table[b, p // page_size]), p % page_size)
+               for b in range(3) for p in range(positions[b], min(positions[b] + 5, 16))}
+    for page in range(pages):
+        for slot in range(page_size):
+            if (page, slot) not in written:
+                np.testing.assert_array_equal(out[page, slot], cache[page, slot])
+
+
+def test_scatter_skips_invalid_positions_and_pages():
+    cache = np.zeros((4, 2, 1, 2))
+    table = np.array([[0, -1], [9, 1]], dtype=np.int32)
+    new = np.ones((2, 3, 1, 2))
+    out = fp64.scatter_tokens(cache, table, np.array([-1, 1]), new)
+    # seq 0: positions -1 (skip), 0 -> page 0 slot 0, 1 -> page 0 slot 1
+    # seq 1: positions 1 (page 9, skip), 2 -> page 1 slot 0, 3 -> page 1 slot 1
+    assert out[0].sum() == 4 and out[1].sum() == 4 and out[2:].sum() == 0
+
+
+def test_append_advance_is_all_or_nothing():
+    cache = np.zeros((4, 2, 1, 1))
+    table = np.array([[0, 1], [2, -1]], dtype=np.int32)
+    new = np.arange(1, 5, dtype=np.float64).reshape(2, 2, 1, 1)
+    out, lengths = fp64.append_advance(cache, table, np.array([1, 1]), new)
+    np.testing.assert_array_equal(lengths, [3, 1])          # seq 1 would need page -1
+    assert out[0, 1, 0, 0] == 1 and out[1, 0, 0, 0] == 2 and out[2:].sum() == 0
