@@ -28,6 +28,9 @@ Protocol
   confirms the HBM peak the roofline is priced against.
 * CPU baseline: the C FP32 split-K restatement on all host cores available to
   the process and on one core, each over a bounded sample of full calls.
+* Comparison rows: the dense PyTorch baselines (gather + GQA expansion +
+  SDPA, or an FP32 eager softmax) timed on the same inputs, and SDPA alone on
+  pre-gathered tensors.
 
 Prints one JSON line.
 """
@@ -63,6 +66,8 @@ def parse_args():
     p.add_argument("--cpu-threads", type=int, default=None)
     p.add_argument("--repetitions", type=int, default=30)
     p.add_argument("--inner", type=int, default=20)
+    p.add_argument("--compare", type=int, default=20,
+                   help="calls per dense PyTorch comparison row (0 skips them)")
     p.add_argument("--quiet", action="store_true", help="suppress progress lines on stderr")
     return p.parse_args()
 
@@ -290,6 +295,38 @@ def main():
     probe_gbps = 2 * PROBE_BYTES / (probe_ms * 1e-3 / 20) / 1e9
     del src, dst
 
+    # --- comparison rows: dense PyTorch baselines on the same inputs ---
+    comparison = None
+    if args.compare > 0:
+        from paged_decode.baselines import dense_decode, expand_gqa, gather_dense, sdpa_attention
+
+        table_d = torch.from_numpy(w.table).to(device)
+        lengths_d = torch.from_numpy(w.lengths).to(device)
+        ours = plan.run(q, ks[0], vs[0]).clone()
+        comparison = {}
+        for kind in ("sdpa", "eager"):
+            got = dense_decode(q, ks[0], vs[0], table_d, lengths_d, kind=kind).float()
+            live = lengths_d > 0
+            diff = float((got[live] - ours[live]).abs().max()) if bool(live.any()) else 0.0
+            for i in range(2):
+                dense_decode(q, ks[i % sets], vs[i % sets], table_d, lengths_d, kind=kind)
+            ms, _ = time_region(torch, lambda i, kind=kind: dense_decode(q, ks[i % sets], vs[i % sets], table_d,
+                                                                          lengths_d, kind=kind), args.compare)
+            us = ms * 1e3 / args.compare
+            comparison[f"torch_{kind}_with_gather"] = {"us_per_call": round(us, 2),
+                                                       "GBps": round(logical / (us * 1e-6) / 1e9, 1),
+                                                       "max_abs_vs_ours": float(f"{diff:.3e}")}
+        dense_k, dense_v, mask = gather_dense(ks[0], vs[0], table_d, lengths_d)
+        dense_k, dense_v = expand_gqa(q, dense_k, dense_v)
+        sdpa_attention(q, dense_k, dense_v, mask)
+        ms, _ = time_region(torch, lambda i: sdpa_attention(q, dense_k, dense_v, mask), args.compare)
+        us = ms * 1e3 / args.compare
+        comparison["torch_sdpa_pregathered"] = {"us_per_call": round(us, 2),
+                                                "GBps": round(logical / (us * 1e-6) / 1e9, 1),
+                                                "note": "dense K/V already gathered and GQA-expanded, one buffer set"}
+        del dense_k, dense_v, mask
+        log(args, "comparison: " + ", ".join(f"{k} {v['us_per_call']} us" for k, v in comparison.items()))
+
     digest = source_digest()
     value = logical / (us_graph * 1e-6) / 1e9
     record = {
@@ -326,6 +363,7 @@ def main():
         "cpu_baseline": cpu_baseline,
         "protocol_p50": protocol,
         "stream_copy_probe_GBps": round(probe_gbps, 1),
+        "comparison": comparison,
         "gate_max_abs_vs_cpu": {m: float(f"{e:.3e}") for m, e in gate.items()},
         "wall_ms": {"graph": round(graph_wall, 3), "eager": round(eager_wall, 3)},
         "source_digest": digest,

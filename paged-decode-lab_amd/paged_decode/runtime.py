@@ -107,6 +107,18 @@ class DecodePlan:
                                 dtype=torch.float32, device=self.device)
         self._extension = load_extension()
 
+    @classmethod
+    def from_csr(cls, layout: Layout, indptr, indices, last_page_len, **kwargs):
+        """Plan from CSR page-list metadata (``indptr``, ``indices``, ``last_page_len``).
+
+        Same keyword arguments as the constructor; the table width is the
+        longest page list unless ``table_width`` is given.
+        """
+        from .csr import from_csr
+
+        table, lengths = from_csr(layout, indptr, indices, last_page_len, table_width=kwargs.pop("table_width", None))
+        return cls(layout, table, lengths, **kwargs)
+
     def refresh(self, table, lengths):
         """Replace the page table and lengths in place, without reallocating.
 
