@@ -152,9 +152,10 @@ def main():
     unique = unique_token_bytes(w.table, w.lengths, L.page_size, L.kv_heads, L.head_dim, w.element_size)
 
     device = torch.device("cuda", 0)
-    q = torch.from_numpy(q_h).to(device)
-    k0 = torch.from_numpy(k_h).to(device)
-    v0 = torch.from_numpy(v_h).to(device)
+    q, k0, v0, k_scale, v_scale = w.tensors(device)
+    scales = {"k_scale": k_scale, "v_scale": v_scale}
+    if not w.native:  # the C restatement reads float32 values
+        q_h, k_h, v_h = (x.astype(np.float32) for x in (q_h, k_h, v_h))
     set_bytes = k0.numel() * k0.element_size() * 2
     sets = max(1, math.ceil(ROTATION_BYTES / set_bytes))
     ks = [k0] + [k0.clone() for _ in range(sets - 1)]
@@ -175,9 +176,9 @@ def main():
     gate = {}
     for name, p in plans.items():
         for i in (0, sets - 1):
-            got = p.run(q, ks[i], vs[i]).cpu().numpy()
+            got = p.run(q, ks[i], vs[i], **scales).cpu().numpy()
             err = float(np.max(np.abs(got.astype(np.float64) - expected)))
-            if w.dtype == np.float16:
+            if w.dtype == np.float16 or not w.native:
                 ok = err <= 2e-3
             else:
                 ok = bool(np.all(np.abs(got - expected) <= 1e-6 + 1e-5 * np.abs(expected)))
@@ -214,7 +215,7 @@ def main():
     # --- warmup, graph capture ---
     stream = torch.cuda.current_stream()
     for i in range(args.warmup):
-        plan.run(q, ks[i % sets], vs[i % sets])
+        plan.run(q, ks[i % sets], vs[i % sets], **scales)
     torch.cuda.synchronize()
 
     def capture(fn):
@@ -230,7 +231,7 @@ def main():
         torch.cuda.synchronize()
         return g
 
-    graphs = {m: [capture(lambda p=p, i=i: p.run(q, ks[i], vs[i])) for i in range(sets)]
+    graphs = {m: [capture(lambda p=p, i=i: p.run(q, ks[i], vs[i], **scales)) for i in range(sets)]
               for m, p in plans.items()}
 
     # --- timed region: exactly K steps ---
@@ -246,18 +247,18 @@ def main():
             g.replay()
         return g
 
-    step_graph = steps_graph(lambda i: plan.run(q, ks[i % sets], vs[i % sets]), args.steps)
+    step_graph = steps_graph(lambda i: plan.run(q, ks[i % sets], vs[i % sets], **scales), args.steps)
     graph_ms, graph_wall = time_region(torch, lambda i: step_graph.replay(), 1)
     for i in range(args.warmup):
-        plan.run(q, ks[i % sets], vs[i % sets])
-    eager_ms, eager_wall = time_region(torch, lambda i: plan.run(q, ks[i % sets], vs[i % sets]), args.steps)
+        plan.run(q, ks[i % sets], vs[i % sets], **scales)
+    eager_ms, eager_wall = time_region(torch, lambda i: plan.run(q, ks[i % sets], vs[i % sets], **scales), args.steps)
     us_graph = graph_ms * 1e3 / args.steps
     us_eager = eager_ms * 1e3 / args.steps
     log(args, f"graph of {args.steps} calls: {us_graph:.2f} us/call; eager {us_eager:.2f} us/call")
     del step_graph
 
     # --- partition kernel alone (roofline numerator): K launches back to back ---
-    partial_graph = steps_graph(lambda i: plan.run_partial(q, ks[i % sets], vs[i % sets]), args.steps)
+    partial_graph = steps_graph(lambda i: plan.run_partial(q, ks[i % sets], vs[i % sets], **scales), args.steps)
     partial_ms, _ = time_region(torch, lambda i: partial_graph.replay(), 1)
     partial_us = partial_ms * 1e3 / args.steps
     achieved = logical / (partial_us * 1e-6) / 1e9
@@ -268,7 +269,7 @@ def main():
     runners = {}
     for m, p in plans.items():
         runners[f"{m}/graph"] = lambda i, m=m: graphs[m][i % sets].replay()
-        runners[f"{m}/eager"] = lambda i, p=p: p.run(q, ks[i % sets], vs[i % sets])
+        runners[f"{m}/eager"] = lambda i, p=p: p.run(q, ks[i % sets], vs[i % sets], **scales)
         runners[f"{m}/graph_warm"] = lambda i, m=m: graphs[m][0].replay()
     rng = random.Random(w.seed)
     samples = {name: ([], []) for name in runners}
@@ -302,29 +303,37 @@ def main():
 
         table_d = torch.from_numpy(w.table).to(device)
         lengths_d = torch.from_numpy(w.lengths).to(device)
-        ours = plan.run(q, ks[0], vs[0]).clone()
+        ours = plan.run(q, ks[0], vs[0], **scales).clone()
         comparison = {}
-        for kind in ("sdpa", "eager"):
-            got = dense_decode(q, ks[0], vs[0], table_d, lengths_d, kind=kind).float()
+        # bfloat16 SDPA would run batched bf16 products on transposed views, which
+        # have faulted GPUs of this pool: bf16 workloads keep the FP32 eager row only.
+        kinds = ("eager",) if w.q_format == "bf16" else ("sdpa", "eager")
+        for kind in kinds:
+            got = dense_decode(q, ks[0], vs[0], table_d, lengths_d, kind=kind, **scales).float()
             live = lengths_d > 0
             diff = float((got[live] - ours[live]).abs().max()) if bool(live.any()) else 0.0
             for i in range(2):
-                dense_decode(q, ks[i % sets], vs[i % sets], table_d, lengths_d, kind=kind)
+                dense_decode(q, ks[i % sets], vs[i % sets], table_d, lengths_d, kind=kind, **scales)
             ms, _ = time_region(torch, lambda i, kind=kind: dense_decode(q, ks[i % sets], vs[i % sets], table_d,
-                                                                          lengths_d, kind=kind), args.compare)
+                                                                          lengths_d, kind=kind, **scales),
+                                args.compare)
             us = ms * 1e3 / args.compare
             comparison[f"torch_{kind}_with_gather"] = {"us_per_call": round(us, 2),
                                                        "GBps": round(logical / (us * 1e-6) / 1e9, 1),
                                                        "max_abs_vs_ours": float(f"{diff:.3e}")}
-        dense_k, dense_v, mask = gather_dense(ks[0], vs[0], table_d, lengths_d)
-        dense_k, dense_v = expand_gqa(q, dense_k, dense_v)
-        sdpa_attention(q, dense_k, dense_v, mask)
-        ms, _ = time_region(torch, lambda i: sdpa_attention(q, dense_k, dense_v, mask), args.compare)
-        us = ms * 1e3 / args.compare
-        comparison["torch_sdpa_pregathered"] = {"us_per_call": round(us, 2),
-                                                "GBps": round(logical / (us * 1e-6) / 1e9, 1),
-                                                "note": "dense K/V already gathered and GQA-expanded, one buffer set"}
-        del dense_k, dense_v, mask
+        if "sdpa" in kinds:
+            k_dense, v_dense = ks[0], vs[0]
+            if w.kv_format:
+                k_dense, v_dense = k_dense.to(q.dtype) * k_scale, v_dense.to(q.dtype) * v_scale
+            dense_k, dense_v, mask = gather_dense(k_dense, v_dense, table_d, lengths_d)
+            dense_k, dense_v = expand_gqa(q, dense_k, dense_v)
+            sdpa_attention(q, dense_k, dense_v, mask)
+            ms, _ = time_region(torch, lambda i: sdpa_attention(q, dense_k, dense_v, mask), args.compare)
+            us = ms * 1e3 / args.compare
+            comparison["torch_sdpa_pregathered"] = {
+                "us_per_call": round(us, 2), "GBps": round(logical / (us * 1e-6) / 1e9, 1),
+                "note": "dense K/V already gathered, dequantized and GQA-expanded, one buffer set"}
+            del dense_k, dense_v, mask, k_dense, v_dense
         log(args, "comparison: " + ", ".join(f"{k} {v['us_per_call']} us" for k, v in comparison.items()))
 
     digest = source_digest()
@@ -343,7 +352,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if w.dtype == np.float16 else "f32",
+        "dtype": w.format_label,
         "accumulate": "f32",
         "data": "synthetic (seeded N(0,1) q/k/v, shuffled page table)",
         "config": {
@@ -356,7 +365,7 @@ def main():
         "unique_kv_bytes_per_call": unique,
         "workspace_bytes": plan.workspace_bytes,
         "roofline": {
-            "bound": "hbm", "kernel": partition_kernel_name(w.dtype == np.float16), "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+            "bound": "hbm", "kernel": partition_kernel_name(w.dtype == np.float16 or not w.native), "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": recorded_traffic(w.name, digest), "avg_launch_us": round(partial_us, 3),
         },

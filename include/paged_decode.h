@@ -2,8 +2,8 @@
  * paged_decode.h -- C ABI of the MI355X (gfx950) split-K paged GQA decode operator.
  *
  * One-token attention decode over a paged KV cache:
- *   q      [batch, query_heads, head_dim]                     float16 or float32
- *   k, v   [physical_pages, page_size, kv_heads, head_dim]      same dtype as q
+ *   q      [batch, query_heads, head_dim]                     float32, float16 or bfloat16
+ *   k, v   [physical_pages, page_size, kv_heads, head_dim]      same dtype as q (FP8 too: pd_decode_ex)
  *   table  [batch, table_width]  int32 physical page of each logical page
  *   lengths[batch]               int32 live tokens per sequence
  *   out    [batch, query_heads, head_dim]                     float32
@@ -48,13 +48,22 @@ enum pd_status {
     PD_OK = 0,
     PD_ERR_NULL_POINTER = 1,  /* a required pointer is NULL */
     PD_ERR_SHAPE = 2,         /* a dimension is outside the supported range */
-    PD_ERR_DTYPE = 3,         /* dtype is not PD_DTYPE_F32 / PD_DTYPE_F16 */
+    PD_ERR_DTYPE = 3,         /* unsupported dtype combination, or a scale not finite and > 0 */
     PD_ERR_SPLIT = 4,         /* splits / split_tokens outside their range */
     PD_ERR_MERGE = 5,         /* unknown merge mode or shared-merge bound exceeded */
     PD_ERR_LAUNCH = 6         /* the HIP runtime rejected a kernel launch */
 };
 
-enum pd_dtype { PD_DTYPE_F32 = 0, PD_DTYPE_F16 = 1 };
+/* Storage formats. q, k and v share F32, F16 or BF16 in pd_decode; the _ex
+ * entries also take K/V in FP8 (OCP e4m3 / e5m2, one byte per element) with
+ * an F16 or BF16 q. */
+enum pd_dtype {
+    PD_DTYPE_F32 = 0,
+    PD_DTYPE_F16 = 1,
+    PD_DTYPE_BF16 = 2,
+    PD_DTYPE_FP8_E4M3 = 3,
+    PD_DTYPE_FP8_E5M2 = 4
+};
 
 /* Merge strategies, numbered as the reference's merge_mode argument. */
 enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
@@ -79,6 +88,33 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype,
               int batch, int query_heads, int kv_heads, int head_dim, int page_size,
               int table_width, int physical_pages, int splits, int split_tokens,
               int merge_mode, void* stream);
+
+/*
+ * pd_decode with separate q and K/V formats and per-tensor K/V scales: the
+ * attention runs over K' = k_scale * k and V' = v_scale * v. Supported pairs
+ * (q_dtype, kv_dtype): (F32, F32), (F16, F16), (BF16, BF16), and F16 or BF16
+ * q with FP8_E4M3 or FP8_E5M2 K/V (dequantized exactly in the gather; the
+ * scales are applied to the scores and to the output, not per element).
+ * Scales must be finite and > 0 (PD_ERR_DTYPE otherwise). Extends the
+ * reference's dtype set (decode.cu:215-218: float16, float32); BF16 and FP8
+ * KV are listed as future work there (docs/DESIGN.md:97-99).
+ */
+int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
+                 float k_scale, float v_scale,
+                 const int32_t* table, const int32_t* lengths,
+                 float* numerator, float* stats, float* out,
+                 int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                 int table_width, int physical_pages, int splits, int split_tokens,
+                 int merge_mode, void* stream);
+
+/* Partition stage of pd_decode_ex. */
+int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
+                         float k_scale, float v_scale,
+                         const int32_t* table, const int32_t* lengths,
+                         float* numerator, float* stats,
+                         int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                         int table_width, int physical_pages, int splits, int split_tokens,
+                         void* stream);
 
 /*
  * Partition stage only (the first launch of pd_decode): fills numerator and
@@ -150,7 +186,8 @@ const char* pd_status_string(int status);
 /* ABI version of this header: bumped on any signature or layout change
  * (3: four states per partition; 4: single-launch entry withdrawn;
  * 5: states past a sequence's end are neither written nor read, so
- * pd_decode_merge takes the lengths; 6: KV-cache append). */
+ * pd_decode_merge takes the lengths; 6: KV-cache append; 7: BF16 and FP8 K/V,
+ * pd_decode_ex). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

@@ -54,8 +54,15 @@ def sdpa_attention(q, dense_k, dense_v, mask):
                                           dropout_p=0.0).squeeze(2)
 
 
-def dense_decode(q, k, v, table, lengths, kind="sdpa"):
-    """Gather + expand + attention in one call (what a timed baseline step does)."""
+def dense_decode(q, k, v, table, lengths, kind="sdpa", k_scale=1.0, v_scale=1.0):
+    """Gather + expand + attention in one call (what a timed baseline step does).
+
+    FP8 caches are dequantized to q's dtype first (``k.to(q.dtype) * k_scale``),
+    as a caller without a quantized-KV operator would.
+    """
+    if k.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        k = k.to(q.dtype) * k_scale
+        v = v.to(q.dtype) * v_scale
     dense_k, dense_v, mask = gather_dense(k, v, table, lengths)
     dense_k, dense_v = expand_gqa(q, dense_k, dense_v)
     return (sdpa_attention if kind == "sdpa" else eager_attention)(q, dense_k, dense_v, mask)

@@ -18,15 +18,21 @@ PD_ERR_MERGE = 5
 PD_ERR_LAUNCH = 6
 PD_DTYPE_F32 = 0
 PD_DTYPE_F16 = 1
+PD_DTYPE_BF16 = 2
+PD_DTYPE_FP8_E4M3 = 3
+PD_DTYPE_FP8_E5M2 = 4
 PD_MERGE_SERIAL = 0
 PD_MERGE_SHARED = 1
 PD_SHARED_MERGE_MAX_PARTS = 4096  # states (4 per split)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
+_F = ctypes.c_float
 PROTOTYPES = {
     "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
+    "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
     "pd_decode_partial": (_I, [_P, _P, _P, _I, _P, _P, _P, _P] + [_I] * 9 + [_P]),
+    "pd_decode_partial_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P] + [_I] * 9 + [_P]),
     "pd_decode_merge": (_I, [_P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_append_kv": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
     "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),

@@ -60,6 +60,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 // Note: reinterpret whole vectors (bit_cast of a u32x4 to f16x8 / f32x4), never
 // a single element: clang 22 lowers __builtin_bit_cast of a vector-element
 // lvalue to a read of element 0.
@@ -293,7 +296,8 @@ struct PartialParams {
     int split_tokens;
     uint32_t token_bytes;  // bytes between consecutive tokens of a page (kv_heads * D * elem)
     uint64_t page_bytes;   // page_size * token_bytes
-    float scale_log2;      // log2(e) / sqrt(D)
+    float scale_log2;      // log2(e) * k_scale / sqrt(D)
+    float v_scale;         // multiplies every stored numerator
 };
 
 // Which KV head, head tile and token range a wave owns. Workgroup x covers
@@ -367,7 +371,8 @@ __device__ __forceinline__ void store_wave_state(const PartialParams& p, const W
             if (g < w.heads_here) {
                 f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + g) * parts + part) * D + col * EPL);
 #pragma unroll
-                for (int e = 0; e < EPL; e += 4) dst[e / 4] = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
+                for (int e = 0; e < EPL; e += 4)
+                    dst[e / 4] = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]} * p.v_scale;
             }
         }
     }
@@ -599,67 +604,148 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 }
 
 // ---------------------------------------------------------------------------
-// FP16 partition kernel: q.K^T and P.V both on the matrix cores.
+// 16-bit partition kernel (q in FP16 or BF16; K/V in the same type or in FP8):
+// q.K^T and P.V both on the matrix cores.
 //
-// A 16-token tile is scored with D/32 v_mfma_f32_16x16x32_f16: K in the A
-// layout (lane l loads 64 contiguous bytes, dims [32 s + 8 (l / 16), +8) of
-// k-step s, of tile token sigma(l % 16)), q in the B layout (lane l: query
-// head l % 16, zero past the group). With sigma(r) = r / 4 + 4 (r % 4) the
-// result leaves lane l with head n = l % 16 and tokens g, g + 4, g + 8, g + 12
-// of the tile (g = l / 16): exactly the A operand of v_mfma_f32_16x16x16_f16
+// A 16-token tile is scored with D/32 v_mfma_f32_16x16x32_{f16,bf16}: K in the
+// A layout (lane l holds 8 consecutive dims, [32 s + 8 (l / 16), +8) of k-step
+// s, of tile token sigma(l % 16)), q in the B layout (lane l: query head
+// l % 16, zero past the group). With sigma(r) = r / 4 + 4 (r % 4) the result
+// leaves lane l with head n = l % 16 and tokens g, g + 4, g + 8, g + 12 of the
+// tile (g = l / 16): exactly the A operand of v_mfma_f32_16x16x16_{f16,bf16}
 // for P (row = head, k = 4 g + e <-> token g + 4 e), so the weights never
 // leave their lanes. V is loaded in the row layout -- load e covers tokens
-// 4 e .. 4 e + 3, lanes [16 r, 16 r + 16) token 4 e + r, VH consecutive halves
+// 4 e .. 4 e + 3, lanes [16 r, 16 r + 16) token 4 e + r, VH consecutive dims
 // per lane -- so lane (g, n) holds tokens g + 4 e of dims n VH .. n VH + VH - 1,
-// and half j of its four V loads is the B operand of MFMA block j (column n
-// <-> dim n VH + j). P is split into FP16 high and low parts (two MFMAs per
-// block), which keeps the weights exact to about 2^-22 relative. Each
-// (head, dim) sum then lives in exactly one lane: lane (g, n) ends with heads
-// 4 g .. 4 g + 3 of dims n VH .. n VH + VH - 1, stored directly. One running
-// max per head is shared by the wave, with lazy rescaling as in the FP32
-// kernel.
+// and element j of its four V loads is the B operand of MFMA block j (column
+// n <-> dim n VH + j). P is split into high and low parts of the compute type
+// (two MFMAs per block), which keeps the weights exact to about 2^-22 (FP16)
+// or 2^-17 (BF16) relative. Each (head, dim) sum lives in exactly one lane:
+// lane (g, n) ends with heads 4 g .. 4 g + 3 of dims n VH .. n VH + VH - 1,
+// stored directly. One running max per head is shared by the wave, with lazy
+// rescaling as in the FP32 kernel.
+//
+// FP8 K/V (OCP e4m3 or e5m2) are loaded as bytes and converted to the compute
+// type after they arrive; both formats convert exactly. The per-tensor scales
+// cost nothing per element: k_scale is folded into the softmax scale and
+// v_scale into the stored numerator.
 constexpr int kTileTokens = 16;
+
+enum KvFormat { kKvNative = 0, kKvE4M3 = 1, kKvE5M2 = 2 };
 
 // Tile token loaded by K lane row r (see above).
 __device__ __forceinline__ int k_token_of_row(int r) { return (r >> 2) + 4 * (r & 3); }
 
-template <int VH>
-struct VLoad;
-template <>
-struct VLoad<8> {
-    using type = u32x4;  // 8 halves: head_dim 128
-};
-template <>
-struct VLoad<4> {
-    using type = u32x2;  // 4 halves: head_dim 64
-};
-
-// Half j of each of the four V loads, packed as an MFMA operand (k = load index).
-template <int VH>
-__device__ __forceinline__ f16x4 v_operand(const typename VLoad<VH>::type (&v)[4], int j) {
-    const uint32_t d0 = v[0][j / 2], d1 = v[1][j / 2], d2 = v[2][j / 2], d3 = v[3][j / 2];
-    uint32_t lo, hi;
-    if (j % 2 == 0) {
-        lo = (d0 & 0xFFFFu) | (d1 << 16);
-        hi = (d2 & 0xFFFFu) | (d3 << 16);
+template <int N>
+__device__ __forceinline__ void load_words(const char* src, uint32_t (&w)[N]) {
+    if constexpr (N == 4) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(src);
+        w[0] = x[0];
+        w[1] = x[1];
+        w[2] = x[2];
+        w[3] = x[3];
+    } else if constexpr (N == 2) {
+        const u32x2 x = *reinterpret_cast<const u32x2*>(src);
+        w[0] = x[0];
+        w[1] = x[1];
     } else {
-        lo = (d0 >> 16) | (d1 & 0xFFFF0000u);
-        hi = (d2 >> 16) | (d3 & 0xFFFF0000u);
+        w[0] = *reinterpret_cast<const uint32_t*>(src);
     }
-    return __builtin_bit_cast(f16x4, u32x2{lo, hi});
 }
 
-template <int D, int GT, int PD, int NC>
+// Matrix-core operations and conversions of one 16-bit compute type.
+template <typename QT>
+struct Compute;
+
+template <>
+struct Compute<_Float16> {
+    static __device__ __forceinline__ f32x4 qk(const u32x4& a, const u32x4& b, const f32x4& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                      0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(const u32x2& a, const u32x2& b, const f32x4& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
+                                                     0, 0);
+    }
+    // Nearest 16-bit value of x, and that value back as FP32.
+    static __device__ __forceinline__ uint16_t round(float x, float& back) {
+        const _Float16 h = static_cast<_Float16>(x);
+        back = static_cast<float>(h);
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    // Bytes 2 HIGH, 2 HIGH + 1 of an FP8 word as a packed pair (exact).
+    template <int KVF, bool HIGH>
+    static __device__ __forceinline__ uint32_t from_fp8(uint32_t word) {
+        f16x2 h;
+        if constexpr (KVF == kKvE4M3) h = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, HIGH);
+        else h = __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(word, 1.0f, HIGH);
+        return __builtin_bit_cast(uint32_t, h);
+    }
+};
+
+template <>
+struct Compute<__bf16> {
+    static __device__ __forceinline__ f32x4 qk(const u32x4& a, const u32x4& b, const f32x4& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                       0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(const u32x2& a, const u32x2& b, const f32x4& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                         0, 0, 0);
+    }
+    static __device__ __forceinline__ uint16_t round(float x, float& back) {
+        const __bf16 h = static_cast<__bf16>(x);
+        back = static_cast<float>(h);
+        return __builtin_bit_cast(uint16_t, h);
+    }
+    template <int KVF, bool HIGH>
+    static __device__ __forceinline__ uint32_t from_fp8(uint32_t word) {
+        f32x2 f;
+        if constexpr (KVF == kKvE4M3) f = __builtin_amdgcn_cvt_pk_f32_fp8(word, HIGH);
+        else f = __builtin_amdgcn_cvt_pk_f32_bf8(word, HIGH);
+        const float f0 = f[0], f1 = f[1];  // FP8 values are exact in BF16: keep the top halves
+        return (__builtin_bit_cast(uint32_t, f0) >> 16) | (__builtin_bit_cast(uint32_t, f1) & 0xFFFF0000u);
+    }
+};
+
+// N stored words of K or V as compute-type pairs (2 N words for FP8).
+template <typename QT, int KVF, int N>
+__device__ __forceinline__ void to_compute(const uint32_t (&raw)[N], uint32_t (&out)[KVF == kKvNative ? N : 2 * N]) {
+    if constexpr (KVF == kKvNative) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = raw[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            out[2 * i] = Compute<QT>::template from_fp8<KVF, false>(raw[i]);
+            out[2 * i + 1] = Compute<QT>::template from_fp8<KVF, true>(raw[i]);
+        }
+    }
+}
+
+// Element j of each of the four V loads (VH elements per load, as VH / 2
+// packed words), packed as an MFMA operand (k = load index).
+template <int VH>
+__device__ __forceinline__ u32x2 v_operand(const uint32_t (&v)[4][VH / 2], int j) {
+    const uint32_t d0 = v[0][j / 2], d1 = v[1][j / 2], d2 = v[2][j / 2], d3 = v[3][j / 2];
+    if (j % 2 == 0) return u32x2{(d0 & 0xFFFFu) | (d1 << 16), (d2 & 0xFFFFu) | (d3 << 16)};
+    return u32x2{(d0 >> 16) | (d1 & 0xFFFF0000u), (d2 >> 16) | (d3 & 0xFFFF0000u)};
+}
+
+template <typename QT, int KVF, int D, int GT, int PD, int NC>
 __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
-    constexpr int KS = D / 32;             // q.K^T k-steps (K loads) per tile
-    constexpr int VH = D / 16;             // V halves per lane per load = P.V MFMA blocks
-    constexpr int VI = 4;                  // V loads per tile
+    using C = Compute<QT>;
+    constexpr int ES = KVF == kKvNative ? 2 : 1;  // stored bytes per K/V element
+    constexpr int KS = D / 32;                    // q.K^T k-steps (K loads) per tile
+    constexpr int VH = D / 16;                    // V elements per lane per load = P.V MFMA blocks
+    constexpr int VI = 4;                         // V loads per tile
+    constexpr int KW = 8 * ES / 4;                // stored words per K load
+    constexpr int VW = VH * ES / 4;               // stored words per V load
     static_assert(GT <= 16, "one MFMA column block holds at most 16 query heads");
-    using VL = typename VLoad<VH>::type;
 
     struct Tile {
-        f16x8 k[KS];
-        VL v[VI];
+        uint32_t k[KS][KW];
+        uint32_t v[VI][VW];
         uint32_t live;
     };
 
@@ -673,14 +759,13 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     int window_ids = pages[min(window + lane, p.table_width - 1)];
     const WaveWork w = wave_work<GT, kTileTokens>(p, wave);
     if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
-    const _Float16* q_base = static_cast<const _Float16*>(p.q) + w.q_row * D;
+    const char* q_row = static_cast<const char*>(p.q) + w.q_row * D * 2;
 
-    f16x8 qb[KS];
+    u32x4 qb[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-        u32x4 x = u32x4{0u, 0u, 0u, 0u};
-        if (n < w.heads_here) x = *reinterpret_cast<const u32x4*>(q_base + n * D + 32 * s + 8 * g);
-        qb[s] = __builtin_bit_cast(f16x8, x);
+        qb[s] = u32x4{0u, 0u, 0u, 0u};
+        if (n < w.heads_here) qb[s] = *reinterpret_cast<const u32x4*>(q_row + (n * D + 32 * s + 8 * g) * 2);
     }
 
     float m_head = kNoToken;  // running max (log2 units) of head n, equal in all lane groups
@@ -689,11 +774,11 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 #pragma unroll
     for (int j = 0; j < VH; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(w.kv_head) * D * 2;
-    const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(w.kv_head) * D * 2;
-    const char* park = reinterpret_cast<const char*>(q_base);
-    const uint32_t k_lane_bytes = static_cast<uint32_t>(g) * 16u;
-    const uint32_t v_lane_bytes = static_cast<uint32_t>(n) * VH * 2u;
+    const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(w.kv_head) * D * ES;
+    const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(w.kv_head) * D * ES;
+    const char* park = q_row;  // dead tiles read the wave's own q row: mapped, D * 2 bytes
+    const uint32_t k_lane_bytes = static_cast<uint32_t>(g) * 8u * ES;
+    const uint32_t v_lane_bytes = static_cast<uint32_t>(n) * VH * ES;
     const int k_row_token = k_token_of_row(n);
     int rb = w.wb, re = w.wb;
 
@@ -712,14 +797,13 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         const uint32_t koff =
             ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-            tl.k[s] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4*>(kp + koff + 64 * s));
+        for (int s = 0; s < KS; ++s) load_words<KW>(kp + koff + 32 * ES * s, tl.k[s]);
 #pragma unroll
         for (int e = 0; e < VI; ++e) {
             const int tv = min(max(t0 + 4 * e + g, lo), hi);
             const uint32_t voff =
                 ok ? static_cast<uint32_t>(tv & (page_size - 1)) * p.token_bytes + v_lane_bytes : v_lane_bytes;
-            tl.v[e] = *reinterpret_cast<const VL*>(vp + voff);
+            load_words<VW>(vp + voff, tl.v[e]);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -727,7 +811,11 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     auto consume = [&](const Tile& tl, int t0) {
         f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(tl.k[s], qb[s], sc, 0, 0, 0);
+        for (int s = 0; s < KS; ++s) {
+            uint32_t kq[4];
+            to_compute<QT, KVF, KW>(tl.k[s], kq);
+            sc = C::qk(u32x4{kq[0], kq[1], kq[2], kq[3]}, qb[s], sc);
+        }
         float x[4];
         float mx = -INFINITY;
 #pragma unroll
@@ -751,23 +839,31 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
                 for (int j = 0; j < VH; ++j) acc[j][i] *= a;
             }
         }
-        float wt[4];
+        uint16_t hi_bits[4], lo_bits[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            wt[e] = fast_exp2(fmaf(x[e], p.scale_log2, -m_head));
-            l_part += wt[e];
+            const float wt = fast_exp2(fmaf(x[e], p.scale_log2, -m_head));
+            l_part += wt;
+            float back, unused;
+            hi_bits[e] = C::round(wt, back);
+            lo_bits[e] = C::round(wt - back, unused);
         }
-        f16x4 p_hi, p_lo;
+        const u32x2 p_hi = {hi_bits[0] | (static_cast<uint32_t>(hi_bits[1]) << 16),
+                            hi_bits[2] | (static_cast<uint32_t>(hi_bits[3]) << 16)};
+        const u32x2 p_lo = {lo_bits[0] | (static_cast<uint32_t>(lo_bits[1]) << 16),
+                            lo_bits[2] | (static_cast<uint32_t>(lo_bits[3]) << 16)};
+        uint32_t vq[VI][VH / 2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const _Float16 h = static_cast<_Float16>(wt[e]);
-            p_hi[e] = h;
-            p_lo[e] = static_cast<_Float16>(wt[e] - static_cast<float>(h));
+        for (int e = 0; e < VI; ++e) {
+            uint32_t raw[VW];
+#pragma unroll
+            for (int i = 0; i < VW; ++i) raw[i] = (KVF == kKvNative || tl.live) ? tl.v[e][i] : 0u;  // FP8 park bytes may decode to NaN
+            to_compute<QT, KVF, VW>(raw, vq[e]);
         }
 #pragma unroll
-        for (int j = 0; j < VH; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(p_hi, v_operand<VH>(tl.v, j), acc[j], 0, 0, 0);
+        for (int j = 0; j < VH; ++j) acc[j] = C::pv(p_hi, v_operand<VH>(vq, j), acc[j]);
 #pragma unroll
-        for (int j = 0; j < VH; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(p_lo, v_operand<VH>(tl.v, j), acc[j], 0, 0, 0);
+        for (int j = 0; j < VH; ++j) acc[j] = C::pv(p_lo, v_operand<VH>(vq, j), acc[j]);
     };
 
     for (rb = w.wb; rb < w.we; rb = re) {
@@ -800,7 +896,8 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         if (h < w.heads_here) {
             f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + h) * parts + part) * D + n * VH);
 #pragma unroll
-            for (int j = 0; j < VH; j += 4) dst[j / 4] = f32x4{acc[j][i], acc[j + 1][i], acc[j + 2][i], acc[j + 3][i]};
+            for (int j = 0; j < VH; j += 4)
+                dst[j / 4] = f32x4{acc[j][i], acc[j + 1][i], acc[j + 2][i], acc[j + 3][i]} * p.v_scale;
         }
     }
     if (lane < w.heads_here) {
@@ -1142,12 +1239,30 @@ __global__ void __launch_bounds__(256) append_kv_advance_kernel(const AppendPara
 // ---------------------------------------------------------------------------
 // Host side.
 
-int check_common(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-                 const int32_t* lengths, const float* numerator, const float* stats, int batch,
-                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                 int physical_pages, int splits, int split_tokens) {
+size_t element_size(int dtype) {
+    switch (dtype) {
+        case PD_DTYPE_F32: return 4;
+        case PD_DTYPE_F16:
+        case PD_DTYPE_BF16: return 2;
+        default: return 1;  // FP8 formats
+    }
+}
+
+// (q dtype, K/V dtype) pairs the partition kernels implement.
+bool supported_formats(int q_dtype, int kv_dtype) {
+    if (q_dtype == PD_DTYPE_F32) return kv_dtype == PD_DTYPE_F32;
+    if (q_dtype == PD_DTYPE_F16 || q_dtype == PD_DTYPE_BF16)
+        return kv_dtype == q_dtype || kv_dtype == PD_DTYPE_FP8_E4M3 || kv_dtype == PD_DTYPE_FP8_E5M2;
+    return false;
+}
+
+int check_common(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
+                 const int32_t* table, const int32_t* lengths, const float* numerator, const float* stats, int batch,
+                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
+                 int splits, int split_tokens) {
     if (!q || !k || !v || !table || !lengths || !numerator || !stats) return PD_ERR_NULL_POINTER;
-    if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_F16) return PD_ERR_DTYPE;
+    if (!supported_formats(q_dtype, kv_dtype)) return PD_ERR_DTYPE;
+    if (!(k_scale > 0.0f && k_scale < INFINITY) || !(v_scale > 0.0f && v_scale < INFINITY)) return PD_ERR_DTYPE;
     if (batch < 1 || batch > 65535 || query_heads < 1 || query_heads > 65535) return PD_ERR_SHAPE;
     if (kv_heads < 1 || query_heads % kv_heads != 0) return PD_ERR_SHAPE;
     if (head_dim != 64 && head_dim != 128) return PD_ERR_SHAPE;
@@ -1205,52 +1320,90 @@ void choose_workgroup(PartialParams& prm, int kv_heads) {
     prm.quarters_per_wg = hw_tw <= 2 ? 4 : hw_tw <= 4 ? 2 : 1;
 }
 
-template <typename T, int D, int GT>
-int launch_partial(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    const int waves = prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
-    const dim3 grid(prm.splits * (kQuarters / prm.quarters_per_wg),
-                    (kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg), batch);
-    if constexpr (std::is_same_v<T, _Float16>) {
-        hipLaunchKernelGGL((partial_mfma_kernel<D, GT, PD_MFMA_PREFETCH, PD_MFMA_BLOCK>), grid, dim3(kWave * waves),
-                           0, stream, prm);
-    } else {
-        hipLaunchKernelGGL((partial_kernel<T, D, GT, PD_CHUNK_LOADS, PD_PREFETCH, PD_BLOCK_CHUNKS>), grid,
-                           dim3(kWave * waves), 0, stream, prm);
-    }
+dim3 partial_grid(const PartialParams& prm, int batch, int kv_heads) {
+    return dim3(prm.splits * (kQuarters / prm.quarters_per_wg),
+                (kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg), batch);
+}
+
+int partial_threads(const PartialParams& prm) {
+    return kWave * prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
+}
+
+template <typename QT, int KVF, int D, int GT>
+int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
+    hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, PD_MFMA_PREFETCH, PD_MFMA_BLOCK>),
+                       partial_grid(prm, batch, kv_heads), dim3(partial_threads(prm)), 0, stream, prm);
     return launch_status();
 }
 
-// Head tile: the GQA group padded to a power of two up to kMaxTile query heads
-// (16 for the FP16 kernel, whose MFMA column block holds 16 heads; 8 for the
-// FP32 kernel, whose accumulators grow with the tile); larger groups are cut
-// into tiles of kMaxTile.
+template <int D, int GT>
+int launch_fp32(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
+    hipLaunchKernelGGL((partial_kernel<float, D, GT, PD_CHUNK_LOADS, PD_PREFETCH, PD_BLOCK_CHUNKS>),
+                       partial_grid(prm, batch, kv_heads), dim3(partial_threads(prm)), 0, stream, prm);
+    return launch_status();
+}
+
+// Head tile: the GQA group padded to a power of two up to max_tile query
+// heads (16 for the matrix-core kernel, whose MFMA column block holds 16
+// heads; 8 for the FP32 kernel, whose accumulators grow with the tile);
+// larger groups are cut into tiles of max_tile.
 int head_tile(int group, int max_tile) {
     int gt = 1;
     while (gt < group && gt < max_tile) gt *= 2;
     return gt;
 }
 
-template <typename T, int D>
-int dispatch_group(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    constexpr bool kHalf = std::is_same_v<T, _Float16>;
-    const int gt = head_tile(prm.group, kHalf ? 16 : 8);
+void plan_tiles(PartialParams& prm, int kv_heads, int max_tile, int& gt) {
+    gt = head_tile(prm.group, max_tile);
     prm.head_tiles = (prm.group + gt - 1) / gt;
     choose_workgroup(prm, kv_heads);
+}
+
+template <typename QT, int KVF, int D>
+int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
+    int gt;
+    plan_tiles(prm, kv_heads, 16, gt);
     switch (gt) {
-        case 1: return launch_partial<T, D, 1>(prm, batch, kv_heads, stream);
-        case 2: return launch_partial<T, D, 2>(prm, batch, kv_heads, stream);
-        case 4: return launch_partial<T, D, 4>(prm, batch, kv_heads, stream);
-        case 8: return launch_partial<T, D, 8>(prm, batch, kv_heads, stream);
-        default:
-            if constexpr (kHalf) return launch_partial<T, D, 16>(prm, batch, kv_heads, stream);
-            return PD_ERR_SHAPE;
+        case 1: return launch_mfma<QT, KVF, D, 1>(prm, batch, kv_heads, stream);
+        case 2: return launch_mfma<QT, KVF, D, 2>(prm, batch, kv_heads, stream);
+        case 4: return launch_mfma<QT, KVF, D, 4>(prm, batch, kv_heads, stream);
+        case 8: return launch_mfma<QT, KVF, D, 8>(prm, batch, kv_heads, stream);
+        default: return launch_mfma<QT, KVF, D, 16>(prm, batch, kv_heads, stream);
     }
 }
 
-int run_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-                const int32_t* lengths, float* numerator, float* stats, int batch, int query_heads, int kv_heads, int head_dim, int page_size,
-                int table_width, int physical_pages, int splits, int split_tokens, hipStream_t stream) {
-    const size_t elem = dtype == PD_DTYPE_F16 ? 2 : 4;
+template <int D>
+int dispatch_fp32(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
+    int gt;
+    plan_tiles(prm, kv_heads, 8, gt);
+    switch (gt) {
+        case 1: return launch_fp32<D, 1>(prm, batch, kv_heads, stream);
+        case 2: return launch_fp32<D, 2>(prm, batch, kv_heads, stream);
+        case 4: return launch_fp32<D, 4>(prm, batch, kv_heads, stream);
+        default: return launch_fp32<D, 8>(prm, batch, kv_heads, stream);
+    }
+}
+
+template <typename QT, int D>
+int dispatch_kv(PartialParams& prm, int kv_dtype, int batch, int kv_heads, hipStream_t stream) {
+    switch (kv_dtype) {
+        case PD_DTYPE_FP8_E4M3: return dispatch_mfma<QT, kKvE4M3, D>(prm, batch, kv_heads, stream);
+        case PD_DTYPE_FP8_E5M2: return dispatch_mfma<QT, kKvE5M2, D>(prm, batch, kv_heads, stream);
+        default: return dispatch_mfma<QT, kKvNative, D>(prm, batch, kv_heads, stream);
+    }
+}
+
+template <int D>
+int dispatch_formats(PartialParams& prm, int q_dtype, int kv_dtype, int batch, int kv_heads, hipStream_t stream) {
+    if (q_dtype == PD_DTYPE_F32) return dispatch_fp32<D>(prm, batch, kv_heads, stream);
+    if (q_dtype == PD_DTYPE_BF16) return dispatch_kv<__bf16, D>(prm, kv_dtype, batch, kv_heads, stream);
+    return dispatch_kv<_Float16, D>(prm, kv_dtype, batch, kv_heads, stream);
+}
+
+int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
+                const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
+                int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
+                int splits, int split_tokens, hipStream_t stream) {
     PartialParams prm{};
     prm.q = q;
     prm.k = k;
@@ -1266,15 +1419,12 @@ int run_partial(const void* q, const void* k, const void* v, int dtype, const in
     prm.physical_pages = physical_pages;
     prm.splits = splits;
     prm.split_tokens = split_tokens;
-    prm.token_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * elem);
+    prm.token_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * element_size(kv_dtype));
     prm.page_bytes = static_cast<uint64_t>(page_size) * prm.token_bytes;
-    prm.scale_log2 = kLog2e / sqrtf(static_cast<float>(head_dim));
-    if (dtype == PD_DTYPE_F16) {
-        return head_dim == 64 ? dispatch_group<_Float16, 64>(prm, batch, kv_heads, stream)
-                              : dispatch_group<_Float16, 128>(prm, batch, kv_heads, stream);
-    }
-    return head_dim == 64 ? dispatch_group<float, 64>(prm, batch, kv_heads, stream)
-                          : dispatch_group<float, 128>(prm, batch, kv_heads, stream);
+    prm.scale_log2 = kLog2e * k_scale / sqrtf(static_cast<float>(head_dim));
+    prm.v_scale = v_scale;
+    return head_dim == 64 ? dispatch_formats<64>(prm, q_dtype, kv_dtype, batch, kv_heads, stream)
+                          : dispatch_formats<128>(prm, q_dtype, kv_dtype, batch, kv_heads, stream);
 }
 
 template <int D>
@@ -1332,7 +1482,7 @@ int check_append(const void* k_new, const void* v_new, int dtype, const int32_t*
                  const void* k_cache, const void* v_cache, int batch, int tokens, int kv_heads, int head_dim,
                  int page_size, int table_width, int physical_pages) {
     if (!k_new || !v_new || !table || !positions || !k_cache || !v_cache) return PD_ERR_NULL_POINTER;
-    if (dtype != PD_DTYPE_F32 && dtype != PD_DTYPE_F16) return PD_ERR_DTYPE;
+    if (dtype < PD_DTYPE_F32 || dtype > PD_DTYPE_FP8_E5M2) return PD_ERR_DTYPE;
     if (batch < 1 || batch > 65535 || tokens < 1 || tokens > 65535 || kv_heads < 1 || kv_heads > 65535)
         return PD_ERR_SHAPE;
     if (head_dim != 64 && head_dim != 128) return PD_ERR_SHAPE;
@@ -1354,7 +1504,7 @@ AppendParams append_params(const void* k_new, const void* v_new, int dtype, cons
     a.table_width = table_width;
     a.page_shift = page_size == 16 ? 4 : 5;
     a.physical_pages = physical_pages;
-    a.row_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * (dtype == PD_DTYPE_F16 ? 2 : 4));
+    a.row_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * element_size(dtype));
     return a;
 }
 
@@ -1362,17 +1512,26 @@ AppendParams append_params(const void* k_new, const void* v_new, int dtype, cons
 
 extern "C" {
 
-int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-                      const int32_t* lengths, float* numerator, float* stats, int batch,
-                      int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                      int physical_pages, int splits, int split_tokens, void* stream) {
-    const int status = check_common(q, k, v, dtype, table, lengths, numerator, stats, batch, query_heads,
-                                    kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                                    split_tokens);
+int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
+                         float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
+                         int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
+                         int physical_pages, int splits, int split_tokens, void* stream) {
+    const int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats,
+                                    batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
+                                    splits, split_tokens);
     if (status != PD_OK) return status;
-    return run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch,
-                       query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                       split_tokens, static_cast<hipStream_t>(stream));
+    return run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
+                       query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
+                       static_cast<hipStream_t>(stream));
+}
+
+int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
+                      const int32_t* lengths, float* numerator, float* stats, int batch, int query_heads,
+                      int kv_heads, int head_dim, int page_size, int table_width, int physical_pages, int splits,
+                      int split_tokens, void* stream) {
+    return pd_decode_partial_ex(q, dtype, k, v, dtype, 1.0f, 1.0f, table, lengths, numerator, stats, batch,
+                                query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                                split_tokens, stream);
 }
 
 int pd_decode_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
@@ -1385,24 +1544,33 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out, cons
                      split_tokens, merge_mode, static_cast<hipStream_t>(stream));
 }
 
-int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
-              const int32_t* lengths, float* numerator, float* stats, float* out, int batch,
-              int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-              int physical_pages, int splits, int split_tokens, int merge_mode, void* stream) {
-    int status = check_common(q, k, v, dtype, table, lengths, numerator, stats, batch, query_heads,
-                              kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
+                 float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
+                 float* out, int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
+                 int physical_pages, int splits, int split_tokens, int merge_mode, void* stream) {
+    int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
+                              query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                               split_tokens);
     if (status == PD_OK)
         status = check_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width,
                              splits, split_tokens, merge_mode);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    status = run_partial(q, k, v, dtype, table, lengths, numerator, stats, batch,
+    status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                          split_tokens, s);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
                      split_tokens, merge_mode, s);
+}
+
+int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
+              const int32_t* lengths, float* numerator, float* stats, float* out, int batch, int query_heads,
+              int kv_heads, int head_dim, int page_size, int table_width, int physical_pages, int splits,
+              int split_tokens, int merge_mode, void* stream) {
+    return pd_decode_ex(q, dtype, k, v, dtype, 1.0f, 1.0f, table, lengths, numerator, stats, out, batch,
+                        query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
+                        merge_mode, stream);
 }
 
 int pd_append_kv(const void* k_new, const void* v_new, int dtype, const int32_t* table, const int32_t* positions,
@@ -1441,7 +1609,7 @@ const char* pd_status_string(int status) {
         case PD_OK: return "success";
         case PD_ERR_NULL_POINTER: return "a required pointer is null";
         case PD_ERR_SHAPE: return "a dimension is outside the supported range";
-        case PD_ERR_DTYPE: return "unsupported dtype (float16 or float32 expected)";
+        case PD_ERR_DTYPE: return "unsupported dtype combination or non-positive/non-finite scale";
         case PD_ERR_SPLIT: return "invalid split configuration";
         case PD_ERR_MERGE: return "unknown merge mode or shared merge requires at most 4096 partial states (4 per split)";
         case PD_ERR_LAUNCH: return "kernel launch failed";
@@ -1449,6 +1617,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 6; }
+int pd_abi_version(void) { return 7; }
 
 }  // extern "C"

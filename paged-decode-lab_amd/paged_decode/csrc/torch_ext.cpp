@@ -1,7 +1,7 @@
 // Thin PyTorch-ROCm extension over the C ABI in include/paged_decode.h.
 //
 // Exposes `decode(q, k, v, table, lengths, numerator, stats, out, split_tokens,
-// merge_mode)` with the argument list of reference
+// merge_mode[, k_scale, v_scale])` with the argument list of reference
 // src/paged_decode/csrc/bindings.cpp:3-9, and repeats the tensor checks of
 // reference decode.cu:201-237 (as TORCH_CHECK -> RuntimeError), including
 // the reference's workspace layout: numerator [B, Hq, 4 * splits, D] and
@@ -28,8 +28,20 @@ hipStream_t current_stream(const torch::Tensor& like) {
     return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(like.get_device()).stream();
 }
 
-int dtype_code(const torch::Tensor& q) {
-    return q.scalar_type() == at::kHalf ? PD_DTYPE_F16 : PD_DTYPE_F32;
+// Storage format code of a tensor (-1 for anything the library does not store).
+int dtype_code(const torch::Tensor& t) {
+    switch (t.scalar_type()) {
+        case at::kFloat: return PD_DTYPE_F32;
+        case at::kHalf: return PD_DTYPE_F16;
+        case at::kBFloat16: return PD_DTYPE_BF16;
+        case at::kFloat8_e4m3fn: return PD_DTYPE_FP8_E4M3;
+        case at::kFloat8_e5m2: return PD_DTYPE_FP8_E5M2;
+        default: return -1;
+    }
+}
+
+bool is_fp8(const torch::Tensor& t) {
+    return t.scalar_type() == at::kFloat8_e4m3fn || t.scalar_type() == at::kFloat8_e5m2;
 }
 
 struct Shape {
@@ -54,9 +66,11 @@ Shape check_inputs(const torch::Tensor& q, const torch::Tensor& k, const torch::
     s.pages = k.size(0);
     s.page_size = k.size(1);
     s.kv_heads = k.size(2);
-    TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(), "q/k/v dtype mismatch");
-    TORCH_CHECK(q.scalar_type() == at::kHalf || q.scalar_type() == at::kFloat,
-                "supported input dtypes: float16,float32");
+    TORCH_CHECK(v.scalar_type() == k.scalar_type() &&
+                    (k.scalar_type() == q.scalar_type() || (is_fp8(k) && q.scalar_type() != at::kFloat)),
+                "q/k/v dtype mismatch");
+    TORCH_CHECK(q.scalar_type() == at::kHalf || q.scalar_type() == at::kFloat || q.scalar_type() == at::kBFloat16,
+                "supported input dtypes: float16,float32,bfloat16 (k/v may also be float8_e4m3fn/float8_e5m2)");
     TORCH_CHECK(table.dim() == 2 && table.size(0) == s.batch && table.size(1) > 0 && table.size(1) <= 65536 &&
                     lengths.dim() == 1 && lengths.size(0) == s.batch,
                 "metadata shape mismatch");
@@ -89,29 +103,31 @@ void check_output(const torch::Tensor& q, const torch::Tensor& out, int64_t merg
 
 void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
             torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t split_tokens,
-            int64_t merge_mode) {
+            int64_t merge_mode, double k_scale, double v_scale) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     check_output(q, out, merge_mode, s.splits);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    check_status(pd_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype_code(q), table.data_ptr<int32_t>(),
-                           lengths.data_ptr<int32_t>(), numerator.data_ptr<float>(), stats.data_ptr<float>(),
-                           out.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
-                           static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
-                           static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
-                           static_cast<int>(split_tokens), static_cast<int>(merge_mode), current_stream(q)));
+    check_status(pd_decode_ex(q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k),
+                              static_cast<float>(k_scale), static_cast<float>(v_scale), table.data_ptr<int32_t>(),
+                              lengths.data_ptr<int32_t>(), numerator.data_ptr<float>(), stats.data_ptr<float>(),
+                              out.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
+                              static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
+                              static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
+                              static_cast<int>(split_tokens), static_cast<int>(merge_mode), current_stream(q)));
 }
 
 // Partition stage alone (first launch of decode); used to time that kernel.
 void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
-             torch::Tensor numerator, torch::Tensor stats, int64_t split_tokens) {
+             torch::Tensor numerator, torch::Tensor stats, int64_t split_tokens, double k_scale, double v_scale) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    check_status(pd_decode_partial(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype_code(q), table.data_ptr<int32_t>(),
-        lengths.data_ptr<int32_t>(), numerator.data_ptr<float>(), stats.data_ptr<float>(),
-        static_cast<int>(s.batch), static_cast<int>(s.heads), static_cast<int>(s.kv_heads),
-        static_cast<int>(s.dim), static_cast<int>(s.page_size), static_cast<int>(s.width),
-        static_cast<int>(s.pages), static_cast<int>(s.splits), static_cast<int>(split_tokens), current_stream(q)));
+    check_status(pd_decode_partial_ex(
+        q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k), static_cast<float>(k_scale),
+        static_cast<float>(v_scale), table.data_ptr<int32_t>(), lengths.data_ptr<int32_t>(),
+        numerator.data_ptr<float>(), stats.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
+        static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
+        static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
+        static_cast<int>(split_tokens), current_stream(q)));
 }
 
 // Merge stage alone (second launch of decode); lengths, page_size,
@@ -156,8 +172,8 @@ void append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor table, to
     TORCH_CHECK(k_new.scalar_type() == k_cache.scalar_type() && v_new.scalar_type() == k_cache.scalar_type() &&
                     v_cache.scalar_type() == k_cache.scalar_type(),
                 "new tokens and cache must share one dtype");
-    TORCH_CHECK(k_cache.scalar_type() == at::kHalf || k_cache.scalar_type() == at::kFloat,
-                "supported cache dtypes: float16,float32");
+    TORCH_CHECK(dtype_code(k_cache) >= 0,
+                "supported cache dtypes: float32,float16,bfloat16,float8_e4m3fn,float8_e5m2");
     TORCH_CHECK(table.dim() == 2 && table.size(0) == k_new.size(0) && positions.dim() == 1 &&
                     positions.size(0) == k_new.size(0),
                 "metadata shape mismatch");
@@ -182,8 +198,12 @@ void append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor table, to
 
 PYBIND11_MODULE(_C, m) {
     m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
-    m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)");
-    m.def("partial", &partial, "Partition stage only");
+    m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
+          py::arg("table"), py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("out"),
+          py::arg("split_tokens"), py::arg("merge_mode"), py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0);
+    m.def("partial", &partial, "Partition stage only", py::arg("q"), py::arg("k"), py::arg("v"), py::arg("table"),
+          py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("split_tokens"),
+          py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0);
     m.def("merge", &merge, "Merge stage only");
     m.def("append_kv", &append_kv, "Paged KV-cache append");
     m.def("workspace_bytes", [](int64_t b, int64_t h, int64_t d, int64_t s) {

@@ -165,32 +165,40 @@ class DecodePlan:
         """Bytes of the partition-state workspace (numerator + stats)."""
         return sum(t.numel() * t.element_size() for t in (self._numerator, self._stats))
 
-    def _check(self, q, k, v):
+    def _check(self, q, k, v, k_scale, v_scale):
         layout = self.layout
         expected_q = (layout.batch, layout.query_heads, layout.head_dim)
         expected_k = (layout.physical_pages, layout.page_size, layout.kv_heads, layout.head_dim)
         if tuple(q.shape) != expected_q or tuple(k.shape) != expected_k or tuple(v.shape) != expected_k:
             raise ValueError("input shape does not match plan")
-        if q.dtype not in (torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
-            raise TypeError("q/k/v must share float16 or float32 dtype")
+        _check_formats(q.dtype, k.dtype, v.dtype)
+        for scale in (k_scale, v_scale):
+            if isinstance(scale, bool) or not isinstance(scale, (int, float)) or not 0 < scale < math.inf:
+                raise ValueError("k_scale and v_scale must be finite and positive")
         for tensor in (q, k, v):
             if tensor.device != self.device or not tensor.is_contiguous():
                 raise ValueError("inputs must be contiguous on the plan device")
             if tensor.requires_grad:
                 raise ValueError("inference only: detach tensors requiring gradients")
 
-    def run(self, q, k, v):
-        """Decode one token per sequence; returns the borrowed FP32 [B, Hq, D] output."""
-        self._check(q, k, v)
+    def run(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
+        """Decode one token per sequence; returns the borrowed FP32 [B, Hq, D] output.
+
+        q, k, v share float16, bfloat16 or float32; k and v may instead be
+        float8_e4m3fn or float8_e5m2 with a float16/bfloat16 q. The attention
+        runs over ``k_scale * k`` and ``v_scale * v`` (per-tensor scales of a
+        quantized cache; 1.0 for the reference's unscaled inputs).
+        """
+        self._check(q, k, v, k_scale, v_scale)
         self._extension.decode(q, k, v, self._table, self._lengths, self._numerator, self._stats,
-                               self._out, self.split_tokens, self._merge_mode)
+                               self._out, self.split_tokens, self._merge_mode, float(k_scale), float(v_scale))
         return self._out
 
-    def run_partial(self, q, k, v):
+    def run_partial(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
         """Partition stage only (fills the workspace); for stage timing."""
-        self._check(q, k, v)
+        self._check(q, k, v, k_scale, v_scale)
         self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
-                                self.split_tokens)
+                                self.split_tokens, float(k_scale), float(v_scale))
 
     def run_merge(self):
         """Merge stage only, from the current workspace; returns the borrowed output."""
@@ -210,12 +218,24 @@ def _token_batch(k_new, v_new, layout):
     return k_new, v_new
 
 
+_FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
+_STORED = (torch.float32, torch.float16, torch.bfloat16) + _FP8
+
+
+def _check_formats(q_dtype, k_dtype, v_dtype):
+    """q/k/v share float16, bfloat16 or float32, or k/v are FP8 under a 16-bit q."""
+    if q_dtype not in (torch.float16, torch.bfloat16, torch.float32) or v_dtype != k_dtype or not (
+            k_dtype == q_dtype or (k_dtype in _FP8 and q_dtype != torch.float32)):
+        raise TypeError("q/k/v must share float16, bfloat16 or float32 dtype "
+                        "(k/v may be float8_e4m3fn/float8_e5m2 with a float16 or bfloat16 q)")
+
+
 def _check_cache(k_cache, v_cache, k_new, v_new, expected_k, device):
     if tuple(k_cache.shape) != expected_k or tuple(v_cache.shape) != expected_k:
         raise ValueError("cache shape does not match the layout")
-    if k_cache.dtype not in (torch.float16, torch.float32) or any(
-            t.dtype != k_cache.dtype for t in (v_cache, k_new, v_new)):
-        raise TypeError("cache and new tokens must share float16 or float32 dtype")
+    if k_cache.dtype not in _STORED or any(t.dtype != k_cache.dtype for t in (v_cache, k_new, v_new)):
+        raise TypeError("cache and new tokens must share one storage dtype "
+                        "(float32, float16, bfloat16, float8_e4m3fn or float8_e5m2)")
     for tensor in (k_cache, v_cache, k_new, v_new):
         if tensor.device != device or not tensor.is_contiguous():
             raise ValueError("cache and new tokens must be contiguous on the plan device")

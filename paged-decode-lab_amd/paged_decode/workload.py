@@ -79,19 +79,73 @@ class Workload:
     description: str
     heavy_key_fraction: float = 0.0
     split_sweep: tuple = field(default_factory=tuple)
+    q_format: str = ""   # "bf16" for a bfloat16 q (and K/V unless kv_format says otherwise)
+    kv_format: str = ""  # "e4m3" / "e5m2": FP8 K/V with per-tensor scales
 
-    def host_tensors(self):
-        """``q, k, v`` NumPy arrays in the workload dtype."""
+    def _values(self):
         q, k, v = host_tensors(self.layout, dtype=np.float32, seed=self.seed)
         if self.heavy_key_fraction:
             # A seeded 5% of key entries scaled x20 stresses max correction.
             mask_rng = np.random.default_rng(self.seed + 1)
             k[mask_rng.random(k.shape) < self.heavy_key_fraction] *= 20.0
-        return q.astype(self.dtype), k.astype(self.dtype), v.astype(self.dtype)
+        return q, k, v
+
+    @property
+    def native(self):
+        """True when q/k/v are NumPy-representable (float16 or float32)."""
+        return not self.q_format and not self.kv_format
+
+    def host_tensors(self):
+        """``q, k, v`` as NumPy arrays holding exactly the values the device uses.
+
+        float16/float32 workloads return arrays in that dtype. BF16 workloads
+        return float32 arrays of the bfloat16 values; FP8 workloads return
+        float64 arrays of ``code * scale`` (exact), the values the attention
+        runs over.
+        """
+        if self.native:
+            q, k, v = self._values()
+            return q.astype(self.dtype), k.astype(self.dtype), v.astype(self.dtype)
+        q, k, v, k_scale, v_scale = self.tensors("cpu")
+        if self.kv_format:
+            return (q.float().numpy(), k.double().numpy() * k_scale, v.double().numpy() * v_scale)
+        return q.float().numpy(), k.float().numpy(), v.float().numpy()
+
+    def tensors(self, device):
+        """``(q, k, v, k_scale, v_scale)``: torch tensors in the storage formats on ``device``."""
+        import torch
+
+        q, k, v = self._values()
+        q_dtype = torch.bfloat16 if self.q_format == "bf16" else torch.from_numpy(np.zeros(0, self.dtype)).dtype
+        qt = torch.from_numpy(q).to(q_dtype)
+        if self.kv_format:
+            fp8 = torch.float8_e4m3fn if self.kv_format == "e4m3" else torch.float8_e5m2
+            largest = float(torch.finfo(fp8).max)
+            k_scale = float(np.abs(k).max()) / largest
+            v_scale = float(np.abs(v).max()) / largest
+            kt = (torch.from_numpy(k) / k_scale).to(fp8)
+            vt = (torch.from_numpy(v) / v_scale).to(fp8)
+        else:
+            k_scale = v_scale = 1.0
+            kt, vt = torch.from_numpy(k).to(q_dtype), torch.from_numpy(v).to(q_dtype)
+        return qt.to(device), kt.to(device), vt.to(device), k_scale, v_scale
 
     @property
     def element_size(self):
+        """Bytes per stored K/V element."""
+        if self.kv_format:
+            return 1
+        if self.q_format == "bf16":
+            return 2
         return np.dtype(self.dtype).itemsize
+
+    @property
+    def format_label(self):
+        if self.kv_format:
+            return f"fp8-{self.kv_format} K/V, {'bf16' if self.q_format == 'bf16' else 'f16'} q"
+        if self.q_format == "bf16":
+            return "bf16"
+        return "f16" if self.dtype == np.float16 else "f32"
 
 
 def _shuffled_table(rng, batch, width):
@@ -163,8 +217,18 @@ def make_workload(name, *, seed=None, split_tokens=None):
         return Workload(name, layout, table, lengths, split_tokens or 512, np.float16, seed,
                         "Long-context MHA FP16 B1 Hq32 Hkv32 D128 T16, context 32768",
                         split_sweep=(128, 256, 512, 1024))
+    if name in ("llama3_8b_b4_l4096_bf16", "llama3_8b_b4_l4096_fp8"):
+        base = make_workload("llama3_8b_b4_l4096", seed=seed, split_tokens=split_tokens)
+        base.name = name
+        if name.endswith("bf16"):
+            base.q_format = "bf16"
+            base.description = base.description.replace("FP16", "BF16")
+        else:
+            base.kv_format = "e4m3"
+            base.description = base.description.replace("FP16", "FP16 q, FP8 e4m3 K/V with per-tensor scales,")
+        return base
     raise ValueError(f"unknown workload {name!r}; choose from {WORKLOAD_NAMES}")
 
 
 WORKLOAD_NAMES = ("fp32_b2_ragged", "llama3_8b_b4_l4096", "ragged_shared_b16",
-                  "mqa_b128_l1024", "long_mha_b1_l32768")
+                  "mqa_b128_l1024", "long_mha_b1_l32768", "llama3_8b_b4_l4096_bf16", "llama3_8b_b4_l4096_fp8")

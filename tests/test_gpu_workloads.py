@@ -1,4 +1,4 @@
-"""GPU parity on the five named decode workloads and full-size properties.
+"""GPU parity on the named decode workloads and full-size properties.
 
 Every workload is compared with the FP64 oracle at its real size (the oracle
 finishes in seconds on these shapes). Size-independent properties add checks
@@ -30,15 +30,15 @@ def device_inputs(w):
 @pytest.mark.parametrize("name", WORKLOAD_NAMES)
 def test_named_workload_parity(name):
     w = make_workload(name)
-    q, k, v = device_inputs(w)
-    expected = dense_attention(*host(q, k, v), w.table, w.lengths)
+    q, k, v, k_scale, v_scale = w.tensors("cuda")
+    expected = dense_attention(*w.host_tensors(), w.table, w.lengths)
     splits = w.split_sweep or (w.split_tokens,)
     for split in splits:
         for merge in ("serial", "shared"):
             announce(f"workload {name} split={split} merge={merge}")
             plan = DecodePlan(w.layout, w.table, w.lengths, split_tokens=split, merge=merge)
-            actual = plan.run(q, k, v).cpu().numpy()
-            assert_parity(actual, expected, w.dtype)
+            actual = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).cpu().numpy()
+            assert_parity(actual, expected, w.dtype if w.native else torch.float16)
     empty = w.lengths == 0
     if empty.any():
         np.testing.assert_array_equal(actual[empty], 0.0)

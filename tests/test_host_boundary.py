@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 6
+    assert lib.pd_abi_version() == 7
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -117,7 +117,8 @@ def call_decode(lib, ptrs, **over):
 
 
 @pytest.mark.parametrize("over,status", [
-    (dict(dtype=2), cabi.PD_ERR_DTYPE),
+    (dict(dtype=7), cabi.PD_ERR_DTYPE),
+    (dict(dtype=cabi.PD_DTYPE_FP8_E4M3), cabi.PD_ERR_DTYPE),   # FP8 q is not a supported pair
     (dict(batch=0), cabi.PD_ERR_SHAPE),
     (dict(batch=65536), cabi.PD_ERR_SHAPE),
     (dict(query_heads=30), cabi.PD_ERR_SHAPE),
@@ -184,3 +185,22 @@ def test_append_entries_reject_invalid_arguments():
         for over in (dict(batch=0), dict(tokens=0), dict(head_dim=96), dict(page_size=8), dict(table_width=0),
                      dict(physical_pages=0)):
             assert call(fn, **over) == cabi.PD_ERR_SHAPE
+
+
+@pytest.mark.parametrize("q_dtype,kv_dtype,k_scale,v_scale", [
+    (cabi.PD_DTYPE_F32, cabi.PD_DTYPE_FP8_E4M3, 1.0, 1.0),   # FP8 K/V need a 16-bit q
+    (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_BF16, 1.0, 1.0),       # mixed 16-bit formats
+    (cabi.PD_DTYPE_BF16, cabi.PD_DTYPE_F32, 1.0, 1.0),
+    (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E5M2, 0.0, 1.0),   # scales must be > 0 and finite
+    (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E5M2, 1.0, float("nan")),
+    (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E4M3, float("inf"), 1.0),
+])
+def test_extended_entry_rejects_formats_and_scales(q_dtype, kv_dtype, k_scale, v_scale):
+    lib = cabi.load()
+    ptrs, _keep = fake(8)
+    status = lib.pd_decode_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3], ptrs[4],
+                              ptrs[5], ptrs[6], ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, None)
+    assert status == cabi.PD_ERR_DTYPE
+    status = lib.pd_decode_partial_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3],
+                                      ptrs[4], ptrs[5], ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, None)
+    assert status == cabi.PD_ERR_DTYPE
