@@ -92,7 +92,7 @@ def read_counter(directory, counter):
 
 
 def pick(per_kernel, needle):
-    names = [n for n in per_kernel if needle in n]
+    names = [n for n in per_kernel if needle in n and "merge" not in n]
     if len(names) != 1:
         raise SystemExit(f"expected one kernel matching {needle!r}, found {names}")
     values = per_kernel[names[0]]
@@ -111,7 +111,9 @@ def summarize(args):
     total = 0.0
     for counter, directory, key in (("FETCH_SIZE", args.fetch_dir, "read"), ("WRITE_SIZE", args.write_dir, "write")):
         per_kernel = read_counter(directory, counter)
-        name, values = pick(per_kernel, kernel + "<")
+        # rocprofv3 prints the symbol mangled when it cannot demangle the
+        # _Float16 / __bf16 template arguments: match the kernel's own name.
+        name, values = pick(per_kernel, kernel)
         _, copies = pick(per_kernel, "neg_kernel")
         copy_kib = sum(copies) / len(copies)
         scale = COPY_BYTES / (copy_kib * 1024.0)
