@@ -1,4 +1,5 @@
-// Split-K paged GQA decode attention for gfx950 (AMD Instinct MI355X).
+// Split-K paged GQA decode attention for gfx950 (AMD Instinct MI355X), and the
+// paged KV-cache append that feeds it.
 //
 // Implements the C ABI declared in include/paged_decode.h. pd_decode makes two
 // launches per call, both on the caller's stream:
@@ -7,18 +8,18 @@
 //     quarters, and each (quarter, KV head, head tile) is one wave's work: it
 //     reads that KV head's K and V rows of the quarter from HBM exactly once,
 //     uses them for every query head of the tile (the GQA group, padded to
-//     GT = 1/2/4/8 heads), and stores one (m, l, n[D]) state per query head in
-//     slot 4 * partition + quarter of the workspace. A workgroup gathers up to
-//     eight KV heads of the same tokens (their head slices of a token row are
-//     then read together) plus enough quarters to make eight waves. Waves
-//     never synchronise with each other.
-//       partial_mfma_kernel (FP16): 16-token tiles; q.K^T on the matrix
-//       cores (v_mfma_f32_16x16x32_f16, K rows as the A operand, the query
-//       heads as B), online softmax with one running max per head and lazy
-//       rescaling (accumulators are rescaled only when a tile's max exceeds
-//       the running max by 2^8), P.V as mixed-precision FMAs on the vector ALU
-//       with P in FP32, then a register reduce-scatter of the token rows
-//       (v_permlane32/16_swap, DPP) so each lane stores its own slice.
+//     GT = 1/2/4/8/16 heads), and stores one (m, l, n[D]) state per query head
+//     in slot 4 * partition + quarter of the workspace. A workgroup gathers up
+//     to eight KV heads of the same tokens (their head slices of a token row
+//     are then read together) plus enough quarters to make eight waves. Waves
+//     never synchronise with each other. Partitions that start at or past
+//     their sequence's end exit before any load and write nothing.
+//       partial_mfma_kernel (q in FP16 or BF16; K/V in the same type or in
+//       OCP FP8): 16-token tiles; q.K^T and P.V on the matrix cores, online
+//       softmax with one running max per head and lazy rescaling (the
+//       accumulators are rescaled only when a tile's max exceeds the running
+//       max by 2^8); each lane ends with its own slice of the state and
+//       stores it directly.
 //       partial_kernel (FP32): the same decomposition on the vector ALU;
 //       q.k is reduced over each token row's lanes with DPP, every token row
 //       keeps its own online-softmax stream, and the rows' streams are
@@ -27,12 +28,16 @@
 //     and indexed with v_readlane; loads stream through a short register
 //     pipeline in fully unrolled blocks. Scores are kept in log2 units
 //     (scale * log2 e) and exponentiated with v_exp_f32.
-//  2. merge_kernel<D, serial | shared weights>: max-corrected combination of
-//     the 4 * splits states of each (sequence, query head) row, with the row's
-//     state loads spread over a 256-lane workgroup. The serial variant has
-//     every wave recompute the maximum and the denominator; the shared variant
-//     forms each state's weight once in LDS and is bounded to
-//     PD_SHARED_MERGE_MAX_PARTS states.
+//  2. Merge: max-corrected combination of the live states of each (sequence,
+//     query head) row. merge_rows_kernel gives a row one wave when it has few
+//     states; merge_cols_kernel cuts a row's columns into 128-byte chunks, one
+//     256-lane workgroup each, so long rows are read by several workgroups at
+//     once. The serial variants have every wave recompute the maximum and the
+//     denominator; the shared variants form each state's weight once in LDS
+//     and are bounded to PD_SHARED_MERGE_MAX_PARTS states.
+//
+// append_kv_kernel / append_kv_advance_kernel copy new token rows into their
+// cache slots through the same page table.
 //
 // Semantics follow reference src/paged_decode/csrc/decode.cu:26-168 (online
 // softmax and merge algebra, empty rows -> 0, l > 0 merge guard, page-id guard)
@@ -171,40 +176,6 @@ __device__ __forceinline__ float sum_over_lane_groups(float x) {
     return swap16_sum(x, x);
 }
 
-constexpr int kDppRowRotate8 = 0x128;  // row_ror:8, lane l reads lane l ^ 8 of its 16-lane row
-
-// Sums v over the wave's R token rows (lanes [r * 64 / R, (r + 1) * 64 / R))
-// and scatters the result: the lanes of row r end with elements
-// [r * N / R, (r + 1) * N / R) of v, summed over all rows. Halving steps over
-// lane bits 5, 4 (swaps) and 3 (DPP), most significant first.
-template <int N, int R>
-__device__ __forceinline__ void row_reduce_scatter(const float (&v)[N], float (&out)[N / R], int lane) {
-    static_assert(R == 4 || R == 8, "four or eight token rows per wave");
-    float h1[N / 2];
-#pragma unroll
-    for (int i = 0; i < N / 2; ++i) h1[i] = swap32_sum(v[i], v[i + N / 2]);
-    float h2[N / 4];
-#pragma unroll
-    for (int i = 0; i < N / 4; ++i) h2[i] = swap16_sum(h1[i], h1[i + N / 4]);
-    if constexpr (R == 4) {
-#pragma unroll
-        for (int i = 0; i < N / 4; ++i) out[i] = h2[i];
-    } else {
-        const bool upper = (lane & 8) != 0;
-#pragma unroll
-        for (int i = 0; i < N / 8; ++i) {
-            const float mine = upper ? h2[i + N / 8] : h2[i];
-            const float send = upper ? h2[i] : h2[i + N / 8];
-            out[i] = mine + dpp_move<kDppRowRotate8>(send);
-        }
-    }
-}
-
-// Merge loops are branch-free and unrolled so the loads of kMergeUnroll states
-// are in flight together; a data-dependent branch per state would chain their
-// latencies.
-constexpr int kMergeUnroll = 8;
-
 // State j of a row, read as one 8-byte load. Callers clamp j into the row and
 // mask the result, so loads are unconditional and issue back to back.
 __device__ __forceinline__ float2 read_state(const float2* st, int j) {
@@ -212,32 +183,9 @@ __device__ __forceinline__ float2 read_state(const float2* st, int j) {
 }
 
 // ---------------------------------------------------------------------------
-// Element types. A lane moves 16 bytes per load: 8 halves or 4 floats.
+// Element types of the vector-ALU kernel. A lane moves 16 bytes per load: 4 floats.
 template <typename T>
 struct Elem;
-
-template <>
-struct Elem<_Float16> {
-    static constexpr int kPerLoad = 8;
-    // q.k over one 16-byte chunk with FP32 accumulation (v_dot2c_f32_f16).
-    static __device__ __forceinline__ float dot(const u32x4& a, const u32x4& b) {
-        const f16x8 ah = __builtin_bit_cast(f16x8, a);
-        const f16x8 bh = __builtin_bit_cast(f16x8, b);
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const f16x2 x = {ah[2 * i], ah[2 * i + 1]};
-            const f16x2 y = {bh[2 * i], bh[2 * i + 1]};
-            acc = __builtin_amdgcn_fdot2(x, y, acc, false);
-        }
-        return acc;
-    }
-    static __device__ __forceinline__ void widen(const u32x4& x, float (&f)[8]) {
-        const f16x8 h = __builtin_bit_cast(f16x8, x);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) f[i] = static_cast<float>(h[i]);
-    }
-};
 
 template <>
 struct Elem<float> {
@@ -381,38 +329,6 @@ __device__ __forceinline__ void store_wave_state(const PartialParams& p, const W
         *st = make_float2(l > 0.0f ? m : kNoToken, l);
     }
 }
-
-// Stores a wave's state when lane (row, col) holds elements
-// [row * CNT, (row + 1) * CNT) of column col's flattened (head, element) array;
-// m and l for head g are in lane g.
-template <int D, int GT, int EPL, int CNT>
-__device__ __forceinline__ void store_scattered_state(const PartialParams& p, const WaveWork& w, int lane, int row,
-                                                      int col, const float (&v)[CNT], float m, float l) {
-    const int parts = kQuarters * p.splits;
-    const int part = w.split * kQuarters + w.quarter;
-    constexpr int kStore = CNT < 4 ? CNT : 4;  // floats per store
-#pragma unroll
-    for (int i = 0; i < CNT; i += kStore) {
-        const int flat = row * CNT + i;
-        const int g = flat / EPL;
-        const int e = flat % EPL;
-        if (g < w.heads_here) {
-            float* dst = p.numerator + ((w.q_row + g) * parts + part) * D + col * EPL + e;
-            if constexpr (kStore == 4) {
-                *reinterpret_cast<f32x4*>(dst) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
-            } else if constexpr (kStore == 2) {
-                *reinterpret_cast<float2*>(dst) = make_float2(v[i], v[i + 1]);
-            } else {
-                *dst = v[i];
-            }
-        }
-    }
-    if (lane < w.heads_here) {
-        float2* st = reinterpret_cast<float2*>(p.stats) + (w.q_row + lane) * parts + part;
-        *st = make_float2(l > 0.0f ? m : kNoToken, l);
-    }
-}
-
 
 // ---------------------------------------------------------------------------
 // FP32 (and generic) partition kernel, VALU only.
@@ -907,21 +823,16 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 }
 
 // ---------------------------------------------------------------------------
-// Merge kernels: one workgroup per (sequence, query head) row, one lane per
-// output dimension. A state with l == 0 is the identity (decode.cu:94-107).
-
-// One 256-lane workgroup per row. Lane t owns the 16-byte column t % TPR of the
-// states j == t / TPR (mod PG), so a row's numerator loads are spread over the
-// whole workgroup and issued together (kMergeBatch per lane per round), while
-// the weights are formed; the PG column sums then meet in LDS.
+// Merge kernels: the max-corrected combination of a (sequence, query head)
+// row's live states. A state with l == 0 is the identity (decode.cu:94-107).
+// Two ways to form the weights, as the reference's two merges:
 //   serial: every wave scans all states itself for the max and the denominator
 //           (lanes share the scan, reduced with DPP), and each lane recomputes
-//           the weight of its own states; no weight storage.
+//           the weight of the states it accumulates; no weight storage.
 //   shared: the workgroup forms each state's weight once, into LDS
-//           (4 bytes per state, hence the 4096-state bound).
+//           (4 bytes per state, hence the PD_SHARED_MERGE_MAX_PARTS bound).
+
 constexpr int kMergeThreads = 256;
-constexpr int kMergeBatch = 8;
-constexpr int kStatsUnroll = 4;
 
 // States of row b that the partition kernel wrote: four per partition up to
 // the last one holding a token of the sequence (none for an empty sequence).
@@ -944,19 +855,35 @@ struct MergeParams {
     int capacity;            // table_width * page_size
 };
 
-template <int D, bool kSharedWeights>
-__global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams mp) {
-    constexpr int TPR = D / 4;               // lanes per state row
-    constexpr int PG = kMergeThreads / TPR;  // state groups
-    constexpr int NB = kMergeBatch;
+// merge_cols_kernel: a row's D columns are cut into 128-byte chunks and each
+// (row, chunk) is one 256-lane workgroup, so D / 32 workgroups read a row's
+// states together. Lane t owns the 16-byte column t % 8 of the chunk for the
+// states j == t / 8 (mod 32) and issues up to NB of those loads in one round
+// (NB = 8 or 32: 256 or 1024 states), together with the first round of the
+// statistics scan, which is kept in registers for the denominator. Longer rows
+// repeat both rounds. All loads use clamped indexes and are masked afterwards,
+// so they issue back to back.
+constexpr int kMergeChunk = 32;                                   // floats per column chunk
+constexpr int kMergeColLanes = kMergeChunk / 4;                   // lanes per state slice
+constexpr int kMergeColGroups = kMergeThreads / kMergeColLanes;  // state groups per workgroup
+constexpr int kMergeColBatchShort = 8;                            // numerator loads per lane per round
+constexpr int kMergeColBatchLong = 32;
+
+template <int D, bool kSharedWeights, int NB>
+__global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergeParams mp) {
+    constexpr int TPR = kMergeColLanes;
+    constexpr int PG = kMergeColGroups;
+    constexpr int SU = NB / 2;  // (m, l) loads per scanning lane per round: a serial wave scans NB * PG states
     constexpr int kWaves = kMergeThreads / kWave;
     constexpr int kScan = kSharedWeights ? kMergeThreads : kWave;  // lanes sharing the state scan
-    constexpr int kScanRound = kStatsUnroll * kScan;
-    extern __shared__ float weight[];        // [parts], shared variant only
+    constexpr int kScanRound = SU * kScan;
+    static_assert(D % kMergeChunk == 0, "whole chunks");
+    extern __shared__ float weight[];  // [parts], shared variant only
     __shared__ f32x4 column_sum[PG][TPR];
     __shared__ float scratch[2][kWaves];
     const int b = blockIdx.y;
-    const int64_t row = static_cast<int64_t>(b) * gridDim.x + blockIdx.x;  // b * Hq + h
+    const int64_t row = static_cast<int64_t>(b) * mp.query_heads + blockIdx.x;
+    const int chunk = blockIdx.z;
     const int parts = mp.parts;
     const int t = threadIdx.x;
     const int lane = t % kWave;
@@ -966,13 +893,9 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams 
     const int scan0 = kSharedWeights ? t : lane;
     const int last = parts - 1;
     const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D) + col;
-    // The live count arrives with the first loads, which are issued for the
-    // allocated row and masked afterwards, so it adds no round trip.
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D + chunk * kMergeChunk) + col;
     const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
 
-    // Rounds of PG states from `base` on, up to `limit` (uniform): loads past
-    // it are skipped as whole instructions.
     auto rounds_from = [&](int base, int limit) { return min(NB, (limit - base + PG - 1) / PG); };
     f32x4 buf[NB];
     float2 own[NB];
@@ -982,33 +905,38 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams 
         for (int k = 0; k < NB; ++k) {
             if (k < rounds) {
                 const int j = min(base + pg + k * PG, last);
-                buf[k] = num[static_cast<int64_t>(j) * TPR];
+                buf[k] = num[static_cast<int64_t>(j) * (D / 4)];
                 if constexpr (!kSharedWeights) own[k] = read_state(st, j);
             }
         }
     };
+    // The first round is issued for the allocated row before the live count
+    // arrives (it comes with these loads) and masked afterwards.
     load_batch(0, parts);
 
-    // Row maximum over live states (index < live and l > 0). The first scan
-    // round is issued at once and kept for the denominator pass.
-    float2 first[kStatsUnroll];
+    auto scan_round = [&](int base, int limit, float2 (&sv)[SU]) {
 #pragma unroll
-    for (int i = 0; i < kStatsUnroll; ++i) first[i] = read_state(st, min(scan0 + i * kScan, last));
-    float mx = kNoToken;
-#pragma unroll
-    for (int i = 0; i < kStatsUnroll; ++i) {
-        const bool ok = (scan0 + i * kScan < live) & (first[i].y > 0.0f);
-        mx = ok ? fmaxf(mx, first[i].x) : mx;
-    }
-    for (int base = kScanRound; base < live; base += kScanRound) {
-        float2 sv[kStatsUnroll];
-#pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i) sv[i] = read_state(st, min(base + scan0 + i * kScan, last));
-#pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i) {
-            const bool ok = (base + scan0 + i * kScan < live) & (sv[i].y > 0.0f);
-            mx = ok ? fmaxf(mx, sv[i].x) : mx;
+        for (int i = 0; i < SU; ++i) {
+            if (base + i * kScan < limit) sv[i] = read_state(st, min(base + scan0 + i * kScan, last));
         }
+    };
+    auto round_max = [&](const float2 (&sv)[SU], int base, int limit, float m) {
+#pragma unroll
+        for (int i = 0; i < SU; ++i) {
+            if (base + i * kScan < limit) {
+                const bool ok = (base + scan0 + i * kScan < live) & (sv[i].y > 0.0f);
+                m = ok ? fmaxf(m, sv[i].x) : m;
+            }
+        }
+        return m;
+    };
+    float2 first[SU];
+    scan_round(0, parts, first);
+    float mx = round_max(first, 0, parts, kNoToken);
+    for (int base = kScanRound; base < live; base += kScanRound) {
+        float2 sv[SU];
+        scan_round(base, live, sv);
+        mx = round_max(sv, base, live, mx);
     }
     mx = wave_max(mx);
     if constexpr (kSharedWeights) {
@@ -1019,26 +947,26 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams 
         for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, scratch[0][w]);
     }
 
-    // Denominator (and, shared variant, every live state's weight in LDS).
     float den = 0.0f;
-    auto accumulate_den = [&](const float2 (&sv)[kStatsUnroll], int base) {
+    auto accumulate_den = [&](const float2 (&sv)[SU], int base, int limit) {
 #pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i) {
-            const int j = base + scan0 + i * kScan;
-            const bool ok = (j < live) & (sv[i].y > 0.0f);
-            const float f = ok ? fast_exp2(sv[i].x - mx) : 0.0f;
-            if constexpr (kSharedWeights) {
-                if (j < live) weight[j] = f;
+        for (int i = 0; i < SU; ++i) {
+            if (base + i * kScan < limit) {
+                const int j = base + scan0 + i * kScan;
+                const bool ok = (j < live) & (sv[i].y > 0.0f);
+                const float f = ok ? fast_exp2(sv[i].x - mx) : 0.0f;
+                if constexpr (kSharedWeights) {
+                    if (j < live) weight[j] = f;
+                }
+                den = fmaf(f, ok ? sv[i].y : 0.0f, den);
             }
-            den = fmaf(f, ok ? sv[i].y : 0.0f, den);
         }
     };
-    accumulate_den(first, 0);
+    accumulate_den(first, 0, parts);
     for (int base = kScanRound; base < live; base += kScanRound) {
-        float2 sv[kStatsUnroll];
-#pragma unroll
-        for (int i = 0; i < kStatsUnroll; ++i) sv[i] = read_state(st, min(base + scan0 + i * kScan, last));
-        accumulate_den(sv, base);
+        float2 sv[SU];
+        scan_round(base, live, sv);
+        accumulate_den(sv, base, live);
     }
     den = wave_sum(den);
     if constexpr (kSharedWeights) {
@@ -1049,9 +977,6 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams 
         for (int w = 1; w < kWaves; ++w) den += scratch[1][w];
     }
 
-    // Weighted column sums; a state of weight 0 (empty partition, clamped
-    // duplicate, or past the live count) contributes nothing, whatever its
-    // numerator holds.
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int base = 0;;) {
         const int rounds = rounds_from(base, base == 0 ? parts : live);
@@ -1063,7 +988,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams 
                 if constexpr (kSharedWeights) {
                     f = j < live ? weight[j] : 0.0f;
                 } else {
-                    f = (j < live) & (own[k].y > 0.0f) ? fast_exp2(own[k].x - mx) : 0.0f;
+                    f = ((j < live) & (own[k].y > 0.0f)) ? fast_exp2(own[k].x - mx) : 0.0f;
                 }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[e] = f > 0.0f ? fmaf(f, buf[k][e], acc[e]) : acc[e];
@@ -1075,11 +1000,11 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const MergeParams 
     }
     column_sum[pg][col] = acc;
     __syncthreads();
-    if (t < D) {
+    if (t < kMergeChunk) {
         float sum = 0.0f;
 #pragma unroll
         for (int g = 0; g < PG; ++g) sum += reinterpret_cast<const float*>(column_sum[g])[t];
-        mp.out[row * D + t] = den > 0.0f ? sum / den : 0.0f;
+        mp.out[row * D + chunk * kMergeChunk + t] = den > 0.0f ? sum / den : 0.0f;
     }
 }
 
@@ -1439,11 +1364,18 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
         }
         return launch_status();
     }
-    const dim3 grid(mp.query_heads, batch);
-    if (shared) {
-        hipLaunchKernelGGL((merge_kernel<D, true>), grid, dim3(kMergeThreads), mp.parts * sizeof(float), stream, mp);
+    const dim3 grid(mp.query_heads, batch, D / kMergeChunk);
+    const dim3 block(kMergeThreads);
+    const size_t lds = shared ? mp.parts * sizeof(float) : 0;
+    const bool long_rows = mp.parts > kMergeColBatchShort * kMergeColGroups;
+    if (shared && long_rows) {
+        hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchLong>), grid, block, lds, stream, mp);
+    } else if (shared) {
+        hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchShort>), grid, block, lds, stream, mp);
+    } else if (long_rows) {
+        hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchLong>), grid, block, lds, stream, mp);
     } else {
-        hipLaunchKernelGGL((merge_kernel<D, false>), grid, dim3(kMergeThreads), 0, stream, mp);
+        hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchShort>), grid, block, lds, stream, mp);
     }
     return launch_status();
 }

@@ -168,6 +168,22 @@ def test_shared_merge_resource_bound_uses_explicit_fallback():
     assert_parity(plan.run(q, k, v).cpu().numpy(), oracle(q, k, v, table, lengths), torch.float32)
 
 
+@pytest.mark.parametrize("merge", ["serial", "shared"])
+@pytest.mark.parametrize("dim", [64, 128])
+def test_rows_of_thousands_of_states(dim, merge):
+    """Split 1 at ~1000 tokens: 4000 states per row, merged over several load rounds."""
+    announce(f"long rows dim={dim} merge={merge}")
+    layout = Layout(4, 4, 2, dim, 16, 4 * 63)
+    table = np.random.default_rng(9).permutation(4 * 63).reshape(4, 63).astype(np.int32)
+    lengths = np.array([1000, 3, 0, 777], dtype=np.int32)
+    q, k, v = make_tensors(layout, dtype=torch.float32)
+    plan = DecodePlan(layout, table, lengths, split_tokens=1, merge=merge)
+    assert plan.merge_implementation == merge
+    actual = plan.run(q, k, v).cpu().numpy()
+    assert_parity(actual, oracle(q, k, v, table, lengths), torch.float32)
+    np.testing.assert_array_equal(actual[2], 0.0)
+
+
 def test_rejects_same_shape_noncontiguous_and_wrong_device():
     layout = Layout(1, 8, 2, 64, 16, 8)
     plan = DecodePlan(layout, np.arange(8, dtype=np.int32)[None], np.array([127]))
