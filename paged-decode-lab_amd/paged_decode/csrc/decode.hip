@@ -248,10 +248,29 @@ struct PartialParams {
     float v_scale;         // multiplies every stored numerator
 };
 
-// Which KV head, head tile and token range a wave owns. Workgroup x covers
-// quarter group (blockIdx.x % (4 / qw)) of partition blockIdx.x / (4 / qw);
-// workgroup y covers KV heads [hg * hw, hg * hw + hw) and head tiles
-// [tg * tw, tg * tw + tw); the wave index splits into (head, tile, quarter).
+// Workgroup coordinates (token group, head group) in dispatch order: the
+// linear dispatch index blockIdx.x + gridDim.x * blockIdx.y is read with the
+// head group varying fastest, so consecutively dispatched (and co-resident)
+// workgroups cover all KV-head groups of the same tokens -- whole token rows
+// -- rather than one head group's slice of many rows.
+struct BlockCoords {
+    int tokens;  // quarter group (tokens % (4 / qw)) of partition tokens / (4 / qw)
+    int heads;   // KV heads [hg * hw, hg * hw + hw), head tiles [tg * tw, tg * tw + tw)
+};
+
+__device__ __forceinline__ BlockCoords block_coords() {
+    const uint32_t gx = gridDim.x, gy = gridDim.y;
+    if (gy == 1) return BlockCoords{static_cast<int>(blockIdx.x), 0};
+    const uint64_t lin = blockIdx.x + static_cast<uint64_t>(gx) * blockIdx.y;
+    if (static_cast<uint64_t>(gx) * gy <= 0xFFFFFFFFull) {
+        const uint32_t l32 = static_cast<uint32_t>(lin);
+        return BlockCoords{static_cast<int>(l32 / gy), static_cast<int>(l32 % gy)};
+    }
+    return BlockCoords{static_cast<int>(lin / gy), static_cast<int>(lin % gy)};
+}
+
+// Which KV head, head tile and token range a wave owns, from its workgroup's
+// coordinates; the wave index splits into (head, tile, quarter).
 struct WaveWork {
     int split, quarter, kv_head, tile, wb, we;
     int64_t q_row;   // first query-head row of the tile
@@ -260,7 +279,7 @@ struct WaveWork {
 };
 
 template <int GT, int ALIGN>
-__device__ __forceinline__ WaveWork wave_work(const PartialParams& p, int wave) {
+__device__ __forceinline__ WaveWork wave_work(const PartialParams& p, const BlockCoords& bc, int wave) {
     WaveWork w;
     const int qw = p.quarters_per_wg;
     const int groups = kQuarters / qw;
@@ -268,10 +287,10 @@ __device__ __forceinline__ WaveWork wave_work(const PartialParams& p, int wave) 
     const int tt = (wave / qw) % p.tiles_per_wg;
     const int hh = wave / (qw * p.tiles_per_wg);
     const int tile_groups = p.head_tiles / p.tiles_per_wg;
-    w.split = blockIdx.x / groups;
-    w.quarter = (blockIdx.x - w.split * groups) * qw + qq;
-    w.kv_head = (blockIdx.y / tile_groups) * p.heads_per_wg + hh;
-    w.tile = (blockIdx.y % tile_groups) * p.tiles_per_wg + tt;
+    w.split = bc.tokens / groups;
+    w.quarter = (bc.tokens - w.split * groups) * qw + qq;
+    w.kv_head = (bc.heads / tile_groups) * p.heads_per_wg + hh;
+    w.tile = (bc.heads % tile_groups) * p.tiles_per_wg + tt;
     const int b = blockIdx.z;
     const int capacity = p.table_width << p.page_shift;
     const int len = max(0, min(p.lengths[b], capacity));  // decode.cu:42-44
@@ -292,11 +311,11 @@ __device__ __forceinline__ WaveWork wave_work(const PartialParams& p, int wave) 
 // The first logical page a wave will read if its partition is full length:
 // lets the page-id window be requested before the sequence length arrives.
 template <int ALIGN>
-__device__ __forceinline__ int speculative_page(const PartialParams& p, int wave) {
+__device__ __forceinline__ int speculative_page(const PartialParams& p, const BlockCoords& bc, int wave) {
     const int qw = p.quarters_per_wg;
     const int groups = kQuarters / qw;
-    const int split = blockIdx.x / groups;
-    const int quarter = (blockIdx.x - split * groups) * qw + wave % qw;
+    const int split = bc.tokens / groups;
+    const int quarter = (bc.tokens - split * groups) * qw + wave % qw;
     const int per_full = ((p.split_tokens + kQuarters - 1) / kQuarters + ALIGN - 1) / ALIGN * ALIGN;
     const int capacity = p.table_width << p.page_shift;
     const int64_t start = static_cast<int64_t>(split) * p.split_tokens + static_cast<int64_t>(quarter) * per_full;
@@ -359,9 +378,10 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
     const int col = lane % LPT;
     const int page_size = 1 << p.page_shift;
     const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
-    int window = speculative_page<TPL>(p, wave);
+    const BlockCoords bc = block_coords();
+    int window = speculative_page<TPL>(p, bc, wave);
     int window_ids = pages[min(window + lane, p.table_width - 1)];
-    const WaveWork w = wave_work<GT, TPL>(p, wave);
+    const WaveWork w = wave_work<GT, TPL>(p, bc, wave);
     if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
     const T* q_base = static_cast<const T*>(p.q) + w.q_row * D;
 
@@ -671,9 +691,10 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     const int g = lane / 16;  // lane group: tokens g + 4 e
     const int page_size = 1 << p.page_shift;
     const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
-    int window = speculative_page<kTileTokens>(p, wave);
+    const BlockCoords bc = block_coords();
+    int window = speculative_page<kTileTokens>(p, bc, wave);
     int window_ids = pages[min(window + lane, p.table_width - 1)];
-    const WaveWork w = wave_work<GT, kTileTokens>(p, wave);
+    const WaveWork w = wave_work<GT, kTileTokens>(p, bc, wave);
     if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
     const char* q_row = static_cast<const char*>(p.q) + w.q_row * D * 2;
 
