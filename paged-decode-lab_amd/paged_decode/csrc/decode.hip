@@ -889,6 +889,7 @@ constexpr int kMergeColLanes = kMergeChunk / 4;                   // lanes per s
 constexpr int kMergeColGroups = kMergeThreads / kMergeColLanes;  // state groups per workgroup
 constexpr int kMergeColBatchShort = 8;                            // numerator loads per lane per round
 constexpr int kMergeColBatchLong = 32;
+constexpr int kOptimisticRounds = 2;  // first-round loads issued before the live count (64 states)
 
 template <int D, bool kSharedWeights, int NB>
 __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergeParams mp) {
@@ -915,25 +916,29 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int last = parts - 1;
     const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * parts;
     const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D + chunk * kMergeChunk) + col;
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
 
     auto rounds_from = [&](int base, int limit) { return min(NB, (limit - base + PG - 1) / PG); };
     f32x4 buf[NB];
     float2 own[NB];
-    auto load_batch = [&](int base, int limit) {
-        const int rounds = rounds_from(base, limit);
+    // Loads k0 <= k < k1 (uniform bounds) of the round starting at state base.
+    auto load_rounds = [&](int base, int k0, int k1) {
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
-            if (k < rounds) {
+            if (k >= k0 && k < k1) {
                 const int j = min(base + pg + k * PG, last);
                 buf[k] = num[static_cast<int64_t>(j) * (D / 4)];
                 if constexpr (!kSharedWeights) own[k] = read_state(st, j);
             }
         }
     };
-    // The first round is issued for the allocated row before the live count
-    // arrives (it comes with these loads) and masked afterwards.
-    load_batch(0, parts);
+    // The first kOptimisticRounds loads are issued for the allocated row
+    // before the live count arrives (it comes with them) and masked
+    // afterwards; the rest of the round covers live states only, so a ragged
+    // batch does not read the states past its sequences' ends.
+    const int optimistic = min(kOptimisticRounds, rounds_from(0, parts));
+    load_rounds(0, 0, optimistic);
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
+    load_rounds(0, optimistic, rounds_from(0, live));
 
     auto scan_round = [&](int base, int limit, float2 (&sv)[SU]) {
 #pragma unroll
@@ -1000,7 +1005,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
 
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int base = 0;;) {
-        const int rounds = rounds_from(base, base == 0 ? parts : live);
+        const int rounds = rounds_from(base, live);
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             if (k < rounds) {
@@ -1017,7 +1022,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
         }
         base += NB * PG;
         if (base >= live) break;
-        load_batch(base, live);
+        load_rounds(base, 0, rounds_from(base, live));
     }
     column_sum[pg][col] = acc;
     __syncthreads();
