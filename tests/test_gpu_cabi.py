@@ -1,0 +1,155 @@
+"""The C ABI's format, stage and append entries called directly through ctypes.
+
+Device pointers and plain integers only, the way an FFI caller binds
+``include/paged_decode.h``. Results are checked against the FP64 oracle
+(attention) and the oracle's scatter (append, bit for bit).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from gpu_util import announce, assert_parity, require_gpu
+
+require_gpu()
+
+import torch  # noqa: E402
+
+from oracle import fp64  # noqa: E402
+from paged_decode import cabi  # noqa: E402
+from paged_decode.layout import Layout  # noqa: E402
+from paged_decode.workload import host_tensors  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+KV_CODES = {torch.float8_e4m3fn: cabi.PD_DTYPE_FP8_E4M3, torch.float8_e5m2: cabi.PD_DTYPE_FP8_E5M2,
+            torch.float16: cabi.PD_DTYPE_F16, torch.bfloat16: cabi.PD_DTYPE_BF16}
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ragged_problem(layout, seed):
+    rng = np.random.default_rng(seed)
+    width = layout.physical_pages // layout.batch
+    table = rng.permutation(layout.physical_pages).reshape(layout.batch, width).astype(np.int32)
+    lengths = np.array([width * layout.page_size, 0, 37, width * layout.page_size - 5][:layout.batch], np.int32)
+    return table, lengths
+
+
+def quantize(layout, kv_dtype, seed):
+    """bf16 q and K/V in kv_dtype with per-tensor scales, plus the exact float64 values."""
+    q, k, v = host_tensors(layout, dtype=np.float32, seed=seed)
+    qt = torch.from_numpy(q).to(torch.bfloat16)
+    largest = float(torch.finfo(kv_dtype).max)
+    k_scale, v_scale = float(np.abs(k).max()) / largest, float(np.abs(v).max()) / largest
+    kt = (torch.from_numpy(k) / k_scale).to(kv_dtype)
+    vt = (torch.from_numpy(v) / v_scale).to(kv_dtype)
+    exact = (qt.double().numpy(), kt.double().numpy() * k_scale, vt.double().numpy() * v_scale)
+    return (qt.cuda(), kt.cuda(), vt.cuda()), (k_scale, v_scale), exact
+
+
+def workspace(layout, splits):
+    shape = (layout.batch, layout.query_heads, 4 * splits)
+    num = torch.full((*shape, layout.head_dim), float("nan"), device="cuda")
+    stats = torch.full((*shape, 2), float("nan"), device="cuda")
+    out = torch.full((layout.batch, layout.query_heads, layout.head_dim), float("nan"), device="cuda")
+    return num, stats, out
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("merge", [cabi.PD_MERGE_SERIAL, cabi.PD_MERGE_SHARED])
+def test_decode_ex_fp8_matches_oracle(kv_dtype, merge):
+    announce(f"pd_decode_ex bf16 q, {kv_dtype} K/V, merge={merge}")
+    lib = cabi.load()
+    layout = Layout(4, 16, 4, 128, 16, 4 * 12)
+    table, lengths = ragged_problem(layout, 3)
+    (q, k, v), (k_scale, v_scale), exact = quantize(layout, kv_dtype, 21)
+    split_tokens = 64
+    splits = -(-int(lengths.max()) // split_tokens)
+    num, stats, out = workspace(layout, splits)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    status = lib.pd_decode_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(), KV_CODES[kv_dtype],
+                              k_scale, v_scale, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
+                              stats.data_ptr(), out.data_ptr(), layout.batch, layout.query_heads, layout.kv_heads,
+                              layout.head_dim, layout.page_size, table.shape[1], layout.physical_pages, splits,
+                              split_tokens, merge, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    actual = out.cpu().numpy()
+    assert_parity(actual, fp64.dense_attention(*exact, table, lengths), torch.bfloat16)
+    np.testing.assert_array_equal(actual[1], 0.0)
+
+
+def test_partial_then_merge_entries_equal_decode_ex():
+    """pd_decode_partial_ex followed by pd_decode_merge gives pd_decode_ex's bits."""
+    announce("pd_decode_partial_ex + pd_decode_merge")
+    lib = cabi.load()
+    layout = Layout(4, 32, 8, 64, 32, 4 * 9)
+    table, lengths = ragged_problem(layout, 8)
+    (q, k, v), (k_scale, v_scale), _ = quantize(layout, torch.float8_e4m3fn, 5)
+    split_tokens = 48
+    splits = -(-int(lengths.max()) // split_tokens)
+    args = (layout.batch, layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size, table.shape[1],
+            layout.physical_pages, splits, split_tokens)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    num, stats, full = workspace(layout, splits)
+    status = lib.pd_decode_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_FP8_E4M3,
+                              k_scale, v_scale, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
+                              stats.data_ptr(), full.data_ptr(), *args, cabi.PD_MERGE_SERIAL, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    num2, stats2, staged = workspace(layout, splits)
+    status = lib.pd_decode_partial_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(),
+                                      cabi.PD_DTYPE_FP8_E4M3, k_scale, v_scale, d_table.data_ptr(),
+                                      d_lengths.data_ptr(), num2.data_ptr(), stats2.data_ptr(), *args, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    status = lib.pd_decode_merge(num2.data_ptr(), stats2.data_ptr(), staged.data_ptr(), d_lengths.data_ptr(),
+                                 layout.batch, layout.query_heads, layout.head_dim, layout.page_size, table.shape[1],
+                                 splits, split_tokens, cabi.PD_MERGE_SERIAL, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(staged, full, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float8_e5m2, torch.bfloat16])
+def test_append_entries_match_scatter(dtype):
+    """pd_append_kv (explicit positions) and pd_append_kv_advance, bit for bit."""
+    announce(f"pd_append_kv / pd_append_kv_advance {dtype}")
+    lib = cabi.load()
+    layout = Layout(3, 8, 2, 128, 16, 12)
+    table = np.arange(12, dtype=np.int32).reshape(3, 4)[:, ::-1].copy()
+    tokens = 2
+    rng = np.random.default_rng(4)
+    k_cache = torch.from_numpy(rng.standard_normal((12, 16, 2, 128)).astype(np.float32)).to(dtype).cuda()
+    v_cache = torch.from_numpy(rng.standard_normal((12, 16, 2, 128)).astype(np.float32)).to(dtype).cuda()
+    k_new = torch.from_numpy(rng.standard_normal((3, tokens, 2, 128)).astype(np.float32)).to(dtype).cuda()
+    v_new = torch.from_numpy(rng.standard_normal((3, tokens, 2, 128)).astype(np.float32)).to(dtype).cuda()
+    as_bytes = (lambda t: t.view(torch.uint8).cpu().numpy()) if dtype.itemsize == 1 else \
+        (lambda t: t.view(torch.int16).cpu().numpy())
+    d_table = torch.from_numpy(table).cuda()
+    dims = (3, tokens, 2, 128, 16, 4, 12)
+
+    positions = np.array([0, 17, 63], dtype=np.int32)  # the last sequence's second token is past the table
+    expected_k = fp64.scatter_tokens(as_bytes(k_cache), table, positions, as_bytes(k_new))
+    expected_v = fp64.scatter_tokens(as_bytes(v_cache), table, positions, as_bytes(v_new))
+    d_positions = torch.from_numpy(positions).cuda()
+    status = lib.pd_append_kv(k_new.data_ptr(), v_new.data_ptr(), KV_CODES[dtype], d_table.data_ptr(),
+                              d_positions.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *dims, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(as_bytes(k_cache), expected_k)
+    np.testing.assert_array_equal(as_bytes(v_cache), expected_v)
+
+    lengths = np.array([5, 62, 63], dtype=np.int32)  # the last sequence has no room for two tokens
+    expected_k, grown = fp64.append_advance(as_bytes(k_cache), table, lengths, as_bytes(k_new))
+    expected_v, _ = fp64.append_advance(as_bytes(v_cache), table, lengths, as_bytes(v_new))
+    d_lengths = torch.from_numpy(lengths).cuda()
+    status = lib.pd_append_kv_advance(k_new.data_ptr(), v_new.data_ptr(), KV_CODES[dtype], d_table.data_ptr(),
+                                      d_lengths.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *dims, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(as_bytes(k_cache), expected_k)
+    np.testing.assert_array_equal(as_bytes(v_cache), expected_v)
+    np.testing.assert_array_equal(d_lengths.cpu().numpy(), grown)
+    assert grown.tolist() == [7, 64, 63]
