@@ -89,6 +89,45 @@ def test_library_exports_every_declared_symbol():
     assert cabi.status_string(lib, 99) == "unknown status"
 
 
+C_CONSUMER = r"""
+#include <stdio.h>
+#include <string.h>
+#include "paged_decode.h"
+
+int main(void) {
+    if (pd_abi_version() != 7) return 1;
+    if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
+    /* Rejected before any launch: no device is touched. */
+    if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
+                  4, 32, 8, 128, 16, 256, 1024, 16, 256, PD_MERGE_SERIAL, NULL) != PD_ERR_NULL_POINTER) return 3;
+    if (pd_append_kv(NULL, NULL, PD_DTYPE_FP8_E4M3, NULL, NULL, NULL, NULL,
+                     4, 1, 8, 128, 16, 256, 1024, NULL) != PD_ERR_NULL_POINTER) return 4;
+    if (strstr(pd_status_string(PD_ERR_SHAPE), "dimension") == NULL) return 5;
+    puts("ok");
+    return 0;
+}
+"""
+
+
+def test_header_is_plain_c_and_library_links_from_c(tmp_path):
+    """A C99 FFI consumer: compiles against the header with gcc, links and runs (no GPU call)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    src = tmp_path / "consumer.c"
+    src.write_text(C_CONSUMER)
+    exe = tmp_path / "consumer"
+    libdir = cabi.LIBRARY.parent
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-pedantic", f"-I{HEADER.parent}", str(src),
+                    f"-L{libdir}", "-lpaged_decode_hip", f"-Wl,-rpath,{libdir}", "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0 and run.stdout.strip() == "ok", (run.returncode, run.stdout, run.stderr)
+
+
 def test_extension_exports_reference_entry():
     from paged_decode.runtime import load_extension
 
