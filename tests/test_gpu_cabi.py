@@ -153,3 +153,44 @@ def test_append_entries_match_scatter(dtype):
     np.testing.assert_array_equal(as_bytes(v_cache), expected_v)
     np.testing.assert_array_equal(d_lengths.cpu().numpy(), grown)
     assert grown.tolist() == [7, 64, 63]
+
+
+def test_context_sharded_over_two_partial_launches():
+    """The page-range sharding design on one GPU: two 'devices' each run the
+    partition stage on their half of every sequence's pages, their states are
+    concatenated (the all-gather), and one merge gives the unsharded result."""
+    announce("context sharded over two partial launches")
+    lib = cabi.load()
+    layout = Layout(2, 8, 2, 128, 16, 2 * 64)
+    rng = np.random.default_rng(12)
+    table = rng.permutation(layout.physical_pages).reshape(2, 64).astype(np.int32)
+    lengths = np.array([1024, 700], dtype=np.int32)
+    q, k, v = (torch.from_numpy(x).cuda() for x in host_tensors(layout, dtype=np.float16, seed=6))
+    split_tokens, half_pages = 128, 32
+    half_tokens = half_pages * layout.page_size            # a multiple of split_tokens
+    shard_splits = half_tokens // split_tokens
+    dims = (layout.batch, layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size)
+    states, stats = [], []
+    for shard in range(2):
+        sub_table = torch.from_numpy(np.ascontiguousarray(table[:, shard * half_pages:(shard + 1) * half_pages])).cuda()
+        sub_lengths = torch.from_numpy(np.clip(lengths - shard * half_tokens, 0, half_tokens).astype(np.int32)).cuda()
+        num, st, _ = workspace(layout, shard_splits)
+        status = lib.pd_decode_partial(q.data_ptr(), k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16,
+                                       sub_table.data_ptr(), sub_lengths.data_ptr(), num.data_ptr(), st.data_ptr(),
+                                       *dims, half_pages, layout.physical_pages, shard_splits, split_tokens, stream())
+        assert status == cabi.PD_OK, cabi.status_string(lib, status)
+        states.append(num)
+        stats.append(st)
+    # Shard 0 is full for every sequence, so the live states of the
+    # concatenation are a prefix: exactly what the merge reads.
+    num = torch.cat(states, dim=2).contiguous()
+    st = torch.cat(stats, dim=2).contiguous()
+    out = torch.full((layout.batch, layout.query_heads, layout.head_dim), float("nan"), device="cuda")
+    d_lengths = torch.from_numpy(lengths).cuda()
+    status = lib.pd_decode_merge(num.data_ptr(), st.data_ptr(), out.data_ptr(), d_lengths.data_ptr(),
+                                 layout.batch, layout.query_heads, layout.head_dim, layout.page_size, table.shape[1],
+                                 2 * shard_splits, split_tokens, cabi.PD_MERGE_SHARED, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    expected = fp64.dense_attention(*(t.cpu().numpy() for t in (q, k, v)), table, lengths)
+    assert_parity(out.cpu().numpy(), expected, torch.float16)
