@@ -7,9 +7,10 @@ reference signature (``workload.py:25-35``) but draws values with NumPy on the
 host and copies them to the device, so the same seed gives the same values on
 every device; the reference draws with a device-dependent torch generator.
 
-``make_workload`` builds the five named decode shapes this operator is measured
-and tested on (Llama-3-8B geometry, ragged/shared-prefix stress, large-batch
-MQA, long-context MHA and the small FP32 case).
+``make_workload`` builds the named decode shapes this operator is measured and
+tested on: Llama-3-8B geometry (FP16, BF16, FP8 K/V), ragged/shared-prefix
+stress, large-batch MQA, long-context MHA, the small FP32 case, and the
+reference's own benchmark shape at batch 1, 4 and 16.
 """
 from dataclasses import dataclass, field
 import math
@@ -227,8 +228,22 @@ def make_workload(name, *, seed=None, split_tokens=None):
             base.kv_format = "e4m3"
             base.description = base.description.replace("FP16", "FP16 q, FP8 e4m3 K/V with per-tensor scales,")
         return base
+    if name in _REFERENCE_BENCH:
+        # The reference's own benchmark shape (benchmarks/bench_competitive.py
+        # defaults: 32/8 heads, D128, context 4096, page 16, split 256, seed
+        # 123) at the batches its published results cover
+        # (results/2026-10-31-h100/SUMMARY.md:34-40): make_metadata's ragged
+        # lengths, e.g. [4096, 2311, 2289, 2568] at batch 4.
+        batch = _REFERENCE_BENCH[name]
+        layout, table, lengths = make_metadata(batch, 32, 8, 128, 4096, 16, seed=123)
+        return Workload(name, layout, table, lengths, split_tokens or 256, np.float16, 123 if seed is None else seed,
+                        f"Reference benchmark shape: FP16 B{batch} Hq32 Hkv8 D128 T16, make_metadata(seed=123) "
+                        "ragged lengths up to 4096")
     raise ValueError(f"unknown workload {name!r}; choose from {WORKLOAD_NAMES}")
 
 
+_REFERENCE_BENCH = {"reference_b1_l4096": 1, "reference_b4_l4096": 4, "reference_b16_l4096": 16}
+
 WORKLOAD_NAMES = ("fp32_b2_ragged", "llama3_8b_b4_l4096", "ragged_shared_b16",
-                  "mqa_b128_l1024", "long_mha_b1_l32768", "llama3_8b_b4_l4096_bf16", "llama3_8b_b4_l4096_fp8")
+                  "mqa_b128_l1024", "long_mha_b1_l32768", "llama3_8b_b4_l4096_bf16", "llama3_8b_b4_l4096_fp8",
+                  *_REFERENCE_BENCH)

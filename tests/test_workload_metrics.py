@@ -63,6 +63,18 @@ def test_named_workload_shapes():
     assert w.lengths.tolist() == [100, 256] and w.layout.physical_pages == 32
 
 
+def test_reference_benchmark_workloads_use_the_recorded_lengths(golden_dir):
+    """The reference's benchmark shape at B1/B4/B16 has the lengths its own reports recorded."""
+    cases = json.loads((golden_dir / "recorded_metadata.json").read_text())
+    recorded = {c["batch"]: c["lengths"] for c in cases
+                if c["context"] == 4096 and not c["uniform"] and c["heads"] == 32 and c["page_size"] == 16}
+    for batch in (1, 4, 16):
+        w = make_workload(f"reference_b{batch}_l4096")
+        assert w.lengths.tolist() == recorded[batch]
+        assert (w.layout.query_heads, w.layout.kv_heads, w.layout.head_dim, w.split_tokens) == (32, 8, 128, 256)
+    assert make_workload("reference_b4_l4096").lengths.tolist() == [4096, 2311, 2289, 2568]
+
+
 def test_percentiles_are_interpolated():
     assert percentile([1, 2, 3, 4, 5], .95) == pytest.approx(4.8)
     assert percentile([5], .95) == 5
