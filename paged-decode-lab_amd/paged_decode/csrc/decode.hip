@@ -566,6 +566,9 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 // cost nothing per element: k_scale is folded into the softmax scale and
 // v_scale into the stored numerator.
 constexpr int kTileTokens = 16;
+#ifndef PD_MFMA_K_ROWS
+#define PD_MFMA_K_ROWS 1  // 16-bit K loaded in whole-row pattern and transposed through LDS
+#endif
 
 enum KvFormat { kKvNative = 0, kKvE4M3 = 1, kKvE5M2 = 2 };
 
@@ -687,6 +690,15 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         uint32_t v[VI][VW];
         uint32_t live;
     };
+    // 16-bit K is loaded whole rows at a time (as V: KR lanes x 16 bytes per
+    // token, TK tokens per load) and turned into the q.K^T operand layout
+    // through a per-wave LDS tile whose rows are padded by 16 bytes, so the
+    // transposed 16-byte reads of 16 different rows fall in distinct banks.
+    constexpr bool kKRows = PD_MFMA_K_ROWS && KVF == kKvNative;
+    constexpr int KR = D * 2 / 16;
+    constexpr int TK = kWave / KR;
+    constexpr int kStageRow = D * 2 + 16;
+    __shared__ __attribute__((aligned(16))) char k_stage[kKRows ? 8 * kTileTokens * kStageRow : 16];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
@@ -733,11 +745,21 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         const uint64_t page_off = static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
         const char* kp = ok ? k_head + page_off : park;
         const char* vp = ok ? v_head + page_off : park;
-        const int tk = min(max(t0 + k_row_token, lo), hi);
-        const uint32_t koff =
-            ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
+        if constexpr (kKRows) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s) load_words<KW, kStream>(kp + koff + 32 * ES * s, tl.k[s]);
+            for (int s = 0; s < KS; ++s) {
+                const int tk = min(max(t0 + TK * s + lane / KR, lo), hi);
+                const uint32_t col = static_cast<uint32_t>(lane % KR) * 16u;
+                const uint32_t koff = ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + col : col;
+                load_words<KW, kStream>(kp + koff, tl.k[s]);
+            }
+        } else {
+            const int tk = min(max(t0 + k_row_token, lo), hi);
+            const uint32_t koff =
+                ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) load_words<KW, kStream>(kp + koff + 32 * ES * s, tl.k[s]);
+        }
 #pragma unroll
         for (int e = 0; e < VI; ++e) {
             const int tv = min(max(t0 + 4 * e + g, lo), hi);
@@ -750,11 +772,27 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 
     auto consume = [&](const Tile& tl, int t0) {
         f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (kKRows) {
+            char* stage = k_stage + wave * (kTileTokens * kStageRow);
+            __builtin_amdgcn_wave_barrier();  // the previous tile's reads are issued before these writes
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            uint32_t kq[4];
-            to_compute<QT, KVF, KW>(tl.k[s], kq);
-            sc = C::qk(u32x4{kq[0], kq[1], kq[2], kq[3]}, qb[s], sc);
+            for (int s = 0; s < KS; ++s) {
+                *reinterpret_cast<u32x4*>(stage + (TK * s + lane / KR) * kStageRow + (lane % KR) * 16) =
+                    u32x4{tl.k[s][0], tl.k[s][1], tl.k[s][2], tl.k[s][3]};
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const u32x4 kq = *reinterpret_cast<const u32x4*>(stage + k_row_token * kStageRow + 64 * s + 16 * g);
+                sc = C::qk(kq, qb[s], sc);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                uint32_t kq[4];
+                to_compute<QT, KVF, KW>(tl.k[s], kq);
+                sc = C::qk(u32x4{kq[0], kq[1], kq[2], kq[3]}, qb[s], sc);
+            }
         }
         float x[4];
         float mx = -INFINITY;
