@@ -546,7 +546,9 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 // A 16-token tile is scored with D/32 v_mfma_f32_16x16x32_{f16,bf16}: K in the
 // A layout (lane l holds 8 consecutive dims, [32 s + 8 (l / 16), +8) of k-step
 // s, of tile token sigma(l % 16)), q in the B layout (lane l: query head
-// l % 16, zero past the group). With sigma(r) = r / 4 + 4 (r % 4) the result
+// l % 16, zero past the group). 16-bit K is loaded as whole token rows (full
+// cache lines, like V) and reaches the A layout through a per-wave LDS tile;
+// FP8 K is loaded in the A layout directly. With sigma(r) = r / 4 + 4 (r % 4) the result
 // leaves lane l with head n = l % 16 and tokens g, g + 4, g + 8, g + 12 of the
 // tile (g = l / 16): exactly the A operand of v_mfma_f32_16x16x16_{f16,bf16}
 // for P (row = head, k = 4 g + e <-> token g + 4 e), so the weights never
