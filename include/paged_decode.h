@@ -173,6 +173,26 @@ int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype,
                          int table_width, int physical_pages, void* stream);
 
 /*
+ * Page table and lengths from CSR page-list metadata held on the device, the
+ * inverse of the CSR form reference src/paged_decode/competitors.py:8-18
+ * builds: for sequence b, n_b = indptr[b + 1] - indptr[b] page ids are taken
+ * from indices[indptr[b]] on (indices must hold indptr[batch] entries),
+ * table[b, n_b .. table_width) = -1, and lengths[b] = (n_b - 1) * page_size +
+ * last_page_len[b], or 0 for an empty list. table is [batch, table_width],
+ * lengths [batch], as pd_decode reads them. A sequence that does not fit
+ * (n_b < 0, n_b > table_width, last_page_len outside [1, page_size], or a
+ * length above max_context -- the context the caller's splits cover) is
+ * written as empty and sets *overflow to 1 if overflow is not NULL (it is
+ * never cleared: zero it before the call with a kernel, not a memset, if the
+ * call is captured). Page ids are not checked; the decode skips ids outside
+ * [0, physical_pages). Lets a caller keeping CSR metadata on the device
+ * refresh a plan without a host round trip, inside a captured graph.
+ */
+int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
+                      int32_t* table, int32_t* lengths, int32_t* overflow,
+                      int batch, int table_width, int page_size, int max_context, void* stream);
+
+/*
  * Bytes of numerator + stats for a plan: batch * query_heads * 4 * splits *
  * (head_dim + 2) * 4, the reference's DecodePlan.workspace_bytes
  * (src/paged_decode/runtime.py:71-73, docs/DESIGN.md:69-76). Returns 0 for
@@ -187,7 +207,7 @@ const char* pd_status_string(int status);
  * (3: four states per partition; 4: single-launch entry withdrawn;
  * 5: states past a sequence's end are neither written nor read, so
  * pd_decode_merge takes the lengths; 6: KV-cache append; 7: BF16 and FP8 K/V,
- * pd_decode_ex). */
+ * pd_decode_ex; 8: pd_table_from_csr). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

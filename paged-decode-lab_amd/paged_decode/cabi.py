@@ -36,6 +36,7 @@ PROTOTYPES = {
     "pd_decode_merge": (_I, [_P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_append_kv": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
     "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
+    "pd_table_from_csr": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 4 + [_P]),
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
     "pd_status_string": (ctypes.c_char_p, [_I]),
     "pd_abi_version": (_I, []),

@@ -1231,6 +1231,44 @@ __global__ void __launch_bounds__(256) append_kv_advance_kernel(const AppendPara
 }
 
 // ---------------------------------------------------------------------------
+// CSR page lists -> page table and lengths on the device: the inverse of the
+// CSR form reference src/paged_decode/competitors.py:8-18 builds from a table.
+// Row b takes the n_b = indptr[b + 1] - indptr[b] page ids from
+// indices[indptr[b]] on and -1 past them; lengths[b] = (n_b - 1) * page_size +
+// last_page_len[b], or 0 for an empty list. A row that does not fit (n_b < 0,
+// n_b > table_width, last_page_len outside [1, page_size], or a length above
+// max_context) is written empty and raises *overflow. Page ids are not
+// checked here: the partition kernel skips ids outside [0, physical_pages).
+struct CsrParams {
+    const int32_t* indptr;
+    const int32_t* indices;
+    const int32_t* last_page_len;
+    int32_t* table;
+    int32_t* lengths;
+    int32_t* overflow;  // may be null
+    int table_width;
+    int page_size;
+    int max_context;
+};
+
+__global__ void __launch_bounds__(256) table_from_csr_kernel(const CsrParams c) {
+    const int b = blockIdx.x;
+    const int64_t begin = c.indptr[b];
+    const int64_t n = static_cast<int64_t>(c.indptr[b + 1]) - begin;
+    const int last = n > 0 ? c.last_page_len[b] : 0;
+    const int64_t length = n > 0 ? (n - 1) * c.page_size + last : 0;
+    const bool fits = n >= 0 && n <= c.table_width && (n == 0 || (last >= 1 && last <= c.page_size)) &&
+                      length <= c.max_context;
+    const int64_t live = fits ? n : 0;
+    int32_t* row = c.table + static_cast<int64_t>(b) * c.table_width;
+    for (int i = threadIdx.x; i < c.table_width; i += blockDim.x) row[i] = i < live ? c.indices[begin + i] : -1;
+    if (threadIdx.x == 0) {
+        c.lengths[b] = fits ? static_cast<int32_t>(length) : 0;
+        if (!fits && c.overflow != nullptr) *c.overflow = 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 
 size_t element_size(int dtype) {
@@ -1612,6 +1650,18 @@ int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype, const 
     return launch_status();
 }
 
+int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len, int32_t* table,
+                      int32_t* lengths, int32_t* overflow, int batch, int table_width, int page_size,
+                      int max_context, void* stream) {
+    if (!indptr || !indices || !last_page_len || !table || !lengths) return PD_ERR_NULL_POINTER;
+    if (batch < 1 || batch > 65535 || table_width < 1 || table_width > 65536) return PD_ERR_SHAPE;
+    if (page_size != 16 && page_size != 32) return PD_ERR_SHAPE;
+    if (max_context < 0 || max_context > (1 << 20)) return PD_ERR_SHAPE;
+    CsrParams c{indptr, indices, last_page_len, table, lengths, overflow, table_width, page_size, max_context};
+    hipLaunchKernelGGL(table_from_csr_kernel, dim3(batch), dim3(256), 0, static_cast<hipStream_t>(stream), c);
+    return launch_status();
+}
+
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {
     if (batch <= 0 || query_heads <= 0 || head_dim <= 0 || splits <= 0) return 0;
     return static_cast<size_t>(batch) * query_heads * kQuarters * splits * (head_dim + 2) * sizeof(float);
@@ -1630,6 +1680,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 7; }
+int pd_abi_version(void) { return 8; }
 
 }  // extern "C"

@@ -196,6 +196,33 @@ void append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor table, to
     }
 }
 
+// CSR page lists (device tensors) -> the plan's page table and lengths.
+void table_from_csr(torch::Tensor indptr, torch::Tensor indices, torch::Tensor last_page_len, torch::Tensor table,
+                    torch::Tensor lengths, c10::optional<torch::Tensor> overflow, int64_t page_size,
+                    int64_t max_context) {
+    for (const auto& t : {indptr, indices, last_page_len, table, lengths}) {
+        TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.device() == table.device() && t.scalar_type() == at::kInt,
+                    "CSR metadata, table and lengths must be contiguous int32 tensors on one GPU");
+    }
+    TORCH_CHECK(table.dim() == 2 && lengths.dim() == 1 && lengths.size(0) == table.size(0) && indptr.dim() == 1 &&
+                    indptr.size(0) == table.size(0) + 1 && last_page_len.dim() == 1 &&
+                    last_page_len.size(0) == table.size(0) && indices.dim() == 1,
+                "expected indptr [B+1], indices [nnz], last_page_len [B], table [B,W], lengths [B]");
+    int32_t* flag = nullptr;
+    if (overflow.has_value()) {
+        const auto& o = *overflow;
+        TORCH_CHECK(o.is_cuda() && o.device() == table.device() && o.scalar_type() == at::kInt && o.numel() >= 1,
+                    "overflow must be an int32 GPU tensor");
+        flag = o.data_ptr<int32_t>();
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(table.device());
+    check_status(pd_table_from_csr(indptr.data_ptr<int32_t>(), indices.data_ptr<int32_t>(),
+                                   last_page_len.data_ptr<int32_t>(), table.data_ptr<int32_t>(),
+                                   lengths.data_ptr<int32_t>(), flag, static_cast<int>(table.size(0)),
+                                   static_cast<int>(table.size(1)), static_cast<int>(page_size),
+                                   static_cast<int>(max_context), current_stream(table)));
+}
+
 PYBIND11_MODULE(_C, m) {
     m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
@@ -206,6 +233,9 @@ PYBIND11_MODULE(_C, m) {
           py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0);
     m.def("merge", &merge, "Merge stage only");
     m.def("append_kv", &append_kv, "Paged KV-cache append");
+    m.def("table_from_csr", &table_from_csr, "CSR page lists to page table and lengths on the device",
+          py::arg("indptr"), py::arg("indices"), py::arg("last_page_len"), py::arg("table"), py::arg("lengths"),
+          py::arg("overflow") = py::none(), py::arg("page_size"), py::arg("max_context"));
     m.def("workspace_bytes", [](int64_t b, int64_t h, int64_t d, int64_t s) {
         return static_cast<int64_t>(pd_workspace_bytes(static_cast<int>(b), static_cast<int>(h),
                                                        static_cast<int>(d), static_cast<int>(s)));

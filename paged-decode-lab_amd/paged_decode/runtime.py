@@ -141,6 +141,31 @@ class DecodePlan:
         self._table_cpu, self._lengths_cpu = table, lengths
         self.max_context = longest
 
+    def refresh_csr(self, indptr, indices, last_page_len, overflow=None):
+        """Load CSR page-list metadata that lives on the device, without a host round trip.
+
+        ``indptr [B+1]``, ``indices [nnz]`` and ``last_page_len [B]`` are
+        contiguous int32 tensors on the plan device (the form
+        ``paged_decode.csr.paged_csr`` produces). They are converted on the
+        current stream into the plan's page table and lengths, so the call can
+        be captured in a graph together with ``run``. A sequence whose page
+        list is longer than the table or whose length exceeds the reserved
+        context is loaded as empty and sets ``overflow[0]`` to 1 when an int32
+        ``overflow`` tensor is given (it is never cleared; zero it first).
+        Page ids are not validated here; the kernel skips ids outside the
+        cache. ``max_context`` keeps the value of the last host-side metadata.
+        """
+        for t in (indptr, indices, last_page_len):
+            if t.device != self.device or t.dtype != torch.int32 or not t.is_contiguous():
+                raise TypeError("CSR metadata must be contiguous int32 tensors on the plan device")
+        if tuple(indptr.shape) != (self.layout.batch + 1,) or tuple(last_page_len.shape) != (self.layout.batch,) \
+                or indices.dim() != 1:
+            raise ValueError("expected indptr [B+1], indices [nnz], last_page_len [B]")
+        if overflow is not None and (overflow.device != self.device or overflow.dtype != torch.int32):
+            raise TypeError("overflow must be an int32 tensor on the plan device")
+        self._extension.table_from_csr(indptr, indices, last_page_len, self._table, self._lengths, overflow,
+                                       self.layout.page_size, self.context_capacity)
+
     def append(self, k_cache, v_cache, k_new, v_new):
         """Append new tokens at the plan's current lengths and advance them on the device.
 

@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 7
+    assert lib.pd_abi_version() == 8
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -95,7 +95,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != 7) return 1;
+    if (pd_abi_version() != 8) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
@@ -103,6 +103,7 @@ int main(void) {
     if (pd_append_kv(NULL, NULL, PD_DTYPE_FP8_E4M3, NULL, NULL, NULL, NULL,
                      4, 1, 8, 128, 16, 256, 1024, NULL) != PD_ERR_NULL_POINTER) return 4;
     if (strstr(pd_status_string(PD_ERR_SHAPE), "dimension") == NULL) return 5;
+    if (pd_table_from_csr(NULL, NULL, NULL, NULL, NULL, NULL, 4, 256, 16, 4096, NULL) != PD_ERR_NULL_POINTER) return 6;
     puts("ok");
     return 0;
 }
@@ -132,7 +133,7 @@ def test_extension_exports_reference_entry():
     from paged_decode.runtime import load_extension
 
     ext = load_extension()
-    for name in ("decode", "partial", "merge", "workspace_bytes", "abi_version"):
+    for name in ("decode", "partial", "merge", "append_kv", "table_from_csr", "workspace_bytes", "abi_version"):
         assert hasattr(ext, name)
     assert ext.workspace_bytes(4, 32, 128, 16) == 4_259_840
 
@@ -243,3 +244,21 @@ def test_extended_entry_rejects_formats_and_scales(q_dtype, kv_dtype, k_scale, v
     status = lib.pd_decode_partial_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3],
                                       ptrs[4], ptrs[5], ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, None)
     assert status == cabi.PD_ERR_DTYPE
+
+
+def test_table_from_csr_rejects_invalid_arguments():
+    """pd_table_from_csr: null pointers (overflow may be NULL) and dimensions, before any launch."""
+    lib = cabi.load()
+    ptrs, _keep = fake(6)
+
+    def call(indptr, indices, last, table, lengths, overflow, batch=4, width=256, page=16, max_context=4096):
+        return lib.pd_table_from_csr(indptr, indices, last, table, lengths, overflow, batch, width, page,
+                                     max_context, None)
+
+    for i in range(5):
+        broken = list(ptrs[:5])
+        broken[i] = None
+        assert call(*broken, ptrs[5]) == cabi.PD_ERR_NULL_POINTER
+    for over in (dict(batch=0), dict(batch=65536), dict(width=0), dict(width=65537), dict(page=8),
+                 dict(max_context=-1), dict(max_context=(1 << 20) + 1)):
+        assert call(*ptrs, **over) == cabi.PD_ERR_SHAPE, over
