@@ -6,4 +6,4 @@ compiles or loads native code; ``paged_decode.runtime.load_extension`` does
 that, once, at plan construction.
 """
 
-__version__ = "0.2.0+mi355x"
+__version__ = "0.3.0+mi355x"

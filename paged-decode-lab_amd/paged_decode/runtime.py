@@ -47,8 +47,10 @@ class DecodePlan:
     table/lengths are CPU integer arrays and are copied during construction.
     KV contents and q can change between runs. New metadata of the same shape
     whose longest sequence fits the reserved context (``max_context``, by
-    default the longest initial sequence) is loaded in place with ``refresh``;
-    anything else requires a new plan.
+    default the longest initial sequence) is loaded in place with ``refresh``
+    (host arrays) or ``refresh_csr`` (CSR page lists already on the device);
+    ``append`` writes new tokens into the cache and advances the lengths on the
+    device. Anything else requires a new plan.
     The output is borrowed storage, overwritten by the next run. A plan may be
     used on one stream at a time; use distinct plans for concurrent streams.
     Device metadata and workspace attributes are internal and must not be edited.
