@@ -546,9 +546,9 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 // A 16-token tile is scored with D/32 v_mfma_f32_16x16x32_{f16,bf16}: K in the
 // A layout (lane l holds 8 consecutive dims, [32 s + 8 (l / 16), +8) of k-step
 // s, of tile token sigma(l % 16)), q in the B layout (lane l: query head
-// l % 16, zero past the group). 16-bit K is loaded as whole token rows (full
-// cache lines, like V) and reaches the A layout through a per-wave LDS tile;
-// FP8 K is loaded in the A layout directly. With sigma(r) = r / 4 + 4 (r % 4) the result
+// l % 16, zero past the group). K is loaded as whole token rows (16 bytes per
+// lane, full cache lines, like V) and reaches the A layout through a per-wave
+// LDS tile. With sigma(r) = r / 4 + 4 (r % 4) the result
 // leaves lane l with head n = l % 16 and tokens g, g + 4, g + 8, g + 12 of the
 // tile (g = l / 16): exactly the A operand of v_mfma_f32_16x16x16_{f16,bf16}
 // for P (row = head, k = 4 g + e <-> token g + 4 e), so the weights never
@@ -569,7 +569,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 // v_scale into the stored numerator.
 constexpr int kTileTokens = 16;
 #ifndef PD_MFMA_K_ROWS
-#define PD_MFMA_K_ROWS 1  // 16-bit K loaded in whole-row pattern and transposed through LDS
+#define PD_MFMA_K_ROWS 1  // K loaded in whole-row pattern and transposed through LDS
 #endif
 
 enum KvFormat { kKvNative = 0, kKvE4M3 = 1, kKvE5M2 = 2 };
@@ -687,20 +687,24 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     constexpr int VW = VH * ES / 4;               // stored words per V load
     static_assert(GT <= 16, "one MFMA column block holds at most 16 query heads");
 
+    // K is loaded whole rows at a time (KR lanes x 16 bytes per token, TK
+    // tokens per load, KL loads per tile) and turned into the q.K^T operand
+    // layout through a per-wave LDS tile. Its rows are padded by the size of
+    // one operand read (16 bytes for 16-bit K, 8 for FP8), so the transposed
+    // reads of 16 different rows fall in distinct banks.
+    constexpr bool kKRows = PD_MFMA_K_ROWS;
+    constexpr int KR = D * ES / 16;
+    constexpr int TK = kWave / KR;
+    constexpr int KL = kTileTokens / TK;
+    constexpr int kStageRow = D * ES + 8 * ES;
+    static_assert(TK <= kTileTokens && kTileTokens % TK == 0, "whole row loads per tile");
+    __shared__ __attribute__((aligned(16))) char k_stage[kKRows ? 8 * kTileTokens * kStageRow : 16];
+
     struct Tile {
-        uint32_t k[KS][KW];
+        uint32_t k[kKRows ? KL : KS][kKRows ? 4 : KW];
         uint32_t v[VI][VW];
         uint32_t live;
     };
-    // 16-bit K is loaded whole rows at a time (as V: KR lanes x 16 bytes per
-    // token, TK tokens per load) and turned into the q.K^T operand layout
-    // through a per-wave LDS tile whose rows are padded by 16 bytes, so the
-    // transposed 16-byte reads of 16 different rows fall in distinct banks.
-    constexpr bool kKRows = PD_MFMA_K_ROWS && KVF == kKvNative;
-    constexpr int KR = D * 2 / 16;
-    constexpr int TK = kWave / KR;
-    constexpr int kStageRow = D * 2 + 16;
-    __shared__ __attribute__((aligned(16))) char k_stage[kKRows ? 8 * kTileTokens * kStageRow : 16];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
@@ -749,11 +753,11 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
         const char* vp = ok ? v_head + page_off : park;
         if constexpr (kKRows) {
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
+            for (int s = 0; s < KL; ++s) {
                 const int tk = min(max(t0 + TK * s + lane / KR, lo), hi);
                 const uint32_t col = static_cast<uint32_t>(lane % KR) * 16u;
                 const uint32_t koff = ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + col : col;
-                load_words<KW, kStream>(kp + koff, tl.k[s]);
+                load_words<4, kStream>(kp + koff, tl.k[s]);
             }
         } else {
             const int tk = min(max(t0 + k_row_token, lo), hi);
@@ -778,15 +782,28 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
             char* stage = k_stage + wave * (kTileTokens * kStageRow);
             __builtin_amdgcn_wave_barrier();  // the previous tile's reads are issued before these writes
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                *reinterpret_cast<u32x4*>(stage + (TK * s + lane / KR) * kStageRow + (lane % KR) * 16) =
-                    u32x4{tl.k[s][0], tl.k[s][1], tl.k[s][2], tl.k[s][3]};
+            for (int s = 0; s < KL; ++s) {
+                char* dst = stage + (TK * s + lane / KR) * kStageRow + (lane % KR) * 16;
+                if constexpr (kStageRow % 16 == 0) {
+                    *reinterpret_cast<u32x4*>(dst) = u32x4{tl.k[s][0], tl.k[s][1], tl.k[s][2], tl.k[s][3]};
+                } else {  // FP8 rows are 8-byte aligned
+                    reinterpret_cast<u32x2*>(dst)[0] = u32x2{tl.k[s][0], tl.k[s][1]};
+                    reinterpret_cast<u32x2*>(dst)[1] = u32x2{tl.k[s][2], tl.k[s][3]};
+                }
             }
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const u32x4 kq = *reinterpret_cast<const u32x4*>(stage + k_row_token * kStageRow + 64 * s + 16 * g);
-                sc = C::qk(kq, qb[s], sc);
+                const char* src = stage + k_row_token * kStageRow + (32 * s + 8 * g) * ES;
+                if constexpr (KVF == kKvNative) {
+                    sc = C::qk(*reinterpret_cast<const u32x4*>(src), qb[s], sc);
+                } else {
+                    const u32x2 raw2 = *reinterpret_cast<const u32x2*>(src);
+                    const uint32_t raw[2] = {raw2[0], raw2[1]};
+                    uint32_t kq[4];
+                    to_compute<QT, KVF, 2>(raw, kq);
+                    sc = C::qk(u32x4{kq[0], kq[1], kq[2], kq[3]}, qb[s], sc);
+                }
             }
         } else {
 #pragma unroll
