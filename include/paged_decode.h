@@ -19,6 +19,12 @@
  *   numerator [batch, query_heads, 4 * splits, head_dim]  float32
  *   stats     [batch, query_heads, 4 * splits, 2]         float32 (max, denominator)
  * (state 4 * split + quarter; the reference's workspace shape, decode.cu:223-231).
+ * Where one workgroup of the partition stage holds several quarters of a
+ * partition (few KV heads: 16-head GQA tiles with four quarters per
+ * workgroup, or two quarters per workgroup), those quarters are stored
+ * combined in the first one's state and the others hold the empty state
+ * (max -FLT_MAX, denominator 0), which every merge reads as an identity;
+ * pd_decode / pd_decode_ex then merge the combined states only.
  * Only partitions that hold at least one token of their sequence are written
  * (partitions 0 .. ceil(len_b / split_tokens) - 1 of row b, len_b clamped to
  * table_width * page_size) and only those are read by the merge, so the
@@ -130,8 +136,11 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype,
 /*
  * Merge stage only (the second launch of pd_decode): combines the live states
  * of each (sequence, query head) row -- 4 * ceil(len_b / split_tokens) of the
- * 4 * splits allocated -- into out. Replaces the merge_decode / merge_shared
- * launches of reference decode.cu:183-193. lengths, page_size, table_width and
+ * 4 * splits allocated, empty states included -- into out. Replaces the
+ * merge_decode / merge_shared launches of reference decode.cu:183-193. Where
+ * the partition stage combined quarters, pd_decode itself merges only the
+ * combined states, so the two can differ in the last bits (sums in another
+ * order). lengths, page_size, table_width and
  * split_tokens are the values the partition stage was called with.
  */
 int pd_decode_merge(const float* numerator, const float* stats, float* out,
@@ -207,7 +216,8 @@ const char* pd_status_string(int status);
  * (3: four states per partition; 4: single-launch entry withdrawn;
  * 5: states past a sequence's end are neither written nor read, so
  * pd_decode_merge takes the lengths; 6: KV-cache append; 7: BF16 and FP8 K/V,
- * pd_decode_ex; 8: pd_table_from_csr). */
+ * pd_decode_ex; 8: pd_table_from_csr; 9: quarters of one workgroup stored
+ * combined, the others as empty states). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

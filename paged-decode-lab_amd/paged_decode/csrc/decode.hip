@@ -246,6 +246,7 @@ struct PartialParams {
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
     float v_scale;         // multiplies every stored numerator
+    int combine;           // host only: the launch stores a workgroup's qw quarters as one state (kCombine)
 };
 
 // Workgroup coordinates (token group, head group) in dispatch order: the
@@ -676,7 +677,17 @@ __device__ __forceinline__ u32x2 v_operand(const uint32_t (&v)[4][VH / 2], int j
     return u32x2{(d0 >> 16) | (d1 & 0xFFFF0000u), (d2 >> 16) | (d3 & 0xFFFF0000u)};
 }
 
-template <typename QT, int KVF, int D, int GT, int PD, int NC, bool kStream>
+// LDS slot of the quarter combine: one quarter's state of one (KV head,
+// head tile) -- per-head max and denominator, and the accumulator in the
+// lanes' own layout (acc[j] of lane l at acc[j][l]).
+template <int VH>
+struct CombineSlot {
+    float m[16];
+    float l[16];
+    f32x4 acc[VH][kWave];
+};
+
+template <typename QT, int KVF, int D, int GT, int PD, int NC, bool kStream, bool kCombine>
 __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
     using C = Compute<QT>;
     constexpr int ES = KVF == kKvNative ? 2 : 1;  // stored bytes per K/V element
@@ -699,6 +710,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     constexpr int kStageRow = D * ES + 8 * ES;
     static_assert(TK <= kTileTokens && kTileTokens % TK == 0, "whole row loads per tile");
     __shared__ __attribute__((aligned(16))) char k_stage[kKRows ? 8 * kTileTokens * kStageRow : 16];
+    extern __shared__ __attribute__((aligned(16))) char combine_lds[];  // [waves / qw][qw - 1] CombineSlot<VH>
 
     struct Tile {
         uint32_t k[kKRows ? KL : KS][kKRows ? 4 : KW];
@@ -884,9 +896,54 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 
     // Lane (g, n) holds heads 4 g + i of dims n VH .. n VH + VH - 1; the
     // denominator of head n is summed over the four lane groups.
-    const float l_head = sum_over_lane_groups(l_part);
+    float l_head = sum_over_lane_groups(l_part);
     const int parts = kQuarters * p.splits;
     const int part = w.split * kQuarters + w.quarter;
+    if constexpr (kCombine) {
+        // The workgroup's qw quarters of one (KV head, head tile) -- waves
+        // wave - wave % qw onwards, all of one partition, so all live or all
+        // gone above -- become one state: quarters 1 .. qw - 1 leave theirs in
+        // LDS, and after one barrier the first quarter folds them into its own
+        // in quarter order (the merge's max-corrected sum) and stores the
+        // result. The other quarters' slots get the empty state (l = 0), which
+        // every merge of the four-states-per-partition layout reads as an
+        // identity.
+        const int qw = p.quarters_per_wg;
+        const int qq = wave % qw;
+        CombineSlot<VH>* slots = reinterpret_cast<CombineSlot<VH>*>(combine_lds) + wave / qw * (qw - 1);
+        if (qq != 0) {
+            CombineSlot<VH>* slot = slots + (qq - 1);
+            if (lane < 16) {
+                slot->m[n] = m_head;
+                slot->l[n] = l_head;
+            }
+#pragma unroll
+            for (int j = 0; j < VH; ++j) slot->acc[j][lane] = acc[j];
+            if (lane < w.heads_here)
+                reinterpret_cast<float2*>(p.stats)[(w.q_row + lane) * parts + part] = make_float2(kNoToken, 0.0f);
+        }
+        __syncthreads();
+        if (qq != 0) return;
+        for (int s = 0; s < qw - 1; ++s) {
+            const CombineSlot<VH>* slot = slots + s;
+            f32x4 in[VH];
+#pragma unroll
+            for (int j = 0; j < VH; ++j) in[j] = slot->acc[j][lane];
+            const float m_in = slot->m[n];
+            const float m_new = fmaxf(m_head, m_in);
+            const float f_in = fast_exp2(m_in - m_new);  // 0 for an empty state, 1 if both are empty
+            const float f_own = fast_exp2(m_head - m_new);
+            l_head = fmaf(f_in, slot->l[n], f_own * l_head);
+            m_head = m_new;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float a_in = __shfl(f_in, 4 * g + i);  // factors of head 4 g + i
+                const float a_own = __shfl(f_own, 4 * g + i);
+#pragma unroll
+                for (int j = 0; j < VH; ++j) acc[j][i] = fmaf(a_in, in[j][i], a_own * acc[j][i]);
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int h = 4 * g + i;
@@ -915,14 +972,14 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 
 constexpr int kMergeThreads = 256;
 
-// States of row b that the partition kernel wrote: four per partition up to
-// the last one holding a token of the sequence (none for an empty sequence).
-// Partitions past the end are never written and never read.
+// States of row b to merge: per_part per partition up to the last one
+// holding a token of the sequence (none for an empty sequence), capped at the
+// row's states. Partitions past the end are never written and never read.
 __device__ __forceinline__ int live_parts(const int32_t* lengths, int b, int split_tokens, int capacity,
-                                          int parts) {
+                                          int per_part, int states) {
     const int len = max(0, min(lengths[b], capacity));  // decode.cu:42-44
     const int64_t live = (static_cast<int64_t>(len) + split_tokens - 1) / split_tokens;
-    return static_cast<int>(min<int64_t>(kQuarters * live, parts));
+    return static_cast<int>(min<int64_t>(per_part * live, states));
 }
 
 struct MergeParams {
@@ -931,6 +988,7 @@ struct MergeParams {
     float* out;              // [B, Hq, D]
     const int32_t* lengths;  // [B]
     int parts;               // allocated states per row (4 * splits)
+    int stride_shift;        // read every (1 << stride_shift)-th state: 0, or log2 of the combined quarters
     int query_heads;
     int split_tokens;
     int capacity;            // table_width * page_size
@@ -966,7 +1024,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int b = blockIdx.y;
     const int64_t row = static_cast<int64_t>(b) * mp.query_heads + blockIdx.x;
     const int chunk = blockIdx.z;
-    const int parts = mp.parts;
+    const int shift = mp.stride_shift;
+    const int parts = mp.parts >> shift;  // states read: j <-> allocated state j << shift
     const int t = threadIdx.x;
     const int lane = t % kWave;
     const int wave = t / kWave;
@@ -974,8 +1033,9 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int pg = t / TPR;
     const int scan0 = kSharedWeights ? t : lane;
     const int last = parts - 1;
-    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D + chunk * kMergeChunk) + col;
+    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * mp.parts;
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D + chunk * kMergeChunk) + col;
+    const int64_t num_step = static_cast<int64_t>(D / 4) << shift;
 
     auto rounds_from = [&](int base, int limit) { return min(NB, (limit - base + PG - 1) / PG); };
     f32x4 buf[NB];
@@ -986,8 +1046,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
         for (int k = 0; k < NB; ++k) {
             if (k >= k0 && k < k1) {
                 const int j = min(base + pg + k * PG, last);
-                buf[k] = num[static_cast<int64_t>(j) * (D / 4)];
-                if constexpr (!kSharedWeights) own[k] = read_state(st, j);
+                buf[k] = num[j * num_step];
+                if constexpr (!kSharedWeights) own[k] = read_state(st, j << shift);
             }
         }
     };
@@ -997,13 +1057,13 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     // batch does not read the states past its sequences' ends.
     const int optimistic = min(kOptimisticRounds, rounds_from(0, parts));
     load_rounds(0, 0, optimistic);
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, kQuarters >> shift, parts);
     load_rounds(0, optimistic, rounds_from(0, live));
 
     auto scan_round = [&](int base, int limit, float2 (&sv)[SU]) {
 #pragma unroll
         for (int i = 0; i < SU; ++i) {
-            if (base + i * kScan < limit) sv[i] = read_state(st, min(base + scan0 + i * kScan, last));
+            if (base + i * kScan < limit) sv[i] = read_state(st, min(base + scan0 + i * kScan, last) << shift);
         }
     };
     auto round_max = [&](const float2 (&sv)[SU], int base, int limit, float m) {
@@ -1104,6 +1164,9 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
 // fit in kMergeWaveBatch loads per lane (at most 64 states); all loads are
 // issued at once and masked with the live count.
 constexpr int kMergeWaveBatch = 8;
+#ifndef PD_MERGE_ROWS_MIN
+#define PD_MERGE_ROWS_MIN 256  // rows (sequences x query heads) from which merge_rows takes rows of > 2 rounds
+#endif
 constexpr int kMergeRowsPerGroup = 4;
 
 template <int D>
@@ -1121,14 +1184,15 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
     if (h >= mp.query_heads) return;  // whole wave; nothing below synchronises across waves
     const int b = blockIdx.y;
     const int64_t row = static_cast<int64_t>(b) * mp.query_heads + h;
-    const int parts = mp.parts;
+    const int shift = mp.stride_shift;
+    const int parts = mp.parts >> shift;  // states read: j <-> allocated state j << shift
     const int col = lane % TPR;
     const int pg = lane / TPR;
     const int last = parts - 1;
-    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * parts * D) + col;
+    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * mp.parts;
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D) + col;
     const int rounds = (parts + PGW - 1) / PGW;  // uniform, <= NB
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, parts);
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, kQuarters >> shift, parts);
 
     f32x4 buf[NB];
     float2 own[NB];
@@ -1136,11 +1200,11 @@ __global__ void __launch_bounds__(kWave * kMergeRowsPerGroup) merge_rows_kernel(
     for (int k = 0; k < NB; ++k) {
         if (k < rounds) {
             const int j = min(pg + k * PGW, last);
-            buf[k] = num[static_cast<int64_t>(j) * TPR];
-            if constexpr (!kSharedWeights) own[k] = read_state(st, j);
+            buf[k] = num[(static_cast<int64_t>(j) << shift) * TPR];
+            if constexpr (!kSharedWeights) own[k] = read_state(st, j << shift);
         }
     }
-    const float2 mine = read_state(st, min(lane, last));
+    const float2 mine = read_state(st, min(lane, last) << shift);
     const bool ok = (lane < live) & (mine.y > 0.0f);
     const float mx = wave_max(ok ? mine.x : kNoToken);
     const float f = ok ? fast_exp2(mine.x - mx) : 0.0f;  // weight of state `lane`
@@ -1387,12 +1451,23 @@ template <typename QT, int KVF, int D, int GT>
 int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const dim3 grid = partial_grid(prm, batch, kv_heads);
     const dim3 block(partial_threads(prm));
-    if (KVF == kKvNative && prm.heads_per_wg < kv_heads) {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, PD_MFMA_PREFETCH, PD_MFMA_BLOCK, KVF == kKvNative>),
-                           grid, block, 0, stream, prm);
+    const size_t lds = prm.combine ? static_cast<size_t>(block.x / kWave / prm.quarters_per_wg) *
+                                         (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
+                                   : 0;
+    const bool stream_loads = KVF == kKvNative && prm.heads_per_wg < kv_heads;
+    constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
+    if (stream_loads && prm.combine) {
+        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, KVF == kKvNative, true>), grid, block, lds,
+                           stream, prm);
+    } else if (stream_loads) {
+        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, KVF == kKvNative, false>), grid, block, 0,
+                           stream, prm);
+    } else if (prm.combine) {
+        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, false, true>), grid, block, lds, stream,
+                           prm);
     } else {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, PD_MFMA_PREFETCH, PD_MFMA_BLOCK, false>), grid, block,
-                           0, stream, prm);
+        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, false, false>), grid, block, 0, stream,
+                           prm);
     }
     return launch_status();
 }
@@ -1424,6 +1499,13 @@ template <typename QT, int KVF, int D>
 int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     int gt;
     plan_tiles(prm, kv_heads, 16, gt);
+    // Combining a workgroup's quarters into one state cuts the state stores
+    // (written back at the kernel's end) and the merge's reads by qw; its
+    // fold runs after the slowest quarter. Measured on MI355X it pays for two
+    // quarters, and for four when the head tile is full (16 query heads:
+    // MQA-like groups, the largest states per KV byte); four quarters of
+    // smaller tiles were 0.3-0.7 us slower per call.
+    prm.combine = prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16);
     switch (gt) {
         case 1: return launch_mfma<QT, KVF, D, 1>(prm, batch, kv_heads, stream);
         case 2: return launch_mfma<QT, KVF, D, 2>(prm, batch, kv_heads, stream);
@@ -1464,7 +1546,7 @@ int dispatch_formats(PartialParams& prm, int q_dtype, int kv_dtype, int batch, i
 int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
                 const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
-                int splits, int split_tokens, hipStream_t stream) {
+                int splits, int split_tokens, hipStream_t stream, int* state_stride = nullptr) {
     PartialParams prm{};
     prm.q = q;
     prm.k = k;
@@ -1484,14 +1566,22 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     prm.page_bytes = static_cast<uint64_t>(page_size) * prm.token_bytes;
     prm.scale_log2 = kLog2e * k_scale / sqrtf(static_cast<float>(head_dim));
     prm.v_scale = v_scale;
-    return head_dim == 64 ? dispatch_formats<64>(prm, q_dtype, kv_dtype, batch, kv_heads, stream)
-                          : dispatch_formats<128>(prm, q_dtype, kv_dtype, batch, kv_heads, stream);
+    const int status = head_dim == 64 ? dispatch_formats<64>(prm, q_dtype, kv_dtype, batch, kv_heads, stream)
+                                      : dispatch_formats<128>(prm, q_dtype, kv_dtype, batch, kv_heads, stream);
+    if (state_stride) *state_stride = prm.combine ? prm.quarters_per_wg : 1;
+    return status;
 }
 
 template <int D>
 int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t stream) {
     const bool shared = merge_mode == PD_MERGE_SHARED;
-    if (mp.parts <= merge_wave_max_parts<D>()) {
+    const int states = mp.parts >> mp.stride_shift;
+    // merge_rows keeps a row in one wave, loading (states / PGW) 16-byte
+    // columns per lane; with few rows of many states, merge_cols (D / 32
+    // workgroups per row) finishes sooner.
+    const int rounds = (states + kWave / (D / 4) - 1) / (kWave / (D / 4));
+    const bool many_rows = static_cast<int64_t>(batch) * mp.query_heads >= PD_MERGE_ROWS_MIN;
+    if (states <= merge_wave_max_parts<D>() && (many_rows || rounds <= 2)) {
         const dim3 grid((mp.query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
         if (shared) {
             hipLaunchKernelGGL((merge_rows_kernel<D, true>), grid, dim3(kWave * kMergeRowsPerGroup), 0, stream, mp);
@@ -1502,8 +1592,8 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
     }
     const dim3 grid(mp.query_heads, batch, D / kMergeChunk);
     const dim3 block(kMergeThreads);
-    const size_t lds = shared ? mp.parts * sizeof(float) : 0;
-    const bool long_rows = mp.parts > kMergeColBatchShort * kMergeColGroups;
+    const size_t lds = shared ? states * sizeof(float) : 0;
+    const bool long_rows = states > kMergeColBatchShort * kMergeColGroups;
     if (shared && long_rows) {
         hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchLong>), grid, block, lds, stream, mp);
     } else if (shared) {
@@ -1532,13 +1622,14 @@ int check_merge(const float* numerator, const float* stats, const float* out, co
 
 int run_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
               int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
-              int merge_mode, hipStream_t stream) {
+              int merge_mode, int stride, hipStream_t stream) {
     MergeParams mp{};
     mp.numerator = numerator;
     mp.stats = stats;
     mp.out = out;
     mp.lengths = lengths;
     mp.parts = kQuarters * splits;
+    mp.stride_shift = stride == 4 ? 2 : stride == 2 ? 1 : 0;
     mp.query_heads = query_heads;
     mp.split_tokens = split_tokens;
     mp.capacity = table_width * page_size;
@@ -1609,7 +1700,7 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out, cons
                                    table_width, splits, split_tokens, merge_mode);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
-                     split_tokens, merge_mode, static_cast<hipStream_t>(stream));
+                     split_tokens, merge_mode, 1, static_cast<hipStream_t>(stream));
 }
 
 int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
@@ -1624,12 +1715,13 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
                              splits, split_tokens, merge_mode);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    int stride = 1;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                         split_tokens, s);
+                         split_tokens, s, &stride);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
-                     split_tokens, merge_mode, s);
+                     split_tokens, merge_mode, stride, s);
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -1697,6 +1789,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 8; }
+int pd_abi_version(void) { return 9; }
 
 }  // extern "C"

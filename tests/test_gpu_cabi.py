@@ -194,3 +194,56 @@ def test_context_sharded_over_two_partial_launches():
     torch.cuda.synchronize()
     expected = fp64.dense_attention(*(t.cpu().numpy() for t in (q, k, v)), table, lengths)
     assert_parity(out.cpu().numpy(), expected, torch.float16)
+
+
+@pytest.mark.parametrize("query_heads,kv_heads,head_dim,stride", [(16, 1, 64, 4), (32, 4, 128, 2), (48, 1, 128, 2),
+                                                                   (8, 2, 64, 1)])
+def test_combined_quarter_states(query_heads, kv_heads, head_dim, stride):
+    """Workgroups holding several quarters of a partition store them combined.
+
+    Four quarters of a full 16-head tile (MQA-like groups) and any two
+    quarters become one state in the first quarter's slot; the other slots
+    get the empty state. pd_decode_partial + pd_decode_merge (which reads
+    every slot) then agrees with pd_decode (which reads the combined slots
+    only), and both match the oracle. stride 1: a shape that keeps four
+    states per partition.
+    """
+    announce(f"combined quarter states Hq{query_heads}/Hkv{kv_heads} D{head_dim}")
+    lib = cabi.load()
+    layout = Layout(4, query_heads, kv_heads, head_dim, 16, 4 * 24)
+    table, lengths = ragged_problem(layout, 17)
+    q, k, v = (torch.from_numpy(x).cuda() for x in host_tensors(layout, dtype=np.float16, seed=9))
+    split_tokens = 64
+    splits = -(-int(lengths.max()) // split_tokens)
+    args = (layout.batch, query_heads, kv_heads, head_dim, layout.page_size, table.shape[1], layout.physical_pages,
+            splits, split_tokens)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    num, stats, fused = workspace(layout, splits)
+    status = lib.pd_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16, d_table.data_ptr(),
+                           d_lengths.data_ptr(), num.data_ptr(), stats.data_ptr(), fused.data_ptr(), *args,
+                           cabi.PD_MERGE_SERIAL, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    num2, stats2, staged = workspace(layout, splits)
+    status = lib.pd_decode_partial(q.data_ptr(), k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16, d_table.data_ptr(),
+                                   d_lengths.data_ptr(), num2.data_ptr(), stats2.data_ptr(), *args, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    status = lib.pd_decode_merge(num2.data_ptr(), stats2.data_ptr(), staged.data_ptr(), d_lengths.data_ptr(),
+                                 layout.batch, query_heads, head_dim, layout.page_size, table.shape[1], splits,
+                                 split_tokens, cabi.PD_MERGE_SHARED, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    st = stats2.cpu().numpy()
+    for b, length in enumerate(lengths):
+        live = -(-int(length) // split_tokens)
+        for s in range(live):
+            slots = st[b, :, 4 * s:4 * s + 4]                      # [Hq, 4, (m, l)]
+            assert np.all(slots[:, 0, 1] > 0)                      # the first quarter always holds tokens
+            for quarter in range(4):
+                if quarter % stride:
+                    assert np.all(slots[:, quarter, 1] == 0.0)
+                    assert np.all(slots[:, quarter, 0] == np.finfo(np.float32).min)
+        assert np.all(np.isnan(st[b, :, 4 * live:]))              # partitions past the end are never written
+    expected = fp64.dense_attention(*(t.cpu().numpy() for t in (q, k, v)), table, lengths)
+    assert_parity(fused.cpu().numpy(), expected, torch.float16)
+    assert_parity(staged.cpu().numpy(), expected, torch.float16)
+    torch.testing.assert_close(staged, fused, rtol=1e-5, atol=1e-6)
