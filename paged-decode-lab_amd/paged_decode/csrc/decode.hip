@@ -12,8 +12,11 @@
 //     in slot 4 * partition + quarter of the workspace. A workgroup gathers up
 //     to eight KV heads of the same tokens (their head slices of a token row
 //     are then read together) plus enough quarters to make eight waves. Waves
-//     never synchronise with each other. Partitions that start at or past
-//     their sequence's end exit before any load and write nothing.
+//     do not synchronise while they stream; where a workgroup holds several
+//     quarters of one partition (few KV heads), one barrier at the end lets
+//     the first quarter fold the others into a single state. Partitions that
+//     start at or past their sequence's end exit before any load and write
+//     nothing.
 //       partial_mfma_kernel (q in FP16 or BF16; K/V in the same type or in
 //       OCP FP8): 16-token tiles; q.K^T and P.V on the matrix cores, online
 //       softmax with one running max per head and lazy rescaling (the
@@ -26,11 +29,13 @@
 //       combined with lane shuffles before the store.
 //     Page ids come from a 64-entry, lane-indexed window read once per wave
 //     and indexed with v_readlane; loads stream through a short register
-//     pipeline in fully unrolled blocks. Scores are kept in log2 units
+//     pipeline in fully unrolled blocks, K and V alike as whole token rows
+//     (K reaches the MFMA operand layout through LDS). Scores are kept in log2 units
 //     (scale * log2 e) and exponentiated with v_exp_f32.
 //  2. Merge: max-corrected combination of the live states of each (sequence,
-//     query head) row. merge_rows_kernel gives a row one wave when it has few
-//     states; merge_cols_kernel cuts a row's columns into 128-byte chunks, one
+//     query head) row (every stride-th one after a quarter combine).
+//     merge_rows_kernel gives a row one wave when it has few states and there
+//     are many rows; merge_cols_kernel cuts a row's columns into 128-byte chunks, one
 //     256-lane workgroup each, so long rows are read by several workgroups at
 //     once. The serial variants have every wave recompute the maximum and the
 //     denominator; the shared variants form each state's weight once in LDS
