@@ -66,3 +66,62 @@ def test_thousand_randomized_cases():
                 raise AssertionError(f"case {seed} merge={merge} split={split} {layout} "
                                      f"lengths={lengths.tolist()} dtype={dtype}") from exc
     announce(f"stress: {CASES} cases x 2 merges, max abs error {worst:.3e}")
+
+
+COMBINE_CASES = 300
+
+
+def test_randomized_combined_quarter_cases():
+    """Randomized shapes whose partition workgroups combine their quarters.
+
+    One or two KV heads with groups of 16, 24, 32 or 48 query heads (16-head
+    tiles: four quarters per workgroup for one tile, two for up to two tiles
+    per KV head pair), FP16 / BF16 / FP8-e4m3 K/V, ragged and empty rows,
+    small splits (rows of up to a few hundred states, merged with a stride)
+    and both merges, each against the FP64 oracle on the values the device
+    holds.
+    """
+    rng = np.random.default_rng(24680)
+    worst = 0.0
+    for seed in range(COMBINE_CASES):
+        b = int(rng.choice([1, 2, 3, 5]))
+        kv = int(rng.choice([1, 2]))
+        h = kv * int(rng.choice([16, 24, 32, 48]))
+        d = int(rng.choice([64, 128]))
+        page = int(rng.choice([16, 32]))
+        length = int(rng.choice([1, 17, 64, 129, 300, 513, 1000]))
+        layout, table, lengths = make_metadata(b, h, kv, d, length, page, seed=seed)
+        if seed % 4 == 0:
+            lengths[-1] = 0
+            table[-1, :] = -1
+        fmt = ("f16", "bf16", "e4m3")[seed % 3]
+        qf, kf, vf = (t.float() for t in make_tensors(layout, dtype=torch.float32, seed=seed + 20000))
+        if fmt == "f16":
+            q, k, v = qf.half(), kf.half(), vf.half()
+            k_scale = v_scale = 1.0
+            exact = host(q.double(), k.double(), v.double())
+        elif fmt == "bf16":
+            q, k, v = qf.bfloat16(), kf.bfloat16(), vf.bfloat16()
+            k_scale = v_scale = 1.0
+            exact = host(q.double(), k.double(), v.double())
+        else:
+            largest = float(torch.finfo(torch.float8_e4m3fn).max)
+            k_scale, v_scale = float(kf.abs().max()) / largest, float(vf.abs().max()) / largest
+            q = qf.half()
+            k = (kf / k_scale).to(torch.float8_e4m3fn)
+            v = (vf / v_scale).to(torch.float8_e4m3fn)
+            exact = (host(q.double())[0], host(k.double())[0] * k_scale, host(v.double())[0] * v_scale)
+        ref = dense_attention(*exact, table, lengths)
+        for merge in ("serial", "shared"):
+            split = int(rng.choice([16, 48, 64, 128, 256]))
+            if seed % 50 == 0 and merge == "serial":
+                announce(f"combine stress case {seed} worst so far {worst:.3e}")
+            plan = DecodePlan(layout, table, lengths, split_tokens=split, merge=merge)
+            out = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).cpu().numpy()
+            worst = max(worst, float(np.max(np.abs(out - ref))))
+            try:
+                assert_parity(out, ref, torch.float16)
+            except AssertionError as exc:
+                raise AssertionError(f"case {seed} merge={merge} split={split} {layout} {fmt} "
+                                     f"lengths={lengths.tolist()}") from exc
+    announce(f"combine stress: {COMBINE_CASES} cases x 2 merges, max abs error {worst:.3e}")
