@@ -52,6 +52,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cfloat>
 #include <cstdint>
 #include <type_traits>
@@ -1577,6 +1578,20 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     return status;
 }
 
+// Compute units of the current device, read once per device.
+int device_compute_units() {
+    static std::atomic<int> cached[64];
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+    int cus = cached[device].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+            cus = 256;  // MI355X
+        cached[device].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
+
 template <int D>
 int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t stream) {
     const bool shared = merge_mode == PD_MERGE_SHARED;
@@ -1598,7 +1613,13 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
     const dim3 grid(mp.query_heads, batch, D / kMergeChunk);
     const dim3 block(kMergeThreads);
     const size_t lds = shared ? states * sizeof(float) : 0;
-    const bool long_rows = states > kMergeColBatchShort * kMergeColGroups;
+    // The long-row variant issues 1024 states' loads per round but holds one
+    // (serial) or two (shared) workgroups per CU: it pays only while the grid
+    // fits the device in one round. Larger grids take 256-state rounds at full
+    // occupancy (rows of a plan whose reserved context exceeds the live one
+    // among them: the variant follows the allocated states).
+    const int64_t workgroups = static_cast<int64_t>(grid.x) * grid.y * grid.z;
+    const bool long_rows = states > kMergeColBatchShort * kMergeColGroups && workgroups <= device_compute_units();
     if (shared && long_rows) {
         hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchLong>), grid, block, lds, stream, mp);
     } else if (shared) {
