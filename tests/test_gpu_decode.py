@@ -184,6 +184,32 @@ def test_rows_of_thousands_of_states(dim, merge):
     np.testing.assert_array_equal(actual[2], 0.0)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("merge", ["serial", "shared"])
+def test_many_long_rows_and_reserved_context(dim, merge):
+    """256 rows of up to 512 live states (split 16), in a plan sized for the
+    longest sequence and in one reserving twice that: rows of more than 256
+    states merged in several load rounds across a grid larger than the
+    device's CUs. Both plans match the oracle and each other bit for bit
+    (the reserved partitions are never written or read)."""
+    announce(f"many long rows dim={dim} merge={merge}")
+    layout = Layout(16, 16, 4, dim, 16, 16 * 256)
+    rng = np.random.default_rng(31)
+    table = rng.permutation(16 * 256).reshape(16, 256).astype(np.int32)
+    lengths = rng.integers(0, 2049, size=16).astype(np.int32)
+    lengths[0], lengths[1] = 2048, 0
+    for b, n in enumerate(lengths):
+        table[b, (n + 15) // 16:] = -1
+    q, k, v = make_tensors(layout, dtype=torch.float16, seed=8)
+    fitted = DecodePlan(layout, table, lengths, split_tokens=16, merge=merge)
+    reserved = DecodePlan(layout, table, lengths, split_tokens=16, merge=merge, max_context=4096)
+    assert fitted.splits == 128 and reserved.splits == 256
+    out = fitted.run(q, k, v).clone()
+    assert_parity(out.cpu().numpy(), oracle(q, k, v, table, lengths), torch.float16)
+    torch.testing.assert_close(reserved.run(q, k, v), out, rtol=0, atol=0)
+    np.testing.assert_array_equal(out[1].cpu().numpy(), 0.0)
+
+
 def test_rejects_same_shape_noncontiguous_and_wrong_device():
     layout = Layout(1, 8, 2, 64, 16, 8)
     plan = DecodePlan(layout, np.arange(8, dtype=np.int32)[None], np.array([127]))
