@@ -1418,8 +1418,22 @@ int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LA
 #endif
 // KV heads per partition workgroup, at most.
 #ifndef PD_WG_HEADS
-#define PD_WG_HEADS 8
+#define PD_WG_HEADS 4  // KV heads per workgroup of the matrix-core kernel (FP32 kernel: 8)
 #endif
+
+// Compute units of the current device, read once per device.
+int device_compute_units() {
+    static std::atomic<int> cached[64];
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+    int cus = cached[device].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+            cus = 256;  // MI355X
+        cached[device].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
 
 // Largest divisor of n not above cap.
 int largest_divisor(int n, int cap) {
@@ -1428,12 +1442,22 @@ int largest_divisor(int n, int cap) {
     return 1;
 }
 
-// Workgroup shape: up to 8 KV heads of the same tokens per workgroup (their
-// slices of a token row are then read together, which the memory system
-// serves best), all head tiles of those heads, and as many partition quarters
-// as fill 8 waves.
-void choose_workgroup(PartialParams& prm, int kv_heads) {
-    prm.heads_per_wg = largest_divisor(kv_heads, PD_WG_HEADS);
+// Workgroup shape: up to max_heads KV heads of the same tokens per workgroup
+// (their slices of a token row are then read together), all head tiles of
+// those heads, and as many partition quarters as fill 8 waves. A KV head
+// count with no divisor in 2..max_heads keeps its whole token row in one
+// workgroup when it fits (5 or 7 heads).
+//
+// The matrix-core kernel takes 4 KV heads: at 8 KV heads, two workgroups of 4
+// heads x 2 quarters (streaming loads, quarters combined) measured 3-15% faster
+// per call than one of 8 heads x 1 quarter, from the Llama-3-8B shape
+// (18.84 -> 18.33 us) to B64 L2048 (122.3 -> 105.1 us) and 32K-context MHA
+// (98.6 -> 92.5 us at split 256); only short single-sequence calls, whose grid
+// does not fill the CUs, were slower, and those do not combine (see
+// dispatch_mfma).
+void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads) {
+    prm.heads_per_wg = largest_divisor(kv_heads, max_heads);
+    if (prm.heads_per_wg == 1 && kv_heads <= 8) prm.heads_per_wg = kv_heads;
     prm.tiles_per_wg = largest_divisor(prm.head_tiles, 8 / prm.heads_per_wg);
     const int hw_tw = prm.heads_per_wg * prm.tiles_per_wg;
     prm.quarters_per_wg = hw_tw <= 2 ? 4 : hw_tw <= 4 ? 2 : 1;
@@ -1450,9 +1474,9 @@ int partial_threads(const PartialParams& prm) {
 
 // When the KV heads need several workgroups (kv_heads > heads_per_wg), each
 // workgroup reads one head group's slice of every token row; 16-byte K/V loads
-// are then issued non-temporal, which measured 8-11% faster on MI355X for 16
-// and 32 KV heads (and neutral or slower when a workgroup reads whole rows).
-// FP8 K/V issue no 16-byte loads, so one variant serves them.
+// are then issued non-temporal, which measured faster on MI355X for 8, 16 and
+// 32 KV heads, in every format (FP8: its 16-byte K row loads), and neutral or
+// slower when a workgroup reads whole rows.
 template <typename QT, int KVF, int D, int GT>
 int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const dim3 grid = partial_grid(prm, batch, kv_heads);
@@ -1460,13 +1484,13 @@ int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t s
     const size_t lds = prm.combine ? static_cast<size_t>(block.x / kWave / prm.quarters_per_wg) *
                                          (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
                                    : 0;
-    const bool stream_loads = KVF == kKvNative && prm.heads_per_wg < kv_heads;
+    const bool stream_loads = prm.heads_per_wg < kv_heads;
     constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
     if (stream_loads && prm.combine) {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, KVF == kKvNative, true>), grid, block, lds,
+        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, true, true>), grid, block, lds,
                            stream, prm);
     } else if (stream_loads) {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, KVF == kKvNative, false>), grid, block, 0,
+        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, true, false>), grid, block, 0,
                            stream, prm);
     } else if (prm.combine) {
         hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, false, true>), grid, block, lds, stream,
@@ -1495,23 +1519,27 @@ int head_tile(int group, int max_tile) {
     return gt;
 }
 
-void plan_tiles(PartialParams& prm, int kv_heads, int max_tile, int& gt) {
+void plan_tiles(PartialParams& prm, int kv_heads, int max_tile, int max_heads, int& gt) {
     gt = head_tile(prm.group, max_tile);
     prm.head_tiles = (prm.group + gt - 1) / gt;
-    choose_workgroup(prm, kv_heads);
+    choose_workgroup(prm, kv_heads, max_heads);
 }
 
 template <typename QT, int KVF, int D>
 int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     int gt;
-    plan_tiles(prm, kv_heads, 16, gt);
+    plan_tiles(prm, kv_heads, 16, PD_WG_HEADS, gt);
     // Combining a workgroup's quarters into one state cuts the state stores
     // (written back at the kernel's end) and the merge's reads by qw; its
     // fold runs after the slowest quarter. Measured on MI355X it pays for two
     // quarters, and for four when the head tile is full (16 query heads:
     // MQA-like groups, the largest states per KV byte); four quarters of
-    // smaller tiles were 0.3-0.7 us slower per call.
-    prm.combine = prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16);
+    // smaller tiles were 0.3-0.7 us slower per call. A grid smaller than the
+    // CUs leaves the fold's tail exposed (B1 L4096: 12.05 us without, 12.43
+    // with), so such launches keep four states per partition.
+    const dim3 grid = partial_grid(prm, batch, kv_heads);
+    const bool fills_device = static_cast<int64_t>(grid.x) * grid.y * grid.z >= device_compute_units();
+    prm.combine = fills_device && (prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16));
     switch (gt) {
         case 1: return launch_mfma<QT, KVF, D, 1>(prm, batch, kv_heads, stream);
         case 2: return launch_mfma<QT, KVF, D, 2>(prm, batch, kv_heads, stream);
@@ -1524,7 +1552,7 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
 template <int D>
 int dispatch_fp32(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     int gt;
-    plan_tiles(prm, kv_heads, 8, gt);
+    plan_tiles(prm, kv_heads, 8, 8, gt);
     switch (gt) {
         case 1: return launch_fp32<D, 1>(prm, batch, kv_heads, stream);
         case 2: return launch_fp32<D, 2>(prm, batch, kv_heads, stream);
@@ -1578,19 +1606,6 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     return status;
 }
 
-// Compute units of the current device, read once per device.
-int device_compute_units() {
-    static std::atomic<int> cached[64];
-    int device = 0;
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
-    int cus = cached[device].load(std::memory_order_relaxed);
-    if (cus == 0) {
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
-            cus = 256;  // MI355X
-        cached[device].store(cus, std::memory_order_relaxed);
-    }
-    return cus;
-}
 
 template <int D>
 int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t stream) {

@@ -196,24 +196,31 @@ def test_context_sharded_over_two_partial_launches():
     assert_parity(out.cpu().numpy(), expected, torch.float16)
 
 
-@pytest.mark.parametrize("query_heads,kv_heads,head_dim,stride", [(16, 1, 64, 4), (32, 4, 128, 2), (48, 1, 128, 2),
-                                                                   (8, 2, 64, 1)])
-def test_combined_quarter_states(query_heads, kv_heads, head_dim, stride):
+@pytest.mark.parametrize("batch,query_heads,kv_heads,head_dim,stride", [
+    (8, 16, 1, 64, 4), (8, 32, 4, 128, 2), (8, 48, 1, 128, 2), (8, 8, 2, 64, 1), (1, 16, 1, 64, 1)])
+def test_combined_quarter_states(batch, query_heads, kv_heads, head_dim, stride):
     """Workgroups holding several quarters of a partition store them combined.
 
     Four quarters of a full 16-head tile (MQA-like groups) and any two
-    quarters become one state in the first quarter's slot; the other slots
-    get the empty state. pd_decode_partial + pd_decode_merge (which reads
+    quarters become one state in the first quarter's slot, and the other slots
+    get the empty state, when the launch fills the device (these grids have
+    320-640 workgroups). pd_decode_partial + pd_decode_merge (which reads
     every slot) then agrees with pd_decode (which reads the combined slots
-    only), and both match the oracle. stride 1: a shape that keeps four
-    states per partition.
+    only), and both match the oracle. stride 1: a shape that keeps four states
+    per partition (four quarters of a 4-head tile), and a one-sequence grid
+    smaller than the device.
     """
-    announce(f"combined quarter states Hq{query_heads}/Hkv{kv_heads} D{head_dim}")
+    announce(f"combined quarter states B{batch} Hq{query_heads}/Hkv{kv_heads} D{head_dim}")
     lib = cabi.load()
-    layout = Layout(4, query_heads, kv_heads, head_dim, 16, 4 * 24)
-    table, lengths = ragged_problem(layout, 17)
+    width, page = 160, 16
+    layout = Layout(batch, query_heads, kv_heads, head_dim, page, batch * width)
+    rng = np.random.default_rng(17)
+    table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+    lengths = np.array([width * page, 0, 37, width * page - 5, 600, 1, 513, 999][:batch], dtype=np.int32)
+    for b, n in enumerate(lengths):
+        table[b, (n + page - 1) // page:] = -1
     q, k, v = (torch.from_numpy(x).cuda() for x in host_tensors(layout, dtype=np.float16, seed=9))
-    split_tokens = 64
+    split_tokens = 64                                              # 16 tokens per quarter: every quarter holds a tile
     splits = -(-int(lengths.max()) // split_tokens)
     args = (layout.batch, query_heads, kv_heads, head_dim, layout.page_size, table.shape[1], layout.physical_pages,
             splits, split_tokens)
@@ -242,6 +249,8 @@ def test_combined_quarter_states(query_heads, kv_heads, head_dim, stride):
                 if quarter % stride:
                     assert np.all(slots[:, quarter, 1] == 0.0)
                     assert np.all(slots[:, quarter, 0] == np.finfo(np.float32).min)
+        if stride == 1 and int(length) >= split_tokens:
+            assert np.all(st[b, :, 1, 1] > 0)                      # four separate states: quarter 1 holds tokens
         assert np.all(np.isnan(st[b, :, 4 * live:]))              # partitions past the end are never written
     expected = fp64.dense_attention(*(t.cpu().numpy() for t in (q, k, v)), table, lengths)
     assert_parity(fused.cpu().numpy(), expected, torch.float16)

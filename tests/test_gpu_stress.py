@@ -72,14 +72,15 @@ COMBINE_CASES = 300
 
 
 def test_randomized_combined_quarter_cases():
-    """Randomized shapes whose partition workgroups combine their quarters.
+    """Randomized few-KV-head shapes (the quarter-combining workgroup layouts).
 
     One or two KV heads with groups of 16, 24, 32 or 48 query heads (16-head
     tiles: four quarters per workgroup for one tile, two for up to two tiles
     per KV head pair), FP16 / BF16 / FP8-e4m3 K/V, ragged and empty rows,
-    small splits (rows of up to a few hundred states, merged with a stride)
-    and both merges, each against the FP64 oracle on the values the device
-    holds.
+    small splits (rows of up to a few hundred states) and both merges, each
+    against the FP64 oracle on the values the device holds. Most of these
+    grids are smaller than the device and keep four states per partition; the
+    larger ones combine (see the large-grid test below).
     """
     rng = np.random.default_rng(24680)
     worst = 0.0
@@ -125,3 +126,49 @@ def test_randomized_combined_quarter_cases():
                 raise AssertionError(f"case {seed} merge={merge} split={split} {layout} {fmt} "
                                      f"lengths={lengths.tolist()}") from exc
     announce(f"combine stress: {COMBINE_CASES} cases x 2 merges, max abs error {worst:.3e}")
+
+
+LARGE_GRID_CASES = 30
+
+
+def test_randomized_combined_quarters_large_grids():
+    """Randomized few-KV-head shapes with grids that fill the device, so the
+    partition kernel combines its quarters (splits of 64 or 128 tokens: every
+    quarter holds tokens), FP16 / BF16 / FP8-e4m3 K/V, ragged and empty rows,
+    both merges, against the FP64 oracle."""
+    rng = np.random.default_rng(13579)
+    worst = 0.0
+    for seed in range(LARGE_GRID_CASES):
+        b = int(rng.choice([24, 32]))
+        kv = int(rng.choice([1, 2]))
+        h = kv * int(rng.choice([16, 24]))
+        d = int(rng.choice([64, 128]))
+        length = int(rng.choice([1100, 1600]))
+        layout, table, lengths = make_metadata(b, h, kv, d, length, 16, seed=seed)
+        lengths[1] = 0
+        table[1, :] = -1
+        fmt = ("f16", "bf16", "e4m3")[seed % 3]
+        qf, kf, vf = make_tensors(layout, dtype=torch.float32, seed=seed + 30000)
+        if fmt == "e4m3":
+            largest = float(torch.finfo(torch.float8_e4m3fn).max)
+            k_scale, v_scale = float(kf.abs().max()) / largest, float(vf.abs().max()) / largest
+            q, k, v = qf.half(), (kf / k_scale).to(torch.float8_e4m3fn), (vf / v_scale).to(torch.float8_e4m3fn)
+            exact = (host(q.double())[0], host(k.double())[0] * k_scale, host(v.double())[0] * v_scale)
+        else:
+            dt = torch.float16 if fmt == "f16" else torch.bfloat16
+            q, k, v = qf.to(dt), kf.to(dt), vf.to(dt)
+            k_scale = v_scale = 1.0
+            exact = host(q.double(), k.double(), v.double())
+        ref = dense_attention(*exact, table, lengths)
+        for merge in ("serial", "shared"):
+            split = int(rng.choice([64, 128]))
+            plan = DecodePlan(layout, table, lengths, split_tokens=split, merge=merge)
+            out = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).cpu().numpy()
+            worst = max(worst, float(np.max(np.abs(out - ref))))
+            try:
+                assert_parity(out, ref, torch.float16)
+            except AssertionError as exc:
+                raise AssertionError(f"case {seed} merge={merge} split={split} {layout} {fmt}") from exc
+        if seed % 10 == 0:
+            announce(f"large-grid combine case {seed} worst so far {worst:.3e}")
+    announce(f"large-grid combine stress: {LARGE_GRID_CASES} cases x 2 merges, max abs error {worst:.3e}")
