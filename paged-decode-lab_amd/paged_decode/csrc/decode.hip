@@ -693,7 +693,9 @@ struct CombineSlot {
     f32x4 acc[VH][kWave];
 };
 
-template <typename QT, int KVF, int D, int GT, int PD, int NC, bool kStream, bool kCombine>
+// kStream: which 16-byte loads are non-temporal (see launch_mfma):
+// 0 none, 1 V (and FP8 K, whose V loads are 8-byte), 2 K and V.
+template <typename QT, int KVF, int D, int GT, int PD, int NC, int kStream, bool kCombine>
 __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
     using C = Compute<QT>;
     constexpr int ES = KVF == kKvNative ? 2 : 1;  // stored bytes per K/V element
@@ -710,6 +712,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     // one operand read (16 bytes for 16-bit K, 8 for FP8), so the transposed
     // reads of 16 different rows fall in distinct banks.
     constexpr bool kKRows = PD_MFMA_K_ROWS;
+    constexpr bool kStreamK = kStream == 2 || (kStream == 1 && KVF != kKvNative);
     constexpr int KR = D * ES / 16;
     constexpr int TK = kWave / KR;
     constexpr int KL = kTileTokens / TK;
@@ -775,21 +778,21 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
                 const int tk = min(max(t0 + TK * s + lane / KR, lo), hi);
                 const uint32_t col = static_cast<uint32_t>(lane % KR) * 16u;
                 const uint32_t koff = ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + col : col;
-                load_words<4, kStream>(kp + koff, tl.k[s]);
+                load_words<4, kStreamK>(kp + koff, tl.k[s]);
             }
         } else {
             const int tk = min(max(t0 + k_row_token, lo), hi);
             const uint32_t koff =
                 ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
 #pragma unroll
-            for (int s = 0; s < KS; ++s) load_words<KW, kStream>(kp + koff + 32 * ES * s, tl.k[s]);
+            for (int s = 0; s < KS; ++s) load_words<KW, kStreamK>(kp + koff + 32 * ES * s, tl.k[s]);
         }
 #pragma unroll
         for (int e = 0; e < VI; ++e) {
             const int tv = min(max(t0 + 4 * e + g, lo), hi);
             const uint32_t voff =
                 ok ? static_cast<uint32_t>(tv & (page_size - 1)) * p.token_bytes + v_lane_bytes : v_lane_bytes;
-            load_words<VW, kStream>(vp + voff, tl.v[e]);
+            load_words<VW, (kStream >= 1)>(vp + voff, tl.v[e]);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -1473,10 +1476,17 @@ int partial_threads(const PartialParams& prm) {
 }
 
 // When the KV heads need several workgroups (kv_heads > heads_per_wg), each
-// workgroup reads one head group's slice of every token row; 16-byte K/V loads
-// are then issued non-temporal, which measured faster on MI355X for 8, 16 and
-// 32 KV heads, in every format (FP8: its 16-byte K row loads), and neutral or
-// slower when a workgroup reads whole rows.
+// workgroup reads one head group's slice of every token row, and some 16-byte
+// loads are issued non-temporal. Measured on MI355X (decode call, us):
+//   - 4 or more head groups per row (16, 32 KV heads): K and V streaming is
+//     fastest without shared pages (32K-context MHA at split 256: 92.2, V only
+//     95.3, neither 98.6), but a batch whose sequences share prefix pages reads
+//     them again from HBM (B8 L4096, 32 KV heads, 25% shared: 48.4, V only
+//     43.0); the 4+-group rule keeps the long-context case.
+//   - 2 head groups (8 KV heads): V only. B64 L2048 103.8 (K and V 104.7,
+//     neither 112.3); a B16 batch with 25% shared prefix pages 52.0 (K and V
+//     59.3, whole-row workgroups 53.6).
+//   - FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads.
 template <typename QT, int KVF, int D, int GT>
 int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const dim3 grid = partial_grid(prm, batch, kv_heads);
@@ -1484,21 +1494,25 @@ int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t s
     const size_t lds = prm.combine ? static_cast<size_t>(block.x / kWave / prm.quarters_per_wg) *
                                          (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
                                    : 0;
-    const bool stream_loads = prm.heads_per_wg < kv_heads;
+    const int groups = kv_heads / prm.heads_per_wg;
     constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
-    if (stream_loads && prm.combine) {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, true, true>), grid, block, lds,
-                           stream, prm);
-    } else if (stream_loads) {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, true, false>), grid, block, 0,
-                           stream, prm);
-    } else if (prm.combine) {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, false, true>), grid, block, lds, stream,
-                           prm);
-    } else {
-        hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, false, false>), grid, block, 0, stream,
-                           prm);
+#define PD_LAUNCH_MFMA(MODE, COMBINE)                                                                             \
+    hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE>), grid, block, lds, stream, prm)
+    if constexpr (KVF == kKvNative) {
+        if (groups >= 4) {
+            if (prm.combine) PD_LAUNCH_MFMA(2, true);
+            else PD_LAUNCH_MFMA(2, false);
+            return launch_status();
+        }
     }
+    if (groups > 1) {
+        if (prm.combine) PD_LAUNCH_MFMA(1, true);
+        else PD_LAUNCH_MFMA(1, false);
+    } else {
+        if (prm.combine) PD_LAUNCH_MFMA(0, true);
+        else PD_LAUNCH_MFMA(0, false);
+    }
+#undef PD_LAUNCH_MFMA
     return launch_status();
 }
 
