@@ -57,7 +57,8 @@ enum pd_status {
     PD_ERR_DTYPE = 3,         /* unsupported dtype combination, or a scale not finite and > 0 */
     PD_ERR_SPLIT = 4,         /* splits / split_tokens outside their range */
     PD_ERR_MERGE = 5,         /* unknown merge mode or shared-merge bound exceeded */
-    PD_ERR_LAUNCH = 6         /* the HIP runtime rejected a kernel launch */
+    PD_ERR_LAUNCH = 6,        /* the HIP runtime rejected a kernel launch */
+    PD_ERR_HINT = 7           /* unknown bits in the hints argument */
 };
 
 /* Storage formats. q, k and v share F32, F16 or BF16 in pd_decode; the _ex
@@ -76,6 +77,17 @@ enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
 
 /* Largest state count (4 * splits) the LDS-bounded (shared) merge accepts. */
 #define PD_SHARED_MERGE_MAX_PARTS 4096
+
+/*
+ * Hints of the _ex entries (a bit set; 0 = none). They never change results,
+ * only how K/V loads use the caches:
+ *   PD_HINT_UNSHARED_PAGES: no physical page holds live tokens of more than
+ *   one sequence (no shared prefix pages). The partition kernel may then
+ *   stream K/V past the caches, which is faster when nothing is read twice;
+ *   without it, pages that several sequences share stay cacheable. Passing it
+ *   for a batch that does share pages is still correct, only slower.
+ */
+enum pd_hint { PD_HINT_NONE = 0, PD_HINT_UNSHARED_PAGES = 1 };
 
 /*
  * Full decode: partition kernel then merge kernel, both on `stream`.
@@ -111,16 +123,16 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
                  float* numerator, float* stats, float* out,
                  int batch, int query_heads, int kv_heads, int head_dim, int page_size,
                  int table_width, int physical_pages, int splits, int split_tokens,
-                 int merge_mode, void* stream);
+                 int merge_mode, int hints, void* stream);
 
-/* Partition stage of pd_decode_ex. */
+/* Partition stage of pd_decode_ex (same hints). */
 int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
                          float k_scale, float v_scale,
                          const int32_t* table, const int32_t* lengths,
                          float* numerator, float* stats,
                          int batch, int query_heads, int kv_heads, int head_dim, int page_size,
                          int table_width, int physical_pages, int splits, int split_tokens,
-                         void* stream);
+                         int hints, void* stream);
 
 /*
  * Partition stage only (the first launch of pd_decode): fills numerator and
@@ -217,7 +229,8 @@ const char* pd_status_string(int status);
  * 5: states past a sequence's end are neither written nor read, so
  * pd_decode_merge takes the lengths; 6: KV-cache append; 7: BF16 and FP8 K/V,
  * pd_decode_ex; 8: pd_table_from_csr; 9: quarters of one workgroup stored
- * combined, the others as empty states). */
+ * combined, the others as empty states; 10: hints argument of the _ex
+ * entries). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

@@ -24,15 +24,18 @@ PD_DTYPE_FP8_E5M2 = 4
 PD_MERGE_SERIAL = 0
 PD_MERGE_SHARED = 1
 PD_SHARED_MERGE_MAX_PARTS = 4096  # states (4 per split)
+PD_HINT_NONE = 0
+PD_HINT_UNSHARED_PAGES = 1
+PD_ERR_HINT = 7
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 PROTOTYPES = {
     "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
-    "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
+    "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 11 + [_P]),
     "pd_decode_partial": (_I, [_P, _P, _P, _I, _P, _P, _P, _P] + [_I] * 9 + [_P]),
-    "pd_decode_partial_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P] + [_I] * 9 + [_P]),
+    "pd_decode_partial_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P] + [_I] * 10 + [_P]),
     "pd_decode_merge": (_I, [_P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_append_kv": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
     "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),

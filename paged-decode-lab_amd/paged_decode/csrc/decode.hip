@@ -253,6 +253,7 @@ struct PartialParams {
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
     float v_scale;         // multiplies every stored numerator
     int combine;           // host only: the launch stores a workgroup's qw quarters as one state (kCombine)
+    int unshared_pages;    // host only: PD_HINT_UNSHARED_PAGES (see launch_mfma)
 };
 
 // Workgroup coordinates (token group, head group) in dispatch order: the
@@ -1477,16 +1478,21 @@ int partial_threads(const PartialParams& prm) {
 
 // When the KV heads need several workgroups (kv_heads > heads_per_wg), each
 // workgroup reads one head group's slice of every token row, and some 16-byte
-// loads are issued non-temporal. Measured on MI355X (decode call, us):
-//   - 4 or more head groups per row (16, 32 KV heads): K and V streaming is
-//     fastest without shared pages (32K-context MHA at split 256: 92.2, V only
-//     95.3, neither 98.6), but a batch whose sequences share prefix pages reads
-//     them again from HBM (B8 L4096, 32 KV heads, 25% shared: 48.4, V only
-//     43.0); the 4+-group rule keeps the long-context case.
-//   - 2 head groups (8 KV heads): V only. B64 L2048 103.8 (K and V 104.7,
-//     neither 112.3); a B16 batch with 25% shared prefix pages 52.0 (K and V
-//     59.3, whole-row workgroups 53.6).
-//   - FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads.
+// loads may be issued non-temporal. That is faster when nothing is read twice
+// and slower when sequences share prefix pages, which streamed loads do not
+// leave in the caches. Measured on MI355X (decode call, us):
+//   - 4 or more head groups per row (16, 32 KV heads), no shared pages: K and
+//     V streaming is fastest (32K-context MHA at split 256: 92.2; V only
+//     95.3; neither 98.6). With 25% shared prefix pages (B8 L4096, 32 KV
+//     heads): K and V 48.4, V only 43.0.
+//   - 2 head groups (8 KV heads), no shared pages: V only (B64 L2048 103.8,
+//     K and V 104.7, neither 112.3; a ragged B16 page-32 batch 57.0 / 62.1 /
+//     64.1). With 25% shared prefix pages (B16 page 32): neither 50.3, V only
+//     52.0, K and V 59.3.
+// So the mode follows the page-sharing hint: unshared pages stream K and V
+// (4+ groups) or V (2 groups); pages that may be shared stream V (4+ groups)
+// or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads
+// wherever 16-bit K/V would stream V.
 template <typename QT, int KVF, int D, int GT>
 int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const dim3 grid = partial_grid(prm, batch, kv_heads);
@@ -1495,17 +1501,18 @@ int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t s
                                          (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
                                    : 0;
     const int groups = kv_heads / prm.heads_per_wg;
+    const int mode = groups == 1 ? 0 : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
     constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
 #define PD_LAUNCH_MFMA(MODE, COMBINE)                                                                             \
     hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE>), grid, block, lds, stream, prm)
     if constexpr (KVF == kKvNative) {
-        if (groups >= 4) {
+        if (mode == 2) {
             if (prm.combine) PD_LAUNCH_MFMA(2, true);
             else PD_LAUNCH_MFMA(2, false);
             return launch_status();
         }
     }
-    if (groups > 1) {
+    if (mode >= 1) {
         if (prm.combine) PD_LAUNCH_MFMA(1, true);
         else PD_LAUNCH_MFMA(1, false);
     } else {
@@ -1594,8 +1601,9 @@ int dispatch_formats(PartialParams& prm, int q_dtype, int kv_dtype, int batch, i
 int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
                 const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
-                int splits, int split_tokens, hipStream_t stream, int* state_stride = nullptr) {
+                int splits, int split_tokens, int hints, hipStream_t stream, int* state_stride = nullptr) {
     PartialParams prm{};
+    prm.unshared_pages = (hints & PD_HINT_UNSHARED_PAGES) != 0;
     prm.q = q;
     prm.k = k;
     prm.v = v;
@@ -1660,6 +1668,8 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
     }
     return launch_status();
 }
+
+int check_hints(int hints) { return (hints & ~PD_HINT_UNSHARED_PAGES) == 0 ? PD_OK : PD_ERR_HINT; }
 
 int check_merge(const float* numerator, const float* stats, const float* out, const int32_t* lengths, int batch,
                 int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
@@ -1729,14 +1739,15 @@ extern "C" {
 int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
                          float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
                          int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                         int physical_pages, int splits, int split_tokens, void* stream) {
-    const int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats,
-                                    batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
-                                    splits, split_tokens);
+                         int physical_pages, int splits, int split_tokens, int hints, void* stream) {
+    int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
+                              query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                              split_tokens);
+    if (status == PD_OK) status = check_hints(hints);
     if (status != PD_OK) return status;
     return run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                        query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                       static_cast<hipStream_t>(stream));
+                       hints, static_cast<hipStream_t>(stream));
 }
 
 int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -1745,7 +1756,7 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, co
                       int split_tokens, void* stream) {
     return pd_decode_partial_ex(q, dtype, k, v, dtype, 1.0f, 1.0f, table, lengths, numerator, stats, batch,
                                 query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                                split_tokens, stream);
+                                split_tokens, PD_HINT_NONE, stream);
 }
 
 int pd_decode_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
@@ -1761,19 +1772,20 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out, cons
 int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
                  float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
                  float* out, int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                 int physical_pages, int splits, int split_tokens, int merge_mode, void* stream) {
+                 int physical_pages, int splits, int split_tokens, int merge_mode, int hints, void* stream) {
     int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                               query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                               split_tokens);
     if (status == PD_OK)
         status = check_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width,
                              splits, split_tokens, merge_mode);
+    if (status == PD_OK) status = check_hints(hints);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     int stride = 1;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                         split_tokens, s, &stride);
+                         split_tokens, hints, s, &stride);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
                      split_tokens, merge_mode, stride, s);
@@ -1785,7 +1797,7 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
               int split_tokens, int merge_mode, void* stream) {
     return pd_decode_ex(q, dtype, k, v, dtype, 1.0f, 1.0f, table, lengths, numerator, stats, out, batch,
                         query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                        merge_mode, stream);
+                        merge_mode, PD_HINT_NONE, stream);
 }
 
 int pd_append_kv(const void* k_new, const void* v_new, int dtype, const int32_t* table, const int32_t* positions,
@@ -1840,10 +1852,11 @@ const char* pd_status_string(int status) {
         case PD_ERR_SPLIT: return "invalid split configuration";
         case PD_ERR_MERGE: return "unknown merge mode or shared merge requires at most 4096 partial states (4 per split)";
         case PD_ERR_LAUNCH: return "kernel launch failed";
+        case PD_ERR_HINT: return "unknown hint bits";
         default: return "unknown status";
     }
 }
 
-int pd_abi_version(void) { return 9; }
+int pd_abi_version(void) { return 10; }
 
 }  // extern "C"

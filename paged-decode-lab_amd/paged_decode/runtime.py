@@ -11,6 +11,7 @@ from functools import lru_cache
 import importlib
 import math
 
+import numpy as np
 import torch
 
 from .layout import Layout, validate_metadata
@@ -100,6 +101,7 @@ class DecodePlan:
         if self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self._table_cpu, self._lengths_cpu = table, lengths
+        self._unshared_pages = unshared_pages(table, layout.page_size, capacity)
         self._table = torch.tensor(table, device=self.device)
         self._lengths = torch.tensor(lengths, device=self.device)
         shape = (layout.batch, layout.query_heads, self.splits * _STATES_PER_SPLIT)
@@ -141,6 +143,7 @@ class DecodePlan:
         self._table.copy_(torch.from_numpy(table))
         self._lengths.copy_(torch.from_numpy(lengths))
         self._table_cpu, self._lengths_cpu = table, lengths
+        self._unshared_pages = unshared_pages(table, self.layout.page_size, self.context_capacity)
         self.max_context = longest
 
     def refresh_csr(self, indptr, indices, last_page_len, overflow=None):
@@ -156,6 +159,8 @@ class DecodePlan:
         ``overflow`` tensor is given (it is never cleared; zero it first).
         Page ids are not validated here; the kernel skips ids outside the
         cache. ``max_context`` keeps the value of the last host-side metadata.
+        The plan no longer knows whether pages are shared between sequences,
+        so later runs keep K/V cacheable (see ``unshared_pages``).
         """
         for t in (indptr, indices, last_page_len):
             if t.device != self.device or t.dtype != torch.int32 or not t.is_contiguous():
@@ -167,6 +172,7 @@ class DecodePlan:
             raise TypeError("overflow must be an int32 tensor on the plan device")
         self._extension.table_from_csr(indptr, indices, last_page_len, self._table, self._lengths, overflow,
                                        self.layout.page_size, self.context_capacity)
+        self._unshared_pages = False
 
     def append(self, k_cache, v_cache, k_new, v_new):
         """Append new tokens at the plan's current lengths and advance them on the device.
@@ -218,14 +224,15 @@ class DecodePlan:
         """
         self._check(q, k, v, k_scale, v_scale)
         self._extension.decode(q, k, v, self._table, self._lengths, self._numerator, self._stats,
-                               self._out, self.split_tokens, self._merge_mode, float(k_scale), float(v_scale))
+                               self._out, self.split_tokens, self._merge_mode, float(k_scale), float(v_scale),
+                               self._unshared_pages)
         return self._out
 
     def run_partial(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
         """Partition stage only (fills the workspace); for stage timing."""
         self._check(q, k, v, k_scale, v_scale)
         self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
-                                self.split_tokens, float(k_scale), float(v_scale))
+                                self.split_tokens, float(k_scale), float(v_scale), self._unshared_pages)
 
     def run_merge(self):
         """Merge stage only, from the current workspace; returns the borrowed output."""
@@ -233,6 +240,21 @@ class DecodePlan:
         self._extension.merge(self._numerator, self._stats, self._out, self._lengths, layout.page_size,
                               self._table.shape[1], self.split_tokens, self._merge_mode)
         return self._out
+
+
+def unshared_pages(table, page_size, capacity):
+    """True when no physical page is mapped twice among the table entries that
+    can hold live tokens: columns up to ``ceil(capacity / page_size)`` of every
+    row (appends can extend a sequence that far), negative padding excluded.
+
+    The plan passes this as the library's page-sharing hint: with no page read
+    twice, the partition kernel may stream K/V past the caches; with shared
+    (prefix) pages it keeps them cacheable. Results are the same either way.
+    """
+    columns = min(table.shape[1], -(-int(capacity) // page_size))
+    ids = np.asarray(table)[:, :columns].ravel()
+    ids = ids[ids >= 0]
+    return bool(np.unique(ids).size == ids.size)
 
 
 def _token_batch(k_new, v_new, layout):

@@ -74,7 +74,7 @@ def test_decode_ex_fp8_matches_oracle(kv_dtype, merge):
                               k_scale, v_scale, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
                               stats.data_ptr(), out.data_ptr(), layout.batch, layout.query_heads, layout.kv_heads,
                               layout.head_dim, layout.page_size, table.shape[1], layout.physical_pages, splits,
-                              split_tokens, merge, stream())
+                              split_tokens, merge, cabi.PD_HINT_UNSHARED_PAGES, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     torch.cuda.synchronize()
     actual = out.cpu().numpy()
@@ -97,12 +97,14 @@ def test_partial_then_merge_entries_equal_decode_ex():
     num, stats, full = workspace(layout, splits)
     status = lib.pd_decode_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_FP8_E4M3,
                               k_scale, v_scale, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
-                              stats.data_ptr(), full.data_ptr(), *args, cabi.PD_MERGE_SERIAL, stream())
+                              stats.data_ptr(), full.data_ptr(), *args, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_NONE,
+                              stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     num2, stats2, staged = workspace(layout, splits)
     status = lib.pd_decode_partial_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(),
                                       cabi.PD_DTYPE_FP8_E4M3, k_scale, v_scale, d_table.data_ptr(),
-                                      d_lengths.data_ptr(), num2.data_ptr(), stats2.data_ptr(), *args, stream())
+                                      d_lengths.data_ptr(), num2.data_ptr(), stats2.data_ptr(), *args,
+                                      cabi.PD_HINT_NONE, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     status = lib.pd_decode_merge(num2.data_ptr(), stats2.data_ptr(), staged.data_ptr(), d_lengths.data_ptr(),
                                  layout.batch, layout.query_heads, layout.head_dim, layout.page_size, table.shape[1],
@@ -256,3 +258,42 @@ def test_combined_quarter_states(batch, query_heads, kv_heads, head_dim, stride)
     assert_parity(fused.cpu().numpy(), expected, torch.float16)
     assert_parity(staged.cpu().numpy(), expected, torch.float16)
     torch.testing.assert_close(staged, fused, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("kv_heads,kv_dtype", [(8, torch.float16), (32, torch.float16), (8, torch.float8_e4m3fn)])
+def test_page_sharing_hint_changes_no_bits(kv_heads, kv_dtype):
+    """PD_HINT_UNSHARED_PAGES only changes how loads use the caches: on a
+    batch whose sequences share prefix pages (so the hint is wrong), hinted
+    and unhinted calls give the same bits, for the 2-group (8 KV heads) and
+    4+-group (32 KV heads) streaming choices and FP8."""
+    announce(f"page-sharing hint Hkv{kv_heads} {kv_dtype}")
+    lib = cabi.load()
+    batch, width, page = 16, 32, 16
+    layout = Layout(batch, 32, kv_heads, 128, page, batch * width)
+    rng = np.random.default_rng(3)
+    table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+    table[1:, :8] = table[0, :8]                                   # an 8-page prefix shared by every sequence
+    lengths = rng.integers(129, width * page + 1, size=batch).astype(np.int32)
+    for b, n in enumerate(lengths):
+        table[b, (n + page - 1) // page:] = -1
+    if kv_dtype == torch.float16:
+        q, k, v = (torch.from_numpy(x).cuda() for x in host_tensors(layout, dtype=np.float16, seed=2))
+        codes, scales = (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_F16), (1.0, 1.0)
+    else:
+        (q, k, v), scales, _ = quantize(layout, kv_dtype, 2)
+        codes = (cabi.PD_DTYPE_BF16, KV_CODES[kv_dtype])
+    split_tokens = 64
+    splits = -(-int(lengths.max()) // split_tokens)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    outs = []
+    for hint in (cabi.PD_HINT_NONE, cabi.PD_HINT_UNSHARED_PAGES):
+        num, stats, out = workspace(layout, splits)
+        status = lib.pd_decode_ex(q.data_ptr(), codes[0], k.data_ptr(), v.data_ptr(), codes[1], *scales,
+                                  d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(), stats.data_ptr(),
+                                  out.data_ptr(), batch, 32, kv_heads, 128, page, width, layout.physical_pages,
+                                  splits, split_tokens, cabi.PD_MERGE_SERIAL, hint, stream())
+        assert status == cabi.PD_OK, cabi.status_string(lib, status)
+        outs.append(out)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(outs[1], outs[0], rtol=0, atol=0)
+    assert torch.isfinite(outs[0]).all()

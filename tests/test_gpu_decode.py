@@ -210,6 +210,29 @@ def test_many_long_rows_and_reserved_context(dim, merge):
     np.testing.assert_array_equal(out[1].cpu().numpy(), 0.0)
 
 
+def test_plan_derives_the_page_sharing_hint():
+    """The plan streams K/V past the caches only when its table maps no page
+    twice: the shared-prefix workload keeps them cacheable, the Llama-3-8B one
+    streams, and a device-side CSR refresh falls back to cacheable."""
+    shared = make_workload("ragged_shared_b16")
+    plan = DecodePlan(shared.layout, shared.table, shared.lengths, split_tokens=shared.split_tokens)
+    assert not plan._unshared_pages
+    w = make_workload("llama3_8b_b4_l4096")
+    plan = DecodePlan(w.layout, w.table, w.lengths, split_tokens=w.split_tokens)
+    assert plan._unshared_pages
+    aliased = w.table.copy()
+    aliased[1, 0] = aliased[0, 0]                                  # one page now backs two sequences
+    plan.refresh(aliased, w.lengths)
+    assert not plan._unshared_pages
+    plan.refresh(w.table, w.lengths)
+    assert plan._unshared_pages
+    indptr = torch.zeros(w.layout.batch + 1, dtype=torch.int32, device="cuda")
+    indices = torch.zeros(1, dtype=torch.int32, device="cuda")
+    last = torch.ones(w.layout.batch, dtype=torch.int32, device="cuda")
+    plan.refresh_csr(indptr, indices, last)
+    assert not plan._unshared_pages
+
+
 def test_rejects_same_shape_noncontiguous_and_wrong_device():
     layout = Layout(1, 8, 2, 64, 16, 8)
     plan = DecodePlan(layout, np.arange(8, dtype=np.int32)[None], np.array([127]))

@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 9
+    assert lib.pd_abi_version() == 10
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -95,7 +95,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != 9) return 1;
+    if (pd_abi_version() != 10) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
@@ -104,6 +104,7 @@ int main(void) {
                      4, 1, 8, 128, 16, 256, 1024, NULL) != PD_ERR_NULL_POINTER) return 4;
     if (strstr(pd_status_string(PD_ERR_SHAPE), "dimension") == NULL) return 5;
     if (pd_table_from_csr(NULL, NULL, NULL, NULL, NULL, NULL, 4, 256, 16, 4096, NULL) != PD_ERR_NULL_POINTER) return 6;
+    if (strstr(pd_status_string(PD_ERR_HINT), "hint") == NULL || PD_HINT_UNSHARED_PAGES != 1) return 7;
     puts("ok");
     return 0;
 }
@@ -239,11 +240,42 @@ def test_extended_entry_rejects_formats_and_scales(q_dtype, kv_dtype, k_scale, v
     lib = cabi.load()
     ptrs, _keep = fake(8)
     status = lib.pd_decode_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3], ptrs[4],
-                              ptrs[5], ptrs[6], ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, None)
+                              ptrs[5], ptrs[6], ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, 0, None)
     assert status == cabi.PD_ERR_DTYPE
     status = lib.pd_decode_partial_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3],
-                                      ptrs[4], ptrs[5], ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, None)
+                                      ptrs[4], ptrs[5], ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, None)
     assert status == cabi.PD_ERR_DTYPE
+
+
+@pytest.mark.parametrize("hints", [2, 4, -1, 1 << 30])
+def test_extended_entries_reject_unknown_hints(hints):
+    """Only PD_HINT_UNSHARED_PAGES is defined; other bits are rejected before any launch."""
+    lib = cabi.load()
+    ptrs, _keep = fake(8)
+    f16 = cabi.PD_DTYPE_F16
+    status = lib.pd_decode_ex(ptrs[0], f16, ptrs[1], ptrs[2], f16, 1.0, 1.0, ptrs[3], ptrs[4], ptrs[5], ptrs[6],
+                              ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, hints, None)
+    assert status == cabi.PD_ERR_HINT
+    status = lib.pd_decode_partial_ex(ptrs[0], f16, ptrs[1], ptrs[2], f16, 1.0, 1.0, ptrs[3], ptrs[4], ptrs[5],
+                                      ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, hints, None)
+    assert status == cabi.PD_ERR_HINT
+    assert "hint" in cabi.status_string(lib, cabi.PD_ERR_HINT)
+
+
+def test_page_sharing_hint_follows_the_table():
+    """unshared_pages: any page id mapped twice among the entries up to the
+    reserved capacity (padding excluded) means shared."""
+    from paged_decode.runtime import unshared_pages
+
+    table = np.array([[0, 1, 2, -1], [3, 4, -1, -1]], dtype=np.int32)
+    assert unshared_pages(table, 16, 64)
+    prefix = np.array([[0, 1, 2, -1], [0, 4, -1, -1]], dtype=np.int32)      # page 0 in both rows
+    assert not unshared_pages(prefix, 16, 64)
+    late = np.array([[0, 1, 2, 5], [3, 4, -1, 5]], dtype=np.int32)          # page 5 aliased in the last column
+    assert not unshared_pages(late, 16, 64)
+    assert unshared_pages(late, 16, 48)                                      # beyond the reserved capacity
+    within = np.array([[7, 7, -1, -1], [3, -1, -1, -1]], dtype=np.int32)    # twice within one sequence
+    assert not unshared_pages(within, 16, 64)
 
 
 def test_table_from_csr_rejects_invalid_arguments():
