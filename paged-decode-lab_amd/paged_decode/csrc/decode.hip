@@ -1453,12 +1453,13 @@ int largest_divisor(int n, int cap) {
 // workgroup when it fits (5 or 7 heads).
 //
 // The matrix-core kernel takes 4 KV heads: at 8 KV heads, two workgroups of 4
-// heads x 2 quarters (streaming loads, quarters combined) measured 3-15% faster
-// per call than one of 8 heads x 1 quarter, from the Llama-3-8B shape
-// (18.84 -> 18.33 us) to B64 L2048 (122.3 -> 105.1 us) and 32K-context MHA
-// (98.6 -> 92.5 us at split 256); only short single-sequence calls, whose grid
-// does not fill the CUs, were slower, and those do not combine (see
-// dispatch_mfma).
+// heads x 2 quarters (quarters combined, V loads streamed when no page is
+// shared) measured faster per call than one of 8 heads x 1 quarter on every
+// shape tried on MI355X: Llama-3-8B B4 L4096 18.86 -> 17.31 us, the B16 L4096
+// batch of the reference's benchmark 50.7 -> 40.2 us, B64 L2048 122.3 ->
+// 103.8 us; with 32 KV heads, 32K-context MHA 97.2 -> 89.8 us at split 256.
+// A one-sequence call, whose grid does not fill the CUs, skips the combine
+// (see dispatch_mfma).
 void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads) {
     prm.heads_per_wg = largest_divisor(kv_heads, max_heads);
     if (prm.heads_per_wg == 1 && kv_heads <= 8) prm.heads_per_wg = kv_heads;
