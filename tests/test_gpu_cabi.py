@@ -199,7 +199,8 @@ def test_context_sharded_over_two_partial_launches():
 
 
 @pytest.mark.parametrize("batch,query_heads,kv_heads,head_dim,stride", [
-    (8, 16, 1, 64, 4), (8, 32, 4, 128, 2), (8, 48, 1, 128, 2), (8, 8, 2, 64, 1), (1, 16, 1, 64, 1)])
+    (8, 16, 1, 64, 4), (8, 32, 4, 128, 2), (8, 48, 1, 128, 2), (8, 8, 2, 64, 1), (1, 16, 1, 64, 1),
+    (8, 24, 6, 128, 2), (4, 40, 20, 64, 2)])
 def test_combined_quarter_states(batch, query_heads, kv_heads, head_dim, stride):
     """Workgroups holding several quarters of a partition store them combined.
 
@@ -210,7 +211,8 @@ def test_combined_quarter_states(batch, query_heads, kv_heads, head_dim, stride)
     every slot) then agrees with pd_decode (which reads the combined slots
     only), and both match the oracle. stride 1: a shape that keeps four states
     per partition (four quarters of a 4-head tile), and a one-sequence grid
-    smaller than the device.
+    smaller than the device. 6 KV heads make workgroups of 3 heads x 2
+    quarters; 20 make five head groups of 4 per token row (streamed loads).
     """
     announce(f"combined quarter states B{batch} Hq{query_heads}/Hkv{kv_heads} D{head_dim}")
     lib = cabi.load()

@@ -3,9 +3,10 @@
 GQA groups that do not fill a head tile (3, 5, 12, 24), groups split into
 several head tiles (24, 32: two tiles of 16 in the matrix-core kernel, three
 or four of 8 in the FP32 kernel), KV head counts that give workgroups of an
-odd number of heads (3, 5, 6, 12) or several head groups per token row (12,
-16: the streaming-load variant), each against the FP64 oracle on ragged
-lengths with empty rows.
+odd number of heads (3, 5, 6, 7, 12; 7 stays one workgroup of 7 waves) or
+several head groups per token row (12, 16, 20, and 11, whose prime count
+gives one head per workgroup: the streaming-load variants), each against
+the FP64 oracle on ragged lengths with empty rows.
 """
 import numpy as np
 import pytest
@@ -23,7 +24,8 @@ from paged_decode.workload import host_tensors  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
-HEADS = [(12, 4), (24, 1), (64, 2), (40, 8), (36, 12), (10, 5), (96, 3), (48, 16), (18, 6)]
+HEADS = [(12, 4), (24, 1), (64, 2), (40, 8), (36, 12), (10, 5), (96, 3), (48, 16), (18, 6), (14, 7), (22, 11),
+         (40, 20)]
 
 
 def problem(query_heads, kv_heads, dim, seed):
