@@ -1448,9 +1448,10 @@ int largest_divisor(int n, int cap) {
 
 // Workgroup shape: up to max_heads KV heads of the same tokens per workgroup
 // (their slices of a token row are then read together), all head tiles of
-// those heads, and as many partition quarters as fill 8 waves. A KV head
-// count with no divisor in 2..max_heads keeps its whole token row in one
-// workgroup when it fits (5 or 7 heads).
+// those heads, and as many partition quarters as fill `waves` waves (8, or
+// fewer for small grids: see dispatch_mfma). A KV head count with no divisor
+// in 2..max_heads keeps its whole token row in one workgroup when it fits
+// (5 or 7 heads in 8 waves).
 //
 // The matrix-core kernel takes 4 KV heads: at 8 KV heads, two workgroups of 4
 // heads x 2 quarters (quarters combined, V loads streamed when no page is
@@ -1460,12 +1461,12 @@ int largest_divisor(int n, int cap) {
 // 103.8 us; with 32 KV heads, 32K-context MHA 97.2 -> 89.8 us at split 256.
 // A one-sequence call, whose grid does not fill the CUs, skips the combine
 // (see dispatch_mfma).
-void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads) {
-    prm.heads_per_wg = largest_divisor(kv_heads, max_heads);
-    if (prm.heads_per_wg == 1 && kv_heads <= 8) prm.heads_per_wg = kv_heads;
-    prm.tiles_per_wg = largest_divisor(prm.head_tiles, 8 / prm.heads_per_wg);
+void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads, int waves = 8) {
+    prm.heads_per_wg = largest_divisor(kv_heads, std::min(max_heads, waves));
+    if (prm.heads_per_wg == 1 && kv_heads <= waves) prm.heads_per_wg = kv_heads;
+    prm.tiles_per_wg = largest_divisor(prm.head_tiles, waves / prm.heads_per_wg);
     const int hw_tw = prm.heads_per_wg * prm.tiles_per_wg;
-    prm.quarters_per_wg = hw_tw <= 2 ? 4 : hw_tw <= 4 ? 2 : 1;
+    prm.quarters_per_wg = hw_tw * 4 <= waves ? 4 : hw_tw * 2 <= waves ? 2 : 1;
 }
 
 dim3 partial_grid(const PartialParams& prm, int batch, int kv_heads) {
@@ -1547,10 +1548,30 @@ void plan_tiles(PartialParams& prm, int kv_heads, int max_tile, int max_heads, i
     choose_workgroup(prm, kv_heads, max_heads);
 }
 
+int64_t workgroups(const dim3& grid) { return static_cast<int64_t>(grid.x) * grid.y * grid.z; }
+
 template <typename QT, int KVF, int D>
 int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     int gt;
     plan_tiles(prm, kv_heads, 16, PD_WG_HEADS, gt);
+    // A grid of at most half as many 8-wave workgroups as CUs leaves most CUs
+    // idle, and each busy CU can keep only so many loads in flight. The same
+    // waves then go in smaller workgroups, the largest of 4, 2 or 1 waves
+    // that still gives two workgroups per CU (else 1 wave). Measured on
+    // MI355X, Llama-3-8B geometry (decode call, us):
+    //   B1 L4096 (64 workgroups of 8 waves): 12.4 -> 10.2 with 1 wave;
+    //   B1 L2048: 11.7 -> 9.9; FP8 B1 L4096: 12.6 -> 10.6-11.1;
+    //   B2 L4096 and B1 L8192 (128 workgroups): 13.2 -> 12.9 and
+    //   13.65 -> 13.1 with 2 waves.
+    // At 192 workgroups (B3 L4096) every smaller shape was slower (14.95 ->
+    // 15.3-19.0), so larger grids keep 8 waves.
+    const int cus = device_compute_units();
+    if (workgroups(partial_grid(prm, batch, kv_heads)) * 2 <= cus) {
+        const int64_t waves_total = workgroups(partial_grid(prm, batch, kv_heads)) * (partial_threads(prm) / kWave);
+        int waves = 4;
+        while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
+        choose_workgroup(prm, kv_heads, PD_WG_HEADS, waves);
+    }
     // Combining a workgroup's quarters into one state cuts the state stores
     // (written back at the kernel's end) and the merge's reads by qw; its
     // fold runs after the slowest quarter. Measured on MI355X it pays for two
@@ -1559,8 +1580,7 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
     // smaller tiles were 0.3-0.7 us slower per call. A grid smaller than the
     // CUs leaves the fold's tail exposed (B1 L4096: 12.05 us without, 12.43
     // with), so such launches keep four states per partition.
-    const dim3 grid = partial_grid(prm, batch, kv_heads);
-    const bool fills_device = static_cast<int64_t>(grid.x) * grid.y * grid.z >= device_compute_units();
+    const bool fills_device = workgroups(partial_grid(prm, batch, kv_heads)) >= cus;
     prm.combine = fills_device && (prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16));
     switch (gt) {
         case 1: return launch_mfma<QT, KVF, D, 1>(prm, batch, kv_heads, stream);
