@@ -210,6 +210,37 @@ def test_many_long_rows_and_reserved_context(dim, merge):
     np.testing.assert_array_equal(out[1].cpu().numpy(), 0.0)
 
 
+@pytest.mark.parametrize("batch,query_heads,kv_heads", [(4, 32, 8), (8, 32, 4), (16, 16, 2)])
+@pytest.mark.parametrize("shared_prefix", [False, True])
+def test_mid_size_grids(batch, query_heads, kv_heads, shared_prefix):
+    """Grids of one to two 8-wave workgroups per CU (4K context at split 256:
+    256 of them for these head counts) run in workgroups of 2 KV heads x 2
+    quarters with the quarters combined, streaming V only when no page is
+    shared. Ragged lengths with a full and an empty row, both merges, against
+    the oracle; the page-sharing hint changes no bits."""
+    announce(f"mid-size grid B{batch} Hq{query_heads}/Hkv{kv_heads} shared={shared_prefix}")
+    width, page = 256, 16
+    layout = Layout(batch, query_heads, kv_heads, 128, page, batch * width)
+    rng = np.random.default_rng(batch + kv_heads)
+    table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+    lengths = rng.integers(1, width * page + 1, size=batch).astype(np.int32)
+    lengths[0], lengths[-1] = width * page, 0
+    if shared_prefix:
+        table[1:, :64] = table[0, :64]                             # every row's first 1024 tokens are row 0's
+    for b, n in enumerate(lengths):
+        table[b, (n + page - 1) // page:] = -1
+    q, k, v = make_tensors(layout, dtype=torch.float16, seed=batch)
+    expected = oracle(q, k, v, table, lengths)
+    for merge in ("serial", "shared"):
+        plan = DecodePlan(layout, table, lengths, split_tokens=256, merge=merge)
+        assert plan.splits == 16 and plan._unshared_pages == (not shared_prefix)
+        out = plan.run(q, k, v).clone()
+        assert_parity(out.cpu().numpy(), expected, torch.float16)
+        np.testing.assert_array_equal(out[-1].cpu().numpy(), 0.0)
+        plan._unshared_pages = shared_prefix                       # the other streaming mode
+        torch.testing.assert_close(plan.run(q, k, v), out, rtol=0, atol=0)
+
+
 def test_plan_derives_the_page_sharing_hint():
     """The plan streams K/V past the caches only when its table maps no page
     twice: the shared-prefix workload keeps them cacheable, the Llama-3-8B one
