@@ -253,8 +253,7 @@ struct PartialParams {
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
     float v_scale;         // multiplies every stored numerator
     int combine;           // host only: the launch stores a workgroup's qw quarters as one state (kCombine)
-    int unshared_pages;    // host only: PD_HINT_UNSHARED_PAGES (see stream_mode)
-    int stream_mode;       // host only: 0 cached loads, 1 stream V (FP8: K), 2 stream K and V
+    int unshared_pages;    // host only: PD_HINT_UNSHARED_PAGES (see launch_mfma)
 };
 
 // Workgroup coordinates (token group, head group) in dispatch order: the
@@ -1492,23 +1491,10 @@ int partial_threads(const PartialParams& prm) {
 //     K and V 104.7, neither 112.3; a ragged B16 page-32 batch 57.0 / 62.1 /
 //     64.1). With 25% shared prefix pages (B16 page 32): neither 50.3, V only
 //     52.0, K and V 59.3.
-//   - The 2-head x 2-quarter workgroups of mid-size grids (see dispatch_mfma)
-//     read 512-byte slices: with unshared pages V only beat K and V on ragged
-//     batches
-//     (B4 L4096, lengths uniform in [0, 4096]: 13.45 vs 14.1; B16 page 32 L8192
-//     at split 128: 58.8 vs 63.2) and was within 0.25-0.45 of it on uniform
-//     ones, so those workgroups never stream K (stream_k false).
 // So the mode follows the page-sharing hint: unshared pages stream K and V
-// (4+ groups, stream_k) or V (otherwise); pages that may be shared stream V
-// (4+ groups) or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte K
-// row loads wherever 16-bit K/V would stream V.
-int stream_mode(const PartialParams& prm, int kv_heads, bool stream_k) {
-    const int groups = kv_heads / prm.heads_per_wg;
-    if (groups == 1) return 0;
-    if (prm.unshared_pages) return groups >= 4 && stream_k ? 2 : 1;
-    return groups >= 4 ? 1 : 0;
-}
-
+// (4+ groups) or V (2 groups); pages that may be shared stream V (4+ groups)
+// or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads
+// wherever 16-bit K/V would stream V.
 template <typename QT, int KVF, int D, int GT>
 int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
     const dim3 grid = partial_grid(prm, batch, kv_heads);
@@ -1516,7 +1502,8 @@ int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t s
     const size_t lds = prm.combine ? static_cast<size_t>(block.x / kWave / prm.quarters_per_wg) *
                                          (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
                                    : 0;
-    const int mode = prm.stream_mode;
+    const int groups = kv_heads / prm.heads_per_wg;
+    const int mode = groups == 1 ? 0 : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
     constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
 #define PD_LAUNCH_MFMA(MODE, COMBINE)                                                                             \
     hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE>), grid, block, lds, stream, prm)
@@ -1578,30 +1565,13 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
     //   13.65 -> 13.1 with 2 waves.
     // At 192 workgroups (B3 L4096) every smaller shape was slower (14.95 ->
     // 15.3-19.0), so larger grids keep 8 waves.
-    //
-    // Grids of one to two 8-wave workgroups per CU with 2, 4 or 8 KV heads
-    // and GQA groups of up to 8 take workgroups of 2 KV heads x 2 quarters
-    // instead (4 waves, quarters combined). Measured on MI355X (decode call,
-    // us): Llama-3-8B B4 L4096 18.57 -> 17.83, B8 L4096 30.94 -> 30.8, B8 with
-    // 4 KV heads 20.07 -> 19.27, B16 with 2 KV heads (GQA 8) 20.96 -> 19.46;
-    // FP8 B4 L4096 flat (14.37 -> 14.38). At four or more 8-wave workgroups
-    // per CU they were slower (B16 L4096 57.0 -> 58.2, B32 L4096 106.2 ->
-    // 108.0, B64 L2048 104.7 -> 107.4), and a grid under one per CU (B3 L4096)
-    // went 14.93 -> 15.5.
     const int cus = device_compute_units();
-    const int64_t wg8 = workgroups(partial_grid(prm, batch, kv_heads));
-    if (wg8 * 2 <= cus) {  // small grid
-        const int64_t waves_total = wg8 * (partial_threads(prm) / kWave);
+    if (workgroups(partial_grid(prm, batch, kv_heads)) * 2 <= cus) {
+        const int64_t waves_total = workgroups(partial_grid(prm, batch, kv_heads)) * (partial_threads(prm) / kWave);
         int waves = 4;
         while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
         choose_workgroup(prm, kv_heads, PD_WG_HEADS, waves);
     }
-    bool stream_k = true;
-    if (wg8 >= cus && wg8 <= 2 * cus && (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
-        choose_workgroup(prm, kv_heads, 2, 4);
-        stream_k = false;
-    }
-    prm.stream_mode = stream_mode(prm, kv_heads, stream_k);
     // Combining a workgroup's quarters into one state cuts the state stores
     // (written back at the kernel's end) and the merge's reads by qw; its
     // fold runs after the slowest quarter. Measured on MI355X it pays for two
