@@ -10,8 +10,10 @@
 //     uses them for every query head of the tile (the GQA group, padded to
 //     GT = 1/2/4/8/16 heads), and stores one (m, l, n[D]) state per query head
 //     in slot 4 * partition + quarter of the workspace. A workgroup gathers up
-//     to eight KV heads of the same tokens (their head slices of a token row
-//     are then read together) plus enough quarters to make eight waves. Waves
+//     to four KV heads (eight in the FP32 kernel) of the same tokens (their
+//     head slices of a token row are then read together) plus enough quarters
+//     to make eight waves, or fewer waves when eight-wave workgroups would
+//     leave most CUs idle. Waves
 //     do not synchronise while they stream; where a workgroup holds several
 //     quarters of one partition (few KV heads), one barrier at the end lets
 //     the first quarter fold the others into a single state. Partitions that
@@ -1459,8 +1461,8 @@ int largest_divisor(int n, int cap) {
 // shape tried on MI355X: Llama-3-8B B4 L4096 18.86 -> 17.31 us, the B16 L4096
 // batch of the reference's benchmark 50.7 -> 40.2 us, B64 L2048 122.3 ->
 // 103.8 us; with 32 KV heads, 32K-context MHA 97.2 -> 89.8 us at split 256.
-// A one-sequence call, whose grid does not fill the CUs, skips the combine
-// (see dispatch_mfma).
+// Grids that would leave most CUs idle take smaller workgroups instead, and
+// grids smaller than the device skip the combine (see dispatch_mfma).
 void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads, int waves = 8) {
     prm.heads_per_wg = largest_divisor(kv_heads, std::min(max_heads, waves));
     if (prm.heads_per_wg == 1 && kv_heads <= waves) prm.heads_per_wg = kv_heads;
