@@ -256,6 +256,7 @@ struct PartialParams {
     float v_scale;         // multiplies every stored numerator
     int combine;           // host only: the launch stores a workgroup's qw quarters as one state (kCombine)
     int unshared_pages;    // host only: PD_HINT_UNSHARED_PAGES (see launch_mfma)
+    int mid_grid;          // host only: 2-head x 2-quarter workgroups of a mid-size grid (see dispatch_mfma)
 };
 
 // Workgroup coordinates (token group, head group) in dispatch order: the
@@ -1493,9 +1494,12 @@ int partial_threads(const PartialParams& prm) {
 //     K and V 104.7, neither 112.3; a ragged B16 page-32 batch 57.0 / 62.1 /
 //     64.1). With 25% shared prefix pages (B16 page 32): neither 50.3, V only
 //     52.0, K and V 59.3.
+//   - The 2-head x 2-quarter workgroups of mid-size grids (see dispatch_mfma):
+//     with 2 KV heads, one head group, streaming V anyway took B16 L4096
+//     (GQA 8) from 19.75 to 18.81 us per call.
 // So the mode follows the page-sharing hint: unshared pages stream K and V
-// (4+ groups) or V (2 groups); pages that may be shared stream V (4+ groups)
-// or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads
+// (4+ groups) or V (2 groups, or one in a mid-size grid); pages that may be
+// shared stream V (4+ groups) or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads
 // wherever 16-bit K/V would stream V.
 template <typename QT, int KVF, int D, int GT>
 int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
@@ -1505,7 +1509,8 @@ int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t s
                                          (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
                                    : 0;
     const int groups = kv_heads / prm.heads_per_wg;
-    const int mode = groups == 1 ? 0 : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+    const int mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
+                     : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
     constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
 #define PD_LAUNCH_MFMA(MODE, COMBINE)                                                                             \
     hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE>), grid, block, lds, stream, prm)
@@ -1567,12 +1572,28 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
     //   13.65 -> 13.1 with 2 waves.
     // At 192 workgroups (B3 L4096) every smaller shape was slower (14.95 ->
     // 15.3-19.0), so larger grids keep 8 waves.
+    //
+    // Grids of one to two 8-wave workgroups per CU with 2 or 4 KV heads and
+    // GQA groups of up to 8 take workgroups of 2 KV heads x 2 quarters instead
+    // (4 waves, quarters combined). Measured on MI355X by graph replay of 200
+    // calls, N(0,1) data, K/V sets allocated in either order (decode call,
+    // us): B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8 L4096
+    // with 4 KV heads 20.05 -> 19.1-19.2. With 8 KV heads the same harness
+    // measured Llama-3-8B B4 L4096 18.0-18.4 -> 17.4-17.6, but the benchmark
+    // itself measured the call flat (17.26 -> 17.25) and the partition kernel
+    // slower (13.72 -> 14.1), so 8 KV heads keep 8-wave workgroups. B3 L4096
+    // (192 workgroups) was slower with smaller workgroups of any kind (14.74
+    // -> 15.05).
     const int cus = device_compute_units();
-    if (workgroups(partial_grid(prm, batch, kv_heads)) * 2 <= cus) {
-        const int64_t waves_total = workgroups(partial_grid(prm, batch, kv_heads)) * (partial_threads(prm) / kWave);
+    const int64_t wg8 = workgroups(partial_grid(prm, batch, kv_heads));
+    if (wg8 * 2 <= cus) {  // small grid
+        const int64_t waves_total = wg8 * (partial_threads(prm) / kWave);
         int waves = 4;
         while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
         choose_workgroup(prm, kv_heads, PD_WG_HEADS, waves);
+    } else if (wg8 >= cus && wg8 <= 2 * cus && (kv_heads == 2 || kv_heads == 4) && gt <= 8) {
+        choose_workgroup(prm, kv_heads, 2, 4);
+        prm.mid_grid = 1;
     }
     // Combining a workgroup's quarters into one state cuts the state stores
     // (written back at the kernel's end) and the merge's reads by qw; its

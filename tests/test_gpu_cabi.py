@@ -199,8 +199,8 @@ def test_context_sharded_over_two_partial_launches():
 
 
 @pytest.mark.parametrize("batch,query_heads,kv_heads,head_dim,stride", [
-    (8, 16, 1, 64, 4), (8, 32, 4, 128, 2), (8, 48, 1, 128, 2), (8, 8, 2, 64, 1), (1, 16, 1, 64, 1),
-    (8, 24, 6, 128, 2), (4, 40, 20, 64, 2)])
+    (8, 16, 1, 64, 4), (8, 32, 4, 128, 2), (8, 48, 1, 128, 2), (8, 4, 1, 64, 1), (1, 16, 1, 64, 1),
+    (8, 24, 6, 128, 2), (4, 40, 20, 64, 2), (8, 8, 2, 64, 2)])
 def test_combined_quarter_states(batch, query_heads, kv_heads, head_dim, stride):
     """Workgroups holding several quarters of a partition store them combined.
 
@@ -212,7 +212,9 @@ def test_combined_quarter_states(batch, query_heads, kv_heads, head_dim, stride)
     only), and both match the oracle. stride 1: a shape that keeps four states
     per partition (four quarters of a 4-head tile), and a one-sequence grid
     smaller than the device. 6 KV heads make workgroups of 3 heads x 2
-    quarters; 20 make five head groups of 4 per token row (streamed loads).
+    quarters; 20 make five head groups of 4 per token row (streamed loads);
+    2 KV heads at 320 8-wave workgroups take the 2-head x 2-quarter
+    workgroups of mid-size grids.
     """
     announce(f"combined quarter states B{batch} Hq{query_heads}/Hkv{kv_heads} D{head_dim}")
     lib = cabi.load()

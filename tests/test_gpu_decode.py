@@ -213,11 +213,12 @@ def test_many_long_rows_and_reserved_context(dim, merge):
 @pytest.mark.parametrize("batch,query_heads,kv_heads", [(4, 32, 8), (8, 32, 4), (16, 16, 2)])
 @pytest.mark.parametrize("shared_prefix", [False, True])
 def test_mid_size_grids(batch, query_heads, kv_heads, shared_prefix):
-    """Grids of one to two workgroups per CU (4K context at split 256: 256
-    8-wave workgroups for these head counts, quarters combined) with ragged
-    lengths, a full and an empty row, and prefix pages shared or not: both
-    merges against the oracle, and the page-sharing hint (which switches the
-    streamed loads) changes no bits."""
+    """Grids of one to two 8-wave workgroups per CU (4K context at split 256:
+    256 of them for these head counts, quarters combined): 8 KV heads in
+    8-wave workgroups, 4 and 2 in workgroups of 2 KV heads x 2 quarters.
+    Ragged lengths with a full and an empty row, prefix pages shared or not,
+    both merges, against the oracle; the page-sharing hint (which switches
+    the streamed loads) changes no bits."""
     announce(f"mid-size grid B{batch} Hq{query_heads}/Hkv{kv_heads} shared={shared_prefix}")
     width, page = 256, 16
     layout = Layout(batch, query_heads, kv_heads, 128, page, batch * width)
