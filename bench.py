@@ -8,8 +8,11 @@ FP32 accumulate and output).
 
 Protocol
 * Inputs are resident in HBM before timing. K/V are replicated into enough
-  buffer sets to cover >= 512 MiB and every step uses the next set, so a step
-  cannot be served from the 256 MB Infinity Cache.
+  buffer sets to cover >= 2 GiB and every step uses the next set, so a step
+  cannot be served from the 256 MB Infinity Cache. (A rotation over exactly
+  512 MiB is not enough: at the Llama-3-8B shape, eight 64 MiB sets ran 17.3
+  us per call against 18.0-18.3 us with 9 to 32 sets, part of each set still
+  being cache-resident when it came round again.)
 * Correctness gate first: the GPU output is compared with the C FP32 split-K
   restatement on the same inputs (this is also the CPU-baseline leg); no
   timing is reported if it fails.
@@ -49,7 +52,7 @@ sys.path.insert(0, str(REPO / "paged-decode-lab_amd"))
 
 METRIC = "µs/decode call and achieved KV HBM GB/s (% of peak), 1 MI355X"
 PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E, public specification
-ROTATION_BYTES = 512 << 20      # > 2x the 256 MB Infinity Cache
+ROTATION_BYTES = 2 << 30        # 8x the 256 MB Infinity Cache
 PROBE_BYTES = 512 << 20         # stream-copy probe: bytes read (and written) per pass
 
 

@@ -1573,17 +1573,15 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
     // At 192 workgroups (B3 L4096) every smaller shape was slower (14.95 ->
     // 15.3-19.0), so larger grids keep 8 waves.
     //
-    // Grids of one to two 8-wave workgroups per CU with 2 or 4 KV heads and
+    // Grids of one to two 8-wave workgroups per CU with 2, 4 or 8 KV heads and
     // GQA groups of up to 8 take workgroups of 2 KV heads x 2 quarters instead
     // (4 waves, quarters combined). Measured on MI355X by graph replay of 200
-    // calls, N(0,1) data, K/V sets allocated in either order (decode call,
-    // us): B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8 L4096
-    // with 4 KV heads 20.05 -> 19.1-19.2. With 8 KV heads the same harness
-    // measured Llama-3-8B B4 L4096 18.0-18.4 -> 17.4-17.6, but the benchmark
-    // itself measured the call flat (17.26 -> 17.25) and the partition kernel
-    // slower (13.72 -> 14.1), so 8 KV heads keep 8-wave workgroups. B3 L4096
-    // (192 workgroups) was slower with smaller workgroups of any kind (14.74
-    // -> 15.05).
+    // calls, N(0,1) data, K/V sets rotated past the Infinity Cache (decode
+    // call, us): Llama-3-8B B4 L4096 18.0-18.4 -> 17.4-17.6, B8 L4096 29.45
+    // -> 28.54, B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8
+    // L4096 with 4 KV heads 20.05 -> 19.1-19.2; ragged B4 batches within
+    // 0.1-0.25. B3 L4096 (192 workgroups) was slower with smaller workgroups
+    // of any kind (14.74 -> 15.05).
     const int cus = device_compute_units();
     const int64_t wg8 = workgroups(partial_grid(prm, batch, kv_heads));
     if (wg8 * 2 <= cus) {  // small grid
@@ -1591,7 +1589,7 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
         int waves = 4;
         while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
         choose_workgroup(prm, kv_heads, PD_WG_HEADS, waves);
-    } else if (wg8 >= cus && wg8 <= 2 * cus && (kv_heads == 2 || kv_heads == 4) && gt <= 8) {
+    } else if (wg8 >= cus && wg8 <= 2 * cus && (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
         choose_workgroup(prm, kv_heads, 2, 4);
         prm.mid_grid = 1;
     }

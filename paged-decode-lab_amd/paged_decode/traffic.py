@@ -1,7 +1,7 @@
 """HBM bytes per partition launch, from two ``rocprofv3 --pmc`` passes.
 
 ``run`` is the program the counter passes profile: it builds a DecodePlan for a
-named workload, replicates K/V into buffer sets covering >= 512 MiB (so no
+named workload, replicates K/V into buffer sets covering >= 2 GiB (so no
 launch is served from the 256 MB Infinity Cache), launches the partition kernel
 ``--launches`` times round-robin over the sets, then runs a plain elementwise
 copy (``torch.neg`` of a float32 tensor, out of place) of a known size. The
@@ -30,7 +30,7 @@ from pathlib import Path
 
 PACKAGE_ROOT = Path(__file__).resolve().parent.parent
 REPO = PACKAGE_ROOT.parent
-ROTATION_BYTES = 512 << 20
+ROTATION_BYTES = 2 << 30
 COPY_BYTES = 256 << 20
 SOURCES = ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "include/paged_decode.h")
 

@@ -214,8 +214,8 @@ def test_many_long_rows_and_reserved_context(dim, merge):
 @pytest.mark.parametrize("shared_prefix", [False, True])
 def test_mid_size_grids(batch, query_heads, kv_heads, shared_prefix):
     """Grids of one to two 8-wave workgroups per CU (4K context at split 256:
-    256 of them for these head counts, quarters combined): 8 KV heads in
-    8-wave workgroups, 4 and 2 in workgroups of 2 KV heads x 2 quarters.
+    256 of them for these head counts) run in workgroups of 2 KV heads x 2
+    quarters with the quarters combined.
     Ragged lengths with a full and an empty row, prefix pages shared or not,
     both merges, against the oracle; the page-sharing hint (which switches
     the streamed loads) changes no bits."""
