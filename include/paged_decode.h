@@ -79,15 +79,21 @@ enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
 #define PD_SHARED_MERGE_MAX_PARTS 4096
 
 /*
- * Hints of the _ex entries (a bit set; 0 = none). They never change results,
- * only how K/V loads use the caches:
+ * Hints of the _ex entries (a bit set; 0 = none). They only choose how the
+ * partition kernel runs, never what it computes:
  *   PD_HINT_UNSHARED_PAGES: no physical page holds live tokens of more than
  *   one sequence (no shared prefix pages). The partition kernel may then
  *   stream K/V past the caches, which is faster when nothing is read twice;
  *   without it, pages that several sequences share stay cacheable. Passing it
- *   for a batch that does share pages is still correct, only slower.
+ *   for a batch that does share pages is still correct, only slower. Results
+ *   are bit-identical with or without it.
+ *   PD_HINT_RAGGED_LENGTHS: the sequence lengths differ widely (live tokens
+ *   under about 80% of batch x longest). Grids of up to eight 8-wave
+ *   workgroups per CU then run in smaller workgroups, which balance ragged
+ *   batches better. Results agree to FP32 rounding (the quarters of a
+ *   partition are folded in another grouping); a wrong hint is only slower.
  */
-enum pd_hint { PD_HINT_NONE = 0, PD_HINT_UNSHARED_PAGES = 1 };
+enum pd_hint { PD_HINT_NONE = 0, PD_HINT_UNSHARED_PAGES = 1, PD_HINT_RAGGED_LENGTHS = 2 };
 
 /*
  * Full decode: partition kernel then merge kernel, both on `stream`.
@@ -230,7 +236,7 @@ const char* pd_status_string(int status);
  * pd_decode_merge takes the lengths; 6: KV-cache append; 7: BF16 and FP8 K/V,
  * pd_decode_ex; 8: pd_table_from_csr; 9: quarters of one workgroup stored
  * combined, the others as empty states; 10: hints argument of the _ex
- * entries). */
+ * entries; 11: PD_HINT_RAGGED_LENGTHS). */
 int pd_abi_version(void);
 
 #ifdef __cplusplus

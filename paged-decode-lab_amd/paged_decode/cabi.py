@@ -26,6 +26,7 @@ PD_MERGE_SHARED = 1
 PD_SHARED_MERGE_MAX_PARTS = 4096  # states (4 per split)
 PD_HINT_NONE = 0
 PD_HINT_UNSHARED_PAGES = 1
+PD_HINT_RAGGED_LENGTHS = 2
 PD_ERR_HINT = 7
 
 _P = ctypes.c_void_p

@@ -257,6 +257,7 @@ struct PartialParams {
     int combine;           // host only: the launch stores a workgroup's qw quarters as one state (kCombine)
     int unshared_pages;    // host only: PD_HINT_UNSHARED_PAGES (see launch_mfma)
     int mid_grid;          // host only: 2-head x 2-quarter workgroups of a mid-size grid (see dispatch_mfma)
+    int ragged_lengths;    // host only: PD_HINT_RAGGED_LENGTHS
 };
 
 // Workgroup coordinates (token group, head group) in dispatch order: the
@@ -1581,7 +1582,13 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
     // -> 28.54, B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8
     // L4096 with 4 KV heads 20.05 -> 19.1-19.2; ragged B4 batches within
     // 0.1-0.25. B3 L4096 (192 workgroups) was slower with smaller workgroups
-    // of any kind (14.74 -> 15.05).
+    // of any kind (14.74 -> 15.05). Larger grids keep 8 waves when lengths
+    // are uniform (B16 L4096 55.1 -> 56.9, B32 L4096 105.7 -> 109.1) but
+    // not when they are ragged (PD_HINT_RAGGED_LENGTHS): then up to eight
+    // 8-wave workgroups per CU take the smaller ones (B16 with lengths
+    // uniform in [0, 4096] 37.8 -> 33.3, B32 65.1 -> 59.7; the reference's
+    // B16 L4096 batch 47.6 -> 44.0 in the benchmark). At sixteen per CU (a
+    // B16 page-32 L8192 batch at split 128) it was flat, so those keep 8.
     const int cus = device_compute_units();
     const int64_t wg8 = workgroups(partial_grid(prm, batch, kv_heads));
     if (wg8 * 2 <= cus) {  // small grid
@@ -1589,7 +1596,8 @@ int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t strea
         int waves = 4;
         while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
         choose_workgroup(prm, kv_heads, PD_WG_HEADS, waves);
-    } else if (wg8 >= cus && wg8 <= 2 * cus && (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
+    } else if (wg8 >= cus && wg8 <= (prm.ragged_lengths ? 8 : 2) * static_cast<int64_t>(cus) &&
+               (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
         choose_workgroup(prm, kv_heads, 2, 4);
         prm.mid_grid = 1;
     }
@@ -1646,6 +1654,7 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
                 int splits, int split_tokens, int hints, hipStream_t stream, int* state_stride = nullptr) {
     PartialParams prm{};
     prm.unshared_pages = (hints & PD_HINT_UNSHARED_PAGES) != 0;
+    prm.ragged_lengths = (hints & PD_HINT_RAGGED_LENGTHS) != 0;
     prm.q = q;
     prm.k = k;
     prm.v = v;
@@ -1711,7 +1720,9 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
     return launch_status();
 }
 
-int check_hints(int hints) { return (hints & ~PD_HINT_UNSHARED_PAGES) == 0 ? PD_OK : PD_ERR_HINT; }
+int check_hints(int hints) {
+    return (hints & ~(PD_HINT_UNSHARED_PAGES | PD_HINT_RAGGED_LENGTHS)) == 0 ? PD_OK : PD_ERR_HINT;
+}
 
 int check_merge(const float* numerator, const float* stats, const float* out, const int32_t* lengths, int batch,
                 int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
@@ -1899,6 +1910,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 10; }
+int pd_abi_version(void) { return 11; }
 
 }  // extern "C"

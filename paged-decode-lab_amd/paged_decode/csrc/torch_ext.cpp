@@ -101,13 +101,15 @@ void check_output(const torch::Tensor& q, const torch::Tensor& out, int64_t merg
 
 // PD_HINT_UNSHARED_PAGES when the caller knows no physical page is shared
 // between sequences (the plan derives it from its metadata).
-int hints(bool unshared_pages) { return unshared_pages ? PD_HINT_UNSHARED_PAGES : PD_HINT_NONE; }
+int hints(bool unshared_pages, bool ragged_lengths) {
+    return (unshared_pages ? PD_HINT_UNSHARED_PAGES : 0) | (ragged_lengths ? PD_HINT_RAGGED_LENGTHS : 0);
+}
 
 }  // namespace
 
 void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
             torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t split_tokens,
-            int64_t merge_mode, double k_scale, double v_scale, bool unshared_pages) {
+            int64_t merge_mode, double k_scale, double v_scale, bool unshared_pages, bool ragged_lengths) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     check_output(q, out, merge_mode, s.splits);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
@@ -117,14 +119,14 @@ void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor tab
                               out.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
                               static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
                               static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
-                              static_cast<int>(split_tokens), static_cast<int>(merge_mode), hints(unshared_pages),
-                              current_stream(q)));
+                              static_cast<int>(split_tokens), static_cast<int>(merge_mode),
+                              hints(unshared_pages, ragged_lengths), current_stream(q)));
 }
 
 // Partition stage alone (first launch of decode); used to time that kernel.
 void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
              torch::Tensor numerator, torch::Tensor stats, int64_t split_tokens, double k_scale, double v_scale,
-             bool unshared_pages) {
+             bool unshared_pages, bool ragged_lengths) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     check_status(pd_decode_partial_ex(
@@ -133,7 +135,7 @@ void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor ta
         numerator.data_ptr<float>(), stats.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
         static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
         static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
-        static_cast<int>(split_tokens), hints(unshared_pages), current_stream(q)));
+        static_cast<int>(split_tokens), hints(unshared_pages, ragged_lengths), current_stream(q)));
 }
 
 // Merge stage alone (second launch of decode); lengths, page_size,
@@ -234,10 +236,11 @@ PYBIND11_MODULE(_C, m) {
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("table"), py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("out"),
           py::arg("split_tokens"), py::arg("merge_mode"), py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0,
-          py::arg("unshared_pages") = false);
+          py::arg("unshared_pages") = false, py::arg("ragged_lengths") = false);
     m.def("partial", &partial, "Partition stage only", py::arg("q"), py::arg("k"), py::arg("v"), py::arg("table"),
           py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("split_tokens"),
-          py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0, py::arg("unshared_pages") = false);
+          py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0, py::arg("unshared_pages") = false,
+          py::arg("ragged_lengths") = false);
     m.def("merge", &merge, "Merge stage only");
     m.def("append_kv", &append_kv, "Paged KV-cache append");
     m.def("table_from_csr", &table_from_csr, "CSR page lists to page table and lengths on the device",

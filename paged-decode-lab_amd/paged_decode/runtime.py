@@ -102,6 +102,7 @@ class DecodePlan:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self._table_cpu, self._lengths_cpu = table, lengths
         self._unshared_pages = unshared_pages(table, layout.page_size, capacity)
+        self._ragged_lengths = ragged_lengths(lengths)
         self._table = torch.tensor(table, device=self.device)
         self._lengths = torch.tensor(lengths, device=self.device)
         shape = (layout.batch, layout.query_heads, self.splits * _STATES_PER_SPLIT)
@@ -144,6 +145,7 @@ class DecodePlan:
         self._lengths.copy_(torch.from_numpy(lengths))
         self._table_cpu, self._lengths_cpu = table, lengths
         self._unshared_pages = unshared_pages(table, self.layout.page_size, self.context_capacity)
+        self._ragged_lengths = ragged_lengths(lengths)
         self.max_context = longest
 
     def refresh_csr(self, indptr, indices, last_page_len, overflow=None):
@@ -159,8 +161,9 @@ class DecodePlan:
         ``overflow`` tensor is given (it is never cleared; zero it first).
         Page ids are not validated here; the kernel skips ids outside the
         cache. ``max_context`` keeps the value of the last host-side metadata.
-        The plan no longer knows whether pages are shared between sequences,
-        so later runs keep K/V cacheable (see ``unshared_pages``).
+        The plan no longer knows whether pages are shared between sequences
+        or how ragged the lengths are, so later runs keep K/V cacheable and
+        the default workgroups (see ``unshared_pages``, ``ragged_lengths``).
         """
         for t in (indptr, indices, last_page_len):
             if t.device != self.device or t.dtype != torch.int32 or not t.is_contiguous():
@@ -173,6 +176,7 @@ class DecodePlan:
         self._extension.table_from_csr(indptr, indices, last_page_len, self._table, self._lengths, overflow,
                                        self.layout.page_size, self.context_capacity)
         self._unshared_pages = False
+        self._ragged_lengths = False
 
     def append(self, k_cache, v_cache, k_new, v_new):
         """Append new tokens at the plan's current lengths and advance them on the device.
@@ -225,14 +229,15 @@ class DecodePlan:
         self._check(q, k, v, k_scale, v_scale)
         self._extension.decode(q, k, v, self._table, self._lengths, self._numerator, self._stats,
                                self._out, self.split_tokens, self._merge_mode, float(k_scale), float(v_scale),
-                               self._unshared_pages)
+                               self._unshared_pages, self._ragged_lengths)
         return self._out
 
     def run_partial(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
         """Partition stage only (fills the workspace); for stage timing."""
         self._check(q, k, v, k_scale, v_scale)
         self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
-                                self.split_tokens, float(k_scale), float(v_scale), self._unshared_pages)
+                                self.split_tokens, float(k_scale), float(v_scale), self._unshared_pages,
+                                self._ragged_lengths)
 
     def run_merge(self):
         """Merge stage only, from the current workspace; returns the borrowed output."""
@@ -255,6 +260,19 @@ def unshared_pages(table, page_size, capacity):
     ids = np.asarray(table)[:, :columns].ravel()
     ids = ids[ids >= 0]
     return bool(np.unique(ids).size == ids.size)
+
+
+def ragged_lengths(lengths):
+    """True when the batch's live tokens are under 80% of batch x longest
+    sequence (lengths spread widely, or some sequences empty).
+
+    The plan passes this as the library's ragged-lengths hint: larger grids
+    then run in smaller workgroups, which balance ragged batches better and
+    uniform ones worse. Results agree to FP32 rounding either way.
+    """
+    lengths = np.asarray(lengths, dtype=np.int64)
+    longest = int(lengths.max(initial=0))
+    return bool(longest > 0 and int(lengths.sum()) < 0.8 * lengths.size * longest)
 
 
 def _token_batch(k_new, v_new, layout):

@@ -242,6 +242,33 @@ def test_mid_size_grids(batch, query_heads, kv_heads, shared_prefix):
         torch.testing.assert_close(plan.run(q, k, v), out, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("batch,query_heads,kv_heads", [(16, 32, 8), (64, 16, 2)])
+def test_ragged_lengths_hint(batch, query_heads, kv_heads):
+    """Ragged batches of four 8-wave workgroups per CU (1024 at split 256):
+    the plan sets the ragged-lengths hint and runs them in 2-head x 2-quarter
+    workgroups; with the hint off they keep 8 waves. Both match the oracle
+    and agree with each other to FP32 rounding."""
+    announce(f"ragged-lengths hint B{batch} Hq{query_heads}/Hkv{kv_heads}")
+    width, page = 256, 16
+    layout = Layout(batch, query_heads, kv_heads, 128, page, batch * width)
+    rng = np.random.default_rng(40 + kv_heads)
+    table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+    lengths = rng.integers(0, width * page + 1, size=batch).astype(np.int32)
+    lengths[0] = width * page
+    for b, n in enumerate(lengths):
+        table[b, (n + page - 1) // page:] = -1
+    q, k, v = make_tensors(layout, dtype=torch.float16, seed=kv_heads)
+    expected = oracle(q, k, v, table, lengths)
+    plan = DecodePlan(layout, table, lengths, split_tokens=256)
+    assert plan._ragged_lengths
+    hinted = plan.run(q, k, v).clone()
+    assert_parity(hinted.cpu().numpy(), expected, torch.float16)
+    plan._ragged_lengths = False
+    plain = plan.run(q, k, v)
+    assert_parity(plain.cpu().numpy(), expected, torch.float16)
+    torch.testing.assert_close(hinted, plain, rtol=1e-5, atol=1e-6)
+
+
 def test_plan_derives_the_page_sharing_hint():
     """The plan streams K/V past the caches only when its table maps no page
     twice: the shared-prefix workload keeps them cacheable, the Llama-3-8B one

@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 10
+    assert lib.pd_abi_version() == 11
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -95,7 +95,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != 10) return 1;
+    if (pd_abi_version() != 11) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
@@ -104,7 +104,8 @@ int main(void) {
                      4, 1, 8, 128, 16, 256, 1024, NULL) != PD_ERR_NULL_POINTER) return 4;
     if (strstr(pd_status_string(PD_ERR_SHAPE), "dimension") == NULL) return 5;
     if (pd_table_from_csr(NULL, NULL, NULL, NULL, NULL, NULL, 4, 256, 16, 4096, NULL) != PD_ERR_NULL_POINTER) return 6;
-    if (strstr(pd_status_string(PD_ERR_HINT), "hint") == NULL || PD_HINT_UNSHARED_PAGES != 1) return 7;
+    if (strstr(pd_status_string(PD_ERR_HINT), "hint") == NULL || PD_HINT_UNSHARED_PAGES != 1 ||
+        PD_HINT_RAGGED_LENGTHS != 2) return 7;
     puts("ok");
     return 0;
 }
@@ -247,9 +248,10 @@ def test_extended_entry_rejects_formats_and_scales(q_dtype, kv_dtype, k_scale, v
     assert status == cabi.PD_ERR_DTYPE
 
 
-@pytest.mark.parametrize("hints", [2, 4, -1, 1 << 30])
+@pytest.mark.parametrize("hints", [4, 8, 7, -1, 1 << 30])
 def test_extended_entries_reject_unknown_hints(hints):
-    """Only PD_HINT_UNSHARED_PAGES is defined; other bits are rejected before any launch."""
+    """Only PD_HINT_UNSHARED_PAGES and PD_HINT_RAGGED_LENGTHS are defined; other bits are rejected before
+    any launch."""
     lib = cabi.load()
     ptrs, _keep = fake(8)
     f16 = cabi.PD_DTYPE_F16
@@ -260,6 +262,21 @@ def test_extended_entries_reject_unknown_hints(hints):
                                       ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, hints, None)
     assert status == cabi.PD_ERR_HINT
     assert "hint" in cabi.status_string(lib, cabi.PD_ERR_HINT)
+
+
+def test_ragged_lengths_hint_follows_the_lengths():
+    """The plan's ragged-lengths hint: live tokens under 80% of batch x longest."""
+    from paged_decode.runtime import ragged_lengths
+
+    assert not ragged_lengths(np.array([4096, 4096, 4096, 4096]))
+    assert not ragged_lengths(np.array([0, 0]))                      # no tokens at all
+    assert not ragged_lengths(np.array([100, 90, 85, 80]))           # 355 of 400: 89%
+    assert ragged_lengths(np.array([100, 60, 60, 60]))               # 280 of 400: 70%
+    assert ragged_lengths(np.array([4096, 0]))
+    assert not ragged_lengths(np.array([5, 4, 4, 4, 4]))             # 21 of 25: exactly 84%
+    assert not ragged_lengths(np.array([5, 4, 4, 4, 3]))             # 20 of 25: 80%, not under it
+    assert ragged_lengths(np.array([5, 4, 4, 4, 2]))                 # 19 of 25: 76%
+    assert not ragged_lengths(np.array([5, 4, 4, 4, 3])[:4])         # 17 of 20: 85%
 
 
 def test_page_sharing_hint_follows_the_table():
