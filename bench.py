@@ -35,14 +35,23 @@ Protocol
   SDPA, or an FP32 eager softmax) timed on the same inputs, and SDPA alone on
   pre-gathered tensors.
 
-Prints one JSON line.
+Prints one JSON line. The record also carries the provenance the reference's
+report keeps (benchmarks/bench_decode.py:47-63,137-170): git revision and
+dirty flag (null where the tree has no git metadata), library build digests,
+the software environment, a device snapshot before and after the timed
+protocol (rocm-smi, or "unavailable"), the raw per-repetition samples and the
+trial order of the 30 x 20 protocol, and steady-state device memory.
+--output PATH also writes the record, indented, to a new file (an existing
+file is never overwritten).
 """
 import argparse
+import datetime
 import json
 import math
 import os
+import platform
 import random
-import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -72,6 +81,8 @@ def parse_args():
     p.add_argument("--compare", type=int, default=20,
                    help="calls per dense PyTorch comparison row (0 skips them)")
     p.add_argument("--quiet", action="store_true", help="suppress progress lines on stderr")
+    p.add_argument("--output", type=Path, default=None,
+                   help="also write the record to this new file (refuses to overwrite)")
     return p.parse_args()
 
 
@@ -94,6 +105,46 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def revision():
+    """git commit and dirty flag of this tree, or nulls where there is no git metadata."""
+    try:
+        sha = subprocess.check_output(["git", "rev-parse", "HEAD"], cwd=REPO, text=True,
+                                      stderr=subprocess.DEVNULL, timeout=10).strip()
+        dirty = bool(subprocess.check_output(["git", "status", "--porcelain", "--untracked-files=no"], cwd=REPO,
+                                             text=True, stderr=subprocess.DEVNULL, timeout=10).strip())
+        return {"sha": sha, "dirty": dirty}
+    except (OSError, subprocess.SubprocessError):
+        return {"sha": None, "dirty": None, "note": "no git metadata in this tree"}
+
+
+def rocm_version():
+    try:
+        return Path(os.environ.get("ROCM_PATH", "/opt/rocm"), ".info", "version").read_text().strip()
+    except OSError:
+        return None
+
+
+def device_snapshot():
+    """Temperature, power, clocks and use of the GPUs, from rocm-smi, or "unavailable"."""
+    try:
+        out = subprocess.check_output(["rocm-smi", "--showtemp", "--showpower", "--showclocks", "--showuse",
+                                       "--json"], text=True, stderr=subprocess.DEVNULL, timeout=15)
+        return json.loads(out)
+    except (OSError, subprocess.SubprocessError, ValueError):
+        return "unavailable"
+
+
+def environment(torch):
+    props = torch.cuda.get_device_properties(0)
+    return {
+        "python": platform.python_version(), "platform": platform.platform(), "numpy": __import__("numpy").__version__,
+        "torch": torch.__version__, "torch_hip_build": getattr(torch.version, "hip", None), "rocm": rocm_version(),
+        "gpu": props.name, "arch": getattr(props, "gcnArchName", None), "compute_units": props.multi_processor_count,
+        "gpu_memory_bytes": props.total_memory, "host_cores_available": len(os.sched_getaffinity(0)),
+        "hip_visible_devices": os.environ.get("HIP_VISIBLE_DEVICES"),
+    }
 
 
 def recorded_traffic(workload, digest):
@@ -134,6 +185,9 @@ def main():
         return 2
     if args.steps <= 0 or args.warmup < 0:
         print("--steps must be positive and --warmup non-negative", file=sys.stderr)
+        return 2
+    if args.output is not None and args.output.exists():
+        print(f"--output {args.output} exists; bench.py never overwrites a report", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -276,13 +330,17 @@ def main():
         runners[f"{m}/graph_warm"] = lambda i, m=m: graphs[m][0].replay()
     rng = random.Random(w.seed)
     samples = {name: ([], []) for name in runners}
+    trial_order = []
+    snapshot_before = device_snapshot()
     for _ in range(args.repetitions):
         order = list(runners)
         rng.shuffle(order)
+        trial_order.append(order)
         for name in order:
             dev, wall = time_region(torch, runners[name], args.inner)
             samples[name][0].append(dev / args.inner)
             samples[name][1].append(wall / args.inner)
+    snapshot_after = device_snapshot()
     protocol = {}
     for name, (dev, wall) in samples.items():
         s = summarize(dev, wall, L.batch)
@@ -340,6 +398,11 @@ def main():
         log(args, "comparison: " + ", ".join(f"{k} {v['us_per_call']} us" for k, v in comparison.items()))
 
     digest = source_digest()
+    from paged_decode import _build
+    memory = {"allocated_bytes": torch.cuda.memory_allocated(device),
+              "max_allocated_bytes": torch.cuda.max_memory_allocated(device),
+              "reserved_bytes": torch.cuda.memory_reserved(device),
+              "kv_rotation_bytes": set_bytes * sets, "plan_workspace_bytes": plan.workspace_bytes}
     value = logical / (us_graph * 1e-6) / 1e9
     record = {
         "metric": METRIC,
@@ -380,7 +443,25 @@ def main():
         "wall_ms": {"graph": round(graph_wall, 3), "eager": round(eager_wall, 3)},
         "source_digest": digest,
         "device": device_label(torch),
+        "created_utc": datetime.datetime.now(datetime.timezone.utc).isoformat(timespec="seconds"),
+        "revision": revision(),
+        "build_digest": {"sources": _build.source_digest(), "extension": plan._extension.build_digest(),
+                         "abi": plan._extension.abi_version()},
+        "environment": environment(torch),
+        "device_snapshot": {"before_protocol": snapshot_before, "after_protocol": snapshot_after},
+        "steady_state_memory": memory,
+        "protocol_raw": {
+            "unit": "us per call: device (HIP events) and wall (host clock), mean of each repetition's inner calls",
+            "repetitions": args.repetitions, "inner": args.inner, "trial_order": trial_order,
+            "device_us": {name: [round(x * 1e3, 3) for x in dev] for name, (dev, _) in samples.items()},
+            "wall_us": {name: [round(x * 1e3, 3) for x in wall] for name, (_, wall) in samples.items()},
+        },
     }
+    if args.output is not None:
+        args.output.parent.mkdir(parents=True, exist_ok=True)
+        with args.output.open("x") as handle:
+            json.dump(record, handle, indent=2)
+            handle.write("\n")
     print(json.dumps(record), flush=True)
     return 0
 

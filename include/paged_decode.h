@@ -122,6 +122,17 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype,
  * Scales must be finite and > 0 (PD_ERR_DTYPE otherwise). Extends the
  * reference's dtype set (decode.cu:215-218: float16, float32); BF16 and FP8
  * KV are listed as future work there (docs/DESIGN.md:97-99).
+ *
+ * length_bounds: NULL, or a HOST array [batch] of upper bounds on the device
+ * lengths the call will find, read during the call (so a captured launch
+ * keeps the values of its capture). With bounds, batches of up to 64
+ * sequences launch only the partitions the bounds reach, plus one workgroup
+ * per 8 partitions past them for lengths that grew on the device since
+ * (ragged-batch work-list compaction, reference docs/DESIGN.md:80-82). A
+ * bound below the device length is still correct, only slower: the
+ * partitions past it run on those fewer workgroups. Results are the same
+ * with or without bounds up to the last bits (other launch shapes fold the
+ * quarters in another grouping).
  */
 int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
                  float k_scale, float v_scale,
@@ -129,16 +140,16 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
                  float* numerator, float* stats, float* out,
                  int batch, int query_heads, int kv_heads, int head_dim, int page_size,
                  int table_width, int physical_pages, int splits, int split_tokens,
-                 int merge_mode, int hints, void* stream);
+                 int merge_mode, int hints, const int32_t* length_bounds, void* stream);
 
-/* Partition stage of pd_decode_ex (same hints). */
+/* Partition stage of pd_decode_ex (same hints and length bounds). */
 int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
                          float k_scale, float v_scale,
                          const int32_t* table, const int32_t* lengths,
                          float* numerator, float* stats,
                          int batch, int query_heads, int kv_heads, int head_dim, int page_size,
                          int table_width, int physical_pages, int splits, int split_tokens,
-                         int hints, void* stream);
+                         int hints, const int32_t* length_bounds, void* stream);
 
 /*
  * Partition stage only (the first launch of pd_decode): fills numerator and
@@ -188,16 +199,19 @@ int pd_append_kv(const void* k_new, const void* v_new, int dtype,
 /*
  * As pd_append_kv with positions[b] = lengths[b], all or nothing per
  * sequence, and lengths advanced on the device: sequence b is written only if
- * all of its `tokens` positions map to valid cache rows, and then lengths[b]
- * grows by `tokens`; otherwise its cache rows and length are left unchanged.
- * An append followed by pd_decode on the same lengths needs no host round
- * trip, so a decode step can be captured in a hipGraph and replayed.
+ * all of its `tokens` positions map to valid cache rows below max_context,
+ * and then lengths[b] grows by `tokens`; otherwise its cache rows and length
+ * are left unchanged. max_context (0 .. 1048576) is the context the caller's
+ * decode partitions cover (splits * split_tokens or less), so appended
+ * lengths never outgrow what pd_decode reads. An append followed by pd_decode
+ * on the same lengths needs no host round trip, so a decode step can be
+ * captured in a hipGraph and replayed.
  */
 int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype,
                          const int32_t* table, int32_t* lengths,
                          void* k_cache, void* v_cache,
                          int batch, int tokens, int kv_heads, int head_dim, int page_size,
-                         int table_width, int physical_pages, void* stream);
+                         int table_width, int physical_pages, int max_context, void* stream);
 
 /*
  * Page table and lengths from CSR page-list metadata held on the device, the
@@ -236,7 +250,10 @@ const char* pd_status_string(int status);
  * pd_decode_merge takes the lengths; 6: KV-cache append; 7: BF16 and FP8 K/V,
  * pd_decode_ex; 8: pd_table_from_csr; 9: quarters of one workgroup stored
  * combined, the others as empty states; 10: hints argument of the _ex
- * entries; 11: PD_HINT_RAGGED_LENGTHS). */
+ * entries; 11: PD_HINT_RAGGED_LENGTHS; 12: max_context argument of
+ * pd_append_kv_advance, length_bounds argument of the _ex entries). PD_ABI_VERSION is the value this header describes;
+ * a binding compares it with what the loaded library returns. */
+#define PD_ABI_VERSION 12
 int pd_abi_version(void);
 
 #ifdef __cplusplus

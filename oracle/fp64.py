@@ -166,11 +166,18 @@ def scatter_tokens(cache, table, positions, new):
     return out
 
 
-def append_advance(cache, table, lengths, new):
-    """All-or-nothing append at the current lengths; returns (cache, lengths)."""
+def append_advance(cache, table, lengths, new, max_context=None):
+    """All-or-nothing append at the current lengths; returns (cache, lengths).
+
+    Sequence b is written only if every new position is below the context
+    capacity -- the table's, or ``max_context`` when that is smaller (the
+    context a plan's partitions cover) -- and lands on a valid page.
+    """
     pages, page_size = cache.shape[0], cache.shape[1]
     table = np.asarray(table)
     capacity = table.shape[1] * page_size
+    if max_context is not None:
+        capacity = min(capacity, int(max_context))
     out, grown = cache.copy(), np.array(lengths, dtype=np.int64).copy()
     for b in range(new.shape[0]):
         base = int(lengths[b])

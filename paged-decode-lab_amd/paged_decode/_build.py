@@ -8,6 +8,7 @@
 Sources are compiled as written: nothing here runs torch's hipify step. Run as
 ``python -m paged_decode._build`` or through ``__graft_entry__.build()``.
 """
+import hashlib
 import os
 import shutil
 import subprocess
@@ -30,6 +31,21 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
              "-Wall", "-Wno-unused-command-line-argument"]
 
 
+def sources():
+    """Every file the two libraries are compiled from."""
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")) + sorted(CSRC.glob("*.h")) + \
+        sorted(INCLUDE.glob("*.h"))
+
+
+def source_digest():
+    """Short digest of the native sources, compiled into ``_C`` as its build digest."""
+    h = hashlib.sha256()
+    for path in sources():
+        h.update(path.name.encode())
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def _run(cmd, verbose):
     if verbose:
         print(" ".join(str(c) for c in cmd), flush=True)
@@ -50,7 +66,7 @@ def _atomic_output(path):
 def build_hip_library(verbose=False):
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
     tmp = _atomic_output(HIP_LIBRARY)
-    _run([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-o", tmp, CSRC / "decode.hip"], verbose)
+    _run([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, "-o", tmp, CSRC / "decode.hip"], verbose)
     os.replace(tmp, HIP_LIBRARY)
     return HIP_LIBRARY
 
@@ -68,6 +84,7 @@ def build_extension(verbose=False):
     cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
            "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_API_INCLUDE_EXTENSION_H",
            "-DTORCH_EXTENSION_NAME=_C", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           f'-DPD_BUILD_DIGEST="{source_digest()}"',
            *[f"-I{p}" for p in includes],
            CSRC / "torch_ext.cpp", "-o", tmp,
            f"-L{PACKAGE}", "-lpaged_decode_hip", f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch",
@@ -85,6 +102,20 @@ def build(verbose=False):
 
 def built():
     return HIP_LIBRARY.exists() and EXTENSION.exists()
+
+
+def check_loaded(extension):
+    """Raise if the imported ``_C`` was built from other sources than the tree
+    holds, or if the HIP library it loaded reports another ABI version than
+    the header ``_C`` was compiled against: a stale build would otherwise run
+    old kernels silently or reject new arguments."""
+    digest = source_digest()
+    if extension.build_digest() != digest:
+        raise RuntimeError(f"paged_decode native build is stale (built from sources {extension.build_digest()}, "
+                           f"tree holds {digest}): run `python -m paged_decode._build` and restart")
+    if extension.abi_version() != extension.header_abi_version():
+        raise RuntimeError(f"libpaged_decode_hip.so reports ABI {extension.abi_version()}, the extension was "
+                           f"compiled for {extension.header_abi_version()}: rebuild both libraries")
 
 
 if __name__ == "__main__":

@@ -34,12 +34,12 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 PROTOTYPES = {
     "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
-    "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 11 + [_P]),
+    "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 11 + [_P, _P]),
     "pd_decode_partial": (_I, [_P, _P, _P, _I, _P, _P, _P, _P] + [_I] * 9 + [_P]),
-    "pd_decode_partial_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P] + [_I] * 10 + [_P]),
+    "pd_decode_partial_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P] + [_I] * 10 + [_P, _P]),
     "pd_decode_merge": (_I, [_P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_append_kv": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
-    "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
+    "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_table_from_csr": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 4 + [_P]),
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
     "pd_status_string": (ctypes.c_char_p, [_I]),

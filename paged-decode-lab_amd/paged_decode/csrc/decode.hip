@@ -60,10 +60,12 @@
 #include <type_traits>
 
 #include "paged_decode.h"
+#include "partition_map.h"
 
 namespace {
 
-constexpr int kWave = 64;
+using namespace pd;
+
 constexpr float kNoToken = -FLT_MAX;  // running max before any live token
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -224,115 +226,9 @@ struct Elem<float> {
 // kernels have no workgroup barrier on the hot path.
 
 
-// States per partition (quarters of the partition).
-constexpr int kQuarters = 4;
-
 // A chunk's scores may exceed the running max by up to 2^kRescaleSlack before
 // the accumulators are rescaled; weights then stay <= 2^8, far from overflow.
 constexpr float kRescaleSlack = 8.0f;
-
-struct PartialParams {
-    const void* q;
-    const void* k;
-    const void* v;
-    const int32_t* table;
-    const int32_t* lengths;
-    float* numerator;   // [B, Hq, 4 * splits, D]
-    float* stats;       // [B, Hq, 4 * splits, 2]
-    int query_heads;
-    int group;          // query heads per KV head
-    int head_tiles;     // ceil(group / GT)
-    int heads_per_wg;   // KV heads per workgroup (hw)
-    int tiles_per_wg;   // head tiles per workgroup (tw)
-    int quarters_per_wg;  // partition quarters per workgroup (qw)
-    int page_shift;     // log2(page_size)
-    int table_width;
-    int physical_pages;
-    int splits;
-    int split_tokens;
-    uint32_t token_bytes;  // bytes between consecutive tokens of a page (kv_heads * D * elem)
-    uint64_t page_bytes;   // page_size * token_bytes
-    float scale_log2;      // log2(e) * k_scale / sqrt(D)
-    float v_scale;         // multiplies every stored numerator
-    int combine;           // host only: the launch stores a workgroup's qw quarters as one state (kCombine)
-    int unshared_pages;    // host only: PD_HINT_UNSHARED_PAGES (see launch_mfma)
-    int mid_grid;          // host only: 2-head x 2-quarter workgroups of a mid-size grid (see dispatch_mfma)
-    int ragged_lengths;    // host only: PD_HINT_RAGGED_LENGTHS
-};
-
-// Workgroup coordinates (token group, head group) in dispatch order: the
-// linear dispatch index blockIdx.x + gridDim.x * blockIdx.y is read with the
-// head group varying fastest, so consecutively dispatched (and co-resident)
-// workgroups cover all KV-head groups of the same tokens -- whole token rows
-// -- rather than one head group's slice of many rows.
-struct BlockCoords {
-    int tokens;  // quarter group (tokens % (4 / qw)) of partition tokens / (4 / qw)
-    int heads;   // KV heads [hg * hw, hg * hw + hw), head tiles [tg * tw, tg * tw + tw)
-};
-
-__device__ __forceinline__ BlockCoords block_coords() {
-    const uint32_t gx = gridDim.x, gy = gridDim.y;
-    if (gy == 1) return BlockCoords{static_cast<int>(blockIdx.x), 0};
-    const uint64_t lin = blockIdx.x + static_cast<uint64_t>(gx) * blockIdx.y;
-    if (static_cast<uint64_t>(gx) * gy <= 0xFFFFFFFFull) {
-        const uint32_t l32 = static_cast<uint32_t>(lin);
-        return BlockCoords{static_cast<int>(l32 / gy), static_cast<int>(l32 % gy)};
-    }
-    return BlockCoords{static_cast<int>(lin / gy), static_cast<int>(lin % gy)};
-}
-
-// Which KV head, head tile and token range a wave owns, from its workgroup's
-// coordinates; the wave index splits into (head, tile, quarter).
-struct WaveWork {
-    int split, quarter, kv_head, tile, wb, we;
-    int64_t q_row;   // first query-head row of the tile
-    int heads_here;  // live query heads in the tile
-    bool dead;       // the partition starts at or past the sequence end: no state is written
-};
-
-template <int GT, int ALIGN>
-__device__ __forceinline__ WaveWork wave_work(const PartialParams& p, const BlockCoords& bc, int wave) {
-    WaveWork w;
-    const int qw = p.quarters_per_wg;
-    const int groups = kQuarters / qw;
-    const int qq = wave % qw;
-    const int tt = (wave / qw) % p.tiles_per_wg;
-    const int hh = wave / (qw * p.tiles_per_wg);
-    const int tile_groups = p.head_tiles / p.tiles_per_wg;
-    w.split = bc.tokens / groups;
-    w.quarter = (bc.tokens - w.split * groups) * qw + qq;
-    w.kv_head = (bc.heads / tile_groups) * p.heads_per_wg + hh;
-    w.tile = (bc.heads % tile_groups) * p.tiles_per_wg + tt;
-    const int b = blockIdx.z;
-    const int capacity = p.table_width << p.page_shift;
-    const int len = max(0, min(p.lengths[b], capacity));  // decode.cu:42-44
-    const int64_t first = static_cast<int64_t>(w.split) * p.split_tokens;
-    w.dead = first >= len;
-    const int tb = static_cast<int>(min<int64_t>(first, len));
-    const int te = static_cast<int>(min<int64_t>(first + p.split_tokens, len));
-    int per = (te - tb + kQuarters - 1) / kQuarters;
-    per = (per + ALIGN - 1) / ALIGN * ALIGN;
-    w.wb = min(tb + w.quarter * per, te);
-    w.we = min(w.wb + per, te);
-    const int member0 = w.tile * GT;
-    w.heads_here = max(0, min(GT, p.group - member0));
-    w.q_row = static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(w.kv_head) * p.group + member0;
-    return w;
-}
-
-// The first logical page a wave will read if its partition is full length:
-// lets the page-id window be requested before the sequence length arrives.
-template <int ALIGN>
-__device__ __forceinline__ int speculative_page(const PartialParams& p, const BlockCoords& bc, int wave) {
-    const int qw = p.quarters_per_wg;
-    const int groups = kQuarters / qw;
-    const int split = bc.tokens / groups;
-    const int quarter = (bc.tokens - split * groups) * qw + wave % qw;
-    const int per_full = ((p.split_tokens + kQuarters - 1) / kQuarters + ALIGN - 1) / ALIGN * ALIGN;
-    const int capacity = p.table_width << p.page_shift;
-    const int64_t start = static_cast<int64_t>(split) * p.split_tokens + static_cast<int64_t>(quarter) * per_full;
-    return static_cast<int>(min<int64_t>(start, capacity - 1)) >> p.page_shift;
-}
 
 // Stores one wave's state for its GT heads. acc[g][e] lives in the row layout
 // (lanes [r*LPT, (r+1)*LPT) = token row r, dims col*EPL .. col*EPL+EPL-1) and
@@ -341,14 +237,13 @@ __device__ __forceinline__ int speculative_page(const PartialParams& p, const Bl
 template <int D, int GT, int EPL, int LPT>
 __device__ __forceinline__ void store_wave_state(const PartialParams& p, const WaveWork& w, int lane,
                                                  const float (&acc)[GT][EPL], float m, float l) {
-    const int parts = kQuarters * p.splits;
     const int part = w.split * kQuarters + w.quarter;
     if (lane < LPT) {
         const int col = lane;
 #pragma unroll
         for (int g = 0; g < GT; ++g) {
             if (g < w.heads_here) {
-                f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + g) * parts + part) * D + col * EPL);
+                f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + numerator_offset(p, w.q_row + g, part, D) + col * EPL);
 #pragma unroll
                 for (int e = 0; e < EPL; e += 4)
                     dst[e / 4] = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]} * p.v_scale;
@@ -356,9 +251,19 @@ __device__ __forceinline__ void store_wave_state(const PartialParams& p, const W
         }
     }
     if (lane < w.heads_here) {
-        float2* st = reinterpret_cast<float2*>(p.stats) + (w.q_row + lane) * parts + part;
+        float2* st = reinterpret_cast<float2*>(p.stats + stats_offset(p, w.q_row + lane, part));
         *st = make_float2(l > 0.0f ? m : kNoToken, l);
     }
+}
+
+// Empty states (m = -FLT_MAX, l = 0: an identity of every merge) for the
+// wave's quarter of the `extra` live partitions after its first one, when a
+// tail item streamed several partitions as one.
+__device__ __forceinline__ void store_empty_states(const PartialParams& p, const WaveWork& w, int lane, int extra) {
+    if (lane >= w.heads_here) return;
+    for (int e = 1; e <= extra; ++e)
+        *reinterpret_cast<float2*>(p.stats + stats_offset(p, w.q_row + lane, (w.split + e) * kQuarters + w.quarter)) =
+            make_float2(kNoToken, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -388,12 +293,13 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
     const int lane = threadIdx.x % kWave;
     const int row = lane / LPT;
     const int col = lane % LPT;
-    const int page_size = 1 << p.page_shift;
-    const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
-    const BlockCoords bc = block_coords();
-    int window = speculative_page<TPL>(p, bc, wave);
-    int window_ids = pages[min(window + lane, p.table_width - 1)];
-    const WaveWork w = wave_work<GT, TPL>(p, bc, wave);
+    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, gridDim.y);
+    const PartitionRange pr = partition_range(p, bc);
+    const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
+    int window = speculative_page<TPL>(p, pr.first, pr.count, pr.qgroup, wave);
+    int window_ids = pages[window_entry(p, window, lane)];
+    const int len_raw = p.lengths[pr.b];
+    const WaveWork w = wave_work<GT, TPL>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
     if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
     const T* q_base = static_cast<const T*>(p.q) + w.q_row * D;
 
@@ -427,18 +333,14 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int g = c0 + i * TPL;
-            int lo = max(g, rb);
-            int hi = min(g + TPL, re) - 1;
-            if (lo > hi) lo = hi = re - 1;
-            const int slot = min(max((lo >> p.page_shift) - win, 0), kWave - 1);
-            const int page = __builtin_amdgcn_readlane(ids, slot);
-            const bool ok = g < re && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
+            const TileSpan span = tile_span(p, g, TPL, rb, re, win);
+            const int page = __builtin_amdgcn_readlane(ids, span.slot);
+            const bool ok = tile_live(p, g, re, page);
             live |= static_cast<uint32_t>(ok) << i;
-            const int t = min(max(g + row, lo), hi);
-            const uint64_t page_off = static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
+            const uint64_t page_off = tile_page_offset(p, ok, page);
             kp[i] = ok ? k_head + page_off : park;
             vp[i] = ok ? v_head + page_off : park;
-            off[i] = ok ? static_cast<uint32_t>(t & (page_size - 1)) * p.token_bytes + lane_bytes : lane_bytes;
+            off[i] = token_offset(p, ok, g + row, span, lane_bytes);
         }
         ch.live = live;
 #pragma unroll
@@ -505,7 +407,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
     for (rb = w.wb; rb < w.we; rb = re) {
         if ((rb >> p.page_shift) != window) {
             window = rb >> p.page_shift;
-            window_ids = pages[min(window + lane, p.table_width - 1)];
+            window_ids = pages[window_entry(p, window, lane)];
         }
         re = min(w.we, (window + kWave) << p.page_shift);
         for (int s0 = rb & ~(TPL - 1); s0 < re; s0 += NC * CT) {
@@ -549,6 +451,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
         l_lane = lane == g ? l[g] : l_lane;
     }
     store_wave_state<D, GT, EPL, LPT>(p, w, lane, acc, m_lane, l_lane);
+    store_empty_states(p, w, lane, extra_live_partitions(p, pr.first, pr.count, len_raw));
 }
 
 // ---------------------------------------------------------------------------
@@ -579,18 +482,12 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
 // type after they arrive; both formats convert exactly. The per-tensor scales
 // cost nothing per element: k_scale is folded into the softmax scale and
 // v_scale into the stored numerator.
-constexpr int kTileTokens = 16;
-#ifndef PD_MFMA_K_ROWS
-#define PD_MFMA_K_ROWS 1  // K loaded in whole-row pattern and transposed through LDS
-#endif
 
 enum KvFormat { kKvNative = 0, kKvE4M3 = 1, kKvE5M2 = 2 };
 
-// Tile token loaded by K lane row r (see above).
-__device__ __forceinline__ int k_token_of_row(int r) { return (r >> 2) + 4 * (r & 3); }
 
 // N stored words from src. kStream marks 16-byte loads non-temporal (see
-// launch_mfma for when that is used).
+// plan_mfma for when that is used).
 template <int N, bool kStream>
 __device__ __forceinline__ void load_words(const char* src, uint32_t (&w)[N]) {
     if constexpr (N == 4) {
@@ -698,7 +595,7 @@ struct CombineSlot {
     f32x4 acc[VH][kWave];
 };
 
-// kStream: which 16-byte loads are non-temporal (see launch_mfma):
+// kStream: which 16-byte loads are non-temporal (see plan_mfma):
 // 0 none, 1 V (and FP8 K, whose V loads are 8-byte), 2 K and V.
 template <typename QT, int KVF, int D, int GT, int PD, int NC, int kStream, bool kCombine>
 __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
@@ -707,7 +604,6 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     constexpr int KS = D / 32;                    // q.K^T k-steps (K loads) per tile
     constexpr int VH = D / 16;                    // V elements per lane per load = P.V MFMA blocks
     constexpr int VI = 4;                         // V loads per tile
-    constexpr int KW = 8 * ES / 4;                // stored words per K load
     constexpr int VW = VH * ES / 4;               // stored words per V load
     static_assert(GT <= 16, "one MFMA column block holds at most 16 query heads");
 
@@ -716,18 +612,20 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     // layout through a per-wave LDS tile. Its rows are padded by the size of
     // one operand read (16 bytes for 16-bit K, 8 for FP8), so the transposed
     // reads of 16 different rows fall in distinct banks.
-    constexpr bool kKRows = PD_MFMA_K_ROWS;
     constexpr bool kStreamK = kStream == 2 || (kStream == 1 && KVF != kKvNative);
     constexpr int KR = D * ES / 16;
     constexpr int TK = kWave / KR;
     constexpr int KL = kTileTokens / TK;
-    constexpr int kStageRow = D * ES + 8 * ES;
+    constexpr int kStageRow = mfma_stage_bytes(D, ES) / kTileTokens;
     static_assert(TK <= kTileTokens && kTileTokens % TK == 0, "whole row loads per tile");
-    __shared__ __attribute__((aligned(16))) char k_stage[kKRows ? 8 * kTileTokens * kStageRow : 16];
-    extern __shared__ __attribute__((aligned(16))) char combine_lds[];  // [waves / qw][qw - 1] CombineSlot<VH>
+    // Dynamic LDS: the waves' K tiles, then (kCombine) the quarter-combine
+    // slots, [waves / qw][qw - 1] CombineSlot<VH>; sized by the launch.
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    char* const k_stage = lds;
+    char* const combine_lds = lds + mfma_stage_bytes(D, ES) * (blockDim.x / kWave);
 
     struct Tile {
-        uint32_t k[kKRows ? KL : KS][kKRows ? 4 : KW];
+        uint32_t k[KL][4];
         uint32_t v[VI][VW];
         uint32_t live;
     };
@@ -736,12 +634,13 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     const int lane = threadIdx.x % kWave;
     const int n = lane % 16;  // head (q.K^T, P) / column (P.V)
     const int g = lane / 16;  // lane group: tokens g + 4 e
-    const int page_size = 1 << p.page_shift;
-    const int32_t* pages = p.table + static_cast<int64_t>(blockIdx.z) * p.table_width;
-    const BlockCoords bc = block_coords();
-    int window = speculative_page<kTileTokens>(p, bc, wave);
-    int window_ids = pages[min(window + lane, p.table_width - 1)];
-    const WaveWork w = wave_work<GT, kTileTokens>(p, bc, wave);
+    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, gridDim.y);
+    const PartitionRange pr = partition_range(p, bc);
+    const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
+    int window = speculative_page<kTileTokens>(p, pr.first, pr.count, pr.qgroup, wave);
+    int window_ids = pages[window_entry(p, window, lane)];
+    const int len_raw = p.lengths[pr.b];
+    const WaveWork w = wave_work<GT, kTileTokens>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
     if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
     const char* q_row = static_cast<const char*>(p.q) + w.q_row * D * 2;
 
@@ -761,81 +660,53 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     const char* k_head = static_cast<const char*>(p.k) + static_cast<size_t>(w.kv_head) * D * ES;
     const char* v_head = static_cast<const char*>(p.v) + static_cast<size_t>(w.kv_head) * D * ES;
     const char* park = q_row;  // dead tiles read the wave's own q row: mapped, D * 2 bytes
-    const uint32_t k_lane_bytes = static_cast<uint32_t>(g) * 8u * ES;
     const uint32_t v_lane_bytes = static_cast<uint32_t>(n) * VH * ES;
     const int k_row_token = k_token_of_row(n);
     int rb = w.wb, re = w.wb;
 
     auto issue = [&](Tile& tl, int t0, int ids, int win) {
-        int lo = max(t0, rb);
-        int hi = min(t0 + kTileTokens, re) - 1;
-        if (lo > hi) lo = hi = re - 1;
-        const int slot = min(max((lo >> p.page_shift) - win, 0), kWave - 1);
-        const int page = __builtin_amdgcn_readlane(ids, slot);
-        const bool ok = t0 < re && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
+        const TileSpan span = tile_span(p, t0, kTileTokens, rb, re, win);
+        const int page = __builtin_amdgcn_readlane(ids, span.slot);
+        const bool ok = tile_live(p, t0, re, page);
         tl.live = ok;
-        const uint64_t page_off = static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
+        const uint64_t page_off = tile_page_offset(p, ok, page);
         const char* kp = ok ? k_head + page_off : park;
         const char* vp = ok ? v_head + page_off : park;
-        if constexpr (kKRows) {
+        const uint32_t k_lane_bytes = static_cast<uint32_t>(lane % KR) * 16u;
 #pragma unroll
-            for (int s = 0; s < KL; ++s) {
-                const int tk = min(max(t0 + TK * s + lane / KR, lo), hi);
-                const uint32_t col = static_cast<uint32_t>(lane % KR) * 16u;
-                const uint32_t koff = ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + col : col;
-                load_words<4, kStreamK>(kp + koff, tl.k[s]);
-            }
-        } else {
-            const int tk = min(max(t0 + k_row_token, lo), hi);
-            const uint32_t koff =
-                ok ? static_cast<uint32_t>(tk & (page_size - 1)) * p.token_bytes + k_lane_bytes : k_lane_bytes;
+        for (int s = 0; s < KL; ++s)
+            load_words<4, kStreamK>(kp + token_offset(p, ok, t0 + TK * s + lane / KR, span, k_lane_bytes), tl.k[s]);
 #pragma unroll
-            for (int s = 0; s < KS; ++s) load_words<KW, kStreamK>(kp + koff + 32 * ES * s, tl.k[s]);
-        }
-#pragma unroll
-        for (int e = 0; e < VI; ++e) {
-            const int tv = min(max(t0 + 4 * e + g, lo), hi);
-            const uint32_t voff =
-                ok ? static_cast<uint32_t>(tv & (page_size - 1)) * p.token_bytes + v_lane_bytes : v_lane_bytes;
-            load_words<VW, (kStream >= 1)>(vp + voff, tl.v[e]);
-        }
+        for (int e = 0; e < VI; ++e)
+            load_words<VW, (kStream >= 1)>(vp + token_offset(p, ok, t0 + 4 * e + g, span, v_lane_bytes), tl.v[e]);
         __builtin_amdgcn_sched_barrier(0);
     };
 
     auto consume = [&](const Tile& tl, int t0) {
         f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (kKRows) {
-            char* stage = k_stage + wave * (kTileTokens * kStageRow);
-            __builtin_amdgcn_wave_barrier();  // the previous tile's reads are issued before these writes
+        char* stage = k_stage + wave * (kTileTokens * kStageRow);
+        __builtin_amdgcn_wave_barrier();  // the previous tile's reads are issued before these writes
 #pragma unroll
-            for (int s = 0; s < KL; ++s) {
-                char* dst = stage + (TK * s + lane / KR) * kStageRow + (lane % KR) * 16;
-                if constexpr (kStageRow % 16 == 0) {
-                    *reinterpret_cast<u32x4*>(dst) = u32x4{tl.k[s][0], tl.k[s][1], tl.k[s][2], tl.k[s][3]};
-                } else {  // FP8 rows are 8-byte aligned
-                    reinterpret_cast<u32x2*>(dst)[0] = u32x2{tl.k[s][0], tl.k[s][1]};
-                    reinterpret_cast<u32x2*>(dst)[1] = u32x2{tl.k[s][2], tl.k[s][3]};
-                }
+        for (int s = 0; s < KL; ++s) {
+            char* dst = stage + (TK * s + lane / KR) * kStageRow + (lane % KR) * 16;
+            if constexpr (kStageRow % 16 == 0) {
+                *reinterpret_cast<u32x4*>(dst) = u32x4{tl.k[s][0], tl.k[s][1], tl.k[s][2], tl.k[s][3]};
+            } else {  // FP8 rows are 8-byte aligned
+                reinterpret_cast<u32x2*>(dst)[0] = u32x2{tl.k[s][0], tl.k[s][1]};
+                reinterpret_cast<u32x2*>(dst)[1] = u32x2{tl.k[s][2], tl.k[s][3]};
             }
-            __builtin_amdgcn_wave_barrier();
+        }
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const char* src = stage + k_row_token * kStageRow + (32 * s + 8 * g) * ES;
-                if constexpr (KVF == kKvNative) {
-                    sc = C::qk(*reinterpret_cast<const u32x4*>(src), qb[s], sc);
-                } else {
-                    const u32x2 raw2 = *reinterpret_cast<const u32x2*>(src);
-                    const uint32_t raw[2] = {raw2[0], raw2[1]};
-                    uint32_t kq[4];
-                    to_compute<QT, KVF, 2>(raw, kq);
-                    sc = C::qk(u32x4{kq[0], kq[1], kq[2], kq[3]}, qb[s], sc);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
+        for (int s = 0; s < KS; ++s) {
+            const char* src = stage + k_row_token * kStageRow + (32 * s + 8 * g) * ES;
+            if constexpr (KVF == kKvNative) {
+                sc = C::qk(*reinterpret_cast<const u32x4*>(src), qb[s], sc);
+            } else {
+                const u32x2 raw2 = *reinterpret_cast<const u32x2*>(src);
+                const uint32_t raw[2] = {raw2[0], raw2[1]};
                 uint32_t kq[4];
-                to_compute<QT, KVF, KW>(tl.k[s], kq);
+                to_compute<QT, KVF, 2>(raw, kq);
                 sc = C::qk(u32x4{kq[0], kq[1], kq[2], kq[3]}, qb[s], sc);
             }
         }
@@ -892,7 +763,7 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     for (rb = w.wb; rb < w.we; rb = re) {
         if ((rb >> p.page_shift) != window) {
             window = rb >> p.page_shift;
-            window_ids = pages[min(window + lane, p.table_width - 1)];
+            window_ids = pages[window_entry(p, window, lane)];
         }
         re = min(w.we, (window + kWave) << p.page_shift);
         for (int s0 = rb & ~(kTileTokens - 1); s0 < re; s0 += NC * kTileTokens) {
@@ -911,8 +782,8 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     // Lane (g, n) holds heads 4 g + i of dims n VH .. n VH + VH - 1; the
     // denominator of head n is summed over the four lane groups.
     float l_head = sum_over_lane_groups(l_part);
-    const int parts = kQuarters * p.splits;
     const int part = w.split * kQuarters + w.quarter;
+    store_empty_states(p, w, lane, extra_live_partitions(p, pr.first, pr.count, len_raw));
     if constexpr (kCombine) {
         // The workgroup's qw quarters of one (KV head, head tile) -- waves
         // wave - wave % qw onwards, all of one partition, so all live or all
@@ -934,7 +805,8 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
 #pragma unroll
             for (int j = 0; j < VH; ++j) slot->acc[j][lane] = acc[j];
             if (lane < w.heads_here)
-                reinterpret_cast<float2*>(p.stats)[(w.q_row + lane) * parts + part] = make_float2(kNoToken, 0.0f);
+                *reinterpret_cast<float2*>(p.stats + stats_offset(p, w.q_row + lane, part)) =
+                    make_float2(kNoToken, 0.0f);
         }
         __syncthreads();
         if (qq != 0) return;
@@ -962,14 +834,14 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     for (int i = 0; i < 4; ++i) {
         const int h = 4 * g + i;
         if (h < w.heads_here) {
-            f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + ((w.q_row + h) * parts + part) * D + n * VH);
+            f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + numerator_offset(p, w.q_row + h, part, D) + n * VH);
 #pragma unroll
             for (int j = 0; j < VH; j += 4)
                 dst[j / 4] = f32x4{acc[j][i], acc[j + 1][i], acc[j + 2][i], acc[j + 3][i]} * p.v_scale;
         }
     }
     if (lane < w.heads_here) {
-        float2* st = reinterpret_cast<float2*>(p.stats) + (w.q_row + lane) * parts + part;
+        float2* st = reinterpret_cast<float2*>(p.stats + stats_offset(p, w.q_row + lane, part));
         *st = make_float2(l_head > 0.0f ? m_head : kNoToken, l_head);
     }
 }
@@ -1034,7 +906,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     static_assert(D % kMergeChunk == 0, "whole chunks");
     extern __shared__ float weight[];  // [parts], shared variant only
     __shared__ f32x4 column_sum[PG][TPR];
-    __shared__ float scratch[2][kWaves];
+    __shared__ float wave_partial[2][kWaves];
     const int b = blockIdx.y;
     const int64_t row = static_cast<int64_t>(b) * mp.query_heads + blockIdx.x;
     const int chunk = blockIdx.z;
@@ -1100,11 +972,11 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     }
     mx = wave_max(mx);
     if constexpr (kSharedWeights) {
-        if (lane == 0) scratch[0][wave] = mx;
+        if (lane == 0) wave_partial[0][wave] = mx;
         __syncthreads();
-        mx = scratch[0][0];
+        mx = wave_partial[0][0];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, scratch[0][w]);
+        for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, wave_partial[0][w]);
     }
 
     float den = 0.0f;
@@ -1130,11 +1002,11 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     }
     den = wave_sum(den);
     if constexpr (kSharedWeights) {
-        if (lane == 0) scratch[1][wave] = den;
+        if (lane == 0) wave_partial[1][wave] = den;
         __syncthreads();  // also publishes weight[]
-        den = scratch[1][0];
+        den = wave_partial[1][0];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) den += scratch[1][w];
+        for (int w = 1; w < kWaves; ++w) den += wave_partial[1][w];
     }
 
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1178,9 +1050,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
 // fit in kMergeWaveBatch loads per lane (at most 64 states); all loads are
 // issued at once and masked with the live count.
 constexpr int kMergeWaveBatch = 8;
-#ifndef PD_MERGE_ROWS_MIN
-#define PD_MERGE_ROWS_MIN 256  // rows (sequences x query heads) from which merge_rows takes rows of > 2 rounds
-#endif
+constexpr int kMergeRowsMin = 256;  // rows (sequences x query heads) from which merge_rows takes rows of > 2 rounds
 constexpr int kMergeRowsPerGroup = 4;
 
 template <int D>
@@ -1273,14 +1143,14 @@ struct AppendParams {
     int table_width;
     int page_shift;
     int physical_pages;
+    int64_t capacity;          // positions [0, capacity) may be written: the table's, or less (advance variant)
     uint32_t row_bytes;        // kv_heads * head_dim * element size
 };
 
-// Physical row of logical position pos, or -1 if pos is outside the table's
-// capacity or its page id is outside [0, physical_pages).
+// Physical row of logical position pos, or -1 if pos is outside
+// [0, capacity) or its page id is outside [0, physical_pages).
 __device__ __forceinline__ int64_t cache_row(const AppendParams& a, const int32_t* pages, int64_t pos) {
-    const int64_t capacity = static_cast<int64_t>(a.table_width) << a.page_shift;
-    if (pos < 0 || pos >= capacity) return -1;
+    if (pos < 0 || pos >= a.capacity) return -1;
     const int page = pages[pos >> a.page_shift];
     if (static_cast<uint32_t>(page) >= static_cast<uint32_t>(a.physical_pages)) return -1;
     return (static_cast<int64_t>(page) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
@@ -1311,8 +1181,10 @@ __global__ void __launch_bounds__(256) append_kv_kernel(const AppendParams a) {
 
 // Positions from lengths, all or nothing per sequence: workgroup b writes its
 // `tokens` tokens at lengths[b] .. lengths[b] + tokens - 1 only if every one of
-// them maps to a valid cache row, then advances lengths[b]; otherwise the
-// sequence and its length are left unchanged.
+// them maps to a valid cache row below the caller's context capacity (the
+// context its partitions cover), then advances lengths[b]; otherwise the
+// sequence and its length are left unchanged, so lengths never outgrow the
+// partitions that decode them.
 __global__ void __launch_bounds__(256) append_kv_advance_kernel(const AppendParams a) {
     const int b = blockIdx.x;
     const int32_t* pages = a.table + static_cast<int64_t>(b) * a.table_width;
@@ -1403,31 +1275,17 @@ int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD_ERR_LA
 
 // FP32 kernel: 16-byte loads of K (and of V) per lane per chunk, chunks in
 // flight ahead of the one being consumed, chunks per straight-line block.
-#ifndef PD_CHUNK_LOADS
-#define PD_CHUNK_LOADS 1
-#endif
-#ifndef PD_PREFETCH
-#define PD_PREFETCH 4
-#endif
-#ifndef PD_BLOCK_CHUNKS
-#define PD_BLOCK_CHUNKS 16
-#endif
-// FP16 kernel (MFMA): 16-token tiles issued ahead of the one being consumed,
+constexpr int kFp32ChunkLoads = 1;
+constexpr int kFp32Prefetch = 4;
+constexpr int kFp32BlockChunks = 16;
+// Matrix-core kernel: 16-token tiles issued ahead of the one being consumed,
 // and tiles per straight-line block (with 2 and 2, each block's two tiles are
 // requested together and consumed in order). Short blocks keep the kernel's
 // code small: with 8 waves per CU running through cold straight-line code,
 // instruction fetch is on the critical path (two-tile blocks measured 1 us
 // faster per Llama-3-8B-shape call than eight-tile blocks, same loads).
-#ifndef PD_MFMA_PREFETCH
-#define PD_MFMA_PREFETCH 2
-#endif
-#ifndef PD_MFMA_BLOCK
-#define PD_MFMA_BLOCK 2
-#endif
-// KV heads per partition workgroup, at most.
-#ifndef PD_WG_HEADS
-#define PD_WG_HEADS 4  // KV heads per workgroup of the matrix-core kernel (FP32 kernel: 8)
-#endif
+constexpr int kMfmaPrefetch = 2;
+constexpr int kMfmaBlock = 2;
 
 // Compute units of the current device, read once per device.
 int device_compute_units() {
@@ -1443,86 +1301,27 @@ int device_compute_units() {
     return cus;
 }
 
-// Largest divisor of n not above cap.
-int largest_divisor(int n, int cap) {
-    for (int d = std::min(n, cap); d > 1; --d)
-        if (n % d == 0) return d;
-    return 1;
-}
+dim3 to_dim3(const Grid& g) { return dim3(g.x, g.y, g.z); }
 
-// Workgroup shape: up to max_heads KV heads of the same tokens per workgroup
-// (their slices of a token row are then read together), all head tiles of
-// those heads, and as many partition quarters as fill `waves` waves (8, or
-// fewer for small grids: see dispatch_mfma). A KV head count with no divisor
-// in 2..max_heads keeps its whole token row in one workgroup when it fits
-// (5 or 7 heads in 8 waves).
-//
-// The matrix-core kernel takes 4 KV heads: at 8 KV heads, two workgroups of 4
-// heads x 2 quarters (quarters combined, V loads streamed when no page is
-// shared) measured faster per call than one of 8 heads x 1 quarter on every
-// shape tried on MI355X: Llama-3-8B B4 L4096 18.86 -> 17.31 us, the B16 L4096
-// batch of the reference's benchmark 50.7 -> 40.2 us, B64 L2048 122.3 ->
-// 103.8 us; with 32 KV heads, 32K-context MHA 97.2 -> 89.8 us at split 256.
-// Grids that would leave most CUs idle take smaller workgroups instead, and
-// grids smaller than the device skip the combine (see dispatch_mfma).
-void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads, int waves = 8) {
-    prm.heads_per_wg = largest_divisor(kv_heads, std::min(max_heads, waves));
-    if (prm.heads_per_wg == 1 && kv_heads <= waves) prm.heads_per_wg = kv_heads;
-    prm.tiles_per_wg = largest_divisor(prm.head_tiles, waves / prm.heads_per_wg);
-    const int hw_tw = prm.heads_per_wg * prm.tiles_per_wg;
-    prm.quarters_per_wg = hw_tw * 4 <= waves ? 4 : hw_tw * 2 <= waves ? 2 : 1;
-}
-
-dim3 partial_grid(const PartialParams& prm, int batch, int kv_heads) {
-    return dim3(prm.splits * (kQuarters / prm.quarters_per_wg),
-                (kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg), batch);
-}
-
-int partial_threads(const PartialParams& prm) {
-    return kWave * prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
-}
-
-// When the KV heads need several workgroups (kv_heads > heads_per_wg), each
-// workgroup reads one head group's slice of every token row, and some 16-byte
-// loads may be issued non-temporal. That is faster when nothing is read twice
-// and slower when sequences share prefix pages, which streamed loads do not
-// leave in the caches. Measured on MI355X (decode call, us):
-//   - 4 or more head groups per row (16, 32 KV heads), no shared pages: K and
-//     V streaming is fastest (32K-context MHA at split 256: 92.2; V only
-//     95.3; neither 98.6). With 25% shared prefix pages (B8 L4096, 32 KV
-//     heads): K and V 48.4, V only 43.0.
-//   - 2 head groups (8 KV heads), no shared pages: V only (B64 L2048 103.8,
-//     K and V 104.7, neither 112.3; a ragged B16 page-32 batch 57.0 / 62.1 /
-//     64.1). With 25% shared prefix pages (B16 page 32): neither 50.3, V only
-//     52.0, K and V 59.3.
-//   - The 2-head x 2-quarter workgroups of mid-size grids (see dispatch_mfma):
-//     with 2 KV heads, one head group, streaming V anyway took B16 L4096
-//     (GQA 8) from 19.75 to 18.81 us per call.
-// So the mode follows the page-sharing hint: unshared pages stream K and V
-// (4+ groups) or V (2 groups, or one in a mid-size grid); pages that may be
-// shared stream V (4+ groups) or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte K row loads
-// wherever 16-bit K/V would stream V.
+// Launches the matrix-core kernel planned by plan_mfma (head tile GT, stream
+// mode and quarter combine chosen there).
 template <typename QT, int KVF, int D, int GT>
-int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    const dim3 grid = partial_grid(prm, batch, kv_heads);
+int launch_mfma(const PartialParams& prm, int kv_heads, hipStream_t stream) {
+    static_assert(sizeof(CombineSlot<D / 16>) == 2 * 16 * 4 + (D / 16) * kWave * 16, "combine_slot_bytes");
+    const dim3 grid = to_dim3(partial_grid(prm, kv_heads));
     const dim3 block(partial_threads(prm));
-    const size_t lds = prm.combine ? static_cast<size_t>(block.x / kWave / prm.quarters_per_wg) *
-                                         (prm.quarters_per_wg - 1) * sizeof(CombineSlot<D / 16>)
-                                   : 0;
-    const int groups = kv_heads / prm.heads_per_wg;
-    const int mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
-                     : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
-    constexpr int kPD = PD_MFMA_PREFETCH, kNC = PD_MFMA_BLOCK;
+    const size_t lds = static_cast<size_t>(mfma_lds_bytes(prm, D, KVF == kKvNative ? 2 : 1));
+    constexpr int kPD = kMfmaPrefetch, kNC = kMfmaBlock;
 #define PD_LAUNCH_MFMA(MODE, COMBINE)                                                                             \
     hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE>), grid, block, lds, stream, prm)
     if constexpr (KVF == kKvNative) {
-        if (mode == 2) {
+        if (prm.stream_mode == 2) {
             if (prm.combine) PD_LAUNCH_MFMA(2, true);
             else PD_LAUNCH_MFMA(2, false);
             return launch_status();
         }
     }
-    if (mode >= 1) {
+    if (prm.stream_mode >= 1) {
         if (prm.combine) PD_LAUNCH_MFMA(1, true);
         else PD_LAUNCH_MFMA(1, false);
     } else {
@@ -1534,125 +1333,58 @@ int launch_mfma(const PartialParams& prm, int batch, int kv_heads, hipStream_t s
 }
 
 template <int D, int GT>
-int launch_fp32(const PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    hipLaunchKernelGGL((partial_kernel<float, D, GT, PD_CHUNK_LOADS, PD_PREFETCH, PD_BLOCK_CHUNKS>),
-                       partial_grid(prm, batch, kv_heads), dim3(partial_threads(prm)), 0, stream, prm);
+int launch_fp32(const PartialParams& prm, int kv_heads, hipStream_t stream) {
+    hipLaunchKernelGGL((partial_kernel<float, D, GT, kFp32ChunkLoads, kFp32Prefetch, kFp32BlockChunks>),
+                       to_dim3(partial_grid(prm, kv_heads)), dim3(partial_threads(prm)), 0, stream, prm);
     return launch_status();
 }
 
-// Head tile: the GQA group padded to a power of two up to max_tile query
-// heads (16 for the matrix-core kernel, whose MFMA column block holds 16
-// heads; 8 for the FP32 kernel, whose accumulators grow with the tile);
-// larger groups are cut into tiles of max_tile.
-int head_tile(int group, int max_tile) {
-    int gt = 1;
-    while (gt < group && gt < max_tile) gt *= 2;
-    return gt;
-}
-
-void plan_tiles(PartialParams& prm, int kv_heads, int max_tile, int max_heads, int& gt) {
-    gt = head_tile(prm.group, max_tile);
-    prm.head_tiles = (prm.group + gt - 1) / gt;
-    choose_workgroup(prm, kv_heads, max_heads);
-}
-
-int64_t workgroups(const dim3& grid) { return static_cast<int64_t>(grid.x) * grid.y * grid.z; }
-
 template <typename QT, int KVF, int D>
-int dispatch_mfma(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    int gt;
-    plan_tiles(prm, kv_heads, 16, PD_WG_HEADS, gt);
-    // A grid of at most half as many 8-wave workgroups as CUs leaves most CUs
-    // idle, and each busy CU can keep only so many loads in flight. The same
-    // waves then go in smaller workgroups, the largest of 4, 2 or 1 waves
-    // that still gives two workgroups per CU (else 1 wave). Measured on
-    // MI355X, Llama-3-8B geometry (decode call, us):
-    //   B1 L4096 (64 workgroups of 8 waves): 12.4 -> 10.2 with 1 wave;
-    //   B1 L2048: 11.7 -> 9.9; FP8 B1 L4096: 12.6 -> 10.6-11.1;
-    //   B2 L4096 and B1 L8192 (128 workgroups): 13.2 -> 12.9 and
-    //   13.65 -> 13.1 with 2 waves.
-    // At 192 workgroups (B3 L4096) every smaller shape was slower (14.95 ->
-    // 15.3-19.0), so larger grids keep 8 waves.
-    //
-    // Grids of one to two 8-wave workgroups per CU with 2, 4 or 8 KV heads and
-    // GQA groups of up to 8 take workgroups of 2 KV heads x 2 quarters instead
-    // (4 waves, quarters combined). Measured on MI355X by graph replay of 200
-    // calls, N(0,1) data, K/V sets rotated past the Infinity Cache (decode
-    // call, us): Llama-3-8B B4 L4096 18.0-18.4 -> 17.4-17.6, B8 L4096 29.45
-    // -> 28.54, B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8
-    // L4096 with 4 KV heads 20.05 -> 19.1-19.2; ragged B4 batches within
-    // 0.1-0.25. B3 L4096 (192 workgroups) was slower with smaller workgroups
-    // of any kind (14.74 -> 15.05). Larger grids keep 8 waves when lengths
-    // are uniform (B16 L4096 55.1 -> 56.9, B32 L4096 105.7 -> 109.1) but
-    // not when they are ragged (PD_HINT_RAGGED_LENGTHS): then up to eight
-    // 8-wave workgroups per CU take the smaller ones (B16 with lengths
-    // uniform in [0, 4096] 37.8 -> 33.3, B32 65.1 -> 59.7; the reference's
-    // B16 L4096 batch 47.6 -> 44.0 in the benchmark). At sixteen per CU (a
-    // B16 page-32 L8192 batch at split 128) it was flat, so those keep 8.
-    const int cus = device_compute_units();
-    const int64_t wg8 = workgroups(partial_grid(prm, batch, kv_heads));
-    if (wg8 * 2 <= cus) {  // small grid
-        const int64_t waves_total = wg8 * (partial_threads(prm) / kWave);
-        int waves = 4;
-        while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
-        choose_workgroup(prm, kv_heads, PD_WG_HEADS, waves);
-    } else if (wg8 >= cus && wg8 <= (prm.ragged_lengths ? 8 : 2) * static_cast<int64_t>(cus) &&
-               (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
-        choose_workgroup(prm, kv_heads, 2, 4);
-        prm.mid_grid = 1;
-    }
-    // Combining a workgroup's quarters into one state cuts the state stores
-    // (written back at the kernel's end) and the merge's reads by qw; its
-    // fold runs after the slowest quarter. Measured on MI355X it pays for two
-    // quarters, and for four when the head tile is full (16 query heads:
-    // MQA-like groups, the largest states per KV byte); four quarters of
-    // smaller tiles were 0.3-0.7 us slower per call. A grid smaller than the
-    // CUs leaves the fold's tail exposed (B1 L4096: 12.05 us without, 12.43
-    // with), so such launches keep four states per partition.
-    const bool fills_device = workgroups(partial_grid(prm, batch, kv_heads)) >= cus;
-    prm.combine = fills_device && (prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16));
-    switch (gt) {
-        case 1: return launch_mfma<QT, KVF, D, 1>(prm, batch, kv_heads, stream);
-        case 2: return launch_mfma<QT, KVF, D, 2>(prm, batch, kv_heads, stream);
-        case 4: return launch_mfma<QT, KVF, D, 4>(prm, batch, kv_heads, stream);
-        case 8: return launch_mfma<QT, KVF, D, 8>(prm, batch, kv_heads, stream);
-        default: return launch_mfma<QT, KVF, D, 16>(prm, batch, kv_heads, stream);
+int dispatch_mfma(PartialParams& prm, int kv_heads, hipStream_t stream) {
+    plan_mfma(prm, kv_heads, device_compute_units());
+    switch (prm.head_tile) {
+        case 1: return launch_mfma<QT, KVF, D, 1>(prm, kv_heads, stream);
+        case 2: return launch_mfma<QT, KVF, D, 2>(prm, kv_heads, stream);
+        case 4: return launch_mfma<QT, KVF, D, 4>(prm, kv_heads, stream);
+        case 8: return launch_mfma<QT, KVF, D, 8>(prm, kv_heads, stream);
+        default: return launch_mfma<QT, KVF, D, 16>(prm, kv_heads, stream);
     }
 }
 
 template <int D>
-int dispatch_fp32(PartialParams& prm, int batch, int kv_heads, hipStream_t stream) {
-    int gt;
-    plan_tiles(prm, kv_heads, 8, 8, gt);
-    switch (gt) {
-        case 1: return launch_fp32<D, 1>(prm, batch, kv_heads, stream);
-        case 2: return launch_fp32<D, 2>(prm, batch, kv_heads, stream);
-        case 4: return launch_fp32<D, 4>(prm, batch, kv_heads, stream);
-        default: return launch_fp32<D, 8>(prm, batch, kv_heads, stream);
+int dispatch_fp32(PartialParams& prm, int kv_heads, hipStream_t stream) {
+    plan_fp32(prm, kv_heads);
+    switch (prm.head_tile) {
+        case 1: return launch_fp32<D, 1>(prm, kv_heads, stream);
+        case 2: return launch_fp32<D, 2>(prm, kv_heads, stream);
+        case 4: return launch_fp32<D, 4>(prm, kv_heads, stream);
+        default: return launch_fp32<D, 8>(prm, kv_heads, stream);
     }
 }
 
 template <typename QT, int D>
-int dispatch_kv(PartialParams& prm, int kv_dtype, int batch, int kv_heads, hipStream_t stream) {
+int dispatch_kv(PartialParams& prm, int kv_dtype, int kv_heads, hipStream_t stream) {
     switch (kv_dtype) {
-        case PD_DTYPE_FP8_E4M3: return dispatch_mfma<QT, kKvE4M3, D>(prm, batch, kv_heads, stream);
-        case PD_DTYPE_FP8_E5M2: return dispatch_mfma<QT, kKvE5M2, D>(prm, batch, kv_heads, stream);
-        default: return dispatch_mfma<QT, kKvNative, D>(prm, batch, kv_heads, stream);
+        case PD_DTYPE_FP8_E4M3: return dispatch_mfma<QT, kKvE4M3, D>(prm, kv_heads, stream);
+        case PD_DTYPE_FP8_E5M2: return dispatch_mfma<QT, kKvE5M2, D>(prm, kv_heads, stream);
+        default: return dispatch_mfma<QT, kKvNative, D>(prm, kv_heads, stream);
     }
 }
 
 template <int D>
-int dispatch_formats(PartialParams& prm, int q_dtype, int kv_dtype, int batch, int kv_heads, hipStream_t stream) {
-    if (q_dtype == PD_DTYPE_F32) return dispatch_fp32<D>(prm, batch, kv_heads, stream);
-    if (q_dtype == PD_DTYPE_BF16) return dispatch_kv<__bf16, D>(prm, kv_dtype, batch, kv_heads, stream);
-    return dispatch_kv<_Float16, D>(prm, kv_dtype, batch, kv_heads, stream);
+int dispatch_formats(PartialParams& prm, int q_dtype, int kv_dtype, int kv_heads, hipStream_t stream) {
+    if (q_dtype == PD_DTYPE_F32) return dispatch_fp32<D>(prm, kv_heads, stream);
+    if (q_dtype == PD_DTYPE_BF16) return dispatch_kv<__bf16, D>(prm, kv_dtype, kv_heads, stream);
+    return dispatch_kv<_Float16, D>(prm, kv_dtype, kv_heads, stream);
 }
 
 int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
                 const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
-                int splits, int split_tokens, int hints, hipStream_t stream, int* state_stride = nullptr) {
+                int splits, int split_tokens, int hints, const int32_t* length_bounds, hipStream_t stream,
+                int* state_stride = nullptr) {
     PartialParams prm{};
+    prm.batch = batch;
     prm.unshared_pages = (hints & PD_HINT_UNSHARED_PAGES) != 0;
     prm.ragged_lengths = (hints & PD_HINT_RAGGED_LENGTHS) != 0;
     prm.q = q;
@@ -1673,8 +1405,9 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     prm.page_bytes = static_cast<uint64_t>(page_size) * prm.token_bytes;
     prm.scale_log2 = kLog2e * k_scale / sqrtf(static_cast<float>(head_dim));
     prm.v_scale = v_scale;
-    const int status = head_dim == 64 ? dispatch_formats<64>(prm, q_dtype, kv_dtype, batch, kv_heads, stream)
-                                      : dispatch_formats<128>(prm, q_dtype, kv_dtype, batch, kv_heads, stream);
+    plan_items(prm, length_bounds);
+    const int status = head_dim == 64 ? dispatch_formats<64>(prm, q_dtype, kv_dtype, kv_heads, stream)
+                                      : dispatch_formats<128>(prm, q_dtype, kv_dtype, kv_heads, stream);
     if (state_stride) *state_stride = prm.combine ? prm.quarters_per_wg : 1;
     return status;
 }
@@ -1688,7 +1421,7 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
     // columns per lane; with few rows of many states, merge_cols (D / 32
     // workgroups per row) finishes sooner.
     const int rounds = (states + kWave / (D / 4) - 1) / (kWave / (D / 4));
-    const bool many_rows = static_cast<int64_t>(batch) * mp.query_heads >= PD_MERGE_ROWS_MIN;
+    const bool many_rows = static_cast<int64_t>(batch) * mp.query_heads >= kMergeRowsMin;
     if (states <= merge_wave_max_parts<D>() && (many_rows || rounds <= 2)) {
         const dim3 grid((mp.query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
         if (shared) {
@@ -1781,6 +1514,7 @@ AppendParams append_params(const void* k_new, const void* v_new, int dtype, cons
     a.table_width = table_width;
     a.page_shift = page_size == 16 ? 4 : 5;
     a.physical_pages = physical_pages;
+    a.capacity = static_cast<int64_t>(table_width) << a.page_shift;
     a.row_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * element_size(dtype));
     return a;
 }
@@ -1792,7 +1526,8 @@ extern "C" {
 int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
                          float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
                          int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                         int physical_pages, int splits, int split_tokens, int hints, void* stream) {
+                         int physical_pages, int splits, int split_tokens, int hints, const int32_t* length_bounds,
+                         void* stream) {
     int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                               query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                               split_tokens);
@@ -1800,7 +1535,7 @@ int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* 
     if (status != PD_OK) return status;
     return run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                        query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                       hints, static_cast<hipStream_t>(stream));
+                       hints, length_bounds, static_cast<hipStream_t>(stream));
 }
 
 int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -1809,7 +1544,7 @@ int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, co
                       int split_tokens, void* stream) {
     return pd_decode_partial_ex(q, dtype, k, v, dtype, 1.0f, 1.0f, table, lengths, numerator, stats, batch,
                                 query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                                split_tokens, PD_HINT_NONE, stream);
+                                split_tokens, PD_HINT_NONE, nullptr, stream);
 }
 
 int pd_decode_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
@@ -1825,7 +1560,8 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out, cons
 int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
                  float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
                  float* out, int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                 int physical_pages, int splits, int split_tokens, int merge_mode, int hints, void* stream) {
+                 int physical_pages, int splits, int split_tokens, int merge_mode, int hints,
+                 const int32_t* length_bounds, void* stream) {
     int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                               query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                               split_tokens);
@@ -1838,7 +1574,7 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
     int stride = 1;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                         split_tokens, hints, s, &stride);
+                         split_tokens, hints, length_bounds, s, &stride);
     if (status != PD_OK) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
                      split_tokens, merge_mode, stride, s);
@@ -1850,7 +1586,7 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
               int split_tokens, int merge_mode, void* stream) {
     return pd_decode_ex(q, dtype, k, v, dtype, 1.0f, 1.0f, table, lengths, numerator, stats, out, batch,
                         query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                        merge_mode, PD_HINT_NONE, stream);
+                        merge_mode, PD_HINT_NONE, nullptr, stream);
 }
 
 int pd_append_kv(const void* k_new, const void* v_new, int dtype, const int32_t* table, const int32_t* positions,
@@ -1868,12 +1604,14 @@ int pd_append_kv(const void* k_new, const void* v_new, int dtype, const int32_t*
 
 int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype, const int32_t* table, int32_t* lengths,
                          void* k_cache, void* v_cache, int batch, int tokens, int kv_heads, int head_dim,
-                         int page_size, int table_width, int physical_pages, void* stream) {
-    const int status = check_append(k_new, v_new, dtype, table, lengths, k_cache, v_cache, batch, tokens, kv_heads,
-                                     head_dim, page_size, table_width, physical_pages);
+                         int page_size, int table_width, int physical_pages, int max_context, void* stream) {
+    int status = check_append(k_new, v_new, dtype, table, lengths, k_cache, v_cache, batch, tokens, kv_heads,
+                              head_dim, page_size, table_width, physical_pages);
+    if (status == PD_OK && (max_context < 0 || max_context > (1 << 20))) status = PD_ERR_SHAPE;
     if (status != PD_OK) return status;
     AppendParams a = append_params(k_new, v_new, dtype, table, k_cache, v_cache, tokens, kv_heads, head_dim,
                                    page_size, table_width, physical_pages);
+    a.capacity = std::min<int64_t>(a.capacity, max_context);
     a.lengths = lengths;
     hipLaunchKernelGGL(append_kv_advance_kernel, dim3(batch), dim3(256), 0, static_cast<hipStream_t>(stream), a);
     return launch_status();
@@ -1910,6 +1648,6 @@ const char* pd_status_string(int status) {
     }
 }
 
-int pd_abi_version(void) { return 11; }
+int pd_abi_version(void) { return PD_ABI_VERSION; }
 
 }  // extern "C"

@@ -1,0 +1,468 @@
+// Work and address map of the partition kernels, shared by the device code in
+// decode.hip and the host: which (sequence, partition, quarter, KV head, head
+// tile) a wave owns, which page-id window and token rows it reads, at which
+// byte offsets, and how a launch is shaped. Everything here is plain integer
+// arithmetic, so the same functions compile for gfx950 (hipcc) and for the
+// host C++ compiler; tests/address_audit.cpp enumerates every workgroup, wave,
+// lane and tile of a launch through them and checks each access against the
+// buffers the caller passes.
+//
+// Partitioning follows reference src/paged_decode/csrc/decode.cu:26-83 (split
+// of each sequence into split_tokens partitions of four states each, end clamp
+// min(len, W * T) at :42-44, page-id guard at :56-58); the decomposition into
+// quarters, tiles, workgroups and the compacted work list are this build's.
+#ifndef PAGED_DECODE_PARTITION_MAP_H
+#define PAGED_DECODE_PARTITION_MAP_H
+
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define PD_HD __host__ __device__ __forceinline__
+#else
+#define PD_HD inline
+#endif
+
+namespace pd {
+
+constexpr int kWave = 64;
+constexpr int kQuarters = 4;     // states per partition (quarters of the partition)
+constexpr int kTileTokens = 16;  // tokens per matrix-core tile
+
+// Compacted work lists are passed in the kernel arguments for batches of up
+// to kCompactMaxBatch sequences; each tail item covers up to kTailSpan of the
+// partitions a sequence may reach only after device-side appends, as one
+// partition of kTailSpan times the tokens.
+constexpr int kCompactMaxBatch = 64;
+constexpr int kTailSpan = 8;
+
+PD_HD int imin(int a, int b) { return a < b ? a : b; }
+PD_HD int imax(int a, int b) { return a > b ? a : b; }
+PD_HD int64_t lmin(int64_t a, int64_t b) { return a < b ? a : b; }
+
+struct PartialParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const int32_t* table;
+    const int32_t* lengths;
+    float* numerator;   // [B, Hq, 4 * splits, D]
+    float* stats;       // [B, Hq, 4 * splits, 2]
+    int batch;
+    int query_heads;
+    int group;          // query heads per KV head
+    int head_tiles;     // ceil(group / GT)
+    int heads_per_wg;   // KV heads per workgroup (hw)
+    int tiles_per_wg;   // head tiles per workgroup (tw)
+    int quarters_per_wg;  // partition quarters per workgroup (qw)
+    int page_shift;     // log2(page_size)
+    int table_width;
+    int physical_pages;
+    int splits;
+    int split_tokens;
+    uint32_t token_bytes;  // bytes between consecutive tokens of a page (kv_heads * D * elem)
+    uint64_t page_bytes;   // page_size * token_bytes
+    float scale_log2;      // log2(e) * k_scale / sqrt(D)
+    float v_scale;         // multiplies every stored numerator
+    // Compacted work list (compact != 0): the grid's items are, per sequence
+    // b in order, live_splits[b] main items (partitions 0 .. live_splits[b] - 1,
+    // one each) and then tail items, item_first[b + 1] - item_first[b] -
+    // live_splits[b] of them, tail item j covering the kTailSpan partitions
+    // from live_splits[b] + j * kTailSpan (fewer at the end), which a
+    // sequence reaches only if it grew on the device past the host's bound.
+    // Otherwise the grid is rectangular: every partition of every sequence is
+    // one item.
+    int compact;
+    int items;             // grid items (compact), else batch * splits
+    int32_t item_first[kCompactMaxBatch + 1];
+    int32_t live_splits[kCompactMaxBatch];
+    // Host only (launch choices, not read by the kernels).
+    int combine;           // the launch stores a workgroup's qw quarters as one state (kCombine)
+    int unshared_pages;    // PD_HINT_UNSHARED_PAGES
+    int mid_grid;          // 2-head x 2-quarter workgroups of a mid-size grid
+    int ragged_lengths;    // PD_HINT_RAGGED_LENGTHS
+    int stream_mode;       // non-temporal loads: 0 none, 1 V (FP8: K), 2 K and V
+    int head_tile;         // GT: query heads per wave's tile (the GQA group padded to 1/2/4/8/16)
+};
+
+// ---------------------------------------------------------------------------
+// Device-side map (also evaluated on the host by the address audit).
+
+// Workgroup coordinates (token group, head group) in dispatch order: the
+// linear dispatch index x + gx * y is read with the head group varying
+// fastest, so consecutively dispatched (and co-resident) workgroups cover all
+// KV-head groups of the same tokens -- whole token rows -- rather than one head
+// group's slice of many rows.
+struct BlockCoords {
+    int tokens;  // item * (4 / qw) + quarter group
+    int heads;   // KV heads [hg * hw, hg * hw + hw), head tiles [tg * tw, tg * tw + tw)
+    int z;       // sequence of a rectangular grid
+};
+
+PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t gx, uint32_t gy) {
+    if (gy == 1) return BlockCoords{static_cast<int>(bx), 0, static_cast<int>(bz)};
+    const uint64_t lin = bx + static_cast<uint64_t>(gx) * by;
+    if (static_cast<uint64_t>(gx) * gy <= 0xFFFFFFFFull) {
+        const uint32_t l32 = static_cast<uint32_t>(lin);
+        return BlockCoords{static_cast<int>(l32 / gy), static_cast<int>(l32 % gy), static_cast<int>(bz)};
+    }
+    return BlockCoords{static_cast<int>(lin / gy), static_cast<int>(lin % gy), static_cast<int>(bz)};
+}
+
+// The partitions one workgroup handles: count consecutive partitions from
+// first, of sequence b, quarter group qgroup. A main item (or a rectangular
+// grid's) is one partition; a tail item is the span of partitions past the
+// host's bound, streamed as one partition whose states go to the first
+// partition's slots (the span's other live partitions get the empty state).
+struct PartitionRange {
+    int b, first, count, qgroup;
+};
+
+PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& bc) {
+    const int groups = kQuarters / p.quarters_per_wg;
+    const int item = bc.tokens / groups;
+    PartitionRange r;
+    r.qgroup = bc.tokens - item * groups;
+    if (!p.compact) {
+        r.b = bc.z;
+        r.first = item;
+        r.count = 1;
+        return r;
+    }
+    // Sequence of the item: the last b with item_first[b] <= item
+    // (item_first is strictly increasing: every sequence has an item).
+    int b = 0, hi = p.batch - 1;
+    while (b < hi) {
+        const int mid = (b + hi + 1) >> 1;
+        if (p.item_first[mid] <= item) b = mid;
+        else hi = mid - 1;
+    }
+    const int local = item - p.item_first[b];
+    const int live = p.live_splits[b];
+    r.b = b;
+    if (local < live) {
+        r.first = local;
+        r.count = 1;
+    } else {
+        r.first = live + (local - live) * kTailSpan;  // tail item local - live
+        r.count = imin(kTailSpan, p.splits - r.first);
+    }
+    return r;
+}
+
+// Which KV head, head tile and token range a wave owns in the `count`
+// partitions from `split` of sequence b (raw device length len_raw), from its
+// workgroup's coordinates; the wave index splits into (head, tile, quarter).
+// The range's tokens are cut into four quarters of whole load groups.
+struct WaveWork {
+    int split, quarter, kv_head, tile, wb, we;
+    int64_t q_row;   // first query-head row of the tile
+    int heads_here;  // live query heads in the tile
+    bool dead;       // the partition starts at or past the sequence end: no state is written
+};
+
+template <int GT, int ALIGN>
+PD_HD WaveWork wave_work(const PartialParams& p, int b, int split, int count, int qgroup, int heads, int wave,
+                         int len_raw) {
+    WaveWork w;
+    const int qw = p.quarters_per_wg;
+    const int qq = wave % qw;
+    const int tt = (wave / qw) % p.tiles_per_wg;
+    const int hh = wave / (qw * p.tiles_per_wg);
+    const int tile_groups = p.head_tiles / p.tiles_per_wg;
+    w.split = split;
+    w.quarter = qgroup * qw + qq;
+    w.kv_head = (heads / tile_groups) * p.heads_per_wg + hh;
+    w.tile = (heads % tile_groups) * p.tiles_per_wg + tt;
+    const int capacity = p.table_width << p.page_shift;
+    const int len = imax(0, imin(len_raw, capacity));  // decode.cu:42-44
+    const int64_t first = static_cast<int64_t>(split) * p.split_tokens;
+    w.dead = first >= len;
+    const int tb = static_cast<int>(lmin(first, len));
+    const int te = static_cast<int>(lmin(first + static_cast<int64_t>(count) * p.split_tokens, len));
+    int per = (te - tb + kQuarters - 1) / kQuarters;
+    per = (per + ALIGN - 1) / ALIGN * ALIGN;
+    w.wb = imin(tb + w.quarter * per, te);
+    w.we = imin(w.wb + per, te);
+    const int member0 = w.tile * GT;
+    w.heads_here = imax(0, imin(GT, p.group - member0));
+    w.q_row = static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(w.kv_head) * p.group + member0;
+    return w;
+}
+
+// The first logical page a wave reads if its partitions are full length: lets
+// the page-id window be requested before the sequence length arrives.
+template <int ALIGN>
+PD_HD int speculative_page(const PartialParams& p, int split, int count, int qgroup, int wave) {
+    const int qw = p.quarters_per_wg;
+    const int quarter = qgroup * qw + wave % qw;
+    const int per_full = ((count * p.split_tokens + kQuarters - 1) / kQuarters + ALIGN - 1) / ALIGN * ALIGN;
+    const int capacity = p.table_width << p.page_shift;
+    const int64_t start = static_cast<int64_t>(split) * p.split_tokens + static_cast<int64_t>(quarter) * per_full;
+    return static_cast<int>(lmin(start, capacity - 1)) >> p.page_shift;
+}
+
+// Table entry lane `lane` of a wave loads for the page-id window at `window`
+// (clamped into the row, so every lane's load is in bounds).
+PD_HD int window_entry(const PartialParams& p, int window, int lane) {
+    return imin(window + lane, p.table_width - 1);
+}
+
+// One load group of `tokens` tokens starting at t0 (a 16-token matrix-core
+// tile, or one token row group of the FP32 kernel) within the wave's current
+// range [rb, re): the live token span [lo, hi] (or the last live token when
+// the group lies past re) and the page-id window slot of its first token.
+struct TileSpan {
+    int lo, hi, slot;
+};
+
+PD_HD TileSpan tile_span(const PartialParams& p, int t0, int tokens, int rb, int re, int window) {
+    TileSpan s;
+    s.lo = imax(t0, rb);
+    s.hi = imin(t0 + tokens, re) - 1;
+    if (s.lo > s.hi) s.lo = s.hi = re - 1;
+    s.slot = imin(imax((s.lo >> p.page_shift) - window, 0), kWave - 1);
+    return s;
+}
+
+// Whether the group's loads go to its page (else to the park row: a group
+// past re, or a page id outside [0, physical_pages), decode.cu:56-58).
+PD_HD bool tile_live(const PartialParams& p, int t0, int re, int page) {
+    return t0 < re && static_cast<uint32_t>(page) < static_cast<uint32_t>(p.physical_pages);
+}
+
+// Byte offset of a live group's page from the head's base: page * page_bytes.
+PD_HD uint64_t tile_page_offset(const PartialParams& p, bool ok, int page) {
+    return static_cast<uint64_t>(ok ? page : 0) * p.page_bytes;
+}
+
+// Byte offset within the page (or the park row) of token t, clamped into
+// [lo, hi], at lane byte offset lane_bytes of the token's head slice.
+PD_HD uint32_t token_offset(const PartialParams& p, bool ok, int t, const TileSpan& s, uint32_t lane_bytes) {
+    const int tk = imin(imax(t, s.lo), s.hi);
+    return ok ? static_cast<uint32_t>(tk & ((1 << p.page_shift) - 1)) * p.token_bytes + lane_bytes : lane_bytes;
+}
+
+// Tile token whose K the q.K^T A operand of matrix-core lane row r (r = lane
+// % 16) holds: sigma(r) = r / 4 + 4 (r % 4), which leaves the scores of
+// tokens g, g + 4, g + 8, g + 12 in lane group g, the P.V A layout.
+PD_HD int k_token_of_row(int r) { return (r >> 2) + 4 * (r & 3); }
+
+// Partitions after the first of a workgroup's span that hold tokens of the
+// sequence: their state slots take the empty state (the span's tokens are all
+// in the first partition's states). Zero for a single-partition item.
+PD_HD int extra_live_partitions(const PartialParams& p, int split, int count, int len_raw) {
+    const int capacity = p.table_width << p.page_shift;
+    const int64_t len = imax(0, imin(len_raw, capacity));
+    const int64_t live = (len + p.split_tokens - 1) / p.split_tokens;  // partitions holding tokens
+    return static_cast<int>(lmin(split + count, live) - lmin(split + 1, live));
+}
+
+// Numerator and stats element offsets of state `part` of query-head row `row`.
+PD_HD int64_t numerator_offset(const PartialParams& p, int64_t row, int part, int head_dim) {
+    return (row * (kQuarters * static_cast<int64_t>(p.splits)) + part) * head_dim;
+}
+PD_HD int64_t stats_offset(const PartialParams& p, int64_t row, int part) {
+    return (row * (kQuarters * static_cast<int64_t>(p.splits)) + part) * 2;
+}
+
+// ---------------------------------------------------------------------------
+// Launch shape (host).
+
+// Largest divisor of n not above cap.
+inline int largest_divisor(int n, int cap) {
+    for (int d = imin(n, cap); d > 1; --d)
+        if (n % d == 0) return d;
+    return 1;
+}
+
+// Workgroup shape: up to max_heads KV heads of the same tokens per workgroup
+// (their slices of a token row are then read together), all head tiles of
+// those heads, and as many partition quarters as fill `waves` waves (8, or
+// fewer for small grids: see plan_mfma). A KV head count with no divisor in
+// 2..max_heads keeps its whole token row in one workgroup when it fits (5 or
+// 7 heads in 8 waves).
+//
+// The matrix-core kernel takes 4 KV heads: at 8 KV heads, two workgroups of 4
+// heads x 2 quarters (quarters combined, V loads streamed when no page is
+// shared) measured faster per call than one of 8 heads x 1 quarter on every
+// shape tried on MI355X: Llama-3-8B B4 L4096 18.86 -> 17.31 us, the B16 L4096
+// batch of the reference's benchmark 50.7 -> 40.2 us, B64 L2048 122.3 ->
+// 103.8 us; with 32 KV heads, 32K-context MHA 97.2 -> 89.8 us at split 256.
+// Grids that would leave most CUs idle take smaller workgroups instead, and
+// grids smaller than the device skip the combine (see plan_mfma).
+inline void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads, int waves = 8) {
+    prm.heads_per_wg = largest_divisor(kv_heads, imin(max_heads, waves));
+    if (prm.heads_per_wg == 1 && kv_heads <= waves) prm.heads_per_wg = kv_heads;
+    prm.tiles_per_wg = largest_divisor(prm.head_tiles, waves / prm.heads_per_wg);
+    const int hw_tw = prm.heads_per_wg * prm.tiles_per_wg;
+    prm.quarters_per_wg = hw_tw * 4 <= waves ? 4 : hw_tw * 2 <= waves ? 2 : 1;
+}
+
+// Head tile: the GQA group padded to a power of two up to max_tile query
+// heads (16 for the matrix-core kernel, whose MFMA column block holds 16
+// heads; 8 for the FP32 kernel, whose accumulators grow with the tile);
+// larger groups are cut into tiles of max_tile.
+inline int head_tile(int group, int max_tile) {
+    int gt = 1;
+    while (gt < group && gt < max_tile) gt *= 2;
+    return gt;
+}
+
+// The work list. With per-sequence upper bounds on the lengths known to the
+// caller at launch (length_bounds, host memory; null if unknown) and a batch
+// of at most kCompactMaxBatch, sequence b gets ceil(bound_b / split_tokens)
+// main items and ceil((splits - that) / kTailSpan) tail items, when that is
+// fewer items than the rectangular batch * splits. A bound below the length
+// the kernel finds on the device only moves that sequence's later partitions
+// onto its tail items: results are the same, the launch slower.
+inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
+    prm.compact = 0;
+    prm.items = prm.batch * prm.splits;
+    if (length_bounds == nullptr || prm.batch > kCompactMaxBatch) return;
+    const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
+    int64_t total = 0;
+    int first[kCompactMaxBatch + 1];
+    int live[kCompactMaxBatch];
+    for (int b = 0; b < prm.batch; ++b) {
+        const int64_t bound = lmin(capacity, length_bounds[b] < 0 ? 0 : length_bounds[b]);
+        live[b] = static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
+        first[b] = static_cast<int>(total);
+        total += live[b] + (prm.splits - live[b] + kTailSpan - 1) / kTailSpan;
+    }
+    if (total >= prm.items) return;
+    first[prm.batch] = static_cast<int>(total);
+    prm.compact = 1;
+    prm.items = static_cast<int>(total);
+    for (int b = 0; b <= prm.batch; ++b) prm.item_first[b] = first[b];
+    for (int b = 0; b < prm.batch; ++b) prm.live_splits[b] = live[b];
+}
+
+struct Grid {
+    uint32_t x, y, z;
+};
+
+inline Grid partial_grid(const PartialParams& prm, int kv_heads) {
+    const uint32_t groups = static_cast<uint32_t>(kQuarters / prm.quarters_per_wg);
+    const uint32_t heads = static_cast<uint32_t>((kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg));
+    if (prm.compact) return Grid{static_cast<uint32_t>(prm.items) * groups, heads, 1};
+    return Grid{static_cast<uint32_t>(prm.splits) * groups, heads, static_cast<uint32_t>(prm.batch)};
+}
+
+inline int64_t workgroups(const Grid& g) { return static_cast<int64_t>(g.x) * g.y * g.z; }
+
+inline int partial_threads(const PartialParams& prm) {
+    return kWave * prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
+}
+
+// KV heads per workgroup of the matrix-core kernel, at most (FP32 kernel: 8).
+constexpr int kMfmaWorkgroupHeads = 4;
+
+// Launch shape of the matrix-core kernel on a device of `cus` compute units:
+// head tile, workgroup shape, quarter combine and streaming mode.
+inline void plan_mfma(PartialParams& prm, int kv_heads, int cus) {
+    const int gt = head_tile(prm.group, 16);
+    prm.head_tile = gt;
+    prm.head_tiles = (prm.group + gt - 1) / gt;
+    choose_workgroup(prm, kv_heads, kMfmaWorkgroupHeads);
+    // A grid of at most half as many 8-wave workgroups as CUs leaves most CUs
+    // idle, and each busy CU can keep only so many loads in flight. The same
+    // waves then go in smaller workgroups, the largest of 4, 2 or 1 waves
+    // that still gives two workgroups per CU (else 1 wave). Measured on
+    // MI355X, Llama-3-8B geometry (decode call, us):
+    //   B1 L4096 (64 workgroups of 8 waves): 12.4 -> 10.2 with 1 wave;
+    //   B1 L2048: 11.7 -> 9.9; FP8 B1 L4096: 12.6 -> 10.6-11.1;
+    //   B2 L4096 and B1 L8192 (128 workgroups): 13.2 -> 12.9 and
+    //   13.65 -> 13.1 with 2 waves.
+    // At 192 workgroups (B3 L4096) every smaller shape was slower (14.95 ->
+    // 15.3-19.0), so larger grids keep 8 waves.
+    //
+    // Grids of one to two 8-wave workgroups per CU with 2, 4 or 8 KV heads and
+    // GQA groups of up to 8 take workgroups of 2 KV heads x 2 quarters instead
+    // (4 waves, quarters combined). Measured on MI355X by graph replay of 200
+    // calls, N(0,1) data, K/V sets rotated past the Infinity Cache (decode
+    // call, us): Llama-3-8B B4 L4096 18.0-18.4 -> 17.4-17.6, B8 L4096 29.45
+    // -> 28.54, B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8
+    // L4096 with 4 KV heads 20.05 -> 19.1-19.2; ragged B4 batches within
+    // 0.1-0.25. B3 L4096 (192 workgroups) was slower with smaller workgroups
+    // of any kind (14.74 -> 15.05). Larger grids keep 8 waves when lengths
+    // are uniform (B16 L4096 55.1 -> 56.9, B32 L4096 105.7 -> 109.1) but
+    // not when they are ragged (PD_HINT_RAGGED_LENGTHS): then up to eight
+    // 8-wave workgroups per CU take the smaller ones (B16 with lengths
+    // uniform in [0, 4096] 37.8 -> 33.3, B32 65.1 -> 59.7; the reference's
+    // B16 L4096 batch 47.6 -> 44.0 in the benchmark). At sixteen per CU (a
+    // B16 page-32 L8192 batch at split 128) it was flat, so those keep 8.
+    const int64_t wg8 = workgroups(partial_grid(prm, kv_heads));
+    if (wg8 * 2 <= cus) {  // small grid
+        const int64_t waves_total = wg8 * (partial_threads(prm) / kWave);
+        int waves = 4;
+        while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
+        choose_workgroup(prm, kv_heads, kMfmaWorkgroupHeads, waves);
+    } else if (wg8 >= cus && wg8 <= (prm.ragged_lengths ? 8 : 2) * static_cast<int64_t>(cus) &&
+               (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
+        choose_workgroup(prm, kv_heads, 2, 4);
+        prm.mid_grid = 1;
+    }
+    // Combining a workgroup's quarters into one state cuts the state stores
+    // (written back at the kernel's end) and the merge's reads by qw; its
+    // fold runs after the slowest quarter. Measured on MI355X it pays for two
+    // quarters, and for four when the head tile is full (16 query heads:
+    // MQA-like groups, the largest states per KV byte); four quarters of
+    // smaller tiles were 0.3-0.7 us slower per call. A grid smaller than the
+    // CUs leaves the fold's tail exposed (B1 L4096: 12.05 us without, 12.43
+    // with), so such launches keep four states per partition.
+    const bool fills_device = workgroups(partial_grid(prm, kv_heads)) >= cus;
+    prm.combine = fills_device && (prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16));
+    // When the KV heads need several workgroups (kv_heads > heads_per_wg),
+    // each workgroup reads one head group's slice of every token row, and
+    // some 16-byte loads may be issued non-temporal. That is faster when
+    // nothing is read twice and slower when sequences share prefix pages,
+    // which streamed loads do not leave in the caches. Measured on MI355X
+    // (decode call, us):
+    //   - 4 or more head groups per row (16, 32 KV heads), no shared pages: K
+    //     and V streaming is fastest (32K-context MHA at split 256: 92.2; V
+    //     only 95.3; neither 98.6). With 25% shared prefix pages (B8 L4096, 32
+    //     KV heads): K and V 48.4, V only 43.0.
+    //   - 2 head groups (8 KV heads), no shared pages: V only (B64 L2048
+    //     103.8, K and V 104.7, neither 112.3; a ragged B16 page-32 batch 57.0
+    //     / 62.1 / 64.1). With 25% shared prefix pages (B16 page 32): neither
+    //     50.3, V only 52.0, K and V 59.3.
+    //   - The 2-head x 2-quarter workgroups of mid-size grids: with 2 KV
+    //     heads, one head group, streaming V anyway took B16 L4096 (GQA 8)
+    //     from 19.75 to 18.81 us per call.
+    // So the mode follows the page-sharing hint: unshared pages stream K and
+    // V (4+ groups) or V (2 groups, or one in a mid-size grid); pages that may
+    // be shared stream V (4+ groups) or nothing. FP8 V loads are 8-byte, so
+    // FP8 streams its 16-byte K row loads wherever 16-bit K/V would stream V.
+    const int groups = kv_heads / prm.heads_per_wg;
+    prm.stream_mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
+                      : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+}
+
+// Launch shape of the FP32 kernel.
+inline void plan_fp32(PartialParams& prm, int kv_heads) {
+    const int gt = head_tile(prm.group, 8);
+    prm.head_tile = gt;
+    prm.head_tiles = (prm.group + gt - 1) / gt;
+    choose_workgroup(prm, kv_heads, 8);
+}
+
+// LDS bytes of one wave's K tile in the matrix-core kernel: 16 token rows of
+// head_dim elements of elem bytes, each padded by one operand read (16 bytes
+// for 16-bit K, 8 for FP8).
+constexpr int mfma_stage_bytes(int head_dim, int elem) { return kTileTokens * (head_dim * elem + 8 * elem); }
+
+// LDS bytes of one quarter-combine slot: per-head max and denominator, and
+// head_dim / 16 float4 accumulators per lane.
+constexpr int combine_slot_bytes(int head_dim) { return 2 * 16 * 4 + (head_dim / 16) * kWave * 16; }
+
+// Dynamic LDS of a matrix-core launch: every wave's K tile, then the combine
+// slots ([waves / qw][qw - 1]) when the launch combines quarters.
+inline int mfma_lds_bytes(const PartialParams& prm, int head_dim, int elem) {
+    const int waves = partial_threads(prm) / kWave;
+    return waves * mfma_stage_bytes(head_dim, elem) +
+           (prm.combine ? waves / prm.quarters_per_wg * (prm.quarters_per_wg - 1) * combine_slot_bytes(head_dim) : 0);
+}
+
+}  // namespace pd
+
+#endif  // PAGED_DECODE_PARTITION_MAP_H

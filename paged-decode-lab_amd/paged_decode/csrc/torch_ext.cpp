@@ -14,9 +14,15 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <string>
 
 #include "paged_decode.h"
+
+#ifndef PD_BUILD_DIGEST
+#define PD_BUILD_DIGEST "unknown"
+#endif
 
 namespace {
 
@@ -105,13 +111,26 @@ int hints(bool unshared_pages, bool ragged_lengths) {
     return (unshared_pages ? PD_HINT_UNSHARED_PAGES : 0) | (ragged_lengths ? PD_HINT_RAGGED_LENGTHS : 0);
 }
 
+// Host pointer of the optional per-sequence length bounds (a CPU int32
+// tensor [batch]), or null.
+const int32_t* bounds_pointer(const c10::optional<torch::Tensor>& bounds, int64_t batch) {
+    if (!bounds.has_value()) return nullptr;
+    const auto& t = *bounds;
+    TORCH_CHECK(t.device().is_cpu() && t.scalar_type() == at::kInt && t.is_contiguous() && t.dim() == 1 &&
+                    t.size(0) == batch,
+                "length_bounds must be a contiguous CPU int32 tensor [batch]");
+    return t.data_ptr<int32_t>();
+}
+
 }  // namespace
 
 void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
             torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t split_tokens,
-            int64_t merge_mode, double k_scale, double v_scale, bool unshared_pages, bool ragged_lengths) {
+            int64_t merge_mode, double k_scale, double v_scale, bool unshared_pages, bool ragged_lengths,
+            c10::optional<torch::Tensor> length_bounds) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     check_output(q, out, merge_mode, s.splits);
+    const int32_t* bounds = bounds_pointer(length_bounds, s.batch);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     check_status(pd_decode_ex(q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k),
                               static_cast<float>(k_scale), static_cast<float>(v_scale), table.data_ptr<int32_t>(),
@@ -120,14 +139,15 @@ void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor tab
                               static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
                               static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
                               static_cast<int>(split_tokens), static_cast<int>(merge_mode),
-                              hints(unshared_pages, ragged_lengths), current_stream(q)));
+                              hints(unshared_pages, ragged_lengths), bounds, current_stream(q)));
 }
 
 // Partition stage alone (first launch of decode); used to time that kernel.
 void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
              torch::Tensor numerator, torch::Tensor stats, int64_t split_tokens, double k_scale, double v_scale,
-             bool unshared_pages, bool ragged_lengths) {
+             bool unshared_pages, bool ragged_lengths, c10::optional<torch::Tensor> length_bounds) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
+    const int32_t* bounds = bounds_pointer(length_bounds, s.batch);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
     check_status(pd_decode_partial_ex(
         q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k), static_cast<float>(k_scale),
@@ -135,7 +155,7 @@ void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor ta
         numerator.data_ptr<float>(), stats.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
         static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
         static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
-        static_cast<int>(split_tokens), hints(unshared_pages, ragged_lengths), current_stream(q)));
+        static_cast<int>(split_tokens), hints(unshared_pages, ragged_lengths), bounds, current_stream(q)));
 }
 
 // Merge stage alone (second launch of decode); lengths, page_size,
@@ -166,9 +186,10 @@ void merge(torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, torc
 
 // KV-cache append: k_new/v_new [B, tokens, Hkv, D] into k_cache/v_cache
 // [P, T, Hkv, D] at positions[b] + j (advance = false) or at lengths[b] + j with
-// lengths advanced on the device (advance = true, all or nothing per sequence).
+// lengths advanced on the device (advance = true, all or nothing per sequence,
+// positions below max_context only; max_context < 0 means the table's capacity).
 void append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor table, torch::Tensor positions,
-               torch::Tensor k_cache, torch::Tensor v_cache, bool advance) {
+               torch::Tensor k_cache, torch::Tensor v_cache, bool advance, int64_t max_context) {
     for (const auto& t : {k_new, v_new, table, positions, k_cache, v_cache}) {
         TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.device() == k_cache.device(),
                     "all tensors must be contiguous GPU tensors on one device");
@@ -194,9 +215,12 @@ void append_kv(torch::Tensor k_new, torch::Tensor v_new, torch::Tensor table, to
     const int pages = static_cast<int>(k_cache.size(0));
     hipStream_t stream = current_stream(k_cache);
     if (advance) {
+        const int64_t capacity = static_cast<int64_t>(width) * page;
+        const int64_t limit = max_context < 0 ? std::min<int64_t>(capacity, 1 << 20) : max_context;
+        TORCH_CHECK(limit <= (1 << 20), "max_context must not exceed 1048576");
         check_status(pd_append_kv_advance(k_new.data_ptr(), v_new.data_ptr(), dtype, table.data_ptr<int32_t>(),
                                           positions.data_ptr<int32_t>(), k_cache.data_ptr(), v_cache.data_ptr(), b,
-                                          tokens, kv, d, page, width, pages, stream));
+                                          tokens, kv, d, page, width, pages, static_cast<int>(limit), stream));
     } else {
         check_status(pd_append_kv(k_new.data_ptr(), v_new.data_ptr(), dtype, table.data_ptr<int32_t>(),
                                   positions.data_ptr<int32_t>(), k_cache.data_ptr(), v_cache.data_ptr(), b, tokens,
@@ -236,13 +260,16 @@ PYBIND11_MODULE(_C, m) {
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("table"), py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("out"),
           py::arg("split_tokens"), py::arg("merge_mode"), py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0,
-          py::arg("unshared_pages") = false, py::arg("ragged_lengths") = false);
+          py::arg("unshared_pages") = false, py::arg("ragged_lengths") = false,
+          py::arg("length_bounds") = py::none());
     m.def("partial", &partial, "Partition stage only", py::arg("q"), py::arg("k"), py::arg("v"), py::arg("table"),
           py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("split_tokens"),
           py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0, py::arg("unshared_pages") = false,
-          py::arg("ragged_lengths") = false);
+          py::arg("ragged_lengths") = false, py::arg("length_bounds") = py::none());
     m.def("merge", &merge, "Merge stage only");
-    m.def("append_kv", &append_kv, "Paged KV-cache append");
+    m.def("append_kv", &append_kv, "Paged KV-cache append", py::arg("k_new"), py::arg("v_new"), py::arg("table"),
+          py::arg("positions"), py::arg("k_cache"), py::arg("v_cache"), py::arg("advance"),
+          py::arg("max_context") = -1);
     m.def("table_from_csr", &table_from_csr, "CSR page lists to page table and lengths on the device",
           py::arg("indptr"), py::arg("indices"), py::arg("last_page_len"), py::arg("table"), py::arg("lengths"),
           py::arg("overflow") = py::none(), py::arg("page_size"), py::arg("max_context"));
@@ -250,5 +277,7 @@ PYBIND11_MODULE(_C, m) {
         return static_cast<int64_t>(pd_workspace_bytes(static_cast<int>(b), static_cast<int>(h),
                                                        static_cast<int>(d), static_cast<int>(s)));
     });
-    m.def("abi_version", &pd_abi_version);
+    m.def("abi_version", &pd_abi_version, "ABI version the loaded HIP library reports");
+    m.def("header_abi_version", [] { return PD_ABI_VERSION; }, "ABI version of the header this module was built with");
+    m.def("build_digest", [] { return std::string(PD_BUILD_DIGEST); }, "Digest of the sources this module was built from");
 }

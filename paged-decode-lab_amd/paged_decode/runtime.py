@@ -37,9 +37,11 @@ def load_extension():
     if not _build.built():
         _build.build()
     try:
-        return importlib.import_module(f"{__package__}._C")
+        extension = importlib.import_module(f"{__package__}._C")
     except ImportError as exc:  # pragma: no cover - exercised only on broken installs
         raise RuntimeError(f"paged_decode native extension failed to load: {exc}") from exc
+    _build.check_loaded(extension)
+    return extension
 
 
 class DecodePlan:
@@ -105,6 +107,11 @@ class DecodePlan:
         self._ragged_lengths = ragged_lengths(lengths)
         self._table = torch.tensor(table, device=self.device)
         self._lengths = torch.tensor(lengths, device=self.device)
+        # Host-side upper bounds on the device lengths: the library launches
+        # only the partitions they reach (ragged-batch compaction), plus a few
+        # workgroups for lengths that grew further on the device.
+        self._bounds = torch.from_numpy(lengths.astype(np.int32, copy=True))
+        self._bounds_known = True
         shape = (layout.batch, layout.query_heads, self.splits * _STATES_PER_SPLIT)
         self._numerator = torch.empty((*shape, layout.head_dim), device=self.device, dtype=torch.float32)
         self._stats = torch.empty((*shape, 2), device=self.device, dtype=torch.float32)
@@ -143,6 +150,8 @@ class DecodePlan:
             raise ValueError("lengths exceed the plan's reserved context; build a plan with a larger max_context")
         self._table.copy_(torch.from_numpy(table))
         self._lengths.copy_(torch.from_numpy(lengths))
+        self._bounds.copy_(torch.from_numpy(lengths))
+        self._bounds_known = True
         self._table_cpu, self._lengths_cpu = table, lengths
         self._unshared_pages = unshared_pages(table, self.layout.page_size, self.context_capacity)
         self._ragged_lengths = ragged_lengths(lengths)
@@ -177,6 +186,7 @@ class DecodePlan:
                                        self.layout.page_size, self.context_capacity)
         self._unshared_pages = False
         self._ragged_lengths = False
+        self._bounds_known = False
 
     def append(self, k_cache, v_cache, k_new, v_new):
         """Append new tokens at the plan's current lengths and advance them on the device.
@@ -184,8 +194,10 @@ class DecodePlan:
         ``k_new``/``v_new`` are ``[B, Hkv, D]`` (one token per sequence) or
         ``[B, tokens, Hkv, D]``; the cache tensors are those later passed to
         ``run``. A sequence is written only if all of its new positions fall on
-        valid pages of the plan's table within ``context_capacity``; otherwise
-        it and its length are unchanged. No host synchronisation: an append and
+        valid pages of the plan's table below ``context_capacity`` (the
+        reserved ``max_context``, which the plan's partitions cover);
+        otherwise it and its length are unchanged, so a plan built without
+        ``max_context`` above its longest sequence never grows that sequence. No host synchronisation: an append and
         a ``run`` can be captured together in one graph. ``max_context`` keeps
         the value of the last host-side metadata (construction or ``refresh``).
         """
@@ -195,7 +207,10 @@ class DecodePlan:
         _check_cache(k_cache, v_cache, k_new, v_new, expected_k, self.device)
         if k_new.shape[1] > self.context_capacity:
             raise ValueError("more new tokens than the plan's reserved context")
-        self._extension.append_kv(k_new, v_new, self._table, self._lengths, k_cache, v_cache, True)
+        self._extension.append_kv(k_new, v_new, self._table, self._lengths, k_cache, v_cache, True,
+                                  self.context_capacity)
+        if self._bounds_known:
+            self._bounds.add_(k_new.shape[1]).clamp_(max=self.context_capacity)
 
     @property
     def workspace_bytes(self):
@@ -229,7 +244,7 @@ class DecodePlan:
         self._check(q, k, v, k_scale, v_scale)
         self._extension.decode(q, k, v, self._table, self._lengths, self._numerator, self._stats,
                                self._out, self.split_tokens, self._merge_mode, float(k_scale), float(v_scale),
-                               self._unshared_pages, self._ragged_lengths)
+                               self._unshared_pages, self._ragged_lengths, self._length_bounds())
         return self._out
 
     def run_partial(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
@@ -237,7 +252,11 @@ class DecodePlan:
         self._check(q, k, v, k_scale, v_scale)
         self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
                                 self.split_tokens, float(k_scale), float(v_scale), self._unshared_pages,
-                                self._ragged_lengths)
+                                self._ragged_lengths, self._length_bounds())
+
+    def _length_bounds(self):
+        """Host upper bounds on the device lengths, or None after a device-side CSR refresh."""
+        return self._bounds if self._bounds_known else None
 
     def run_merge(self):
         """Merge stage only, from the current workspace; returns the borrowed output."""

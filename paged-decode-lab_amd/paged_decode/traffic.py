@@ -32,7 +32,8 @@ PACKAGE_ROOT = Path(__file__).resolve().parent.parent
 REPO = PACKAGE_ROOT.parent
 ROTATION_BYTES = 2 << 30
 COPY_BYTES = 256 << 20
-SOURCES = ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "include/paged_decode.h")
+SOURCES = ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "paged-decode-lab_amd/paged_decode/csrc/partition_map.h",
+           "include/paged_decode.h")
 
 
 def source_digest():

@@ -1,0 +1,121 @@
+"""Host memory checks: the partition kernels' address map and the C restatement.
+
+The reference ran compute-sanitizer memcheck over its GPU tests
+(tools/gpu_acceptance.sh:4-15). Here the same question -- does any access
+leave its buffer? -- is answered on the CPU:
+
+* ``tests/address_audit.cpp`` walks every workgroup, wave, lane and load group
+  of the partition launches for the measured workloads and the edge cases
+  (lengths around page and partition boundaries, invalid page ids, uncommon
+  head layouts, a 1M-token context in a 65536-wide table, pages above 4 GiB,
+  compacted work lists with exact, low and zero length bounds) through the
+  same ``partition_map.h`` functions the kernels call, and checks every load,
+  store and LDS access against its buffer, every live token against the page
+  its table entry names, and that every live state slot is written exactly
+  once. It is compiled with AddressSanitizer and UndefinedBehaviorSanitizer.
+* ``oracle/cpu_decode.c`` (the FP32 restatement the bench times) runs under
+  the same sanitizers on ragged, empty-row, invalid-page-id and both-format
+  cases through a small C driver.
+"""
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+CSRC = REPO / "paged-decode-lab_amd" / "paged_decode" / "csrc"
+SANITIZE = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer"]
+ENV = {**os.environ, "ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1", "UBSAN_OPTIONS": "print_stacktrace=1"}
+
+
+def compiler(name):
+    path = shutil.which(name)
+    if path is None:
+        pytest.skip(f"{name} not available")
+    return path
+
+
+def test_partition_address_map_stays_in_bounds(tmp_path):
+    exe = tmp_path / "address_audit"
+    subprocess.run([compiler("g++"), "-std=c++17", "-O1", "-g", "-Wall", "-Wno-unknown-pragmas", *SANITIZE,
+                    f"-I{CSRC}", str(REPO / "tests" / "address_audit.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600, env=ENV)
+    assert run.returncode == 0, run.stdout[-4000:] + run.stderr[-4000:]
+    assert ", 0 failures" in run.stdout
+    # The walk covered the measured workloads and the compacted launches.
+    for needle in ("llama3-8b B4 L4096 fp16", "ragged shared B16", "mqa B128", "long mha B1", "compact",
+                   "1M context", "pages above 4 GiB", "invalid page ids fp8"):
+        assert needle in run.stdout, needle
+
+
+CPU_DRIVER = r"""
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+int pd_cpu_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
+                  const int32_t* lengths, float* out, int batch, int q_heads, int kv_heads, int head_dim,
+                  int page_size, int table_width, int physical_pages, int split_tokens, int threads);
+
+static uint32_t state = 12345u;
+static float next_value(void) {
+    state = state * 1664525u + 1013904223u;
+    return (float)((state >> 8) & 0xFFFF) / 32768.0f - 1.0f;
+}
+
+/* One case: exact-size heap buffers, so any out-of-bounds access trips ASan. */
+static int run_case(int dtype, int batch, int hq, int hkv, int dim, int page, int width, int pages,
+                    const int32_t* lengths, int poison_ids, int split) {
+    size_t elem = dtype == 0 ? 4 : 2;
+    size_t qn = (size_t)batch * hq * dim, kn = (size_t)pages * page * hkv * dim;
+    unsigned char* q = malloc(qn * elem);
+    unsigned char* k = malloc(kn * elem);
+    unsigned char* v = malloc(kn * elem);
+    int32_t* table = malloc(sizeof(int32_t) * batch * width);
+    int32_t* lens = malloc(sizeof(int32_t) * batch);
+    float* out = malloc(sizeof(float) * qn);
+    for (size_t i = 0; i < qn * elem / 2; ++i) ((uint16_t*)q)[i] = dtype == 0 ? 0 : 0x3C00;
+    if (dtype == 0) for (size_t i = 0; i < qn; ++i) ((float*)q)[i] = next_value();
+    if (dtype == 0) for (size_t i = 0; i < kn; ++i) { ((float*)k)[i] = next_value(); ((float*)v)[i] = next_value(); }
+    else for (size_t i = 0; i < kn; ++i) { ((uint16_t*)k)[i] = 0x3800; ((uint16_t*)v)[i] = 0x3400; }
+    for (int i = 0; i < batch * width; ++i) table[i] = (i * 7) % pages;
+    if (poison_ids) { table[0] = -1; table[width + 1] = pages; table[2 * width] = 0x7FFFFFFF; }
+    memcpy(lens, lengths, sizeof(int32_t) * batch);
+    int status = pd_cpu_decode(q, k, v, dtype, table, lens, out, batch, hq, hkv, dim, page, width, pages, split, 2);
+    for (size_t i = 0; status == 0 && i < qn; ++i) if (!isfinite(out[i])) status = 9;
+    free(q); free(k); free(v); free(table); free(lens); free(out);
+    return status;
+}
+
+int main(void) {
+    const int32_t ragged[4] = {100, 0, 256, 17};
+    const int32_t beyond[4] = {1 << 20, 1, 33, 255};   /* first length past the table: clamped */
+    int failures = 0;
+    for (int dtype = 0; dtype < 2; ++dtype) {
+        for (int split = 1; split <= 256; split *= 16) {
+            failures += run_case(dtype, 4, 8, 2, 64, 16, 16, 64, ragged, 0, split) != 0;
+            failures += run_case(dtype, 4, 8, 2, 128, 32, 8, 32, beyond, 1, split) != 0;
+            failures += run_case(dtype, 4, 12, 4, 64, 16, 16, 64, ragged, 1, split) != 0;
+        }
+    }
+    printf("cpu restatement sanitizer cases: %d failures\n", failures);
+    return failures != 0;
+}
+"""
+
+
+def test_cpu_restatement_stays_in_bounds(tmp_path):
+    driver = tmp_path / "driver.c"
+    driver.write_text(CPU_DRIVER)
+    exe = tmp_path / "cpu_driver"
+    subprocess.run([compiler("gcc"), "-O1", "-g", "-march=x86-64-v3", "-fopenmp", *SANITIZE,
+                    str(REPO / "oracle" / "cpu_decode.c"), str(driver), "-o", str(exe), "-lm"],
+                   check=True, capture_output=True, text=True)
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300, env=ENV)
+    assert run.returncode == 0, run.stdout[-4000:] + run.stderr[-4000:]
+    assert "0 failures" in run.stdout

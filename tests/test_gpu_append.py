@@ -113,3 +113,51 @@ def test_captured_decode_loop_append_then_attend(merge):
         np.testing.assert_array_equal(plan._lengths.cpu().numpy(), host_lengths)
     np.testing.assert_array_equal(k.cpu().numpy(), host_k)
     assert host_lengths.tolist() == [106, 7, 256]
+
+
+@pytest.mark.parametrize("max_context", [None, 132])
+def test_captured_appends_stop_at_the_reserved_context(max_context):
+    """Appends never grow a sequence past the context the plan's partitions
+    cover: with the default plan (reserved context = the longest initial
+    length, 100) the length stays at 100; with 132 reserved it stops at 132.
+    Every replay's output matches the FP64 oracle on the tokens that are live."""
+    announce(f"captured appends bounded by the reserved context, max_context={max_context}")
+    layout = Layout(1, 8, 2, 128, 16, 16)
+    table = np.arange(16, dtype=np.int32)[None, ::-1].copy()    # 16 pages x 16 tokens: room for 256
+    lengths = np.array([100], dtype=np.int32)
+    plan = DecodePlan(layout, table, lengths, split_tokens=64, max_context=max_context)
+    limit = plan.context_capacity
+    assert limit == (100 if max_context is None else 132)
+    q, k, v = make_tensors(layout, seed=91)
+    k_step = torch.empty((1, 2, 128), device="cuda", dtype=torch.float16)
+    v_step = torch.empty_like(k_step)
+    plan.run(q, k, v)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            plan.append(k, v, k_step, v_step)
+            out = plan.run(q, k, v)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    host_q = q.cpu().numpy()
+    host_k, host_v = (t.cpu().numpy() for t in (k, v))
+    host_lengths = lengths.copy()
+    rng = np.random.default_rng(17)
+    for step in range(40):
+        ks = rng.standard_normal(k_step.shape).astype(np.float16)
+        vs = rng.standard_normal(v_step.shape).astype(np.float16)
+        k_step.copy_(torch.from_numpy(ks))
+        v_step.copy_(torch.from_numpy(vs))
+        graph.replay()
+        torch.cuda.synchronize()
+        host_k, _ = fp64.append_advance(host_k, table, host_lengths, ks[:, None], max_context=limit)
+        host_v, host_lengths = fp64.append_advance(host_v, table, host_lengths, vs[:, None], max_context=limit)
+        np.testing.assert_array_equal(plan._lengths.cpu().numpy(), host_lengths)
+        expected = fp64.dense_attention(host_q, host_k, host_v, table, host_lengths)
+        assert_parity(out.cpu().numpy(), expected, torch.float16)
+    assert host_lengths.tolist() == [min(limit, 140)]
+    np.testing.assert_array_equal(k.cpu().numpy(), host_k)
+    np.testing.assert_array_equal(v.cpu().numpy(), host_v)

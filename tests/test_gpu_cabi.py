@@ -74,7 +74,7 @@ def test_decode_ex_fp8_matches_oracle(kv_dtype, merge):
                               k_scale, v_scale, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
                               stats.data_ptr(), out.data_ptr(), layout.batch, layout.query_heads, layout.kv_heads,
                               layout.head_dim, layout.page_size, table.shape[1], layout.physical_pages, splits,
-                              split_tokens, merge, cabi.PD_HINT_UNSHARED_PAGES, stream())
+                              split_tokens, merge, cabi.PD_HINT_UNSHARED_PAGES, None, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     torch.cuda.synchronize()
     actual = out.cpu().numpy()
@@ -98,13 +98,13 @@ def test_partial_then_merge_entries_equal_decode_ex():
     status = lib.pd_decode_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_FP8_E4M3,
                               k_scale, v_scale, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
                               stats.data_ptr(), full.data_ptr(), *args, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_NONE,
-                              stream())
+                              None, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     num2, stats2, staged = workspace(layout, splits)
     status = lib.pd_decode_partial_ex(q.data_ptr(), cabi.PD_DTYPE_BF16, k.data_ptr(), v.data_ptr(),
                                       cabi.PD_DTYPE_FP8_E4M3, k_scale, v_scale, d_table.data_ptr(),
                                       d_lengths.data_ptr(), num2.data_ptr(), stats2.data_ptr(), *args,
-                                      cabi.PD_HINT_NONE, stream())
+                                      cabi.PD_HINT_NONE, None, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     status = lib.pd_decode_merge(num2.data_ptr(), stats2.data_ptr(), staged.data_ptr(), d_lengths.data_ptr(),
                                  layout.batch, layout.query_heads, layout.head_dim, layout.page_size, table.shape[1],
@@ -148,13 +148,28 @@ def test_append_entries_match_scatter(dtype):
     expected_v, _ = fp64.append_advance(as_bytes(v_cache), table, lengths, as_bytes(v_new))
     d_lengths = torch.from_numpy(lengths).cuda()
     status = lib.pd_append_kv_advance(k_new.data_ptr(), v_new.data_ptr(), KV_CODES[dtype], d_table.data_ptr(),
-                                      d_lengths.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *dims, stream())
+                                      d_lengths.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *dims, 64,
+                                      stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(as_bytes(k_cache), expected_k)
     np.testing.assert_array_equal(as_bytes(v_cache), expected_v)
     np.testing.assert_array_equal(d_lengths.cpu().numpy(), grown)
     assert grown.tolist() == [7, 64, 63]
+
+    # A context capacity below the table's (what the caller's partitions
+    # cover): sequence 0 grows 7 -> 9, the others would cross 9 and stay.
+    expected_k, grown = fp64.append_advance(expected_k, table, grown, as_bytes(k_new), max_context=9)
+    expected_v, _ = fp64.append_advance(expected_v, table, d_lengths.cpu().numpy(), as_bytes(v_new), max_context=9)
+    status = lib.pd_append_kv_advance(k_new.data_ptr(), v_new.data_ptr(), KV_CODES[dtype], d_table.data_ptr(),
+                                      d_lengths.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), *dims, 9,
+                                      stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(as_bytes(k_cache), expected_k)
+    np.testing.assert_array_equal(as_bytes(v_cache), expected_v)
+    np.testing.assert_array_equal(d_lengths.cpu().numpy(), grown)
+    assert grown.tolist() == [9, 64, 63]
 
 
 def test_context_sharded_over_two_partial_launches():
@@ -295,9 +310,105 @@ def test_page_sharing_hint_changes_no_bits(kv_heads, kv_dtype):
         status = lib.pd_decode_ex(q.data_ptr(), codes[0], k.data_ptr(), v.data_ptr(), codes[1], *scales,
                                   d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(), stats.data_ptr(),
                                   out.data_ptr(), batch, 32, kv_heads, 128, page, width, layout.physical_pages,
-                                  splits, split_tokens, cabi.PD_MERGE_SERIAL, hint, stream())
+                                  splits, split_tokens, cabi.PD_MERGE_SERIAL, hint, None, stream())
         assert status == cabi.PD_OK, cabi.status_string(lib, status)
         outs.append(out)
     torch.cuda.synchronize()
     torch.testing.assert_close(outs[1], outs[0], rtol=0, atol=0)
     assert torch.isfinite(outs[0]).all()
+
+
+def int32_array(values):
+    return np.ascontiguousarray(values, dtype=np.int32)
+
+
+BOUND_CASES = {
+    # name: (layout args (B, Hq, Hkv, D, T, pages per sequence), lengths, split_tokens, dtype)
+    "gqa_ragged": ((4, 32, 8, 128, 16, 64), [1024, 0, 517, 1000], 64, np.float16),
+    "mqa_combined_tail": ((64, 16, 1, 64, 16, 64), None, 64, np.float16),
+    "mid_grid_combined_tail": ((16, 32, 8, 128, 16, 256), [4096, 4000, 2500, 4096, 4096, 3000, 4096, 1] * 2, 256,
+                               np.float16),
+    "fp32": ((2, 8, 2, 64, 16, 16), [100, 256], 32, np.float32),
+}
+
+
+@pytest.mark.parametrize("bounds_kind", ["exact", "half", "zero", "above"])
+@pytest.mark.parametrize("case", sorted(BOUND_CASES))
+def test_length_bounds_compact_the_grid_without_changing_results(case, bounds_kind):
+    """Host length bounds (pd_decode_ex's length_bounds) only reshape the grid:
+    exact bounds drop the partitions past each sequence's end; bounds below
+    the device lengths ("half", "zero") put the later partitions on the tail
+    workgroups, which stride over them (with the quarter combine in the MQA
+    and mid-grid cases, so the combine slots are reused across partitions);
+    bounds above them change nothing. Every variant matches the FP64 oracle
+    and the unbounded call to FP32 rounding."""
+    (b, hq, hkv, d, t, per_seq), lengths, split_tokens, dtype = BOUND_CASES[case]
+    announce(f"length bounds {case} {bounds_kind}")
+    lib = cabi.load()
+    layout = Layout(b, hq, hkv, d, t, b * per_seq)
+    rng = np.random.default_rng(41)
+    table = rng.permutation(layout.physical_pages).reshape(b, per_seq).astype(np.int32)
+    if lengths is None:
+        lengths = rng.integers(0, per_seq * t + 1, size=b)
+        lengths[0] = per_seq * t
+    lengths = int32_array(lengths)
+    bounds = {"exact": lengths, "half": lengths // 2, "zero": np.zeros_like(lengths),
+              "above": np.minimum(lengths + 3 * split_tokens, per_seq * t)}[bounds_kind]
+    bounds = int32_array(bounds)
+    host = host_tensors(layout, dtype=dtype, seed=9)
+    q, k, v = (torch.from_numpy(x).cuda() for x in host)
+    code = cabi.PD_DTYPE_F32 if dtype == np.float32 else cabi.PD_DTYPE_F16
+    splits = -(-int(lengths.max()) // split_tokens)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    outs = []
+    for bound_ptr in (None, bounds.ctypes.data_as(ctypes.c_void_p)):
+        num, stats, out = workspace(layout, splits)
+        status = lib.pd_decode_ex(q.data_ptr(), code, k.data_ptr(), v.data_ptr(), code, 1.0, 1.0,
+                                  d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(), stats.data_ptr(),
+                                  out.data_ptr(), b, hq, hkv, d, t, per_seq, layout.physical_pages, splits,
+                                  split_tokens, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_UNSHARED_PAGES, bound_ptr,
+                                  stream())
+        assert status == cabi.PD_OK, cabi.status_string(lib, status)
+        outs.append(out)
+    torch.cuda.synchronize()
+    expected = fp64.dense_attention(*host, table, lengths)
+    for out in outs:
+        assert_parity(out.cpu().numpy(), expected, dtype)
+    torch.testing.assert_close(outs[1], outs[0], rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(outs[1].cpu().numpy()[lengths == 0], 0.0)
+
+
+def test_length_bounds_partition_stage_writes_every_live_state():
+    """pd_decode_partial_ex with bounds far below the device lengths still writes
+    every live state (tail workgroups cover them) and none past each sequence's
+    end: NaN-poisoned slots past the end stay NaN, and pd_decode_merge over the
+    workspace matches the FP64 oracle."""
+    announce("length bounds: partition stage coverage")
+    lib = cabi.load()
+    layout = Layout(3, 16, 4, 128, 16, 3 * 32)
+    rng = np.random.default_rng(5)
+    table = rng.permutation(layout.physical_pages).reshape(3, 32).astype(np.int32)
+    lengths = int32_array([512, 77, 300])
+    bounds = int32_array([16, 0, 100])
+    host = host_tensors(layout, dtype=np.float16, seed=4)
+    q, k, v = (torch.from_numpy(x).cuda() for x in host)
+    split_tokens = 32
+    splits = 16
+    num, stats, out = workspace(layout, splits)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    dims = (3, 16, 4, 128, 16, 32, layout.physical_pages, splits, split_tokens)
+    status = lib.pd_decode_partial_ex(q.data_ptr(), cabi.PD_DTYPE_F16, k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16,
+                                      1.0, 1.0, d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(),
+                                      stats.data_ptr(), *dims, cabi.PD_HINT_NONE,
+                                      bounds.ctypes.data_as(ctypes.c_void_p), stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    status = lib.pd_decode_merge(num.data_ptr(), stats.data_ptr(), out.data_ptr(), d_lengths.data_ptr(), 3, 16, 128,
+                                 16, 32, splits, split_tokens, cabi.PD_MERGE_SERIAL, stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    torch.cuda.synchronize()
+    st = stats.cpu().numpy()
+    for b, n in enumerate(lengths):
+        live_states = 4 * (-(-int(n) // split_tokens))
+        assert np.isfinite(st[b, :, :live_states]).all()
+        assert np.isnan(st[b, :, live_states:]).all()
+    assert_parity(out.cpu().numpy(), fp64.dense_attention(*host, table, lengths), np.float16)

@@ -366,7 +366,12 @@ def test_nan_poisoned_workspace_live_states_written_dead_states_untouched():
 
 @pytest.mark.parametrize("merge", ["serial", "shared"])
 def test_refresh_loads_new_metadata_in_place(merge):
-    """refresh(): new table and lengths, same buffers; graphs replay the new metadata."""
+    """refresh(): new table and lengths, same buffers; graphs replay the new metadata.
+
+    The captured launch keeps the host length bounds of its capture, so after a
+    refresh it may run another (compacted) grid than an eager call: lengths
+    past the captured bounds go to tail workgroups. Both match the FP64
+    oracle, and each other to FP32 rounding."""
     layout = Layout(3, 16, 4, 128, 16, 3 * 64)
     rng = np.random.default_rng(11)
     q, k, v = make_tensors(layout, seed=11)
@@ -397,7 +402,8 @@ def test_refresh_loads_new_metadata_in_place(merge):
         captured.fill_(float("nan"))
         graph.replay()
         torch.cuda.synchronize()
-        torch.testing.assert_close(captured, eager, rtol=0, atol=0)
+        assert_parity(captured.cpu().numpy(), expected, torch.float16)
+        torch.testing.assert_close(captured, eager, rtol=1e-5, atol=1e-6)
 
 
 def test_refresh_rejects_what_does_not_fit():

@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 11
+    assert lib.pd_abi_version() == 12
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -95,7 +95,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != 11) return 1;
+    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 12) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
@@ -212,13 +212,16 @@ def test_append_entries_reject_invalid_arguments():
     base = dict(dtype=1, batch=4, tokens=1, kv_heads=8, head_dim=128, page_size=16, table_width=256,
                 physical_pages=1024)
 
-    def call(fn, ptr_over=None, **over):
+    def call(fn, ptr_over=None, max_context=None, **over):
         a = {**base, **over}
         p = list(ptrs)
         for i, value in (ptr_over or {}).items():
             p[i] = value
-        return fn(p[0], p[1], a["dtype"], p[2], p[3], p[4], p[5], a["batch"], a["tokens"], a["kv_heads"],
-                  a["head_dim"], a["page_size"], a["table_width"], a["physical_pages"], None)
+        args = [p[0], p[1], a["dtype"], p[2], p[3], p[4], p[5], a["batch"], a["tokens"], a["kv_heads"],
+                a["head_dim"], a["page_size"], a["table_width"], a["physical_pages"]]
+        if fn is lib.pd_append_kv_advance:
+            args.append(4096 if max_context is None else max_context)
+        return fn(*args, None)
 
     for fn in (lib.pd_append_kv, lib.pd_append_kv_advance):
         for i in range(6):
@@ -227,6 +230,9 @@ def test_append_entries_reject_invalid_arguments():
         for over in (dict(batch=0), dict(tokens=0), dict(head_dim=96), dict(page_size=8), dict(table_width=0),
                      dict(physical_pages=0)):
             assert call(fn, **over) == cabi.PD_ERR_SHAPE
+    # The advance entry's context capacity: 0 .. 1048576 tokens.
+    for max_context in (-1, (1 << 20) + 1):
+        assert call(lib.pd_append_kv_advance, max_context=max_context) == cabi.PD_ERR_SHAPE
 
 
 @pytest.mark.parametrize("q_dtype,kv_dtype,k_scale,v_scale", [
@@ -241,10 +247,10 @@ def test_extended_entry_rejects_formats_and_scales(q_dtype, kv_dtype, k_scale, v
     lib = cabi.load()
     ptrs, _keep = fake(8)
     status = lib.pd_decode_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3], ptrs[4],
-                              ptrs[5], ptrs[6], ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, 0, None)
+                              ptrs[5], ptrs[6], ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, 0, None, None)
     assert status == cabi.PD_ERR_DTYPE
     status = lib.pd_decode_partial_ex(ptrs[0], q_dtype, ptrs[1], ptrs[2], kv_dtype, k_scale, v_scale, ptrs[3],
-                                      ptrs[4], ptrs[5], ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, None)
+                                      ptrs[4], ptrs[5], ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, None, None)
     assert status == cabi.PD_ERR_DTYPE
 
 
@@ -256,10 +262,10 @@ def test_extended_entries_reject_unknown_hints(hints):
     ptrs, _keep = fake(8)
     f16 = cabi.PD_DTYPE_F16
     status = lib.pd_decode_ex(ptrs[0], f16, ptrs[1], ptrs[2], f16, 1.0, 1.0, ptrs[3], ptrs[4], ptrs[5], ptrs[6],
-                              ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, hints, None)
+                              ptrs[7], 4, 32, 8, 128, 16, 256, 1024, 16, 256, 0, hints, None, None)
     assert status == cabi.PD_ERR_HINT
     status = lib.pd_decode_partial_ex(ptrs[0], f16, ptrs[1], ptrs[2], f16, 1.0, 1.0, ptrs[3], ptrs[4], ptrs[5],
-                                      ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, hints, None)
+                                      ptrs[6], 4, 32, 8, 128, 16, 256, 1024, 16, 256, hints, None, None)
     assert status == cabi.PD_ERR_HINT
     assert "hint" in cabi.status_string(lib, cabi.PD_ERR_HINT)
 

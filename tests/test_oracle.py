@@ -209,3 +209,19 @@ def test_append_advance_is_all_or_nothing():
     out, lengths = fp64.append_advance(cache, table, np.array([1, 1]), new)
     np.testing.assert_array_equal(lengths, [3, 1])          # seq 1 would need page -1
     assert out[0, 1, 0, 0] == 1 and out[1, 0, 0, 0] == 2 and out[2:].sum() == 0
+
+
+def test_append_advance_stops_at_the_context_capacity():
+    """A capacity below the table's refuses any append that would cross it,
+    all or nothing, and leaves the cache untouched."""
+    cache = np.zeros((4, 2, 1, 1))
+    table = np.array([[0, 1], [2, 3]], dtype=np.int32)
+    new = np.arange(1, 5, dtype=np.float64).reshape(2, 2, 1, 1)
+    out, lengths = fp64.append_advance(cache, table, np.array([0, 1]), new, max_context=2)
+    np.testing.assert_array_equal(lengths, [2, 1])          # seq 1 would reach position 2
+    assert out[0, 0, 0, 0] == 1 and out[0, 1, 0, 0] == 2 and out[1:].sum() == 0
+    same, lengths = fp64.append_advance(out, table, lengths, new, max_context=2)
+    np.testing.assert_array_equal(lengths, [2, 1])
+    np.testing.assert_array_equal(same, out)
+    _, lengths = fp64.append_advance(cache, table, np.array([0, 1]), new, max_context=100)
+    np.testing.assert_array_equal(lengths, [2, 3])          # above the table's 4: the table bounds it
