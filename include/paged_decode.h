@@ -58,7 +58,8 @@ enum pd_status {
     PD_ERR_SPLIT = 4,         /* splits / split_tokens outside their range */
     PD_ERR_MERGE = 5,         /* unknown merge mode or shared-merge bound exceeded */
     PD_ERR_LAUNCH = 6,        /* the HIP runtime rejected a kernel launch */
-    PD_ERR_HINT = 7           /* unknown bits in the hints argument */
+    PD_ERR_HINT = 7,          /* unknown bits in the hints argument */
+    PD_ERR_SCRATCH = 8        /* pd_decode_scratch: the workspace does not fit PD_SCRATCH_BYTES */
 };
 
 /* Storage formats. q, k and v share F32, F16 or BF16 in pd_decode; the _ex
@@ -176,6 +177,38 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out,
                     const int32_t* lengths, int batch, int query_heads, int head_dim,
                     int page_size, int table_width, int splits, int split_tokens,
                     int merge_mode, void* stream);
+
+/*
+ * pd_decode_ex without a caller workspace: the partition states live in a
+ * static device array of the library, PD_SCRATCH_BYTES per device, held
+ * from the library's load on a device until the process exits. No
+ * counterpart in the reference (whose workspace the plan allocates,
+ * src/paged_decode/runtime.py:64-68); it is for callers that cannot
+ * allocate: code under hipGraph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. The call allocates and frees nothing.
+ *
+ * Limit: the states must fit, numerator bytes rounded up to 256 plus stats
+ * bytes <= PD_SCRATCH_BYTES, i.e.
+ *   ceil(batch * query_heads * 4 * splits * head_dim * 4 / 256) * 256
+ *     + batch * query_heads * 4 * splits * 2 * 4 <= PD_SCRATCH_BYTES
+ * (Llama-3-8B B4 L4096 at split 256: 4.3 MB; 32 heads x 32K context at
+ * split 128: 17 MB); larger requests return PD_ERR_SCRATCH before anything
+ * is launched. The states need no initialisation (each call writes every
+ * state it reads), so nothing is cleared between calls. Every call on one
+ * device shares that device's array: calls that overlap on one device (on
+ * different streams, or from several threads) race and must be serialised
+ * by the caller. The first call on each device looks up the array's device
+ * address (hipGetSymbolAddress); make that first call outside graph capture.
+ * Otherwise as pd_decode_ex: same arguments minus numerator and stats, same
+ * results bit for bit.
+ */
+#define PD_SCRATCH_BYTES (32u << 20)
+int pd_decode_scratch(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
+                      float k_scale, float v_scale,
+                      const int32_t* table, const int32_t* lengths, float* out,
+                      int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                      int table_width, int physical_pages, int splits, int split_tokens,
+                      int merge_mode, int hints, const int32_t* length_bounds, void* stream);
 
 /*
  * Paged KV-cache append, the write step before decode. Writes `tokens` new

@@ -28,6 +28,8 @@ PD_HINT_NONE = 0
 PD_HINT_UNSHARED_PAGES = 1
 PD_HINT_RAGGED_LENGTHS = 2
 PD_ERR_HINT = 7
+PD_ERR_SCRATCH = 8
+PD_SCRATCH_BYTES = 32 << 20
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -35,6 +37,7 @@ _F = ctypes.c_float
 PROTOTYPES = {
     "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
     "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 11 + [_P, _P]),
+    "pd_decode_scratch": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P] + [_I] * 11 + [_P, _P]),
     "pd_decode_partial": (_I, [_P, _P, _P, _I, _P, _P, _P, _P] + [_I] * 9 + [_P]),
     "pd_decode_partial_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P] + [_I] * 10 + [_P, _P]),
     "pd_decode_merge": (_I, [_P, _P, _P, _P] + [_I] * 8 + [_P]),

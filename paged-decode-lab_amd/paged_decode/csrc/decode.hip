@@ -1519,6 +1519,43 @@ AppendParams append_params(const void* k_new, const void* v_new, int dtype, cons
     return a;
 }
 
+// ---------------------------------------------------------------------------
+// Static scratch for pd_decode_scratch: the partition states of callers that
+// cannot allocate (graph capture, serving loops, harnesses that forbid
+// hipMalloc). One array per device, PD_SCRATCH_BYTES long, held by the
+// process until it exits; every pd_decode_scratch call on a device uses the
+// same array, so calls that overlap on one device race. Host code never
+// passes `scratch` itself to a kernel (in host code the name is a stand-in,
+// not a device address): the device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current, and only that pointer
+// is used.
+static __device__ __align__(256) float scratch[PD_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the current device, or nullptr if the
+// runtime cannot give it.
+float* scratch_address() {
+    static std::atomic<float*> cached[kMaxDevices];
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return nullptr;
+    float* ptr = cached[device].load(std::memory_order_acquire);
+    if (ptr == nullptr) {
+        void* address = nullptr;
+        if (hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)) != hipSuccess || address == nullptr) return nullptr;
+        ptr = static_cast<float*>(address);
+        cached[device].store(ptr, std::memory_order_release);
+    }
+    return ptr;
+}
+
+// The scratch holds numerator [B, Hq, 4 * splits, D] at offset 0 and stats
+// [B, Hq, 4 * splits, 2] after it, at the next 256-byte boundary.
+size_t scratch_stats_offset(int batch, int query_heads, int head_dim, int splits) {
+    const size_t numerator = static_cast<size_t>(batch) * query_heads * kQuarters * splits * head_dim * sizeof(float);
+    return (numerator + 255) / 256 * 256;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1589,6 +1626,34 @@ int pd_decode(const void* q, const void* k, const void* v, int dtype, const int3
                         merge_mode, PD_HINT_NONE, nullptr, stream);
 }
 
+int pd_decode_scratch(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
+                      float v_scale, const int32_t* table, const int32_t* lengths, float* out, int batch,
+                      int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
+                      int physical_pages, int splits, int split_tokens, int merge_mode, int hints,
+                      const int32_t* length_bounds, void* stream) {
+    // Shapes are checked before any runtime call, so a rejected request
+    // touches no device; the stand-in pointers only pass the null checks.
+    float* const stand_in = reinterpret_cast<float*>(alignof(float));
+    int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, stand_in, stand_in,
+                              batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
+                              splits, split_tokens);
+    if (status == PD_OK)
+        status = check_merge(stand_in, stand_in, out, lengths, batch, query_heads, head_dim, page_size, table_width,
+                             splits, split_tokens, merge_mode);
+    if (status == PD_OK) status = check_hints(hints);
+    if (status != PD_OK) return status;
+    const size_t stats_offset = scratch_stats_offset(batch, query_heads, head_dim, splits);
+    const size_t stats_bytes = static_cast<size_t>(batch) * query_heads * kQuarters * splits * 2 * sizeof(float);
+    if (stats_offset + stats_bytes > PD_SCRATCH_BYTES) return PD_ERR_SCRATCH;
+    float* const base = scratch_address();
+    if (base == nullptr) return PD_ERR_SCRATCH;
+    float* const numerator = base;
+    float* const stats = base + stats_offset / sizeof(float);
+    return pd_decode_ex(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, out, batch,
+                        query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
+                        merge_mode, hints, length_bounds, stream);
+}
+
 int pd_append_kv(const void* k_new, const void* v_new, int dtype, const int32_t* table, const int32_t* positions,
                  void* k_cache, void* v_cache, int batch, int tokens, int kv_heads, int head_dim, int page_size,
                  int table_width, int physical_pages, void* stream) {
@@ -1644,6 +1709,9 @@ const char* pd_status_string(int status) {
         case PD_ERR_MERGE: return "unknown merge mode or shared merge requires at most 4096 partial states (4 per split)";
         case PD_ERR_LAUNCH: return "kernel launch failed";
         case PD_ERR_HINT: return "unknown hint bits";
+        case PD_ERR_SCRATCH:
+            return "the workspace does not fit the library's static scratch (PD_SCRATCH_BYTES), or its device "
+                   "address could not be obtained";
         default: return "unknown status";
     }
 }

@@ -317,3 +317,26 @@ def test_table_from_csr_rejects_invalid_arguments():
     for over in (dict(batch=0), dict(batch=65536), dict(width=0), dict(width=65537), dict(page=8),
                  dict(max_context=-1), dict(max_context=(1 << 20) + 1)):
         assert call(*ptrs, **over) == cabi.PD_ERR_SHAPE, over
+
+
+def test_scratch_entry_rejects_before_touching_a_device():
+    """pd_decode_scratch checks pointers, shapes and the PD_SCRATCH_BYTES bound on the host, before any
+    runtime call (no GPU here)."""
+    lib = cabi.load()
+    ptrs, _keep = fake(6)
+    f16 = cabi.PD_DTYPE_F16
+
+    def call(out=ptrs[5], batch=4, heads=32, splits=16, merge=0, hints=0):
+        return lib.pd_decode_scratch(ptrs[0], f16, ptrs[1], ptrs[2], f16, 1.0, 1.0, ptrs[3], ptrs[4], out, batch,
+                                     heads, 8, 128, 16, 256, 1024, splits, 256, merge, hints, None, None)
+
+    assert call(out=None) == cabi.PD_ERR_NULL_POINTER
+    assert call(batch=0) == cabi.PD_ERR_SHAPE
+    assert call(merge=3) == cabi.PD_ERR_MERGE
+    assert call(hints=4) == cabi.PD_ERR_HINT
+    # 64 x 64 rows of 4 x 64 states of 520 bytes: 545 MB of states, far above the 32 MiB scratch.
+    assert call(batch=64, heads=64, splits=64) == cabi.PD_ERR_SCRATCH
+    # B1 Hq32 D128 takes 32 * 4 * 520 B = 66,560 B of states per split: 504 splits fit, 505 do not.
+    assert call(batch=1, heads=32, splits=505) == cabi.PD_ERR_SCRATCH
+    assert "scratch" in cabi.status_string(lib, cabi.PD_ERR_SCRATCH)
+    assert cabi.PD_SCRATCH_BYTES == 32 << 20
