@@ -63,11 +63,28 @@ def _atomic_output(path):
     return path.with_name(path.name + f".tmp{os.getpid()}")
 
 
-def build_hip_library(verbose=False):
+def build_hip_library(verbose=False, jobs=None):
+    """Compile every csrc/*.hip unit for gfx950 in parallel, then link the library."""
+    from concurrent.futures import ThreadPoolExecutor
+
     hipcc = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
+    units = sorted(CSRC.glob("*.hip"))
+    objects_dir = PACKAGE / "_build_objects"
+    objects_dir.mkdir(exist_ok=True)
+    compile_flags = [f for f in HIP_FLAGS if f != "-shared"]
+
+    def compile_unit(unit):
+        obj = objects_dir / (unit.stem + ".o")
+        _run([hipcc, *compile_flags, "-c", "-I", INCLUDE, "-I", CSRC, "-o", obj, unit], verbose)
+        return obj
+
+    workers = jobs or max(1, min(len(units), len(os.sched_getaffinity(0)), 16))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(compile_unit, units))
     tmp = _atomic_output(HIP_LIBRARY)
-    _run([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, "-o", tmp, CSRC / "decode.hip"], verbose)
+    _run([hipcc, *HIP_FLAGS, "-o", tmp, *objects], verbose)
     os.replace(tmp, HIP_LIBRARY)
+    shutil.rmtree(objects_dir, ignore_errors=True)
     return HIP_LIBRARY
 
 

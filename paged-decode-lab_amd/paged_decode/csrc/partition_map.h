@@ -63,18 +63,21 @@ struct PartialParams {
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
     float v_scale;         // multiplies every stored numerator
-    // Compacted work list (compact != 0): the grid's items are, per sequence
-    // b in order, live_splits[b] main items (partitions 0 .. live_splits[b] - 1,
-    // one each) and then tail items, item_first[b + 1] - item_first[b] -
-    // live_splits[b] of them, tail item j covering the kTailSpan partitions
-    // from live_splits[b] + j * kTailSpan (fewer at the end), which a
-    // sequence reaches only if it grew on the device past the host's bound.
-    // Otherwise the grid is rectangular: every partition of every sequence is
-    // one item.
+    // Compacted work list (compact != 0): the grid's items are first the main
+    // items of every sequence, in sequence order -- sequence b has
+    // main_first[b + 1] - main_first[b] of them, partitions 0, 1, ... one
+    // each -- and then the tail items, again in sequence order: sequence b's
+    // tail_first[b + 1] - tail_first[b] tail items, tail item j covering the
+    // kTailSpan partitions after its main ones from j * kTailSpan on (fewer
+    // at the end), which a sequence reaches only if it grew on the device
+    // past the host's bound. Main items come first so that the live
+    // workgroups are dispatched, and placed on the CUs, as they would be
+    // with no tail at all. Otherwise the grid is rectangular: every partition
+    // of every sequence is one item.
     int compact;
     int items;             // grid items (compact), else batch * splits
-    int32_t item_first[kCompactMaxBatch + 1];
-    int32_t live_splits[kCompactMaxBatch];
+    int32_t main_first[kCompactMaxBatch + 1];
+    int32_t tail_first[kCompactMaxBatch + 1];
     // Host only (launch choices, not read by the kernels).
     int combine;           // the launch stores a workgroup's qw quarters as one state (kCombine)
     int unshared_pages;    // PD_HINT_UNSHARED_PAGES
@@ -117,33 +120,40 @@ struct PartitionRange {
     int b, first, count, qgroup;
 };
 
+// kCompact is the launch's p.compact, fixed at compile time: a kernel built
+// for rectangular grids carries no work-list search, whose control flow would
+// otherwise keep the compiler from loading the kernel arguments in one batch
+// before the first page-id load (measured on MI355X: 0.5 us per launch).
+template <bool kCompact>
 PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& bc) {
     const int groups = kQuarters / p.quarters_per_wg;
     const int item = bc.tokens / groups;
     PartitionRange r;
     r.qgroup = bc.tokens - item * groups;
-    if (!p.compact) {
+    if (!kCompact) {
         r.b = bc.z;
         r.first = item;
         r.count = 1;
         return r;
     }
-    // Sequence of the item: the last b with item_first[b] <= item
-    // (item_first is strictly increasing: every sequence has an item).
+    const int mains = p.main_first[p.batch];
+    const bool tail = item >= mains;
+    const int32_t* first = tail ? p.tail_first : p.main_first;
+    const int index = tail ? item - mains : item;
+    // Sequence of the item: the last b with first[b] <= index (a sequence
+    // without items of this kind repeats its predecessor's entry).
     int b = 0, hi = p.batch - 1;
     while (b < hi) {
         const int mid = (b + hi + 1) >> 1;
-        if (p.item_first[mid] <= item) b = mid;
+        if (first[mid] <= index) b = mid;
         else hi = mid - 1;
     }
-    const int local = item - p.item_first[b];
-    const int live = p.live_splits[b];
     r.b = b;
-    if (local < live) {
-        r.first = local;
+    if (!tail) {
+        r.first = index - first[b];
         r.count = 1;
     } else {
-        r.first = live + (local - live) * kTailSpan;  // tail item local - live
+        r.first = p.main_first[b + 1] - p.main_first[b] + (index - first[b]) * kTailSpan;
         r.count = imin(kTailSpan, p.splits - r.first);
     }
     return r;
@@ -314,27 +324,37 @@ inline int head_tile(int group, int max_tile) {
 // main items and ceil((splits - that) / kTailSpan) tail items, when that is
 // fewer items than the rectangular batch * splits. A bound below the length
 // the kernel finds on the device only moves that sequence's later partitions
-// onto its tail items: results are the same, the launch slower.
+// onto its tail items: results are the same to rounding, the launch slower.
+//
+// Why the tail items go last: a launch whose workgroups all fit on the device
+// at once is placed round-robin over the XCDs and CUs in dispatch order, and
+// it lasts as long as its most loaded CU. Measured on MI355X (Llama-3-8B B4
+// L4096, split 256, partition kernel, cold K/V), a rectangular grid reserving
+// 17 splits instead of 16 -- eight dead workgroups after each sequence's 128
+// live ones -- took 17.5 us instead of 14.6: the dead workgroups shift the
+// next sequence's placement so that some CUs hold three live workgroups and
+// others one. (24 splits happened to land evenly again: 15.0 us.)
 inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.compact = 0;
     prm.items = prm.batch * prm.splits;
     if (length_bounds == nullptr || prm.batch > kCompactMaxBatch) return;
     const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
-    int64_t total = 0;
-    int first[kCompactMaxBatch + 1];
-    int live[kCompactMaxBatch];
+    int mains[kCompactMaxBatch + 1], tails[kCompactMaxBatch + 1];
+    mains[0] = tails[0] = 0;
     for (int b = 0; b < prm.batch; ++b) {
         const int64_t bound = lmin(capacity, length_bounds[b] < 0 ? 0 : length_bounds[b]);
-        live[b] = static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
-        first[b] = static_cast<int>(total);
-        total += live[b] + (prm.splits - live[b] + kTailSpan - 1) / kTailSpan;
+        const int live = static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
+        mains[b + 1] = mains[b] + live;
+        tails[b + 1] = tails[b] + (prm.splits - live + kTailSpan - 1) / kTailSpan;
     }
+    const int64_t total = static_cast<int64_t>(mains[prm.batch]) + tails[prm.batch];
     if (total >= prm.items) return;
-    first[prm.batch] = static_cast<int>(total);
     prm.compact = 1;
     prm.items = static_cast<int>(total);
-    for (int b = 0; b <= prm.batch; ++b) prm.item_first[b] = first[b];
-    for (int b = 0; b < prm.batch; ++b) prm.live_splits[b] = live[b];
+    for (int b = 0; b <= prm.batch; ++b) {
+        prm.main_first[b] = mains[b];
+        prm.tail_first[b] = tails[b];
+    }
 }
 
 struct Grid {

@@ -45,18 +45,22 @@ def load_extension():
 
 
 class DecodePlan:
-    """Static metadata + reusable workspace for one decode shape.
+    """A decode problem prepared once and replayed many times.
 
-    table/lengths are CPU integer arrays and are copied during construction.
-    KV contents and q can change between runs. New metadata of the same shape
-    whose longest sequence fits the reserved context (``max_context``, by
-    default the longest initial sequence) is loaded in place with ``refresh``
-    (host arrays) or ``refresh_csr`` (CSR page lists already on the device);
-    ``append`` writes new tokens into the cache and advances the lengths on the
-    device. Anything else requires a new plan.
-    The output is borrowed storage, overwritten by the next run. A plan may be
-    used on one stream at a time; use distinct plans for concurrent streams.
-    Device metadata and workspace attributes are internal and must not be edited.
+    Construction validates the host page table and lengths, copies them to the
+    device, and allocates the partition-state workspace and the output: ``run``
+    then only launches kernels (no allocation, copy or synchronisation), so it
+    can be timed or captured in a graph. q and the K/V cache are passed to
+    every ``run`` and may hold new values each time; the metadata may change
+    in place within the plan's shape and reserved context (``max_context``,
+    default: the longest initial sequence) through ``refresh`` (host arrays),
+    ``refresh_csr`` (CSR page lists on the device) or ``append`` (new tokens,
+    lengths advanced on the device). Any other change needs a new plan.
+
+    ``run`` returns the plan's own output tensor; the next ``run`` overwrites
+    it, so copy it to keep it. The workspace and device metadata belong to the
+    plan: callers must not modify them, and one plan serves one stream at a
+    time (concurrent streams need separate plans).
     """
 
     def __init__(self, layout: Layout, table, lengths, *, device="cuda", split_tokens=256, merge="serial",

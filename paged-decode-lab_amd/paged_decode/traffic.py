@@ -32,8 +32,9 @@ PACKAGE_ROOT = Path(__file__).resolve().parent.parent
 REPO = PACKAGE_ROOT.parent
 ROTATION_BYTES = 2 << 30
 COPY_BYTES = 256 << 20
-SOURCES = ("paged-decode-lab_amd/paged_decode/csrc/decode.hip", "paged-decode-lab_amd/paged_decode/csrc/partition_map.h",
-           "include/paged_decode.h")
+SOURCES = tuple(str(p.relative_to(REPO)) for p in sorted((PACKAGE_ROOT / "paged_decode" / "csrc").glob("*.hip"))) + \
+    tuple(str(p.relative_to(REPO)) for p in sorted((PACKAGE_ROOT / "paged_decode" / "csrc").glob("*.h"))) + \
+    ("include/paged_decode.h",)
 
 
 def source_digest():
@@ -56,25 +57,22 @@ def run(args):
     from paged_decode.workload import make_workload
 
     w = make_workload(args.workload)
-    q_h, k_h, v_h = w.host_tensors()
     dev = torch.device("cuda", 0)
-    q = torch.from_numpy(q_h).to(dev)
-    k0, v0 = torch.from_numpy(k_h).to(dev), torch.from_numpy(v_h).to(dev)
+    q, k0, v0, k_scale, v_scale = w.tensors(dev)  # K/V in the workload's storage format (FP8 with scales)
     sets = max(1, math.ceil(ROTATION_BYTES / (2 * k0.numel() * k0.element_size())))
     ks = [k0] + [k0.clone() for _ in range(sets - 1)]
     vs = [v0] + [v0.clone() for _ in range(sets - 1)]
     plan = DecodePlan(w.layout, w.table, w.lengths, device=dev, split_tokens=w.split_tokens)
     print(f"[traffic] {w.name}: {args.launches} partition launches over {sets} K/V sets", flush=True)
     for i in range(args.launches):
-        plan.run_partial(q, ks[i % sets], vs[i % sets])
+        plan.run_partial(q, ks[i % sets], vs[i % sets], k_scale=k_scale, v_scale=v_scale)
     torch.cuda.synchronize()
     src = torch.randn(COPY_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
     for _ in range(args.copies):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    print(f"[traffic] {args.copies} calibration copies of {COPY_BYTES} bytes; half={w.dtype == np.float16}",
-          flush=True)
+    print(f"[traffic] {args.copies} calibration copies of {COPY_BYTES} bytes", flush=True)
 
 
 def read_counter(directory, counter):
@@ -101,14 +99,17 @@ def pick(per_kernel, needle):
 
 
 def summarize(args):
-    from paged_decode.metrics import kv_bytes
+    from paged_decode.metrics import kv_bytes, unique_token_bytes
     from paged_decode.workload import make_workload
     import numpy as np
 
     w = make_workload(args.workload)
-    logical = kv_bytes(w.lengths, w.layout.kv_heads, w.layout.head_dim, w.element_size)
-    kernel = partition_kernel_name(w.dtype == np.float16)
-    record = {"workload": w.name, "kernel": kernel, "algorithmic_bytes_per_launch": logical}
+    L = w.layout
+    logical = kv_bytes(w.lengths, L.kv_heads, L.head_dim, w.element_size)
+    unique = unique_token_bytes(w.table, w.lengths, L.page_size, L.kv_heads, L.head_dim, w.element_size)
+    kernel = partition_kernel_name(w.dtype == np.float16 or not w.native)
+    record = {"workload": w.name, "kernel": kernel, "algorithmic_bytes_per_launch": logical,
+              "unique_page_bytes_per_launch": unique}
     total = 0.0
     for counter, directory, key in (("FETCH_SIZE", args.fetch_dir, "read"), ("WRITE_SIZE", args.write_dir, "write")):
         per_kernel = read_counter(directory, counter)
@@ -129,6 +130,7 @@ def summarize(args):
         record["kernel_symbol"] = name
     record["hbm_bytes_per_launch"] = round(total)
     record["traffic_over_algorithmic"] = round(total / logical, 4)
+    record["traffic_over_unique_pages"] = round(total / unique, 4)
     record["copy_bytes"] = COPY_BYTES
     record["source_digest"] = source_digest()
     record["commands"] = [

@@ -212,7 +212,7 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
         for (uint32_t by = 0; by < grid.y; ++by) {
             for (uint32_t bx = 0; bx < grid.x; ++bx) {
                 const BlockCoords bc = block_coords(bx, by, bz, grid.x, grid.y);
-                const PartitionRange r = partition_range(p, bc);
+                const PartitionRange r = p.compact ? partition_range<true>(p, bc) : partition_range<false>(p, bc);
                 AUDIT(r.b >= 0 && r.b < pr.batch, "sequence %d", r.b);
                 AUDIT(r.first >= 0 && r.count >= 1 && r.first + r.count <= pr.splits && r.count <= kTailSpan,
                       "partition range %d + %d", r.first, r.count);
