@@ -39,8 +39,13 @@ Prints one JSON line. The record also carries the provenance the reference's
 report keeps (benchmarks/bench_decode.py:47-63,137-170): git revision and
 dirty flag (null where the tree has no git metadata), library build digests,
 the software environment, a device snapshot before and after the timed
-protocol (rocm-smi, or "unavailable"), the raw per-repetition samples and the
-trial order of the 30 x 20 protocol, and steady-state device memory.
+protocol (clocks, activity, temperature and power read from the amdgpu sysfs
+files, or "unavailable"), the raw per-repetition samples and the trial order
+of the 30 x 20 protocol, and steady-state device memory. bench.py starts no
+child process: under rocprofv3 every process it started would itself load
+the profiler and open the GPU. The git revision is read from .git's files;
+the dirty flag needs git and is computed only before the GPU is touched and
+only when no profiler is loaded.
 --output PATH also writes the record, indented, to a new file (an existing
 file is never overwritten).
 """
@@ -107,16 +112,47 @@ def cpu_model():
     return "unknown"
 
 
-def revision():
-    """git commit and dirty flag of this tree, or nulls where there is no git metadata."""
+def profiler_loaded():
+    """True when a profiler library is loaded into this process (rocprofv3 sets these)."""
+    return ("rocprof" in os.environ.get("LD_PRELOAD", "") or "HSA_TOOLS_LIB" in os.environ
+            or any(k.startswith(("ROCPROF", "ROCP_")) for k in os.environ))
+
+
+def git_head():
+    """Commit of this tree's HEAD, read from .git's files (no git process), or None."""
+    git = REPO / ".git"
     try:
-        sha = subprocess.check_output(["git", "rev-parse", "HEAD"], cwd=REPO, text=True,
-                                      stderr=subprocess.DEVNULL, timeout=10).strip()
+        head = (git / "HEAD").read_text().strip()
+        if not head.startswith("ref: "):
+            return head
+        ref = head[5:]
+        if (git / ref).exists():
+            return (git / ref).read_text().strip()
+        for line in (git / "packed-refs").read_text().splitlines():
+            if line.endswith(" " + ref):
+                return line.split()[0]
+    except OSError:
+        pass
+    return None
+
+
+def revision():
+    """git commit and dirty flag of this tree (nulls where there is no git metadata).
+
+    Call before the GPU is initialised: the dirty flag needs a git child
+    process, which is started only then and only without a profiler loaded.
+    """
+    sha = git_head()
+    if sha is None:
+        return {"sha": None, "dirty": None, "note": "no git metadata in this tree"}
+    if profiler_loaded():
+        return {"sha": sha, "dirty": None, "note": "dirty flag not computed under a profiler"}
+    try:
         dirty = bool(subprocess.check_output(["git", "status", "--porcelain", "--untracked-files=no"], cwd=REPO,
                                              text=True, stderr=subprocess.DEVNULL, timeout=10).strip())
-        return {"sha": sha, "dirty": dirty}
     except (OSError, subprocess.SubprocessError):
-        return {"sha": None, "dirty": None, "note": "no git metadata in this tree"}
+        dirty = None
+    return {"sha": sha, "dirty": dirty}
 
 
 def rocm_version():
@@ -127,13 +163,39 @@ def rocm_version():
 
 
 def device_snapshot():
-    """Temperature, power, clocks and use of the GPUs, from rocm-smi, or "unavailable"."""
-    try:
-        out = subprocess.check_output(["rocm-smi", "--showtemp", "--showpower", "--showclocks", "--showuse",
-                                       "--json"], text=True, stderr=subprocess.DEVNULL, timeout=15)
-        return json.loads(out)
-    except (OSError, subprocess.SubprocessError, ValueError):
-        return "unavailable"
+    """Clocks, activity, temperature and power of the AMD GPUs from the amdgpu
+    sysfs files (read directly: no child process), or "unavailable"."""
+    cards = {}
+    for dev in sorted(Path("/sys/class/drm").glob("card[0-9]*/device")):
+        try:
+            if (dev / "vendor").read_text().strip() != "0x1002":
+                continue
+        except OSError:
+            continue
+        info = {}
+        for name in ("gpu_busy_percent", "mem_busy_percent"):
+            try:
+                info[name] = int((dev / name).read_text())
+            except (OSError, ValueError):
+                pass
+        for name in ("pp_dpm_sclk", "pp_dpm_mclk"):
+            try:
+                current = [line for line in (dev / name).read_text().splitlines() if line.rstrip().endswith("*")]
+                if current:
+                    info[name] = current[0].split(":", 1)[1].strip(" *")
+            except OSError:
+                pass
+        for hwmon in sorted(dev.glob("hwmon/hwmon*")):
+            for sensor in sorted(hwmon.glob("temp*_input")) + sorted(hwmon.glob("power*_average")):
+                try:
+                    label_file = hwmon / sensor.name.replace("_input", "_label").replace("_average", "_label")
+                    label = label_file.read_text().strip() if label_file.exists() else sensor.name
+                    info[label] = int(sensor.read_text()) / (1000.0 if "temp" in sensor.name else 1e6)
+                except (OSError, ValueError):
+                    pass
+        if info:
+            cards[dev.parent.name] = info
+    return cards or "unavailable"
 
 
 def environment(torch):
@@ -190,6 +252,7 @@ def main():
         print(f"--output {args.output} exists; bench.py never overwrites a report", file=sys.stderr)
         return 2
 
+    rev = revision()  # before anything touches the GPU (it may start a git process)
     import numpy as np
     import torch
 
@@ -366,8 +429,10 @@ def main():
         lengths_d = torch.from_numpy(w.lengths).to(device)
         ours = plan.run(q, ks[0], vs[0], **scales).clone()
         comparison = {}
-        # bfloat16 SDPA would run batched bf16 products on transposed views, which
-        # have faulted GPUs of this pool: bf16 workloads keep the FP32 eager row only.
+        # bfloat16 SDPA issues batched bf16 products on transposed views; on this
+        # ROCm 7 / torch 2.10 stack, torch.bmm in bfloat16 with a transposed right
+        # operand is a documented cause of GPU faults, so BF16 workloads keep the
+        # FP32 eager row only (no BF16 SDPA call was ever made).
         kinds = ("eager",) if w.q_format == "bf16" else ("sdpa", "eager")
         for kind in kinds:
             got = dense_decode(q, ks[0], vs[0], table_d, lengths_d, kind=kind, **scales).float()
@@ -444,7 +509,7 @@ def main():
         "source_digest": digest,
         "device": device_label(torch),
         "created_utc": datetime.datetime.now(datetime.timezone.utc).isoformat(timespec="seconds"),
-        "revision": revision(),
+        "revision": rev,
         "build_digest": {"sources": _build.source_digest(), "extension": plan._extension.build_digest(),
                          "abi": plan._extension.abi_version()},
         "environment": environment(torch),

@@ -86,14 +86,21 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
     const int lane = threadIdx.x % kWave;
     const int row = lane / LPT;
     const int col = lane % LPT;
-    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, gridDim.y);
+    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y);
     const PartitionRange pr = partition_range<kCompact>(p, bc);
     const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
     int window = speculative_page<TPL>(p, pr.first, pr.count, pr.qgroup, wave);
     int window_ids = pages[window_entry(p, window, lane)];
     const int len_raw = p.lengths[pr.b];
     const WaveWork w = wave_work<GT, TPL>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
-    if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
+    if (w.dead) {
+        // Never read: the merge stops at the sequence's last live partition.
+        // The speculative page-id window is consumed here (an empty asm
+        // operand) so that its load is issued before this branch, alongside
+        // the length's, rather than sunk into the live path after it.
+        asm volatile("" ::"v"(window_ids));
+        return;
+    }
     const T* q_base = static_cast<const T*>(p.q) + w.q_row * D;
 
     u32x4 qv[GT];
@@ -427,14 +434,21 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     const int lane = threadIdx.x % kWave;
     const int n = lane % 16;  // head (q.K^T, P) / column (P.V)
     const int g = lane / 16;  // lane group: tokens g + 4 e
-    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, gridDim.y);
+    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y);
     const PartitionRange pr = partition_range<kCompact>(p, bc);
     const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
     int window = speculative_page<kTileTokens>(p, pr.first, pr.count, pr.qgroup, wave);
     int window_ids = pages[window_entry(p, window, lane)];
     const int len_raw = p.lengths[pr.b];
     const WaveWork w = wave_work<GT, kTileTokens>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
-    if (w.dead) return;  // never read: the merge stops at the sequence's last live partition
+    if (w.dead) {
+        // Never read: the merge stops at the sequence's last live partition.
+        // The speculative page-id window is consumed here (an empty asm
+        // operand) so that its load is issued before this branch, alongside
+        // the length's, rather than sunk into the live path after it.
+        asm volatile("" ::"v"(window_ids));
+        return;
+    }
     const char* q_row = static_cast<const char*>(p.q) + w.q_row * D * 2;
 
     u32x4 qb[KS];

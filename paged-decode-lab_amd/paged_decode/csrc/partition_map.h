@@ -47,6 +47,7 @@ struct PartialParams {
     const int32_t* lengths;
     float* numerator;   // [B, Hq, 4 * splits, D]
     float* stats;       // [B, Hq, 4 * splits, 2]
+    uint32_t grid_x, grid_y;  // the launch's grid (kernel arguments: no dependent load of the dispatch packet)
     int batch;
     int query_heads;
     int group;          // query heads per KV head
@@ -102,9 +103,10 @@ struct BlockCoords {
 };
 
 PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t gx, uint32_t gy) {
-    if (gy == 1) return BlockCoords{static_cast<int>(bx), 0, static_cast<int>(bz)};
+    // Every path reads gx and gy, so the kernel loads them with its other
+    // arguments instead of after a branch.
     const uint64_t lin = bx + static_cast<uint64_t>(gx) * by;
-    if (static_cast<uint64_t>(gx) * gy <= 0xFFFFFFFFull) {
+    if (lin <= 0xFFFFFFFFull) {
         const uint32_t l32 = static_cast<uint32_t>(lin);
         return BlockCoords{static_cast<int>(l32 / gy), static_cast<int>(l32 % gy), static_cast<int>(bz)};
     }
@@ -456,6 +458,9 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus) {
     const int groups = kv_heads / prm.heads_per_wg;
     prm.stream_mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
                       : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+    const Grid grid = partial_grid(prm, kv_heads);
+    prm.grid_x = grid.x;
+    prm.grid_y = grid.y;
 }
 
 // Launch shape of the FP32 kernel.
@@ -464,6 +469,9 @@ inline void plan_fp32(PartialParams& prm, int kv_heads) {
     prm.head_tile = gt;
     prm.head_tiles = (prm.group + gt - 1) / gt;
     choose_workgroup(prm, kv_heads, 8);
+    const Grid grid = partial_grid(prm, kv_heads);
+    prm.grid_x = grid.x;
+    prm.grid_y = grid.y;
 }
 
 // LDS bytes of one wave's K tile in the matrix-core kernel: 16 token rows of

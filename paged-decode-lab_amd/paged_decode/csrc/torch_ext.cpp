@@ -11,6 +11,10 @@
 
 #include <torch/extension.h>
 
+// PyTorch-ROCm tags HIP devices with torch's "cuda" device type. c10::hip's
+// guard and stream accessors for such tensors are the *MasqueradingAsCUDA
+// variants (the plain HIP ones expect DeviceType::HIP and reject them); both
+// give a HIP device guard and the current hipStream_t, nothing CUDA-specific.
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 

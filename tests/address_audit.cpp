@@ -202,6 +202,8 @@ template <int D, int GT>
 void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage& cov) {
     const Buffers buf = buffers(pr);
     const Grid grid = partial_grid(p, pr.kv_heads);
+    AUDIT(p.grid_x == grid.x && p.grid_y == grid.y, "kernel-argument grid %ux%u, launch %ux%u", p.grid_x, p.grid_y,
+          grid.x, grid.y);
     const int waves = partial_threads(p) / kWave;
     AUDIT(waves >= 1 && waves <= 8, "workgroup of %d waves", waves);
     if (mfma) AUDIT(mfma_lds_bytes(p, D, pr.kv_elem) <= 160 * 1024, "LDS %d bytes", mfma_lds_bytes(p, D, pr.kv_elem));
@@ -211,7 +213,7 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
     for (uint32_t bz = 0; bz < grid.z; ++bz) {
         for (uint32_t by = 0; by < grid.y; ++by) {
             for (uint32_t bx = 0; bx < grid.x; ++bx) {
-                const BlockCoords bc = block_coords(bx, by, bz, grid.x, grid.y);
+                const BlockCoords bc = block_coords(bx, by, bz, p.grid_x, p.grid_y);
                 const PartitionRange r = p.compact ? partition_range<true>(p, bc) : partition_range<false>(p, bc);
                 AUDIT(r.b >= 0 && r.b < pr.batch, "sequence %d", r.b);
                 AUDIT(r.first >= 0 && r.count >= 1 && r.first + r.count <= pr.splits && r.count <= kTailSpan,
