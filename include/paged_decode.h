@@ -97,7 +97,15 @@ enum pd_merge { PD_MERGE_SERIAL = 0, PD_MERGE_SHARED = 1 };
 enum pd_hint { PD_HINT_NONE = 0, PD_HINT_UNSHARED_PAGES = 1, PD_HINT_RAGGED_LENGTHS = 2 };
 
 /*
- * Full decode: partition kernel then merge kernel, both on `stream`.
+ * Full decode on `stream`: a partition launch that writes 4 * splits states
+ * per (sequence, query head) row into numerator/stats, then a merge launch
+ * that combines them into out. A call whose rows hold at most 128 KB of K and
+ * V per (sequence, KV head) -- min(splits * split_tokens, table_width *
+ * page_size) tokens -- is instead one whole-row launch: each workgroup
+ * folds a row's states in LDS and writes out itself, and numerator/stats
+ * are left unwritten (they remain required arguments, the workspace of the
+ * reference's plan). Results agree with the two-launch path to FP32
+ * rounding; pd_decode_launch_count says which a call takes.
  * Replaces the native entry `decode(q, k, v, table, lengths, numerator, stats,
  * out, split_tokens, merge_mode)` of reference
  * src/paged_decode/csrc/bindings.cpp:3-9 / decode.cu:197-246, with the tensor
@@ -274,6 +282,18 @@ int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, const int32
  */
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits);
 
+/*
+ * Kernel launches pd_decode / pd_decode_ex / pd_decode_scratch make for a call
+ * of these formats and shapes (any lengths, bounds and stream): 1 for a
+ * whole-row launch, 2 for the partition and merge launches. Returns a status
+ * (the shape and format checks of pd_decode_ex) and writes *launches on
+ * success. No counterpart in the reference, whose decode always launches
+ * twice (decode.cu:170-194); for callers that profile or account per kernel.
+ */
+int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                           int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                           int hints, int* launches);
+
 /* Static description of a status code (never NULL). */
 const char* pd_status_string(int status);
 
@@ -284,9 +304,10 @@ const char* pd_status_string(int status);
  * pd_decode_ex; 8: pd_table_from_csr; 9: quarters of one workgroup stored
  * combined, the others as empty states; 10: hints argument of the _ex
  * entries; 11: PD_HINT_RAGGED_LENGTHS; 12: max_context argument of
- * pd_append_kv_advance, length_bounds argument of the _ex entries). PD_ABI_VERSION is the value this header describes;
+ * pd_append_kv_advance, length_bounds argument of the _ex entries; 13: whole-row launches of small rows,
+ * pd_decode_launch_count). PD_ABI_VERSION is the value this header describes;
  * a binding compares it with what the loaded library returns. */
-#define PD_ABI_VERSION 12
+#define PD_ABI_VERSION 13
 int pd_abi_version(void);
 
 #ifdef __cplusplus

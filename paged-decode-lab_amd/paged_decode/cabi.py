@@ -45,6 +45,7 @@ PROTOTYPES = {
     "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_table_from_csr": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 4 + [_P]),
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
+    "pd_decode_launch_count": (_I, [_I] * 12 + [_P]),
     "pd_status_string": (ctypes.c_char_p, [_I]),
     "pd_abi_version": (_I, []),
 }
@@ -62,3 +63,17 @@ def load(path=LIBRARY):
 
 def status_string(lib, status):
     return lib.pd_status_string(status).decode()
+
+
+def launch_count(lib, q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size, table_width,
+                 physical_pages, splits, split_tokens, hints=PD_HINT_NONE):
+    """Kernel launches of a full decode call of these formats and shapes: 1 (whole
+    rows: the partition launch writes the output) or 2 (partition and merge).
+    Raises ValueError with the library's message for shapes it rejects."""
+    launches = ctypes.c_int(0)
+    status = lib.pd_decode_launch_count(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
+                                        table_width, physical_pages, splits, split_tokens, hints,
+                                        ctypes.byref(launches))
+    if status != PD_OK:
+        raise ValueError(status_string(lib, status))
+    return launches.value

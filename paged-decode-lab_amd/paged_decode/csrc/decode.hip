@@ -502,11 +502,14 @@ int dispatch_partial(PartialParams& prm, int q_dtype, int kv_dtype, int kv_heads
                           : dispatch_partial_f16_d128(prm, kv_dtype, kv_heads, stream);
 }
 
-int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
-                const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
-                int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
-                int splits, int split_tokens, int hints, const int32_t* length_bounds, hipStream_t stream,
-                int* state_stride = nullptr) {
+// Partition-launch parameters of a call (pointers may be null for a plan
+// query). With out given, the planner may choose a whole-row launch, which
+// writes out itself.
+PartialParams partial_params(const void* q, const void* k, const void* v, int kv_dtype, float k_scale,
+                             float v_scale, const int32_t* table, const int32_t* lengths, float* numerator,
+                             float* stats, float* out, int batch, int query_heads, int kv_heads, int head_dim,
+                             int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                             int hints, const int32_t* length_bounds) {
     PartialParams prm{};
     prm.batch = batch;
     prm.unshared_pages = (hints & PD_HINT_UNSHARED_PAGES) != 0;
@@ -518,6 +521,8 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     prm.lengths = lengths;
     prm.numerator = numerator;
     prm.stats = stats;
+    prm.out = out;
+    prm.row_allowed = out != nullptr;
     prm.query_heads = query_heads;
     prm.group = query_heads / kv_heads;
     prm.page_shift = page_size == 16 ? 4 : 5;
@@ -530,8 +535,21 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     prm.scale_log2 = kLog2e * k_scale / sqrtf(static_cast<float>(head_dim));
     prm.v_scale = v_scale;
     plan_items(prm, length_bounds);
+    return prm;
+}
+
+// state_stride (if given) receives the merge's stride over the states: 1,
+// the quarters combined per state, or 0 after a whole-row launch (no merge).
+int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
+                const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
+                int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
+                int splits, int split_tokens, int hints, const int32_t* length_bounds, hipStream_t stream,
+                float* out = nullptr, int* state_stride = nullptr) {
+    PartialParams prm = partial_params(q, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, out,
+                                       batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
+                                       splits, split_tokens, hints, length_bounds);
     const int status = dispatch_partial(prm, q_dtype, kv_dtype, kv_heads, head_dim, stream);
-    if (state_stride) *state_stride = prm.combine ? prm.quarters_per_wg : 1;
+    if (state_stride) *state_stride = prm.row_mode ? 0 : prm.combine ? prm.quarters_per_wg : 1;
     return status;
 }
 
@@ -736,8 +754,8 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
     int stride = 1;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                         split_tokens, hints, length_bounds, s, &stride);
-    if (status != PD_OK) return status;
+                         split_tokens, hints, length_bounds, s, out, &stride);
+    if (status != PD_OK || stride == 0) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
                      split_tokens, merge_mode, stride, s);
 }
@@ -817,6 +835,28 @@ int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, const int32
     CsrParams c{indptr, indices, last_page_len, table, lengths, overflow, table_width, page_size, max_context};
     hipLaunchKernelGGL(table_from_csr_kernel, dim3(batch), dim3(256), 0, static_cast<hipStream_t>(stream), c);
     return launch_status();
+}
+
+int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                           int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                           int hints, int* launches) {
+    if (!launches) return PD_ERR_NULL_POINTER;
+    // The shape checks of pd_decode_ex, with stand-ins for the buffers.
+    const char* const stand_in = reinterpret_cast<const char*>(alignof(float));
+    float* const f_stand_in = reinterpret_cast<float*>(alignof(float));
+    int status = check_common(stand_in, q_dtype, stand_in, stand_in, kv_dtype, 1.0f, 1.0f,
+                              reinterpret_cast<const int32_t*>(stand_in), reinterpret_cast<const int32_t*>(stand_in),
+                              f_stand_in, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size, table_width,
+                              physical_pages, splits, split_tokens);
+    if (status == PD_OK) status = check_hints(hints);
+    if (status != PD_OK) return status;
+    PartialParams prm = partial_params(nullptr, nullptr, nullptr, kv_dtype, 1.0f, 1.0f, nullptr, nullptr, nullptr,
+                                       nullptr, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size,
+                                       table_width, physical_pages, splits, split_tokens, hints, nullptr);
+    if (q_dtype == PD_DTYPE_F32) plan_fp32(prm, kv_heads, head_dim);
+    else plan_mfma(prm, kv_heads, device_compute_units(), head_dim, element_size(kv_dtype));
+    *launches = prm.row_mode ? 1 : 2;
+    return PD_OK;
 }
 
 size_t pd_workspace_bytes(int batch, int query_heads, int head_dim, int splits) {

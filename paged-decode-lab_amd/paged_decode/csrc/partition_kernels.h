@@ -67,8 +67,11 @@ __device__ __forceinline__ void store_empty_states(const PartialParams& p, const
 // every token row keeps its own online-softmax stream, combined across rows at
 // the end of the wave. Chunks of NL loads stream through PD + 1 register
 // buffers in fully unrolled blocks of NC chunks.
-template <typename T, int D, int GT, int NL, int PD, int NC, bool kCompact>
-__global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams p) {
+// kRow: a whole-row workgroup (up to kRowMaxWaves waves) that folds its
+// waves' states in LDS and writes the output rows instead of states.
+template <typename T, int D, int GT, int NL, int PD, int NC, bool kCompact, bool kRow = false>
+__global__ void __launch_bounds__(kRow ? kWave * fp32_row_max_waves(GT) : kWave * 8)
+    partial_kernel(const PartialParams p) {
     using E = Elem<T>;
     constexpr int EPL = E::kPerLoad;
     constexpr int LPT = D / EPL;
@@ -88,12 +91,16 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
     const int col = lane % LPT;
     const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y);
     const PartitionRange pr = partition_range<kCompact>(p, bc);
+    const int waves_wg = blockDim.x / kWave;
     const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
-    int window = speculative_page<TPL>(p, pr.first, pr.count, pr.qgroup, wave);
+    int window = kRow ? row_speculative_page<TPL>(p, wave, waves_wg)
+                      : speculative_page<TPL>(p, pr.first, pr.count, pr.qgroup, wave);
     int window_ids = pages[window_entry(p, window, lane)];
     const int len_raw = p.lengths[pr.b];
-    const WaveWork w = wave_work<GT, TPL>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
-    if (w.dead) {
+    const WaveWork w = kRow ? row_wave_work<GT, TPL>(p, pr.b, bc.heads, wave, waves_wg, len_raw)
+                            : wave_work<GT, TPL>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
+    // Whole-row waves with an empty slice stay for the fold (empty state).
+    if (!kRow && w.dead) {
         // Never read: the merge stops at the sequence's last live partition.
         // The speculative page-id window is consumed here (an empty asm
         // operand) so that its load is issued before this branch, alongside
@@ -242,6 +249,48 @@ __global__ void __launch_bounds__(kWave * 8) partial_kernel(const PartialParams 
         }
         m[g] = mw;
         l[g] = lw;
+    }
+    if constexpr (kRow) {
+        // Every wave leaves its state in its LDS slot -- m[8], l[8], then
+        // acc[8][D] -- and after one barrier the workgroup forms each output
+        // element of the tile's live heads as the merge does (max over the
+        // states with l > 0, weights 2^(m - max), sum(weight * n) * v_scale /
+        // sum(weight * l), or 0 for a row without tokens; decode.cu:94-107).
+        extern __shared__ __attribute__((aligned(16))) float row_lds[];
+        constexpr int kSlot = row_slot_bytes_fp32(D) / 4;
+        float* slot = row_lds + wave * kSlot;
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < GT; ++g) {
+                slot[g] = m[g];
+                slot[8 + g] = l[g];
+            }
+        }
+        if (lane < LPT) {
+#pragma unroll
+            for (int g = 0; g < GT; ++g)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) slot[16 + g * D + col * EPL + e] = acc[g][e];
+        }
+        __syncthreads();
+        for (int o = threadIdx.x; o < w.heads_here * D; o += blockDim.x) {
+            const int h = o / D;
+            float mx = kNoToken;
+            for (int s = 0; s < waves_wg; ++s) {
+                const float* st = row_lds + s * kSlot;
+                mx = st[8 + h] > 0.0f ? fmaxf(mx, st[h]) : mx;
+            }
+            float den = 0.0f, num = 0.0f;
+            for (int s = 0; s < waves_wg; ++s) {
+                const float* st = row_lds + s * kSlot;
+                const float ls = st[8 + h];
+                const float f = ls > 0.0f ? fast_exp2(st[h] - mx) : 0.0f;
+                den = fmaf(f, ls, den);
+                num = fmaf(f, st[16 + o], num);
+            }
+            p.out[w.q_row * D + o] = den > 0.0f ? num * p.v_scale / den : 0.0f;
+        }
+        return;
     }
     // Lane g needs head g's (m, l): every lane holds every head's values.
     float m_lane = m[0], l_lane = l[0];
@@ -397,8 +446,12 @@ struct CombineSlot {
 
 // kStream: which 16-byte loads are non-temporal (see plan_mfma):
 // 0 none, 1 V (and FP8 K, whose V loads are 8-byte), 2 K and V.
-template <typename QT, int KVF, int D, int GT, int PD, int NC, int kStream, bool kCombine, bool kCompact>
-__global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialParams p) {
+// kFold: what the workgroup stores -- 0 one state per wave; 1 one state per
+// qw quarters of a partition (quarter combine); 2 the output rows of a whole
+// row's states (whole-row launch, up to kRowMaxWaves waves: 1024 lanes).
+template <typename QT, int KVF, int D, int GT, int PD, int NC, int kStream, int kFold, bool kCompact>
+__global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
+    partial_mfma_kernel(const PartialParams p) {
     using C = Compute<QT>;
     constexpr int ES = KVF == kKvNative ? 2 : 1;  // stored bytes per K/V element
     constexpr int KS = D / 32;                    // q.K^T k-steps (K loads) per tile
@@ -418,8 +471,9 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     constexpr int KL = kTileTokens / TK;
     constexpr int kStageRow = mfma_stage_bytes(D, ES) / kTileTokens;
     static_assert(TK <= kTileTokens && kTileTokens % TK == 0, "whole row loads per tile");
-    // Dynamic LDS: the waves' K tiles, then (kCombine) the quarter-combine
-    // slots, [waves / qw][qw - 1] CombineSlot<VH>; sized by the launch.
+    // Dynamic LDS: the waves' K tiles, then the quarter-combine slots
+    // ([waves / qw][qw - 1] CombineSlot<VH>, kFold 1) or one slot per wave
+    // (kFold 2); sized by the launch.
     extern __shared__ __attribute__((aligned(16))) char lds[];
     char* const k_stage = lds;
     char* const combine_lds = lds + mfma_stage_bytes(D, ES) * (blockDim.x / kWave);
@@ -436,12 +490,21 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     const int g = lane / 16;  // lane group: tokens g + 4 e
     const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y);
     const PartitionRange pr = partition_range<kCompact>(p, bc);
+    // A whole-row workgroup's wave runs slice `wave` of its row (one KV head,
+    // one head tile); otherwise the wave index splits into (head, tile,
+    // quarter) within the workgroup's partition.
+    const int waves_wg = blockDim.x / kWave;
     const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
-    int window = speculative_page<kTileTokens>(p, pr.first, pr.count, pr.qgroup, wave);
+    int window = kFold == 2 ? row_speculative_page<kTileTokens>(p, wave, waves_wg)
+                            : speculative_page<kTileTokens>(p, pr.first, pr.count, pr.qgroup, wave);
     int window_ids = pages[window_entry(p, window, lane)];
     const int len_raw = p.lengths[pr.b];
-    const WaveWork w = wave_work<GT, kTileTokens>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave, len_raw);
-    if (w.dead) {
+    const WaveWork w = kFold == 2 ? row_wave_work<GT, kTileTokens>(p, pr.b, bc.heads, wave, waves_wg, len_raw)
+                                  : wave_work<GT, kTileTokens>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave,
+                                                               len_raw);
+    // A whole-row workgroup's waves with an empty slice stay to contribute
+    // the empty state to the fold.
+    if (kFold != 2 && w.dead) {
         // Never read: the merge stops at the sequence's last live partition.
         // The speculative page-id window is consumed here (an empty asm
         // operand) so that its load is issued before this branch, alongside
@@ -589,9 +652,45 @@ __global__ void __launch_bounds__(kWave * 8) partial_mfma_kernel(const PartialPa
     // Lane (g, n) holds heads 4 g + i of dims n VH .. n VH + VH - 1; the
     // denominator of head n is summed over the four lane groups.
     float l_head = sum_over_lane_groups(l_part);
+    if constexpr (kFold == 2) {
+        // Every wave leaves its state in its slot; after one barrier the
+        // workgroup forms each output element of the tile's live heads as the
+        // merge does: the max over the states with l > 0, their weights
+        // 2^(m - max), and sum(weight * n) * v_scale / sum(weight * l), or 0
+        // for a row without tokens (decode.cu:94-107). Thread o covers
+        // elements o, o + blockDim.x, ...: column n of dims n VH + j, head h,
+        // with n fastest, so a slot's accumulators are read in lane order.
+        CombineSlot<VH>* slots = reinterpret_cast<CombineSlot<VH>*>(combine_lds);
+        CombineSlot<VH>* mine = slots + wave;
+        if (lane < 16) {
+            mine->m[n] = m_head;
+            mine->l[n] = l_head;
+        }
+#pragma unroll
+        for (int j = 0; j < VH; ++j) mine->acc[j][lane] = acc[j];
+        __syncthreads();
+        const int waves = waves_wg;
+        for (int o = threadIdx.x; o < w.heads_here * D; o += blockDim.x) {
+            const int col = o % 16;
+            const int j = (o / 16) % VH;
+            const int h = o / D;
+            const int src_lane = 16 * (h / 4) + col;
+            float mx = kNoToken;
+            for (int s = 0; s < waves; ++s) mx = slots[s].l[h] > 0.0f ? fmaxf(mx, slots[s].m[h]) : mx;
+            float den = 0.0f, num = 0.0f;
+            for (int s = 0; s < waves; ++s) {
+                const float ls = slots[s].l[h];
+                const float f = ls > 0.0f ? fast_exp2(slots[s].m[h] - mx) : 0.0f;
+                den = fmaf(f, ls, den);
+                num = fmaf(f, slots[s].acc[j][src_lane][h % 4], num);
+            }
+            p.out[(w.q_row + h) * D + col * VH + j] = den > 0.0f ? num * p.v_scale / den : 0.0f;
+        }
+        return;
+    }
     const int part = w.split * kQuarters + w.quarter;
     store_empty_states(p, w, lane, extra_live_partitions(p, pr.first, pr.count, len_raw));
-    if constexpr (kCombine) {
+    if constexpr (kFold == 1) {
         // The workgroup's qw quarters of one (KV head, head tile) -- waves
         // wave - wave % qw onwards, all of one partition, so all live or all
         // gone above -- become one state: quarters 1 .. qw - 1 leave theirs in
@@ -660,6 +759,9 @@ inline int launch_status() { return hipGetLastError() == hipSuccess ? PD_OK : PD
 constexpr int kFp32ChunkLoads = 1;
 constexpr int kFp32Prefetch = 4;
 constexpr int kFp32BlockChunks = 16;
+// Whole-row FP32 launches give each wave a slice of a few chunks (16 tokens
+// at most rows' sizes): a block of four keeps the straight-line code short.
+constexpr int kFp32RowBlockChunks = 4;
 // Matrix-core kernel: 16-token tiles issued ahead of the one being consumed,
 // and tiles per straight-line block (with 2 and 2, each block's two tiles are
 // requested together and consumed in order). Short blocks keep the kernel's
@@ -694,29 +796,34 @@ int launch_mfma(const PartialParams& prm, int kv_heads, hipStream_t stream) {
     const dim3 block(partial_threads(prm));
     const size_t lds = static_cast<size_t>(mfma_lds_bytes(prm, D, KVF == kKvNative ? 2 : 1));
     constexpr int kPD = kMfmaPrefetch, kNC = kMfmaBlock;
-#define PD_LAUNCH_MFMA(MODE, COMBINE)                                                                             \
+    // Whole-row launches are rectangular (one workgroup per row).
+#define PD_LAUNCH_MFMA(MODE, FOLD)                                                                                \
     do {                                                                                                          \
-        if (prm.compact)                                                                                          \
-            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE, true>), grid, block, \
+        if constexpr (FOLD == 2)                                                                                  \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, 2, false>), grid, block, lds, \
+                               stream, prm);                                                                      \
+        else if (prm.compact)                                                                                     \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, true>), grid, block,    \
                                lds, stream, prm);                                                                 \
         else                                                                                                      \
-            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, COMBINE, false>), grid,       \
-                               block, lds, stream, prm);                                                          \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, false>), grid, block,   \
+                               lds, stream, prm);                                                                 \
+    } while (0)
+#define PD_LAUNCH_MFMA_FOLDS(MODE)                      \
+    do {                                                \
+        if (prm.row_mode) PD_LAUNCH_MFMA(MODE, 2);      \
+        else if (prm.combine) PD_LAUNCH_MFMA(MODE, 1);  \
+        else PD_LAUNCH_MFMA(MODE, 0);                   \
     } while (0)
     if constexpr (KVF == kKvNative) {
         if (prm.stream_mode == 2) {
-            if (prm.combine) PD_LAUNCH_MFMA(2, true);
-            else PD_LAUNCH_MFMA(2, false);
+            PD_LAUNCH_MFMA_FOLDS(2);
             return launch_status();
         }
     }
-    if (prm.stream_mode >= 1) {
-        if (prm.combine) PD_LAUNCH_MFMA(1, true);
-        else PD_LAUNCH_MFMA(1, false);
-    } else {
-        if (prm.combine) PD_LAUNCH_MFMA(0, true);
-        else PD_LAUNCH_MFMA(0, false);
-    }
+    if (prm.stream_mode >= 1) PD_LAUNCH_MFMA_FOLDS(1);
+    else PD_LAUNCH_MFMA_FOLDS(0);
+#undef PD_LAUNCH_MFMA_FOLDS
 #undef PD_LAUNCH_MFMA
     return launch_status();
 }
@@ -725,7 +832,11 @@ template <int D, int GT>
 int launch_fp32(const PartialParams& prm, int kv_heads, hipStream_t stream) {
     const dim3 grid = to_dim3(partial_grid(prm, kv_heads));
     const dim3 block(partial_threads(prm));
-    if (prm.compact)
+    if (prm.row_mode)
+        hipLaunchKernelGGL(
+            (partial_kernel<float, D, GT, kFp32ChunkLoads, kFp32Prefetch, kFp32RowBlockChunks, false, true>), grid, block,
+            static_cast<size_t>(prm.row_waves) * row_slot_bytes_fp32(D), stream, prm);
+    else if (prm.compact)
         hipLaunchKernelGGL((partial_kernel<float, D, GT, kFp32ChunkLoads, kFp32Prefetch, kFp32BlockChunks, true>), grid,
                            block, 0, stream, prm);
     else
@@ -736,7 +847,7 @@ int launch_fp32(const PartialParams& prm, int kv_heads, hipStream_t stream) {
 
 template <typename QT, int KVF, int D>
 int dispatch_mfma(PartialParams& prm, int kv_heads, hipStream_t stream) {
-    plan_mfma(prm, kv_heads, device_compute_units());
+    plan_mfma(prm, kv_heads, device_compute_units(), D, KVF == kKvNative ? 2 : 1);
     switch (prm.head_tile) {
         case 1: return launch_mfma<QT, KVF, D, 1>(prm, kv_heads, stream);
         case 2: return launch_mfma<QT, KVF, D, 2>(prm, kv_heads, stream);
@@ -748,7 +859,7 @@ int dispatch_mfma(PartialParams& prm, int kv_heads, hipStream_t stream) {
 
 template <int D>
 int dispatch_fp32(PartialParams& prm, int kv_heads, hipStream_t stream) {
-    plan_fp32(prm, kv_heads);
+    plan_fp32(prm, kv_heads, D);
     switch (prm.head_tile) {
         case 1: return launch_fp32<D, 1>(prm, kv_heads, stream);
         case 2: return launch_fp32<D, 2>(prm, kv_heads, stream);

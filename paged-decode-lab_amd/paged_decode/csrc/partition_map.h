@@ -47,6 +47,7 @@ struct PartialParams {
     const int32_t* lengths;
     float* numerator;   // [B, Hq, 4 * splits, D]
     float* stats;       // [B, Hq, 4 * splits, 2]
+    float* out;         // [B, Hq, D]: written by a whole-row launch (row_mode), which stores no states
     uint32_t grid_x, grid_y;  // the launch's grid (kernel arguments: no dependent load of the dispatch packet)
     int batch;
     int query_heads;
@@ -55,6 +56,7 @@ struct PartialParams {
     int heads_per_wg;   // KV heads per workgroup (hw)
     int tiles_per_wg;   // head tiles per workgroup (tw)
     int quarters_per_wg;  // partition quarters per workgroup (qw)
+    int row_waves;        // waves of a whole-row workgroup (row_mode)
     int page_shift;     // log2(page_size)
     int table_width;
     int physical_pages;
@@ -80,7 +82,9 @@ struct PartialParams {
     int32_t main_first[kCompactMaxBatch + 1];
     int32_t tail_first[kCompactMaxBatch + 1];
     // Host only (launch choices, not read by the kernels).
-    int combine;           // the launch stores a workgroup's qw quarters as one state (kCombine)
+    int combine;           // the launch stores a workgroup's qw quarters as one state (kFold 1)
+    int row_allowed;       // the caller takes the output from the partition launch when row_mode is chosen
+    int row_mode;          // whole-row workgroups fold every state of a row into out (kFold 2): no merge launch
     int unshared_pages;    // PD_HINT_UNSHARED_PAGES
     int mid_grid;          // 2-head x 2-quarter workgroups of a mid-size grid
     int ragged_lengths;    // PD_HINT_RAGGED_LENGTHS
@@ -211,6 +215,42 @@ PD_HD int speculative_page(const PartialParams& p, int split, int count, int qgr
     const int capacity = p.table_width << p.page_shift;
     const int64_t start = static_cast<int64_t>(split) * p.split_tokens + static_cast<int64_t>(quarter) * per_full;
     return static_cast<int>(lmin(start, capacity - 1)) >> p.page_shift;
+}
+
+// Whole-row launch (row_mode): one workgroup per (sequence, KV head, head
+// tile) -- heads = kv_head * head_tiles + tile -- whose `waves` waves cut the
+// row's tokens [0, min(len, splits * split_tokens)) into slices of whole load
+// groups, wave w taking slice w. Its states stay in LDS, so the slices need
+// not follow the partitions. A wave with an empty slice (dead) still joins
+// the workgroup's fold, with the empty state.
+template <int GT, int ALIGN>
+PD_HD WaveWork row_wave_work(const PartialParams& p, int b, int heads, int wave, int waves, int len_raw) {
+    WaveWork w;
+    w.split = 0;
+    w.quarter = wave;
+    w.kv_head = heads / p.head_tiles;
+    w.tile = heads % p.head_tiles;
+    const int capacity = p.table_width << p.page_shift;
+    const int len = imax(0, imin(len_raw, capacity));  // decode.cu:42-44
+    const int te = static_cast<int>(lmin(static_cast<int64_t>(p.splits) * p.split_tokens, len));
+    int per = (te + waves - 1) / waves;
+    per = (per + ALIGN - 1) / ALIGN * ALIGN;
+    w.wb = imin(wave * per, te);
+    w.we = imin(w.wb + per, te);
+    w.dead = w.wb >= w.we;
+    const int member0 = w.tile * GT;
+    w.heads_here = imax(0, imin(GT, p.group - member0));
+    w.q_row = static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(w.kv_head) * p.group + member0;
+    return w;
+}
+
+// First logical page of a whole-row wave's slice if the row is full length.
+template <int ALIGN>
+PD_HD int row_speculative_page(const PartialParams& p, int wave, int waves) {
+    const int capacity = p.table_width << p.page_shift;
+    const int span = static_cast<int>(lmin(static_cast<int64_t>(p.splits) * p.split_tokens, capacity));
+    const int per_full = ((span + waves - 1) / waves + ALIGN - 1) / ALIGN * ALIGN;
+    return imin(wave * per_full, capacity - 1) >> p.page_shift;
 }
 
 // Table entry lane `lane` of a wave loads for the page-id window at `window`
@@ -367,21 +407,91 @@ inline Grid partial_grid(const PartialParams& prm, int kv_heads) {
     const uint32_t groups = static_cast<uint32_t>(kQuarters / prm.quarters_per_wg);
     const uint32_t heads = static_cast<uint32_t>((kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg));
     if (prm.compact) return Grid{static_cast<uint32_t>(prm.items) * groups, heads, 1};
+    if (prm.row_mode) return Grid{1, heads, static_cast<uint32_t>(prm.batch)};
     return Grid{static_cast<uint32_t>(prm.splits) * groups, heads, static_cast<uint32_t>(prm.batch)};
 }
 
 inline int64_t workgroups(const Grid& g) { return static_cast<int64_t>(g.x) * g.y * g.z; }
 
 inline int partial_threads(const PartialParams& prm) {
+    if (prm.row_mode) return kWave * prm.row_waves;
     return kWave * prm.heads_per_wg * prm.tiles_per_wg * prm.quarters_per_wg;
 }
 
 // KV heads per workgroup of the matrix-core kernel, at most (FP32 kernel: 8).
 constexpr int kMfmaWorkgroupHeads = 4;
 
-// Launch shape of the matrix-core kernel on a device of `cus` compute units:
-// head tile, workgroup shape, quarter combine and streaming mode.
-inline void plan_mfma(PartialParams& prm, int kv_heads, int cus) {
+// LDS bytes of one wave's K tile in the matrix-core kernel: 16 token rows of
+// head_dim elements of elem bytes, each padded by one operand read (16 bytes
+// for 16-bit K, 8 for FP8).
+constexpr int mfma_stage_bytes(int head_dim, int elem) { return kTileTokens * (head_dim * elem + 8 * elem); }
+
+// LDS bytes of one quarter-combine slot: per-head max and denominator, and
+// head_dim / 16 float4 accumulators per lane. A whole-row launch gives every
+// wave one such slot.
+constexpr int combine_slot_bytes(int head_dim) { return 2 * 16 * 4 + (head_dim / 16) * kWave * 16; }
+
+// Waves of a whole-row workgroup, at most: the kernel is built for 1024-lane
+// workgroups in that mode.
+constexpr int kRowMaxWaves = 16;
+
+// Dynamic LDS of a matrix-core launch: every wave's K tile, then the combine
+// slots ([waves / qw][qw - 1]) when the launch combines quarters, or one slot
+// per wave for a whole-row launch.
+inline int mfma_lds_bytes(const PartialParams& prm, int head_dim, int elem) {
+    const int waves = partial_threads(prm) / kWave;
+    const int slots = prm.row_mode ? waves : prm.combine ? waves / prm.quarters_per_wg * (prm.quarters_per_wg - 1) : 0;
+    return waves * mfma_stage_bytes(head_dim, elem) + slots * combine_slot_bytes(head_dim);
+}
+
+// Whole-row launch: a full decode call whose rows are small enough to be
+// latency-bound -- at most kRowMaxBytes of K and V per (sequence, KV head) --
+// runs one workgroup per (sequence, KV head, head tile), its waves on
+// consecutive slices of the row, folds their states in LDS with the merge's
+// max-corrected sum and writes the output rows: one launch instead of two,
+// and as many waves per row as fit (up to one 16-token group each), however
+// few partitions the row has. Larger rows keep the partition launch spread
+// over all CUs: measured on MI355X, MQA B128 L1024 (256 KB per row) as 128
+// workgroups of 16 waves took 14.5 us per call, against 13.9 us for the
+// partition launch and the merge.
+constexpr int64_t kRowMaxBytes = 128 * 1024;
+constexpr int kRowWaveTokens = 16;
+
+// Bytes of one whole-row LDS slot of the FP32 kernel (per-head max and
+// denominator, and the head tile's accumulators, GT <= 8).
+constexpr int row_slot_bytes_fp32(int head_dim) { return (2 * 8 + 8 * head_dim) * 4; }
+
+// Waves of an FP32 whole-row workgroup, at most: 16, except for head tiles of
+// 8, whose q, accumulators and load pipeline (about 160 VGPRs) would not fit
+// the 128 VGPRs of a 1024-lane workgroup without spilling: 8.
+constexpr int fp32_row_max_waves(int gt) { return gt >= 8 ? 8 : kRowMaxWaves; }
+
+// Sets up a whole-row launch if the call allows it and its rows qualify;
+// slot_bytes and stage_bytes are the kernel's LDS per wave.
+inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes, int stage_bytes,
+                      int max_waves = kRowMaxWaves) {
+    prm.row_mode = 0;
+    if (!prm.row_allowed) return;
+    const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
+    const int64_t span = lmin(static_cast<int64_t>(prm.splits) * prm.split_tokens, capacity);
+    if (span * head_dim * elem * 2 > kRowMaxBytes) return;
+    int waves = static_cast<int>(lmin(max_waves, (span + kRowWaveTokens - 1) / kRowWaveTokens));
+    while (waves > 1 && waves * (slot_bytes + stage_bytes) > 160 * 1024) --waves;
+    prm.row_mode = 1;
+    prm.row_waves = imax(1, waves);
+    prm.heads_per_wg = 1;
+    prm.tiles_per_wg = 1;
+    prm.quarters_per_wg = kQuarters;
+    prm.combine = 0;
+    prm.mid_grid = 0;
+    prm.compact = 0;
+    prm.items = prm.batch * prm.splits;
+}
+
+// Launch shape of the matrix-core kernel on a device of `cus` compute units,
+// for head_dim and K/V elements of elem bytes: head tile, workgroup shape,
+// quarter combine or whole rows, and streaming mode.
+inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, int elem) {
     const int gt = head_tile(prm.group, 16);
     prm.head_tile = gt;
     prm.head_tiles = (prm.group + gt - 1) / gt;
@@ -458,37 +568,23 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus) {
     const int groups = kv_heads / prm.heads_per_wg;
     prm.stream_mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
                       : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+    plan_rows(prm, head_dim, elem, combine_slot_bytes(head_dim), mfma_stage_bytes(head_dim, elem));
     const Grid grid = partial_grid(prm, kv_heads);
     prm.grid_x = grid.x;
     prm.grid_y = grid.y;
 }
 
-// Launch shape of the FP32 kernel.
-inline void plan_fp32(PartialParams& prm, int kv_heads) {
+// Launch shape of the FP32 kernel (and whole rows, as for the matrix-core
+// kernel).
+inline void plan_fp32(PartialParams& prm, int kv_heads, int head_dim) {
     const int gt = head_tile(prm.group, 8);
     prm.head_tile = gt;
     prm.head_tiles = (prm.group + gt - 1) / gt;
     choose_workgroup(prm, kv_heads, 8);
+    plan_rows(prm, head_dim, 4, row_slot_bytes_fp32(head_dim), 0, fp32_row_max_waves(gt));
     const Grid grid = partial_grid(prm, kv_heads);
     prm.grid_x = grid.x;
     prm.grid_y = grid.y;
-}
-
-// LDS bytes of one wave's K tile in the matrix-core kernel: 16 token rows of
-// head_dim elements of elem bytes, each padded by one operand read (16 bytes
-// for 16-bit K, 8 for FP8).
-constexpr int mfma_stage_bytes(int head_dim, int elem) { return kTileTokens * (head_dim * elem + 8 * elem); }
-
-// LDS bytes of one quarter-combine slot: per-head max and denominator, and
-// head_dim / 16 float4 accumulators per lane.
-constexpr int combine_slot_bytes(int head_dim) { return 2 * 16 * 4 + (head_dim / 16) * kWave * 16; }
-
-// Dynamic LDS of a matrix-core launch: every wave's K tile, then the combine
-// slots ([waves / qw][qw - 1]) when the launch combines quarters.
-inline int mfma_lds_bytes(const PartialParams& prm, int head_dim, int elem) {
-    const int waves = partial_threads(prm) / kWave;
-    return waves * mfma_stage_bytes(head_dim, elem) +
-           (prm.combine ? waves / prm.quarters_per_wg * (prm.quarters_per_wg - 1) * combine_slot_bytes(head_dim) : 0);
 }
 
 }  // namespace pd

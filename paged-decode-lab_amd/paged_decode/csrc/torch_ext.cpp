@@ -38,9 +38,10 @@ hipStream_t current_stream(const torch::Tensor& like) {
     return c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(like.get_device()).stream();
 }
 
-// Storage format code of a tensor (-1 for anything the library does not store).
-int dtype_code(const torch::Tensor& t) {
-    switch (t.scalar_type()) {
+// Storage format code of a dtype or tensor (-1 for anything the library does
+// not store).
+int dtype_code(at::ScalarType t) {
+    switch (t) {
         case at::kFloat: return PD_DTYPE_F32;
         case at::kHalf: return PD_DTYPE_F16;
         case at::kBFloat16: return PD_DTYPE_BF16;
@@ -49,6 +50,8 @@ int dtype_code(const torch::Tensor& t) {
         default: return -1;
     }
 }
+
+int dtype_code(const torch::Tensor& t) { return dtype_code(t.scalar_type()); }
 
 bool is_fp8(const torch::Tensor& t) {
     return t.scalar_type() == at::kFloat8_e4m3fn || t.scalar_type() == at::kFloat8_e5m2;
@@ -259,6 +262,22 @@ void table_from_csr(torch::Tensor indptr, torch::Tensor indices, torch::Tensor l
                                    static_cast<int>(max_context), current_stream(table)));
 }
 
+// Kernel launches decode makes for these formats and shapes (1: whole rows,
+// 2: partition and merge).
+int64_t launch_count(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t batch, int64_t query_heads,
+                     int64_t kv_heads, int64_t head_dim, int64_t page_size, int64_t table_width,
+                     int64_t physical_pages, int64_t splits, int64_t split_tokens, bool unshared_pages,
+                     bool ragged_lengths) {
+    int launches = 0;
+    check_status(pd_decode_launch_count(dtype_code(q_dtype), dtype_code(kv_dtype), static_cast<int>(batch),
+                                        static_cast<int>(query_heads), static_cast<int>(kv_heads),
+                                        static_cast<int>(head_dim), static_cast<int>(page_size),
+                                        static_cast<int>(table_width), static_cast<int>(physical_pages),
+                                        static_cast<int>(splits), static_cast<int>(split_tokens),
+                                        hints(unshared_pages, ragged_lengths), &launches));
+    return launches;
+}
+
 PYBIND11_MODULE(_C, m) {
     m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
@@ -281,6 +300,7 @@ PYBIND11_MODULE(_C, m) {
         return static_cast<int64_t>(pd_workspace_bytes(static_cast<int>(b), static_cast<int>(h),
                                                        static_cast<int>(d), static_cast<int>(s)));
     });
+    m.def("launch_count", &launch_count, "Kernel launches of a decode call (1: whole rows, 2: partition + merge)");
     m.def("abi_version", &pd_abi_version, "ABI version the loaded HIP library reports");
     m.def("header_abi_version", [] { return PD_ABI_VERSION; }, "ABI version of the header this module was built with");
     m.def("build_digest", [] { return std::string(PD_BUILD_DIGEST); }, "Digest of the sources this module was built from");

@@ -251,8 +251,19 @@ class DecodePlan:
                                self._unshared_pages, self._ragged_lengths, self._length_bounds())
         return self._out
 
+    def launches(self, q_dtype, kv_dtype=None):
+        """Kernel launches ``run`` makes for q (and K/V) of these dtypes: 1 when the
+        rows are small enough for one whole-row launch that writes the output
+        (the workspace is then left unwritten), else 2 (partition, merge)."""
+        layout = self.layout
+        return self._extension.launch_count(q_dtype, q_dtype if kv_dtype is None else kv_dtype, layout.batch,
+                                            layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size,
+                                            self._table.shape[1], layout.physical_pages, self.splits,
+                                            self.split_tokens, self._unshared_pages, self._ragged_lengths)
+
     def run_partial(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
-        """Partition stage only (fills the workspace); for stage timing."""
+        """Partition stage only (fills the workspace with the states; never a
+        whole-row launch); for stage timing."""
         self._check(q, k, v, k_scale, v_scale)
         self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
                                 self.split_tokens, float(k_scale), float(v_scale), self._unshared_pages,

@@ -45,8 +45,11 @@ def source_digest():
     return h.hexdigest()[:16]
 
 
-def partition_kernel_name(dtype_is_half):
-    return "partial_mfma_kernel" if dtype_is_half else "partial_kernel"
+def partition_kernel_name(dtype_is_half, whole_rows=False):
+    """Name of the partition kernel (the launch that reads K and V); a whole-row
+    launch is the same kernel built to fold the states and write the output."""
+    name = "partial_mfma_kernel" if dtype_is_half else "partial_kernel"
+    return name + " (whole rows)" if whole_rows else name
 
 
 def run(args):
@@ -63,9 +66,11 @@ def run(args):
     ks = [k0] + [k0.clone() for _ in range(sets - 1)]
     vs = [v0] + [v0.clone() for _ in range(sets - 1)]
     plan = DecodePlan(w.layout, w.table, w.lengths, device=dev, split_tokens=w.split_tokens)
+    # A call that is one whole-row launch is measured as such (it is the call's only kernel).
+    stage = plan.run if plan.launches(q.dtype, k0.dtype) == 1 else plan.run_partial
     print(f"[traffic] {w.name}: {args.launches} partition launches over {sets} K/V sets", flush=True)
     for i in range(args.launches):
-        plan.run_partial(q, ks[i % sets], vs[i % sets], k_scale=k_scale, v_scale=v_scale)
+        stage(q, ks[i % sets], vs[i % sets], k_scale=k_scale, v_scale=v_scale)
     torch.cuda.synchronize()
     src = torch.randn(COPY_BYTES // 4, device=dev)
     dst = torch.empty_like(src)

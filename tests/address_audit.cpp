@@ -71,8 +71,9 @@ Buffers buffers(const Problem& pr) {
     return b;
 }
 
-PartialParams params(const Problem& pr, int cus, bool mfma) {
+PartialParams params(const Problem& pr, int cus, bool mfma, bool rows) {
     PartialParams p{};
+    p.row_allowed = rows;
     p.batch = pr.batch;
     p.query_heads = pr.q_heads;
     p.group = pr.q_heads / pr.kv_heads;
@@ -86,8 +87,8 @@ PartialParams params(const Problem& pr, int cus, bool mfma) {
     p.unshared_pages = pr.unshared;
     p.ragged_lengths = pr.ragged;
     plan_items(p, pr.bounds.empty() ? nullptr : pr.bounds.data());
-    if (mfma) plan_mfma(p, pr.kv_heads, cus);
-    else plan_fp32(p, pr.kv_heads);
+    if (mfma) plan_mfma(p, pr.kv_heads, cus, pr.head_dim, pr.kv_elem);
+    else plan_fp32(p, pr.kv_heads, pr.head_dim);
     return p;
 }
 
@@ -98,6 +99,16 @@ struct Coverage {
     void store(uint64_t slot) {
         AUDIT(slot < writes.size(), "state slot %" PRIu64 " past the workspace", slot);
         if (slot < writes.size() && writes[slot] < 255) ++writes[slot];
+    }
+};
+
+// Writers of each output element of a whole-row launch.
+struct OutCoverage {
+    std::vector<uint8_t> writes;
+    explicit OutCoverage(uint64_t elems) : writes(elems, 0) {}
+    void store(int64_t e) {
+        AUDIT(e >= 0 && static_cast<uint64_t>(e) < writes.size(), "output element %" PRId64 " past out", e);
+        if (e >= 0 && static_cast<uint64_t>(e) < writes.size() && writes[e] < 255) ++writes[e];
     }
 };
 
@@ -199,16 +210,19 @@ void window_loads(const Problem& pr, const PartialParams& p, const Buffers& buf,
 }
 
 template <int D, int GT>
-void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage& cov) {
+void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage& cov, OutCoverage& out) {
+    constexpr int TPLV = kWave / (D / 4);  // FP32 kernel: token rows per 16-byte load group
     const Buffers buf = buffers(pr);
     const Grid grid = partial_grid(p, pr.kv_heads);
     AUDIT(p.grid_x == grid.x && p.grid_y == grid.y, "kernel-argument grid %ux%u, launch %ux%u", p.grid_x, p.grid_y,
           grid.x, grid.y);
     const int waves = partial_threads(p) / kWave;
-    AUDIT(waves >= 1 && waves <= 8, "workgroup of %d waves", waves);
+    AUDIT(waves >= 1 && waves <= (p.row_mode ? kRowMaxWaves : 8), "workgroup of %d waves", waves);
     if (mfma) AUDIT(mfma_lds_bytes(p, D, pr.kv_elem) <= 160 * 1024, "LDS %d bytes", mfma_lds_bytes(p, D, pr.kv_elem));
     const int align = mfma ? kTileTokens : kWave / (D / 4);
-    const int block = mfma ? 2 : 16, ahead = mfma ? 2 : 4, group_tokens = align;
+    // Load groups per straight-line block and issued ahead: matrix-core 2 and
+    // 2; FP32 16 and 4, whole-row FP32 launches 4 and 4.
+    const int block = mfma ? 2 : p.row_mode ? 4 : 16, ahead = mfma ? 2 : 4, group_tokens = align;
     const int qw = p.quarters_per_wg;
     for (uint32_t bz = 0; bz < grid.z; ++bz) {
         for (uint32_t by = 0; by < grid.y; ++by) {
@@ -222,25 +236,68 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                 const int b = r.b;
                 const int len_raw = pr.lengths[b];
                 const int len = imax(0, imin(len_raw, pr.width * pr.page_size));
+                const bool rows = p.row_mode != 0;
+                const int row_limit = mfma ? kRowMaxWaves : fp32_row_max_waves(GT);
+                if (rows) {
+                    AUDIT(!p.compact && waves == p.row_waves && waves <= row_limit, "whole-row launch of %d waves",
+                          waves);
+                    AUDIT(grid.x == 1 && r.first == 0 && r.count == 1 && r.qgroup == 0, "whole-row workgroup item");
+                }
+                int64_t row_q = -1;
+                int row_heads = -1, row_next = 0;
+                const int row_end = static_cast<int>(lmin(static_cast<int64_t>(pr.splits) * pr.split_tokens, len));
                 for (int wave = 0; wave < waves; ++wave) {
-                    int window = mfma ? speculative_page<kTileTokens>(p, r.first, r.count, r.qgroup, wave)
-                                      : speculative_page<kWave / (D / 4)>(p, r.first, r.count, r.qgroup, wave);
+                    const int split = r.first;
+                    int window = rows ? (mfma ? row_speculative_page<kTileTokens>(p, wave, waves)
+                                              : row_speculative_page<TPLV>(p, wave, waves))
+                                      : mfma ? speculative_page<kTileTokens>(p, split, r.count, r.qgroup, wave)
+                                             : speculative_page<TPLV>(p, split, r.count, r.qgroup, wave);
                     window_loads(pr, p, buf, b, window);
                     {
-                        const int split = r.first;
                         const WaveWork w =
-                            mfma ? wave_work<GT, kTileTokens>(p, b, split, r.count, r.qgroup, bc.heads, wave, len_raw)
-                                 : wave_work<GT, kWave / (D / 4)>(p, b, split, r.count, r.qgroup, bc.heads, wave,
-                                                                   len_raw);
-                        if (w.dead) continue;
+                            rows ? (mfma ? row_wave_work<GT, kTileTokens>(p, b, bc.heads, wave, waves, len_raw)
+                                         : row_wave_work<GT, TPLV>(p, b, bc.heads, wave, waves, len_raw))
+                            : mfma ? wave_work<GT, kTileTokens>(p, b, split, r.count, r.qgroup, bc.heads, wave,
+                                                                len_raw)
+                                   : wave_work<GT, TPLV>(p, b, split, r.count, r.qgroup, bc.heads, wave, len_raw);
+                        if (rows) {
+                            // Every wave writes its LDS slot (an empty slice
+                            // the empty state); the slices tile the row's
+                            // tokens [0, min(len, splits * split_tokens)) in
+                            // wave order; all waves share the row.
+                            if (mfma) {
+                                const int lds = mfma_lds_bytes(p, D, pr.kv_elem);
+                                const int base = waves * mfma_stage_bytes(D, pr.kv_elem);
+                                AUDIT(base + (wave + 1) * combine_slot_bytes(D) <= lds && lds <= 160 * 1024,
+                                      "row slot write");
+                            } else {
+                                AUDIT(waves * row_slot_bytes_fp32(D) <= 160 * 1024, "row slots");
+                            }
+                            if (row_q < 0) {
+                                row_q = w.q_row;
+                                row_heads = w.heads_here;
+                            }
+                            AUDIT(w.q_row == row_q && w.heads_here == row_heads, "waves of one row disagree");
+                            if (!w.dead) {
+                                AUDIT(w.wb == row_next, "slice %d starts at %d, expected %d", wave, w.wb, row_next);
+                                row_next = w.we;
+                            }
+                            if (wave == waves - 1) AUDIT(row_next == row_end, "slices end at %d of %d", row_next, row_end);
+                        }
+                        if (w.dead) {
+                            AUDIT(!rows || w.wb == w.we, "dead row wave with tokens");
+                            continue;
+                        }
                         AUDIT(w.kv_head >= 0 && w.kv_head < pr.kv_heads, "KV head %d", w.kv_head);
                         AUDIT(w.tile >= 0 && w.tile < p.head_tiles, "head tile %d", w.tile);
                         AUDIT(w.q_row >= 0 && w.q_row + w.heads_here <= static_cast<int64_t>(pr.batch) * pr.q_heads,
                               "q row %" PRId64, w.q_row);
-                        const int64_t first = static_cast<int64_t>(split) * pr.split_tokens;
-                        AUDIT(w.wb >= first && w.we <= first + static_cast<int64_t>(r.count) * pr.split_tokens &&
-                                  w.wb <= w.we && w.we <= len,
-                              "wave range [%d, %d) of partitions %d + %d", w.wb, w.we, split, r.count);
+                        // A wave's tokens lie in its partitions (a whole-row
+                        // wave's: in the row's, [0, splits * split_tokens)).
+                        const int64_t first = rows ? 0 : static_cast<int64_t>(split) * pr.split_tokens;
+                        const int64_t parts = rows ? pr.splits : r.count;
+                        AUDIT(w.wb >= first && w.we <= first + parts * pr.split_tokens && w.wb <= w.we && w.we <= len,
+                              "wave range [%d, %d) of partitions %d + %" PRId64, w.wb, w.we, split, parts);
                         // q loads of the tile's live heads.
                         for (int lane = 0; lane < kWave; ++lane) {
                             if (mfma) {
@@ -276,6 +333,7 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                                 }
                             }
                         }
+                        if (rows) continue;  // no state stores: the fold below writes out
                         // State stores: one state per live head of the tile;
                         // a combining workgroup's later quarters store the empty
                         // state in their own slots.
@@ -308,35 +366,63 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                         }
                     }
                 }
+                if (rows) {
+                    // The fold. Matrix-core kernel: output element o of the
+                    // row's live heads, o < heads_here * D, is column o % 16,
+                    // dims (o / 16) % (D / 16) of head o / D, read from lane
+                    // 16 (h / 4) + col of each slot. FP32 kernel: element o is
+                    // slot word 16 + o.
+                    const int vh = D / 16;
+                    for (int o = 0; o < row_heads * D; ++o) {
+                        if (mfma) {
+                            const int col = o % 16, j = (o / 16) % vh, h = o / D;
+                            AUDIT(h < GT && 16 * (h / 4) + col < kWave && j < vh, "fold element %d", o);
+                            out.store((row_q + h) * D + col * vh + j);
+                        } else {
+                            AUDIT(16 + o < row_slot_bytes_fp32(D) / 4 && o / D < GT, "fold element %d", o);
+                            out.store(row_q * D + o);
+                        }
+                    }
+                }
             }
         }
     }
 }
 
 template <int D>
-void audit_gt(const Problem& pr, const PartialParams& p, bool mfma, Coverage& cov) {
+void audit_gt(const Problem& pr, const PartialParams& p, bool mfma, Coverage& cov, OutCoverage& out) {
     switch (p.head_tile) {
-        case 1: return audit_launch<D, 1>(pr, p, mfma, cov);
-        case 2: return audit_launch<D, 2>(pr, p, mfma, cov);
-        case 4: return audit_launch<D, 4>(pr, p, mfma, cov);
-        case 8: return audit_launch<D, 8>(pr, p, mfma, cov);
-        default: return audit_launch<D, 16>(pr, p, mfma, cov);
+        case 1: return audit_launch<D, 1>(pr, p, mfma, cov, out);
+        case 2: return audit_launch<D, 2>(pr, p, mfma, cov, out);
+        case 4: return audit_launch<D, 4>(pr, p, mfma, cov, out);
+        case 8: return audit_launch<D, 8>(pr, p, mfma, cov, out);
+        default: return audit_launch<D, 16>(pr, p, mfma, cov, out);
     }
 }
 
-bool audit(const Problem& pr) {
+// Audits the launch planned for a partition-only call (states), and for a
+// full decode call (rows: the planner may choose a whole-row launch).
+bool audit(const Problem& pr, bool rows) {
     const int before = g_failures;
     const uint64_t checks_before = g_checks;
     const bool mfma = pr.q_elem == 2;
-    const PartialParams p = params(pr, 256, mfma);
+    const PartialParams p = params(pr, 256, mfma, rows);
     Coverage cov(static_cast<uint64_t>(pr.batch) * pr.q_heads * kQuarters * pr.splits);
-    if (pr.head_dim == 64) audit_gt<64>(pr, p, mfma, cov);
-    else audit_gt<128>(pr, p, mfma, cov);
-    check_coverage(pr, cov);
+    OutCoverage out(static_cast<uint64_t>(pr.batch) * pr.q_heads * pr.head_dim);
+    if (pr.head_dim == 64) audit_gt<64>(pr, p, mfma, cov, out);
+    else audit_gt<128>(pr, p, mfma, cov, out);
+    if (p.row_mode) {
+        AUDIT(mfma_lds_bytes(p, pr.head_dim, pr.kv_elem) <= 160 * 1024, "whole-row LDS");
+        for (size_t e = 0; e < out.writes.size(); ++e)
+            AUDIT(out.writes[e] == 1, "output element %zu written %d times", e, out.writes[e]);
+    } else {
+        check_coverage(pr, cov);
+    }
     const Grid grid = partial_grid(p, pr.kv_heads);
-    std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s, %" PRIu64 " checks: %s\n", pr.name.c_str(),
-                mfma ? "mfma" : "fp32", grid.x, grid.y, grid.z, partial_threads(p) / kWave, p.head_tile,
-                p.quarters_per_wg, p.compact ? "compact" : "rectangular", p.combine ? ", combined" : "",
+    std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s, %" PRIu64 " checks: %s\n",
+                (pr.name + (rows ? " [call]" : "")).c_str(), mfma ? "mfma" : "fp32", grid.x, grid.y, grid.z,
+                partial_threads(p) / kWave, p.head_tile, p.quarters_per_wg,
+                p.row_mode ? "whole rows" : p.compact ? "compact" : "rectangular", p.combine ? ", combined" : "",
                 g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
     std::fflush(stdout);
     return g_failures == before;
@@ -475,6 +561,26 @@ int main(int argc, char** argv) {
                  hk.second, 64, 16, 12, {192, 77, 150}, 64, 4, 4, 11),
             false);
     }
+    // Whole-row launches (a full decode call of at most four partitions per
+    // row): ragged lengths with empty rows and partial partitions, GQA and
+    // MQA tiles, both head dimensions, FP8 K/V, page 32, a single partition
+    // per row, invalid page ids.
+    add(make("rows mqa B128 D64 ragged split 256", 128, 16, 1, 64, 16, 64, ragged(128, 1024, 51), 256, 2, 2, 51),
+        false);
+    add(make("rows B64 Hq32/8 D128 ragged split 192", 64, 32, 8, 128, 16, 32, ragged(64, 512, 53), 192, 2, 2, 53),
+        false);
+    add(make("rows B64 Hq32/8 D128 fp8 split 192", 64, 32, 8, 128, 32, 16, ragged(64, 512, 55), 192, 2, 1, 55),
+        false);
+    add(make("rows B2 Hq8/2 D64 L[100,256] split 256", 2, 8, 2, 64, 16, 16, {100, 256}, 256, 2, 2, 57), false);
+    add(make("rows B3 Hq20/4 D128 split 512 page 32", 3, 20, 4, 128, 32, 16, {512, 1, 0}, 512, 2, 2, 59), false);
+    {
+        Problem pr = make("rows invalid page ids B32 Hq16/4 split 64", 32, 16, 4, 64, 16, 16, ragged(32, 256, 61), 64,
+                          2, 2, 61);
+        pr.table[3] = -1;
+        pr.table[16 + 5] = pr.pages;
+        pr.table[32 + 0] = 2147483647;
+        add(pr, false);
+    }
     if (!quick) {
         // A 1M-token context in a 65536-wide table (16384 states per row).
         add(make("1M context W65536 fp16", 1, 8, 2, 128, 16, 65536, uniform(1, 1 << 20), 256, 2, 2, 13), false);
@@ -485,7 +591,11 @@ int main(int argc, char** argv) {
         add(big);
     }
     int failed = 0;
-    for (const auto& pr : problems) failed += audit(pr) ? 0 : 1;
+    for (const auto& pr : problems) {
+        failed += audit(pr, false) ? 0 : 1;
+        // The plan for a full decode call, when it is a whole-row launch.
+        if (params(pr, 256, pr.q_elem == 2, true).row_mode) failed += audit(pr, true) ? 0 : 1;
+    }
     std::printf("%zu problems, %" PRIu64 " checks, %d failures\n", problems.size(), g_checks, g_failures);
     return failed == 0 ? 0 : 1;
 }

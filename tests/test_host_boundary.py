@@ -82,11 +82,32 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 12
+    assert lib.pd_abi_version() == 13
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
     assert cabi.status_string(lib, 99) == "unknown status"
+
+
+def test_launch_count_query():
+    """Whole-row launches (one kernel) for rows of at most 128 KB of K and V per
+    (sequence, KV head); partition + merge otherwise; shape errors as pd_decode_ex."""
+    lib = cabi.load()
+    f32, f16, fp8 = cabi.PD_DTYPE_F32, cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E4M3
+    # FP32 oracle case: B2, 8/2 heads, D64, page 16, 16 pages per row, split 256 (256 tokens: 128 KB).
+    assert cabi.launch_count(lib, f32, f32, 2, 8, 2, 64, 16, 16, 32, 1, 256) == 1
+    # Llama-3-8B decode shape (4096 tokens per row) and MQA B128 L1024 D64 (256 KB per row).
+    assert cabi.launch_count(lib, f16, f16, 4, 32, 8, 128, 16, 256, 1024, 16, 256) == 2
+    assert cabi.launch_count(lib, f16, f16, 128, 16, 1, 64, 16, 64, 8192, 4, 256) == 2
+    # The bound is on splits * split_tokens, capped by the table: 512 FP16 tokens at D128 is 256 KB,
+    # 512 FP8 tokens 128 KB; a 4096-token reservation in a 256-token table still fits.
+    assert cabi.launch_count(lib, f16, f16, 8, 32, 8, 128, 16, 32, 256, 2, 256) == 2
+    assert cabi.launch_count(lib, f16, fp8, 8, 32, 8, 128, 16, 32, 256, 2, 256) == 1
+    assert cabi.launch_count(lib, f16, f16, 8, 32, 8, 64, 16, 16, 128, 16, 256) == 1
+    with pytest.raises(ValueError, match="dimension"):
+        cabi.launch_count(lib, f16, f16, 8, 32, 8, 96, 16, 16, 128, 1, 256)
+    with pytest.raises(ValueError, match="dtype"):
+        cabi.launch_count(lib, f32, fp8, 8, 32, 8, 64, 16, 16, 128, 1, 256)
 
 
 C_CONSUMER = r"""
@@ -95,7 +116,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 12) return 1;
+    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 13) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
