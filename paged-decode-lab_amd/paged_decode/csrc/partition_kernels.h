@@ -69,7 +69,7 @@ __device__ __forceinline__ void store_empty_states(const PartialParams& p, const
 // buffers in fully unrolled blocks of NC chunks.
 // kRow: a whole-row workgroup (up to kRowMaxWaves waves) that folds its
 // waves' states in LDS and writes the output rows instead of states.
-template <typename T, int D, int GT, int NL, int PD, int NC, bool kCompact, bool kRow = false>
+template <typename T, int D, int GT, int NL, int PD, int NC, int kList, bool kRow = false>
 __global__ void __launch_bounds__(kRow ? kWave * fp32_row_max_waves(GT) : kWave * 8)
     partial_kernel(const PartialParams p) {
     using E = Elem<T>;
@@ -90,7 +90,7 @@ __global__ void __launch_bounds__(kRow ? kWave * fp32_row_max_waves(GT) : kWave 
     const int row = lane / LPT;
     const int col = lane % LPT;
     const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y);
-    const PartitionRange pr = partition_range<kCompact>(p, bc);
+    const PartitionRange pr = partition_range<kList>(p, bc);
     const int waves_wg = blockDim.x / kWave;
     const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
     int window = kRow ? row_speculative_page<TPL>(p, wave, waves_wg)
@@ -449,7 +449,7 @@ struct CombineSlot {
 // kFold: what the workgroup stores -- 0 one state per wave; 1 one state per
 // qw quarters of a partition (quarter combine); 2 the output rows of a whole
 // row's states (whole-row launch, up to kRowMaxWaves waves: 1024 lanes).
-template <typename QT, int KVF, int D, int GT, int PD, int NC, int kStream, int kFold, bool kCompact>
+template <typename QT, int KVF, int D, int GT, int PD, int NC, int kStream, int kFold, int kList>
 __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
     partial_mfma_kernel(const PartialParams p) {
     using C = Compute<QT>;
@@ -489,7 +489,7 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
     const int n = lane % 16;  // head (q.K^T, P) / column (P.V)
     const int g = lane / 16;  // lane group: tokens g + 4 e
     const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y);
-    const PartitionRange pr = partition_range<kCompact>(p, bc);
+    const PartitionRange pr = partition_range<kList>(p, bc);
     // A whole-row workgroup's wave runs slice `wave` of its row (one KV head,
     // one head tile); otherwise the wave index splits into (head, tile,
     // quarter) within the workgroup's partition.
@@ -795,19 +795,23 @@ int launch_mfma(const PartialParams& prm, int kv_heads, hipStream_t stream) {
     const dim3 grid = to_dim3(partial_grid(prm, kv_heads));
     const dim3 block(partial_threads(prm));
     const size_t lds = static_cast<size_t>(mfma_lds_bytes(prm, D, KVF == kKvNative ? 2 : 1));
+    const int kind = grid_kind(prm);
     constexpr int kPD = kMfmaPrefetch, kNC = kMfmaBlock;
     // Whole-row launches are rectangular (one workgroup per row).
 #define PD_LAUNCH_MFMA(MODE, FOLD)                                                                                \
     do {                                                                                                          \
         if constexpr (FOLD == 2)                                                                                  \
-            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, 2, false>), grid, block, lds, \
-                               stream, prm);                                                                      \
-        else if (prm.compact)                                                                                     \
-            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, true>), grid, block,    \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, 2, kGridRect>), grid, block,  \
                                lds, stream, prm);                                                                 \
+        else if (kind == kGridList)                                                                               \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, kGridList>), grid,      \
+                               block, lds, stream, prm);                                                          \
+        else if (kind == kGridRectTails)                                                                          \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, kGridRectTails>), grid, \
+                               block, lds, stream, prm);                                                          \
         else                                                                                                      \
-            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, false>), grid, block,   \
-                               lds, stream, prm);                                                                 \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, kGridRect>), grid,      \
+                               block, lds, stream, prm);                                                          \
     } while (0)
 #define PD_LAUNCH_MFMA_FOLDS(MODE)                      \
     do {                                                \
@@ -832,16 +836,17 @@ template <int D, int GT>
 int launch_fp32(const PartialParams& prm, int kv_heads, hipStream_t stream) {
     const dim3 grid = to_dim3(partial_grid(prm, kv_heads));
     const dim3 block(partial_threads(prm));
+    constexpr int NL = kFp32ChunkLoads, PD = kFp32Prefetch, NC = kFp32BlockChunks;
+    const int kind = grid_kind(prm);
     if (prm.row_mode)
-        hipLaunchKernelGGL(
-            (partial_kernel<float, D, GT, kFp32ChunkLoads, kFp32Prefetch, kFp32RowBlockChunks, false, true>), grid, block,
-            static_cast<size_t>(prm.row_waves) * row_slot_bytes_fp32(D), stream, prm);
-    else if (prm.compact)
-        hipLaunchKernelGGL((partial_kernel<float, D, GT, kFp32ChunkLoads, kFp32Prefetch, kFp32BlockChunks, true>), grid,
-                           block, 0, stream, prm);
+        hipLaunchKernelGGL((partial_kernel<float, D, GT, NL, PD, kFp32RowBlockChunks, kGridRect, true>), grid, block,
+                           static_cast<size_t>(prm.row_waves) * row_slot_bytes_fp32(D), stream, prm);
+    else if (kind == kGridList)
+        hipLaunchKernelGGL((partial_kernel<float, D, GT, NL, PD, NC, kGridList>), grid, block, 0, stream, prm);
+    else if (kind == kGridRectTails)
+        hipLaunchKernelGGL((partial_kernel<float, D, GT, NL, PD, NC, kGridRectTails>), grid, block, 0, stream, prm);
     else
-        hipLaunchKernelGGL((partial_kernel<float, D, GT, kFp32ChunkLoads, kFp32Prefetch, kFp32BlockChunks, false>),
-                           grid, block, 0, stream, prm);
+        hipLaunchKernelGGL((partial_kernel<float, D, GT, NL, PD, NC, kGridRect>), grid, block, 0, stream, prm);
     return launch_status();
 }
 

@@ -66,6 +66,16 @@ struct PartialParams {
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
     float v_scale;         // multiplies every stored numerator
+    // Rectangular grid (compact == 0): sequence b's partitions 0 ..
+    // main_splits - 1 are items of z-slice b; when main_splits < splits (host
+    // bounds reach fewer partitions than reserved), z-slices batch, batch + 1,
+    // ... hold the tail items, (1 << tail_shift) per sequence in sequence
+    // order, tail item j covering tail_span partitions from main_splits + j *
+    // tail_span -- no lookup, so the main items' prologue is that of a plain
+    // rectangular grid. Items past the last tail are empty.
+    int main_splits;
+    int tail_shift;
+    int tail_span;
     // Compacted work list (compact != 0): the grid's items are first the main
     // items of every sequence, in sequence order -- sequence b has
     // main_first[b + 1] - main_first[b] of them, partitions 0, 1, ... one
@@ -89,6 +99,8 @@ struct PartialParams {
     int mid_grid;          // 2-head x 2-quarter workgroups of a mid-size grid
     int ragged_lengths;    // PD_HINT_RAGGED_LENGTHS
     int stream_mode;       // non-temporal loads: 0 none, 1 V (FP8: K), 2 K and V
+    int shape_splits;      // partitions per sequence the bounds reach: the workgroup shape's grid (plan_items)
+    int live_items;        // items holding tokens as far as the bounds tell (plan_items)
     int head_tile;         // GT: query heads per wave's tile (the GQA group padded to 1/2/4/8/16)
 };
 
@@ -126,40 +138,80 @@ struct PartitionRange {
     int b, first, count, qgroup;
 };
 
-// kCompact is the launch's p.compact, fixed at compile time: a kernel built
-// for rectangular grids carries no work-list search, whose control flow would
-// otherwise keep the compiler from loading the kernel arguments in one batch
-// before the first page-id load (measured on MI355X: 0.5 us per launch).
-template <bool kCompact>
+// Kinds of grid, fixed at compile time per kernel (kList): a kernel built for
+// plain rectangular grids carries neither the tail arithmetic nor the
+// work-list lookup. The lookup's control flow kept the compiler from loading
+// the kernel arguments in one batch before the first page-id load (measured
+// on MI355X: 0.5 us per launch), and the tail arithmetic took the 8-wave
+// kernel from 128 to 131 VGPRs, one wave per SIMD fewer (ragged + shared B16
+// partition kernel 36 -> 48 us).
+enum GridKind { kGridRect = 0, kGridRectTails = 1, kGridList = 2 };
+
+inline int grid_kind(const PartialParams& prm) {
+    return prm.compact ? kGridList : prm.main_splits < prm.splits ? kGridRectTails : kGridRect;
+}
+
+template <int kList>
 PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& bc) {
     const int groups = kQuarters / p.quarters_per_wg;
     const int item = bc.tokens / groups;
     PartitionRange r;
     r.qgroup = bc.tokens - item * groups;
-    if (!kCompact) {
+    if (kList == kGridRect) {
         r.b = bc.z;
         r.first = item;
         r.count = 1;
         return r;
     }
+    if (kList == kGridRectTails) {
+        // Branch-free: a main item's values come out of the same arithmetic.
+        const int zt = bc.z - p.batch;  // tail slice, negative for main items
+        const int lin = zt * p.main_splits + item;
+        const int tb = lin >> p.tail_shift;
+        const int tfirst = p.main_splits + (lin & ((1 << p.tail_shift) - 1)) * p.tail_span;
+        const bool tail = zt >= 0;
+        const bool none = tail && (tb >= p.batch || tfirst >= p.splits);
+        r.b = tail ? imin(tb, p.batch - 1) : bc.z;
+        r.first = tail ? imin(tfirst, p.splits - 1) : item;
+        r.count = none ? 0 : tail ? imin(p.tail_span, p.splits - tfirst) : 1;
+        return r;
+    }
     const int mains = p.main_first[p.batch];
     const bool tail = item >= mains;
-    const int32_t* first = tail ? p.tail_first : p.main_first;
     const int index = tail ? item - mains : item;
     // Sequence of the item: the last b with first[b] <= index (a sequence
-    // without items of this kind repeats its predecessor's entry).
-    int b = 0, hi = p.batch - 1;
-    while (b < hi) {
-        const int mid = (b + hi + 1) >> 1;
-        if (first[mid] <= index) b = mid;
-        else hi = mid - 1;
-    }
+    // without items of this kind repeats its predecessor's entry), i.e. the
+    // number of sequences b < batch with first[b] <= index, minus one (first
+    // is non-decreasing and first[0] = 0). On the device lane l loads both
+    // arrays' entry l at once (batch <= kCompactMaxBatch = one wave) and a
+    // ballot counts: one round of loads, where a search would chain several.
+    int b, first_b, next_main, main_b;
+#if defined(__HIP_DEVICE_COMPILE__)
+    static_assert(kCompactMaxBatch <= kWave, "one lane per sequence");
+    const int lane = __lane_id();
+    const bool in_batch = lane < p.batch;
+    const int mf = in_batch ? p.main_first[lane] : 0x7FFFFFFF;
+    const int tf = in_batch ? p.tail_first[lane] : 0x7FFFFFFF;
+    const int f = tail ? tf : mf;
+    b = static_cast<int>(__popcll(__ballot(f <= index))) - 1;
+    first_b = __builtin_amdgcn_readlane(f, b);
+    main_b = __builtin_amdgcn_readlane(mf, b);
+    next_main = b + 1 < p.batch ? __builtin_amdgcn_readlane(mf, b + 1) : mains;
+#else
+    const int32_t* first = tail ? p.tail_first : p.main_first;
+    int count = 0;
+    for (int s = 0; s < p.batch; ++s) count += first[s] <= index;
+    b = count - 1;
+    first_b = first[b];
+    main_b = p.main_first[b];
+    next_main = p.main_first[b + 1];
+#endif
     r.b = b;
     if (!tail) {
-        r.first = index - first[b];
+        r.first = index - first_b;
         r.count = 1;
     } else {
-        r.first = p.main_first[b + 1] - p.main_first[b] + (index - first[b]) * kTailSpan;
+        r.first = next_main - main_b + (index - first_b) * kTailSpan;
         r.count = imin(kTailSpan, p.splits - r.first);
     }
     return r;
@@ -192,7 +244,7 @@ PD_HD WaveWork wave_work(const PartialParams& p, int b, int split, int count, in
     const int capacity = p.table_width << p.page_shift;
     const int len = imax(0, imin(len_raw, capacity));  // decode.cu:42-44
     const int64_t first = static_cast<int64_t>(split) * p.split_tokens;
-    w.dead = first >= len;
+    w.dead = first >= len || count <= 0;  // count 0: an empty item of the grid
     const int tb = static_cast<int>(lmin(first, len));
     const int te = static_cast<int>(lmin(first + static_cast<int64_t>(count) * p.split_tokens, len));
     int per = (te - tb + kQuarters - 1) / kQuarters;
@@ -376,27 +428,67 @@ inline int head_tile(int group, int max_tile) {
 // live ones -- took 17.5 us instead of 14.6: the dead workgroups shift the
 // next sequence's placement so that some CUs hold three live workgroups and
 // others one. (24 splits happened to land evenly again: 15.0 us.)
+//
+// The workgroup shape (plan_mfma) does not follow the launched grid, whose
+// size depends on the reserve (tail items) and on the dead partitions a work
+// list drops: shape_splits is the partitions per sequence the bounds reach
+// (the rectangular grid the shape rules were measured on), live_items the
+// main items. Before this, reserving twice the context of the ragged +
+// shared B16 batch crossed the mid-size-grid limit and took the partition
+// kernel from 33.4 to 44.7 us, and the work list of the reference's ragged
+// B4 L4096 batch lost the mid-size shape (14.7 -> 16.0 us per call).
 inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.compact = 0;
     prm.items = prm.batch * prm.splits;
-    if (length_bounds == nullptr || prm.batch > kCompactMaxBatch) return;
+    prm.main_splits = prm.splits;
+    prm.tail_shift = 0;
+    prm.tail_span = kTailSpan;
+    prm.shape_splits = prm.splits;
+    prm.live_items = prm.items;
+    if (length_bounds == nullptr) return;
     const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
-    int mains[kCompactMaxBatch + 1], tails[kCompactMaxBatch + 1];
-    mains[0] = tails[0] = 0;
-    for (int b = 0; b < prm.batch; ++b) {
+    auto live_of = [&](int b) {
         const int64_t bound = lmin(capacity, length_bounds[b] < 0 ? 0 : length_bounds[b]);
-        const int live = static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
-        mains[b + 1] = mains[b] + live;
-        tails[b + 1] = tails[b] + (prm.splits - live + kTailSpan - 1) / kTailSpan;
+        return static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
+    };
+    int64_t live_total = 0;
+    int longest = 1;
+    for (int b = 0; b < prm.batch; ++b) {
+        const int live = live_of(b);
+        live_total += live;
+        longest = imax(longest, live);
     }
-    const int64_t total = static_cast<int64_t>(mains[prm.batch]) + tails[prm.batch];
-    if (total >= prm.items) return;
-    prm.compact = 1;
-    prm.items = static_cast<int>(total);
-    for (int b = 0; b <= prm.batch; ++b) {
-        prm.main_first[b] = mains[b];
-        prm.tail_first[b] = tails[b];
+    prm.shape_splits = longest;
+    prm.live_items = static_cast<int>(lmin(live_total > 0 ? live_total : 1, prm.items));
+    if (prm.batch <= kCompactMaxBatch && live_total * 2 <= static_cast<int64_t>(prm.batch) * longest) {
+        // Very ragged: the work list.
+        int mains[kCompactMaxBatch + 1], tails[kCompactMaxBatch + 1];
+        mains[0] = tails[0] = 0;
+        for (int b = 0; b < prm.batch; ++b) {
+            const int live = live_of(b);
+            mains[b + 1] = mains[b] + live;
+            tails[b + 1] = tails[b] + (prm.splits - live + kTailSpan - 1) / kTailSpan;
+        }
+        prm.compact = 1;
+        prm.items = mains[prm.batch] + tails[prm.batch];
+        for (int b = 0; b <= prm.batch; ++b) {
+            prm.main_first[b] = mains[b];
+            prm.tail_first[b] = tails[b];
+        }
+        return;
     }
+    if (longest >= prm.splits) return;
+    // Otherwise the rectangular grid of the partitions the bounds reach, then
+    // the tail items in z-slices of their own (at most 65535 slices in all).
+    const int tails = (prm.splits - longest + kTailSpan - 1) / kTailSpan;
+    int shift = 0;
+    while ((1 << shift) < tails) ++shift;
+    const int64_t tail_items = static_cast<int64_t>(prm.batch) << shift;
+    const int64_t slices = (tail_items + longest - 1) / longest;
+    if (tail_items > (int64_t{1} << 30) || prm.batch + slices > 65535) return;
+    prm.main_splits = longest;
+    prm.tail_shift = shift;
+    prm.items = static_cast<int>(static_cast<int64_t>(prm.batch) * longest + tail_items);
 }
 
 struct Grid {
@@ -408,10 +500,27 @@ inline Grid partial_grid(const PartialParams& prm, int kv_heads) {
     const uint32_t heads = static_cast<uint32_t>((kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg));
     if (prm.compact) return Grid{static_cast<uint32_t>(prm.items) * groups, heads, 1};
     if (prm.row_mode) return Grid{1, heads, static_cast<uint32_t>(prm.batch)};
-    return Grid{static_cast<uint32_t>(prm.splits) * groups, heads, static_cast<uint32_t>(prm.batch)};
+    const uint32_t tail_slices = prm.main_splits < prm.splits
+        ? static_cast<uint32_t>(((static_cast<int64_t>(prm.batch) << prm.tail_shift) + prm.main_splits - 1) /
+                                prm.main_splits)
+        : 0u;
+    return Grid{static_cast<uint32_t>(prm.main_splits) * groups, heads, static_cast<uint32_t>(prm.batch) + tail_slices};
 }
 
 inline int64_t workgroups(const Grid& g) { return static_cast<int64_t>(g.x) * g.y * g.z; }
+
+// Workgroups of `items` partitions in the current workgroup shape.
+inline int64_t item_workgroups(const PartialParams& prm, int kv_heads, int64_t items) {
+    const int64_t groups = kQuarters / prm.quarters_per_wg;
+    const int64_t heads = static_cast<int64_t>(kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg);
+    return items * groups * heads;
+}
+
+// The rectangular grid of shape_splits partitions per sequence, the one the
+// workgroup-shape rules were measured on (see plan_items).
+inline int64_t shape_workgroups(const PartialParams& prm, int kv_heads) {
+    return item_workgroups(prm, kv_heads, static_cast<int64_t>(prm.shape_splits) * prm.batch);
+}
 
 inline int partial_threads(const PartialParams& prm) {
     if (prm.row_mode) return kWave * prm.row_waves;
@@ -486,6 +595,8 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
     prm.mid_grid = 0;
     prm.compact = 0;
     prm.items = prm.batch * prm.splits;
+    prm.main_splits = prm.splits;
+    prm.tail_shift = 0;
 }
 
 // Launch shape of the matrix-core kernel on a device of `cus` compute units,
@@ -523,16 +634,33 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     // uniform in [0, 4096] 37.8 -> 33.3, B32 65.1 -> 59.7; the reference's
     // B16 L4096 batch 47.6 -> 44.0 in the benchmark). At sixteen per CU (a
     // B16 page-32 L8192 batch at split 128) it was flat, so those keep 8.
-    const int64_t wg8 = workgroups(partial_grid(prm, kv_heads));
+    const int64_t wg8 = shape_workgroups(prm, kv_heads);
     if (wg8 * 2 <= cus) {  // small grid
         const int64_t waves_total = wg8 * (partial_threads(prm) / kWave);
         int waves = 4;
         while (waves > 1 && waves_total / waves < 2 * cus) waves /= 2;
         choose_workgroup(prm, kv_heads, kMfmaWorkgroupHeads, waves);
-    } else if (wg8 >= cus && wg8 <= (prm.ragged_lengths ? 8 : 2) * static_cast<int64_t>(cus) &&
+    } else if (wg8 >= cus &&
+               item_workgroups(prm, kv_heads, prm.live_items) <= (prm.ragged_lengths ? 8 : 2) * static_cast<int64_t>(cus) &&
                (kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
         choose_workgroup(prm, kv_heads, 2, 4);
         prm.mid_grid = 1;
+    }
+    // The kernels for grids with tail items or a work list need 129-136 VGPRs
+    // (three waves per SIMD; the plain rectangular one fits 128, four): an
+    // 8-wave workgroup of theirs would hold a CU alone, so they take 4-wave
+    // workgroups. Measured on MI355X, uniform B32 L4096 with twice the
+    // context reserved and host bounds: 120.2 us per call in 8-wave
+    // workgroups; 113.2 us as a plain rectangular grid, dead partitions
+    // included. Forcing those kernels to 128 VGPRs spilled and cost more
+    // elsewhere (ragged + shared B16 40.7 -> 44.9 us).
+    if (grid_kind(prm) != kGridRect && partial_threads(prm) / kWave > 4) {
+        if ((kv_heads == 2 || kv_heads == 4 || kv_heads == 8) && gt <= 8) {
+            choose_workgroup(prm, kv_heads, 2, 4);
+            prm.mid_grid = 1;
+        } else {
+            choose_workgroup(prm, kv_heads, kMfmaWorkgroupHeads, 4);
+        }
     }
     // Combining a workgroup's quarters into one state cuts the state stores
     // (written back at the kernel's end) and the merge's reads by qw; its
@@ -542,7 +670,7 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     // smaller tiles were 0.3-0.7 us slower per call. A grid smaller than the
     // CUs leaves the fold's tail exposed (B1 L4096: 12.05 us without, 12.43
     // with), so such launches keep four states per partition.
-    const bool fills_device = workgroups(partial_grid(prm, kv_heads)) >= cus;
+    const bool fills_device = shape_workgroups(prm, kv_heads) >= cus;
     prm.combine = fills_device && (prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16));
     // When the KV heads need several workgroups (kv_heads > heads_per_wg),
     // each workgroup reads one head group's slice of every token row, and

@@ -228,9 +228,13 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
         for (uint32_t by = 0; by < grid.y; ++by) {
             for (uint32_t bx = 0; bx < grid.x; ++bx) {
                 const BlockCoords bc = block_coords(bx, by, bz, p.grid_x, p.grid_y);
-                const PartitionRange r = p.compact ? partition_range<true>(p, bc) : partition_range<false>(p, bc);
+                const int kind = grid_kind(p);
+                const PartitionRange r = kind == kGridList        ? partition_range<kGridList>(p, bc)
+                                         : kind == kGridRectTails ? partition_range<kGridRectTails>(p, bc)
+                                                                  : partition_range<kGridRect>(p, bc);
                 AUDIT(r.b >= 0 && r.b < pr.batch, "sequence %d", r.b);
-                AUDIT(r.first >= 0 && r.count >= 1 && r.first + r.count <= pr.splits && r.count <= kTailSpan,
+                AUDIT(r.first >= 0 && r.count >= 0 && r.first + r.count <= pr.splits && r.count <= kTailSpan &&
+                          r.first < pr.splits,
                       "partition range %d + %d", r.first, r.count);
                 if (r.b < 0 || r.b >= pr.batch) continue;
                 const int b = r.b;
@@ -284,6 +288,7 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                             }
                             if (wave == waves - 1) AUDIT(row_next == row_end, "slices end at %d of %d", row_next, row_end);
                         }
+                        AUDIT(r.count > 0 || w.dead, "an empty grid item is not dead");
                         if (w.dead) {
                             AUDIT(!rows || w.wb == w.we, "dead row wave with tokens");
                             continue;
@@ -422,7 +427,9 @@ bool audit(const Problem& pr, bool rows) {
     std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s, %" PRIu64 " checks: %s\n",
                 (pr.name + (rows ? " [call]" : "")).c_str(), mfma ? "mfma" : "fp32", grid.x, grid.y, grid.z,
                 partial_threads(p) / kWave, p.head_tile, p.quarters_per_wg,
-                p.row_mode ? "whole rows" : p.compact ? "compact" : "rectangular", p.combine ? ", combined" : "",
+                p.row_mode ? "whole rows" : p.compact ? "compact" : p.main_splits < p.splits ? "rectangular+tails"
+                                                                                              : "rectangular",
+                p.combine ? ", combined" : "",
                 g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
     std::fflush(stdout);
     return g_failures == before;

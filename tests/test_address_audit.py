@@ -8,7 +8,8 @@ leave its buffer? -- is answered on the CPU:
   of the partition launches for the measured workloads and the edge cases
   (lengths around page and partition boundaries, invalid page ids, uncommon
   head layouts, a 1M-token context in a 65536-wide table, pages above 4 GiB,
-  compacted work lists with exact, low and zero length bounds) through the
+  work lists and rectangular grids with tail items under exact, low and zero
+  length bounds, whole-row launches) through the
   same ``partition_map.h`` functions the kernels call, and checks every load,
   store and LDS access against its buffer, every live token against the page
   its table entry names, and that every live state slot is written exactly
@@ -47,7 +48,7 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
     assert ", 0 failures" in run.stdout
     # The walk covered the measured workloads and the compacted launches.
     for needle in ("llama3-8b B4 L4096 fp16", "ragged shared B16", "mqa B128", "long mha B1", "compact",
-                   "1M context", "pages above 4 GiB", "invalid page ids fp8"):
+                   "rectangular+tails", "whole rows", "1M context", "pages above 4 GiB", "invalid page ids fp8"):
         assert needle in run.stdout, needle
 
 

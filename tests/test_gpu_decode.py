@@ -269,6 +269,40 @@ def test_ragged_lengths_hint(batch, query_heads, kv_heads):
     torch.testing.assert_close(hinted, plain, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("batch,q_dtype,kv_dtype", [
+    (32, torch.float16, None),                  # 2048 eight-wave workgroups: eight per CU, the rule's top
+    (16, torch.bfloat16, None),
+    (16, torch.float16, torch.float8_e4m3fn),
+    (16, torch.bfloat16, torch.float8_e5m2),
+])
+def test_ragged_lengths_hint_formats(batch, q_dtype, kv_dtype):
+    """The ragged-lengths hint at the top of its range (eight 8-wave workgroups per
+    CU) and with BF16 and FP8 K/V: hinted (2-head x 2-quarter workgroups) and plain
+    (8-wave) launches both match the FP64 oracle on the device's exact values and
+    agree with each other to FP32 rounding."""
+    from test_gpu_formats import quantized
+
+    announce(f"ragged-lengths hint B{batch} q={q_dtype} kv={kv_dtype}")
+    width, page = 256, 16
+    layout = Layout(batch, 32, 8, 128, page, batch * width)
+    rng = np.random.default_rng(60 + batch)
+    table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+    lengths = rng.integers(0, width * page + 1, size=batch).astype(np.int32)
+    lengths[0] = width * page
+    for b, n in enumerate(lengths):
+        table[b, (n + page - 1) // page:] = -1
+    (q, k, v), (k_scale, v_scale), exact = quantized(layout, q_dtype, kv_dtype, seed=batch)
+    expected = dense_attention(*exact, table, lengths)
+    plan = DecodePlan(layout, table, lengths, split_tokens=256)
+    assert plan._ragged_lengths and plan.launches(q.dtype, k.dtype) == 2
+    hinted = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).clone()
+    assert_parity(hinted.cpu().numpy(), expected, torch.float16)
+    plan._ragged_lengths = False
+    plain = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale)
+    assert_parity(plain.cpu().numpy(), expected, torch.float16)
+    torch.testing.assert_close(hinted, plain, rtol=1e-5, atol=1e-6)
+
+
 def test_plan_derives_the_page_sharing_hint():
     """The plan streams K/V past the caches only when its table maps no page
     twice: the shared-prefix workload keeps them cacheable, the Llama-3-8B one
