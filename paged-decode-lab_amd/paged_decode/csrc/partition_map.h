@@ -29,11 +29,12 @@ constexpr int kQuarters = 4;     // states per partition (quarters of the partit
 constexpr int kTileTokens = 16;  // tokens per matrix-core tile
 
 // Compacted work lists are passed in the kernel arguments for batches of up
-// to kCompactMaxBatch sequences; each tail item covers up to kTailSpan of the
-// partitions a sequence may reach only after device-side appends, as one
-// partition of kTailSpan times the tokens.
+// to kCompactMaxBatch sequences. A tail item covers tail_span (at least
+// kTailSpan) of the partitions a sequence may reach only after device-side
+// appends, as one partition of tail_span times the tokens.
 constexpr int kCompactMaxBatch = 64;
-constexpr int kTailSpan = 8;
+constexpr int kTailSpan = 8;      // partitions per tail item, at least
+constexpr int kMaxTailItems = 4;  // tail items per sequence, at most (wider spans above that)
 
 PD_HD int imin(int a, int b) { return a < b ? a : b; }
 PD_HD int imax(int a, int b) { return a > b ? a : b; }
@@ -81,7 +82,7 @@ struct PartialParams {
     // main_first[b + 1] - main_first[b] of them, partitions 0, 1, ... one
     // each -- and then the tail items, again in sequence order: sequence b's
     // tail_first[b + 1] - tail_first[b] tail items, tail item j covering the
-    // kTailSpan partitions after its main ones from j * kTailSpan on (fewer
+    // tail_span partitions after its main ones from j * tail_span on (fewer
     // at the end), which a sequence reaches only if it grew on the device
     // past the host's bound. Main items come first so that the live
     // workgroups are dispatched, and placed on the CUs, as they would be
@@ -211,8 +212,8 @@ PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& 
         r.first = index - first_b;
         r.count = 1;
     } else {
-        r.first = next_main - main_b + (index - first_b) * kTailSpan;
-        r.count = imin(kTailSpan, p.splits - r.first);
+        r.first = next_main - main_b + (index - first_b) * p.tail_span;
+        r.count = imin(p.tail_span, p.splits - r.first);
     }
     return r;
 }
@@ -412,11 +413,12 @@ inline int head_tile(int group, int max_tile) {
     return gt;
 }
 
-// The work list. With per-sequence upper bounds on the lengths known to the
-// caller at launch (length_bounds, host memory; null if unknown) and a batch
-// of at most kCompactMaxBatch, sequence b gets ceil(bound_b / split_tokens)
-// main items and ceil((splits - that) / kTailSpan) tail items, when that is
-// fewer items than the rectangular batch * splits. A bound below the length
+// Grids under host bounds. With per-sequence upper bounds on the lengths
+// known to the caller at launch (length_bounds, host memory; null if
+// unknown), the partitions past sequence b's bound, splits -
+// ceil(bound_b / split_tokens) of them, become at most kMaxTailItems tail
+// items; the partitions before it are the main items, of a rectangular grid
+// or (very ragged batches of at most kCompactMaxBatch) a work list. A bound below the length
 // the kernel finds on the device only moves that sequence's later partitions
 // onto its tail items: results are the same to rounding, the launch slower.
 //
@@ -437,6 +439,14 @@ inline int head_tile(int group, int max_tile) {
 // shared B16 batch crossed the mid-size-grid limit and took the partition
 // kernel from 33.4 to 44.7 us, and the work list of the reference's ragged
 // B4 L4096 batch lost the mid-size shape (14.7 -> 16.0 us per call).
+// Partitions per tail item for a sequence with `reserved` partitions past
+// its bound: kTailSpan, or wider so that it has at most kMaxTailItems. Each
+// dead tail workgroup costs about 1 ns of the launch; a live one (lengths
+// grown past the captured bounds) streams its span in four waves.
+inline int tail_span_for(int reserved) {
+    return imax(kTailSpan, (reserved + kMaxTailItems - 1) / kMaxTailItems);
+}
+
 inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.compact = 0;
     prm.items = prm.batch * prm.splits;
@@ -462,12 +472,15 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.live_items = static_cast<int>(lmin(live_total > 0 ? live_total : 1, prm.items));
     if (prm.batch <= kCompactMaxBatch && live_total * 2 <= static_cast<int64_t>(prm.batch) * longest) {
         // Very ragged: the work list.
+        int shortest = prm.splits;
+        for (int b = 0; b < prm.batch; ++b) shortest = imin(shortest, live_of(b));
+        prm.tail_span = tail_span_for(prm.splits - shortest);
         int mains[kCompactMaxBatch + 1], tails[kCompactMaxBatch + 1];
         mains[0] = tails[0] = 0;
         for (int b = 0; b < prm.batch; ++b) {
             const int live = live_of(b);
             mains[b + 1] = mains[b] + live;
-            tails[b + 1] = tails[b] + (prm.splits - live + kTailSpan - 1) / kTailSpan;
+            tails[b + 1] = tails[b] + (prm.splits - live + prm.tail_span - 1) / prm.tail_span;
         }
         prm.compact = 1;
         prm.items = mains[prm.batch] + tails[prm.batch];
@@ -480,7 +493,8 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     if (longest >= prm.splits) return;
     // Otherwise the rectangular grid of the partitions the bounds reach, then
     // the tail items in z-slices of their own (at most 65535 slices in all).
-    const int tails = (prm.splits - longest + kTailSpan - 1) / kTailSpan;
+    const int span = tail_span_for(prm.splits - longest);
+    const int tails = (prm.splits - longest + span - 1) / span;
     int shift = 0;
     while ((1 << shift) < tails) ++shift;
     const int64_t tail_items = static_cast<int64_t>(prm.batch) << shift;
@@ -488,6 +502,7 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     if (tail_items > (int64_t{1} << 30) || prm.batch + slices > 65535) return;
     prm.main_splits = longest;
     prm.tail_shift = shift;
+    prm.tail_span = span;
     prm.items = static_cast<int>(static_cast<int64_t>(prm.batch) * longest + tail_items);
 }
 

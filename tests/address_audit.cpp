@@ -233,7 +233,7 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                                          : kind == kGridRectTails ? partition_range<kGridRectTails>(p, bc)
                                                                   : partition_range<kGridRect>(p, bc);
                 AUDIT(r.b >= 0 && r.b < pr.batch, "sequence %d", r.b);
-                AUDIT(r.first >= 0 && r.count >= 0 && r.first + r.count <= pr.splits && r.count <= kTailSpan &&
+                AUDIT(r.first >= 0 && r.count >= 0 && r.first + r.count <= pr.splits && r.count <= p.tail_span &&
                           r.first < pr.splits,
                       "partition range %d + %d", r.first, r.count);
                 if (r.b < 0 || r.b >= pr.batch) continue;
