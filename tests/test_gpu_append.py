@@ -115,6 +115,55 @@ def test_captured_decode_loop_append_then_attend(merge):
     assert host_lengths.tolist() == [106, 7, 256]
 
 
+@pytest.mark.parametrize("lengths0", [[0, 40, 0, 3000], [300, 290, 280, 310]], ids=["work-list", "rectangular-tails"])
+def test_captured_growth_far_past_the_captured_bounds(lengths0):
+    """A graph captured at short lengths keeps decoding correctly while its appends
+    grow the sequences thousands of tokens past the bounds baked into the capture:
+    the partitions past them run as tail items (at most four per sequence, here 16
+    partitions each) in both grids that carry them, the work list (very ragged
+    lengths) and the rectangular grid with tail slices."""
+    announce(f"captured growth past the captured bounds, lengths {lengths0}")
+    layout = Layout(4, 8, 2, 128, 16, 4 * 512)
+    rng = np.random.default_rng(11)
+    table = rng.permutation(4 * 512).reshape(4, 512).astype(np.int32)
+    lengths = np.array(lengths0, dtype=np.int32)
+    plan = DecodePlan(layout, table, lengths, split_tokens=128, max_context=8192)
+    assert plan.splits == 64 and plan.launches(torch.float16) == 2
+    q, k, v = make_tensors(layout, seed=78)
+    tokens = 512
+    q_step = torch.empty_like(q)
+    k_step = torch.empty((4, tokens, 2, 128), device="cuda", dtype=torch.float16)
+    v_step = torch.empty_like(k_step)
+    plan.run(q, k, v)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            plan.append(k, v, k_step, v_step)
+            out = plan.run(q_step, k, v)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    host_k, host_v = (t.cpu().numpy() for t in (k, v))
+    host_lengths = lengths.copy()
+    for step in range(8):
+        qs = rng.standard_normal(q.shape).astype(np.float16)
+        ks = rng.standard_normal(k_step.shape).astype(np.float16)
+        vs = rng.standard_normal(v_step.shape).astype(np.float16)
+        q_step.copy_(torch.from_numpy(qs))
+        k_step.copy_(torch.from_numpy(ks))
+        v_step.copy_(torch.from_numpy(vs))
+        graph.replay()
+        torch.cuda.synchronize()
+        host_k, _ = fp64.append_advance(host_k, table, host_lengths, ks, max_context=8192)
+        host_v, host_lengths = fp64.append_advance(host_v, table, host_lengths, vs, max_context=8192)
+        expected = fp64.dense_attention(qs, host_k, host_v, table, host_lengths)
+        assert_parity(out.cpu().numpy(), expected, torch.float16)
+        np.testing.assert_array_equal(plan._lengths.cpu().numpy(), host_lengths)
+    assert (host_lengths == np.array(lengths0) + 8 * tokens).all()
+
+
 @pytest.mark.parametrize("max_context", [None, 132])
 def test_captured_appends_stop_at_the_reserved_context(max_context):
     """Appends never grow a sequence past the context the plan's partitions
