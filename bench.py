@@ -37,15 +37,16 @@ Protocol
 
 Prints one JSON line. The record also carries the provenance the reference's
 report keeps (benchmarks/bench_decode.py:47-63,137-170): git revision and
-dirty flag (null where the tree has no git metadata), library build digests,
+dirty flag (in a copy without git metadata, those the native libraries were
+built from, as the build recorded them), library build digests,
 the software environment, a device snapshot before and after the timed
 protocol (clocks, activity, temperature and power read from the amdgpu sysfs
 files, or "unavailable"), the raw per-repetition samples and the trial order
-of the 30 x 20 protocol, and steady-state device memory. bench.py starts no
-child process: under rocprofv3 every process it started would itself load
-the profiler and open the GPU. The git revision is read from .git's files;
-the dirty flag needs git and is computed only before the GPU is touched and
-only when no profiler is loaded.
+of the 30 x 20 protocol, and steady-state device memory. Under a profiler
+bench.py starts no child process: under rocprofv3 every process it started
+would itself load the profiler and open the GPU. The git revision is read
+from .git's files; the dirty flag needs a git process and is computed only
+before the GPU is touched and only when no profiler is loaded.
 --output PATH also writes the record, indented, to a new file (an existing
 file is never overwritten).
 """
@@ -56,7 +57,6 @@ import math
 import os
 import platform
 import random
-import subprocess
 import sys
 import time
 from pathlib import Path
@@ -118,41 +118,28 @@ def profiler_loaded():
             or any(k.startswith(("ROCPROF", "ROCP_")) for k in os.environ))
 
 
-def git_head():
-    """Commit of this tree's HEAD, read from .git's files (no git process), or None."""
-    git = REPO / ".git"
-    try:
-        head = (git / "HEAD").read_text().strip()
-        if not head.startswith("ref: "):
-            return head
-        ref = head[5:]
-        if (git / ref).exists():
-            return (git / ref).read_text().strip()
-        for line in (git / "packed-refs").read_text().splitlines():
-            if line.endswith(" " + ref):
-                return line.split()[0]
-    except OSError:
-        pass
-    return None
-
-
 def revision():
-    """git commit and dirty flag of this tree (nulls where there is no git metadata).
+    """git commit and dirty flag of this tree; in a copy without git metadata,
+    the commit and dirty flag the native libraries were built from (recorded
+    by the build next to them), with whether those sources match the tree's.
 
     Call before the GPU is initialised: the dirty flag needs a git child
     process, which is started only then and only without a profiler loaded.
     """
-    sha = git_head()
+    from paged_decode import _build
+
+    sha = _build.git_head()
     if sha is None:
-        return {"sha": None, "dirty": None, "note": "no git metadata in this tree"}
+        info = _build.build_info()
+        if info is None:
+            return {"sha": None, "dirty": None, "note": "no git metadata in this tree and no build record"}
+        return {"sha": info.get("sha"), "dirty": info.get("dirty"), "source": "build record",
+                "built_utc": info.get("built_utc"),
+                "build_sources_match_tree": info.get("source_digest") == _build.source_digest(),
+                "note": "no git metadata in this tree: the revision the native libraries were built from"}
     if profiler_loaded():
         return {"sha": sha, "dirty": None, "note": "dirty flag not computed under a profiler"}
-    try:
-        dirty = bool(subprocess.check_output(["git", "status", "--porcelain", "--untracked-files=no"], cwd=REPO,
-                                             text=True, stderr=subprocess.DEVNULL, timeout=10).strip())
-    except (OSError, subprocess.SubprocessError):
-        dirty = None
-    return {"sha": sha, "dirty": dirty}
+    return {"sha": sha, "dirty": _build.git_dirty(REPO)}
 
 
 def rocm_version():

@@ -22,6 +22,7 @@ REPO = PACKAGE.parent.parent
 INCLUDE = REPO / "include"
 HIP_LIBRARY = PACKAGE / "libpaged_decode_hip.so"
 EXTENSION = PACKAGE / "_C.so"
+BUILD_INFO = PACKAGE / "_build_info.json"  # git revision and source digest of the last build
 ARCH = os.environ.get("PAGED_DECODE_ARCH", "gfx950")
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
@@ -112,9 +113,64 @@ def build_extension(verbose=False):
     return EXTENSION
 
 
+def git_head(repo=REPO):
+    """Commit of the repository's HEAD, read from .git's files (no git process), or None."""
+    git = Path(repo) / ".git"
+    try:
+        head = (git / "HEAD").read_text().strip()
+        if not head.startswith("ref: "):
+            return head
+        ref = head[5:]
+        if (git / ref).exists():
+            return (git / ref).read_text().strip()
+        for line in (git / "packed-refs").read_text().splitlines():
+            if line.endswith(" " + ref):
+                return line.split()[0]
+    except OSError:
+        pass
+    return None
+
+
+def git_dirty(repo=REPO):
+    """True when tracked files differ from HEAD, None when git cannot tell."""
+    try:
+        status = subprocess.check_output(["git", "status", "--porcelain", "--untracked-files=no"], cwd=repo,
+                                         text=True, stderr=subprocess.DEVNULL, timeout=10)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return bool(status.strip())
+
+
+def write_build_info():
+    """Record which revision and sources the libraries were built from, next to
+    them (a copy of the tree without .git, e.g. on another machine, keeps it)."""
+    import json
+    from datetime import datetime, timezone
+
+    sha = git_head()
+    info = {"sha": sha, "dirty": git_dirty() if sha else None, "source_digest": source_digest(),
+            "built_utc": datetime.now(timezone.utc).isoformat(timespec="seconds")}
+    tmp = _atomic_output(BUILD_INFO)
+    tmp.write_text(json.dumps(info, indent=1) + "\n")
+    os.replace(tmp, BUILD_INFO)
+    return info
+
+
+def build_info():
+    """The record write_build_info left, or None."""
+    import json
+
+    try:
+        return json.loads(BUILD_INFO.read_text())
+    except (OSError, ValueError):
+        return None
+
+
 def build(verbose=False):
-    """Compile both libraries; returns their paths."""
-    return build_hip_library(verbose), build_extension(verbose)
+    """Compile both libraries and record their revision; returns their paths."""
+    paths = build_hip_library(verbose), build_extension(verbose)
+    write_build_info()
+    return paths
 
 
 def built():

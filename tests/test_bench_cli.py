@@ -29,3 +29,43 @@ def test_existing_output_file_is_never_overwritten(tmp_path):
 def test_invalid_step_counts_are_refused():
     assert run_bench("--steps", "0").returncode == 2
     assert run_bench("--warmup", "-1").returncode == 2
+
+
+def load_bench():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_under_test", REPO / "bench.py")
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+def test_revision_without_git_metadata_reports_the_build_record(monkeypatch, tmp_path):
+    """A copy of the tree without .git (as shipped to a GPU host) reports the
+    commit and dirty flag the native libraries were built from."""
+    bench = load_bench()
+    from paged_decode import _build
+
+    record = tmp_path / "_build_info.json"
+    monkeypatch.setattr(_build, "BUILD_INFO", record)
+    monkeypatch.setattr(_build, "git_head", lambda repo=None: None)
+    assert bench.revision()["sha"] is None  # no record yet
+    record.write_text('{"sha": "0123abcd", "dirty": false, "source_digest": "%s", "built_utc": "t"}'
+                      % _build.source_digest())
+    rev = bench.revision()
+    assert rev["sha"] == "0123abcd" and rev["dirty"] is False and rev["build_sources_match_tree"] is True
+    record.write_text('{"sha": "0123abcd", "dirty": true, "source_digest": "stale", "built_utc": "t"}')
+    rev = bench.revision()
+    assert rev["dirty"] is True and rev["build_sources_match_tree"] is False
+
+
+def test_build_record_names_this_checkout(monkeypatch, tmp_path):
+    """The record a build writes: this checkout's HEAD (None without git metadata) and the sources' digest."""
+    from paged_decode import _build
+
+    monkeypatch.setattr(_build, "BUILD_INFO", tmp_path / "_build_info.json")
+    info = _build.write_build_info()
+    assert _build.build_info() == info
+    assert info["sha"] == _build.git_head() and info["source_digest"] == _build.source_digest()
+    if info["sha"] is not None:
+        assert len(info["sha"]) == 40 and info["dirty"] in (True, False, None)
