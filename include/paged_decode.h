@@ -105,7 +105,11 @@ enum pd_hint { PD_HINT_NONE = 0, PD_HINT_UNSHARED_PAGES = 1, PD_HINT_RAGGED_LENG
  * folds a row's states in LDS and writes out itself, and numerator/stats
  * are left unwritten (they remain required arguments, the workspace of the
  * reference's plan). Results agree with the two-launch path to FP32
- * rounding; pd_decode_launch_count says which a call takes.
+ * rounding; pd_decode_launch_count says which a call takes. On grids with
+ * many waves per CU the two launches run over coarser partitions, a power
+ * of two times split_tokens, whose fewer states the workspace holds
+ * (pd_decode_kernel_split says which); the workspace's contents are
+ * internal to the call.
  * Replaces the native entry `decode(q, k, v, table, lengths, numerator, stats,
  * out, split_tokens, merge_mode)` of reference
  * src/paged_decode/csrc/bindings.cpp:3-9 / decode.cu:197-246, with the tensor
@@ -294,6 +298,24 @@ int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads
                            int page_size, int table_width, int physical_pages, int splits, int split_tokens,
                            int hints, int* launches);
 
+/*
+ * Partitions the two launches of pd_decode / pd_decode_ex / pd_decode_scratch
+ * run over for a call of these formats, shapes and host length bounds (NULL:
+ * unknown) on a device of compute_units CUs (<= 0: the current device's):
+ * *kernel_splits partitions of *kernel_split_tokens tokens per row, with
+ * kernel_split_tokens = c * split_tokens for a power of two c and
+ * kernel_splits = ceil(splits / c) (c = 1 for whole-row calls and FP32
+ * inputs). A caller that runs the stages itself (pd_decode_partial_ex, then
+ * pd_decode_merge) passes these two values to both to match the full call's
+ * partitioning. Returns a status (the checks of pd_decode_ex). No
+ * counterpart in the reference, whose partition count is the caller's
+ * (decode.cu:170-194).
+ */
+int pd_decode_kernel_split(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                           int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                           const int32_t* length_bounds, int compute_units, int* kernel_splits,
+                           int* kernel_split_tokens);
+
 /* Static description of a status code (never NULL). */
 const char* pd_status_string(int status);
 
@@ -305,9 +327,10 @@ const char* pd_status_string(int status);
  * combined, the others as empty states; 10: hints argument of the _ex
  * entries; 11: PD_HINT_RAGGED_LENGTHS; 12: max_context argument of
  * pd_append_kv_advance, length_bounds argument of the _ex entries; 13: whole-row launches of small rows,
- * pd_decode_launch_count). PD_ABI_VERSION is the value this header describes;
- * a binding compares it with what the loaded library returns. */
-#define PD_ABI_VERSION 13
+ * pd_decode_launch_count; 14: coarser partitions for full calls on large
+ * grids, pd_decode_kernel_split). PD_ABI_VERSION is the value this header
+ * describes; a binding compares it with what the loaded library returns. */
+#define PD_ABI_VERSION 14
 int pd_abi_version(void);
 
 #ifdef __cplusplus

@@ -46,6 +46,7 @@ PROTOTYPES = {
     "pd_table_from_csr": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 4 + [_P]),
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
     "pd_decode_launch_count": (_I, [_I] * 12 + [_P]),
+    "pd_decode_kernel_split": (_I, [_I] * 11 + [_P, _I, _P, _P]),
     "pd_status_string": (ctypes.c_char_p, [_I]),
     "pd_abi_version": (_I, []),
 }
@@ -77,3 +78,24 @@ def launch_count(lib, q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim,
     if status != PD_OK:
         raise ValueError(status_string(lib, status))
     return launches.value
+
+
+def kernel_split(lib, q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size, table_width,
+                 physical_pages, splits, split_tokens, length_bounds=None, compute_units=0):
+    """(partitions, tokens per partition) of a full decode call's two launches:
+    the caller's (splits, split_tokens), or a coarser split on large grids.
+    length_bounds: None or host int32 upper bounds on the lengths [batch].
+    Raises ValueError with the library's message for shapes it rejects."""
+    import numpy as np
+
+    bounds = None
+    if length_bounds is not None:
+        bounds = np.ascontiguousarray(length_bounds, dtype=np.int32)
+    splits_out, tokens_out = ctypes.c_int(0), ctypes.c_int(0)
+    status = lib.pd_decode_kernel_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
+                                        table_width, physical_pages, splits, split_tokens,
+                                        None if bounds is None else bounds.ctypes.data, compute_units,
+                                        ctypes.byref(splits_out), ctypes.byref(tokens_out))
+    if status != PD_OK:
+        raise ValueError(status_string(lib, status))
+    return splits_out.value, tokens_out.value

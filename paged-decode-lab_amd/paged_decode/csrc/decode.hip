@@ -692,6 +692,15 @@ float* scratch_address() {
     return ptr;
 }
 
+// Partitions the two launches of a full decode call run over: the caller's
+// split for FP32 inputs and whole-row calls, else coarse_split's.
+KernelSplit call_split(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                       int page_size, int table_width, int splits, int split_tokens, const int32_t* length_bounds,
+                       int cus) {
+    return full_call_split(q_dtype == PD_DTYPE_F32, element_size(kv_dtype), batch, query_heads, kv_heads, head_dim,
+                           page_size, table_width, splits, split_tokens, length_bounds, cus);
+}
+
 // The scratch holds numerator [B, Hq, 4 * splits, D] at offset 0 and stats
 // [B, Hq, 4 * splits, 2] after it, at the next 256-byte boundary.
 size_t scratch_stats_offset(int batch, int query_heads, int head_dim, int splits) {
@@ -751,13 +760,17 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
     if (status == PD_OK) status = check_hints(hints);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    // Both launches run over the same partitions, at most `splits` of them
+    // per row, so the states fit the caller's workspace.
+    const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
+                                      table_width, splits, split_tokens, length_bounds, device_compute_units());
     int stride = 1;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
-                         query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                         split_tokens, hints, length_bounds, s, out, &stride);
+                         query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, ks.splits,
+                         ks.split_tokens, hints, length_bounds, s, out, &stride);
     if (status != PD_OK || stride == 0) return status;
-    return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, splits,
-                     split_tokens, merge_mode, stride, s);
+    return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, ks.splits,
+                     ks.split_tokens, merge_mode, stride, s);
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -856,6 +869,27 @@ int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads
     if (q_dtype == PD_DTYPE_F32) plan_fp32(prm, kv_heads, head_dim);
     else plan_mfma(prm, kv_heads, device_compute_units(), head_dim, element_size(kv_dtype));
     *launches = prm.row_mode ? 1 : 2;
+    return PD_OK;
+}
+
+int pd_decode_kernel_split(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                           int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                           const int32_t* length_bounds, int compute_units, int* kernel_splits,
+                           int* kernel_split_tokens) {
+    if (!kernel_splits || !kernel_split_tokens) return PD_ERR_NULL_POINTER;
+    const char* const stand_in = reinterpret_cast<const char*>(alignof(float));
+    float* const f_stand_in = reinterpret_cast<float*>(alignof(float));
+    const int status = check_common(stand_in, q_dtype, stand_in, stand_in, kv_dtype, 1.0f, 1.0f,
+                                    reinterpret_cast<const int32_t*>(stand_in),
+                                    reinterpret_cast<const int32_t*>(stand_in), f_stand_in, f_stand_in, batch,
+                                    query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                                    split_tokens);
+    if (status != PD_OK) return status;
+    const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
+                                      table_width, splits, split_tokens, length_bounds,
+                                      compute_units > 0 ? compute_units : device_compute_units());
+    *kernel_splits = ks.splits;
+    *kernel_split_tokens = ks.split_tokens;
     return PD_OK;
 }
 

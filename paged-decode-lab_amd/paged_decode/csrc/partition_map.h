@@ -581,6 +581,90 @@ inline int mfma_lds_bytes(const PartialParams& prm, int head_dim, int elem) {
 constexpr int64_t kRowMaxBytes = 128 * 1024;
 constexpr int kRowWaveTokens = 16;
 
+// Whether a call's rows -- min(splits * split_tokens, table capacity) tokens
+// of K and V per (sequence, KV head), elem bytes per element -- are small
+// enough for a whole-row launch.
+inline bool rows_fit_one_launch(int64_t splits, int64_t split_tokens, int64_t capacity, int head_dim, int elem) {
+    const int64_t span = lmin(splits * split_tokens, capacity);
+    return span * head_dim * elem * 2 <= kRowMaxBytes;
+}
+
+// Coarser partitions for a whole decode call on a large grid. The caller's
+// split_tokens sizes the workspace (four states per partition) and is what
+// the separate partition and merge entries use; a whole call (partition
+// launch, then merge launch, both internal) may instead run over partitions
+// of c x split_tokens tokens, c a power of two, which need ceil(splits / c)
+// partitions per row: fewer states, so the caller's workspace holds them.
+// The attention does not depend on the partitioning; results agree to FP32
+// rounding. Longer partitions mean longer waves, so the per-wave latencies
+// (page ids and first K/V loads, the last tile, the state stores) and the
+// merge's states weigh less per byte -- while the grid keeps enough waves to
+// cover the device. c doubles while a wave would read at most
+// kCoarseWaveBytes of K and V and the live partitions (as far as the host
+// bounds tell; all of them without bounds) still give kCoarseWavesPerCu
+// waves per CU. Measured on MI355X (decode call, us, graph of 200 calls, K/V
+// rotated over 2 GiB; the split the rule picks in brackets):
+//   ragged + shared-prefix B16, page 32, split 128: 40.8 -> 31.9 [512]
+//     (1024: 32.5, 2048: 37.7);
+//   uniform B16 / B32 L4096, 8 KV heads, split 256: 53.6 -> 48.0 [1024] /
+//     102.6 -> 90.6 [1024]; B64 L2048: 101.6 -> 91.3 [1024];
+//   FP8 K/V B16 L4096: 36.6 -> 32.4 [1024]; MQA B512 L1024 D64: 36.8 ->
+//     32.7 [1024];
+//   the reference's B16 L4096 batch: 44.3 -> 41.1 [512] (1024: 39.3);
+//   32K-context MHA at split 128: 93.3 -> 85.7 [1024];
+//   grids of at most eight waves per CU keep their split: doubling it made
+//     the Llama-3-8B B4 L4096 FP8 call 14.8 -> 17.9, MQA B128 L1024 14.1 ->
+//     16.3, the reference's B4 batch 14.7 -> 16.2 (FP16 Llama-3-8B: 17.4 ->
+//     17.2).
+// Whole-row calls and FP32 inputs keep the caller's split.
+constexpr int64_t kCoarseWaveBytes = 128 * 1024;
+constexpr int kCoarseWavesPerCu = 8;
+
+struct KernelSplit {
+    int splits, split_tokens;
+};
+
+inline KernelSplit coarse_split(int batch, int kv_heads, int head_tiles, int head_dim, int elem, int page_size,
+                                int table_width, int splits, int split_tokens, const int32_t* length_bounds,
+                                int cus) {
+    const int64_t capacity = static_cast<int64_t>(table_width) * page_size;
+    // Tokens the caller's partitions reach; no partition of a coarser split goes past them.
+    const int64_t reach = lmin(static_cast<int64_t>(splits) * split_tokens, capacity);
+    auto waves = [&](int64_t span) {
+        int64_t parts = 0;
+        for (int b = 0; b < batch; ++b) {
+            const int64_t bound = length_bounds ? lmin(reach, length_bounds[b] < 0 ? 0 : length_bounds[b]) : reach;
+            parts += (bound + span - 1) / span;
+        }
+        return parts * kQuarters * kv_heads * head_tiles;
+    };
+    int c = 1;
+    while (2 * c <= splits) {
+        const int64_t span = static_cast<int64_t>(split_tokens) * 2 * c;
+        if (span > (int64_t{1} << 20)) break;
+        if ((span + kQuarters - 1) / kQuarters * head_dim * elem * 2 > kCoarseWaveBytes) break;
+        if (waves(span) < static_cast<int64_t>(kCoarseWavesPerCu) * cus) break;
+        c *= 2;
+    }
+    return KernelSplit{(splits + c - 1) / c, split_tokens * c};
+}
+
+// The partitions of a full decode call's two launches: coarse_split's for a
+// matrix-core call (16-bit q) that is not a whole-row launch, else the
+// caller's. kv_elem: bytes per stored K/V element.
+inline KernelSplit full_call_split(bool fp32, int kv_elem, int batch, int query_heads, int kv_heads, int head_dim,
+                                   int page_size, int table_width, int splits, int split_tokens,
+                                   const int32_t* length_bounds, int cus) {
+    const KernelSplit same{splits, split_tokens};
+    if (fp32 || rows_fit_one_launch(splits, split_tokens, static_cast<int64_t>(table_width) * page_size, head_dim,
+                                    kv_elem))
+        return same;
+    const int group = query_heads / kv_heads;
+    const int gt = head_tile(group, 16);
+    return coarse_split(batch, kv_heads, (group + gt - 1) / gt, head_dim, kv_elem, page_size, table_width, splits,
+                        split_tokens, length_bounds, cus);
+}
+
 // Bytes of one whole-row LDS slot of the FP32 kernel (per-head max and
 // denominator, and the head tile's accumulators, GT <= 8).
 constexpr int row_slot_bytes_fp32(int head_dim) { return (2 * 8 + 8 * head_dim) * 4; }
@@ -597,8 +681,8 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
     prm.row_mode = 0;
     if (!prm.row_allowed) return;
     const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
+    if (!rows_fit_one_launch(prm.splits, prm.split_tokens, capacity, head_dim, elem)) return;
     const int64_t span = lmin(static_cast<int64_t>(prm.splits) * prm.split_tokens, capacity);
-    if (span * head_dim * elem * 2 > kRowMaxBytes) return;
     int waves = static_cast<int>(lmin(max_waves, (span + kRowWaveTokens - 1) / kRowWaveTokens));
     while (waves > 1 && waves * (slot_bytes + stage_bytes) > 160 * 1024) --waves;
     prm.row_mode = 1;

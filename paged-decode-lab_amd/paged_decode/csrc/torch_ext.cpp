@@ -278,6 +278,25 @@ int64_t launch_count(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t ba
     return launches;
 }
 
+// Partitions (count, tokens per partition) decode's two launches run over for
+// these formats, shapes and optional host length bounds: the caller's split
+// or a coarser one (see pd_decode_kernel_split).
+std::tuple<int64_t, int64_t> kernel_split(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t batch,
+                                          int64_t query_heads, int64_t kv_heads, int64_t head_dim,
+                                          int64_t page_size, int64_t table_width, int64_t physical_pages,
+                                          int64_t splits, int64_t split_tokens,
+                                          c10::optional<torch::Tensor> length_bounds, int64_t compute_units) {
+    const int32_t* bounds = bounds_pointer(length_bounds, batch);
+    int kernel_splits = 0, kernel_split_tokens = 0;
+    check_status(pd_decode_kernel_split(dtype_code(q_dtype), dtype_code(kv_dtype), static_cast<int>(batch),
+                                        static_cast<int>(query_heads), static_cast<int>(kv_heads),
+                                        static_cast<int>(head_dim), static_cast<int>(page_size),
+                                        static_cast<int>(table_width), static_cast<int>(physical_pages),
+                                        static_cast<int>(splits), static_cast<int>(split_tokens), bounds,
+                                        static_cast<int>(compute_units), &kernel_splits, &kernel_split_tokens));
+    return {kernel_splits, kernel_split_tokens};
+}
+
 PYBIND11_MODULE(_C, m) {
     m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
@@ -301,6 +320,11 @@ PYBIND11_MODULE(_C, m) {
                                                        static_cast<int>(d), static_cast<int>(s)));
     });
     m.def("launch_count", &launch_count, "Kernel launches of a decode call (1: whole rows, 2: partition + merge)");
+    m.def("kernel_split", &kernel_split, "Partitions (count, tokens) a decode call's launches run over",
+          py::arg("q_dtype"), py::arg("kv_dtype"), py::arg("batch"), py::arg("query_heads"), py::arg("kv_heads"),
+          py::arg("head_dim"), py::arg("page_size"), py::arg("table_width"), py::arg("physical_pages"),
+          py::arg("splits"), py::arg("split_tokens"), py::arg("length_bounds") = py::none(),
+          py::arg("compute_units") = 0);
     m.def("abi_version", &pd_abi_version, "ABI version the loaded HIP library reports");
     m.def("header_abi_version", [] { return PD_ABI_VERSION; }, "ABI version of the header this module was built with");
     m.def("build_digest", [] { return std::string(PD_BUILD_DIGEST); }, "Digest of the sources this module was built from");

@@ -121,6 +121,8 @@ class DecodePlan:
         self._stats = torch.empty((*shape, 2), device=self.device, dtype=torch.float32)
         self._out = torch.empty((layout.batch, layout.query_heads, layout.head_dim),
                                 dtype=torch.float32, device=self.device)
+        self._stage_views = {}
+        self._staged_split = (self.splits, split_tokens)
         self._extension = load_extension()
 
     @classmethod
@@ -261,23 +263,55 @@ class DecodePlan:
                                             self._table.shape[1], layout.physical_pages, self.splits,
                                             self.split_tokens, self._unshared_pages, self._ragged_lengths)
 
+    def kernel_split(self, q_dtype, kv_dtype=None):
+        """``(partitions, tokens per partition)`` per row that ``run``'s launches use
+        for q (and K/V) of these dtypes at the current host length bounds: the
+        plan's ``(splits, split_tokens)``, or on grids with many waves per CU a
+        coarser split (a power of two times ``split_tokens``, with fewer
+        partitions, so the workspace holds their states)."""
+        layout = self.layout
+        return self._extension.kernel_split(q_dtype, q_dtype if kv_dtype is None else kv_dtype, layout.batch,
+                                            layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size,
+                                            self._table.shape[1], layout.physical_pages, self.splits,
+                                            self.split_tokens, self._length_bounds())
+
+    def _stage_workspace(self, splits):
+        """Numerator and stats views for ``splits`` partitions per row: the leading
+        part of the workspace buffers, as the full call uses them."""
+        views = self._stage_views.get(splits)
+        if views is None:
+            layout = self.layout
+            shape = (layout.batch, layout.query_heads, splits * _STATES_PER_SPLIT)
+            states = math.prod(shape)
+            views = (self._numerator.view(-1)[:states * layout.head_dim].view(*shape, layout.head_dim),
+                     self._stats.view(-1)[:states * 2].view(*shape, 2))
+            self._stage_views[splits] = views
+        return views
+
     def run_partial(self, q, k, v, *, k_scale=1.0, v_scale=1.0):
         """Partition stage only (fills the workspace with the states; never a
-        whole-row launch); for stage timing."""
+        whole-row launch), over the partitions ``run``'s launches use
+        (``kernel_split``); for stage timing."""
         self._check(q, k, v, k_scale, v_scale)
-        self._extension.partial(q, k, v, self._table, self._lengths, self._numerator, self._stats,
-                                self.split_tokens, float(k_scale), float(v_scale), self._unshared_pages,
-                                self._ragged_lengths, self._length_bounds())
+        splits, split_tokens = self.kernel_split(q.dtype, k.dtype)
+        numerator, stats = self._stage_workspace(splits)
+        self._extension.partial(q, k, v, self._table, self._lengths, numerator, stats, split_tokens,
+                                float(k_scale), float(v_scale), self._unshared_pages, self._ragged_lengths,
+                                self._length_bounds())
+        self._staged_split = (splits, split_tokens)
 
     def _length_bounds(self):
         """Host upper bounds on the device lengths, or None after a device-side CSR refresh."""
         return self._bounds if self._bounds_known else None
 
     def run_merge(self):
-        """Merge stage only, from the current workspace; returns the borrowed output."""
+        """Merge stage only, from the states the last ``run_partial`` left in the
+        workspace (over its partitions); returns the borrowed output."""
         layout = self.layout
-        self._extension.merge(self._numerator, self._stats, self._out, self._lengths, layout.page_size,
-                              self._table.shape[1], self.split_tokens, self._merge_mode)
+        splits, split_tokens = self._staged_split
+        numerator, stats = self._stage_workspace(splits)
+        self._extension.merge(numerator, stats, self._out, self._lengths, layout.page_size, self._table.shape[1],
+                              split_tokens, self._merge_mode)
         return self._out
 
 

@@ -602,6 +602,23 @@ int main(int argc, char** argv) {
         failed += audit(pr, false) ? 0 : 1;
         // The plan for a full decode call, when it is a whole-row launch.
         if (params(pr, 256, pr.q_elem == 2, true).row_mode) failed += audit(pr, true) ? 0 : 1;
+        // A full call over coarser partitions: fewer of them, covering at
+        // least the caller's, their states inside the caller's workspace
+        // (the audited buffers are those of the coarser split, a prefix).
+        const KernelSplit ks = full_call_split(pr.q_elem == 4, pr.kv_elem, pr.batch, pr.q_heads, pr.kv_heads,
+                                               pr.head_dim, pr.page_size, pr.width, pr.splits, pr.split_tokens,
+                                               pr.bounds.empty() ? nullptr : pr.bounds.data(), 256);
+        if (ks.splits != pr.splits || ks.split_tokens != pr.split_tokens) {
+            AUDIT(ks.splits < pr.splits && ks.split_tokens % pr.split_tokens == 0 &&
+                      static_cast<int64_t>(ks.splits) * ks.split_tokens >=
+                          static_cast<int64_t>(pr.splits) * pr.split_tokens,
+                  "coarse split %d x %d for %d x %d", ks.splits, ks.split_tokens, pr.splits, pr.split_tokens);
+            Problem coarse = pr;
+            coarse.name += " coarse x" + std::to_string(ks.split_tokens / pr.split_tokens);
+            coarse.splits = ks.splits;
+            coarse.split_tokens = ks.split_tokens;
+            failed += audit(coarse, true) ? 0 : 1;
+        }
     }
     std::printf("%zu problems, %" PRIu64 " checks, %d failures\n", problems.size(), g_checks, g_failures);
     return failed == 0 ? 0 : 1;

@@ -9,7 +9,8 @@ leave its buffer? -- is answered on the CPU:
   (lengths around page and partition boundaries, invalid page ids, uncommon
   head layouts, a 1M-token context in a 65536-wide table, pages above 4 GiB,
   work lists and rectangular grids with tail items under exact, low and zero
-  length bounds, whole-row launches) through the
+  length bounds, whole-row launches, full calls over the coarser partitions
+  of large grids) through the
   same ``partition_map.h`` functions the kernels call, and checks every load,
   store and LDS access against its buffer, every live token against the page
   its table entry names, and that every live state slot is written exactly
@@ -48,7 +49,9 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
     assert ", 0 failures" in run.stdout
     # The walk covered the measured workloads and the compacted launches.
     for needle in ("llama3-8b B4 L4096 fp16", "ragged shared B16", "mqa B128", "long mha B1", "compact",
-                   "rectangular+tails", "whole rows", "1M context", "pages above 4 GiB", "invalid page ids fp8"):
+                   "rectangular+tails", "whole rows", "1M context", "pages above 4 GiB", "invalid page ids fp8",
+                   "ragged shared B16 T32 split 128 coarse x8", "bounds=half coarse x4",
+                   "long mha B1 Hq32/32 L32768 split 128 coarse x8"):
         assert needle in run.stdout, needle
 
 

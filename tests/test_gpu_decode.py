@@ -190,8 +190,10 @@ def test_many_long_rows_and_reserved_context(dim, merge):
     """256 rows of up to 512 live states (split 16), in a plan sized for the
     longest sequence and in one reserving twice that: rows of more than 256
     states merged in several load rounds across a grid larger than the
-    device's CUs. Both plans match the oracle and each other bit for bit
-    (the reserved partitions are never written or read)."""
+    device's CUs. Both plans match the oracle and each other to FP32
+    rounding: the reserved partitions are never written or read, but the
+    call runs over coarser partitions (kernel_split) and the merge kernel's
+    variant follows the allocated states per row, which differ."""
     announce(f"many long rows dim={dim} merge={merge}")
     layout = Layout(16, 16, 4, dim, 16, 16 * 256)
     rng = np.random.default_rng(31)
@@ -206,7 +208,7 @@ def test_many_long_rows_and_reserved_context(dim, merge):
     assert fitted.splits == 128 and reserved.splits == 256
     out = fitted.run(q, k, v).clone()
     assert_parity(out.cpu().numpy(), oracle(q, k, v, table, lengths), torch.float16)
-    torch.testing.assert_close(reserved.run(q, k, v), out, rtol=0, atol=0)
+    torch.testing.assert_close(reserved.run(q, k, v), out, rtol=1e-5, atol=1e-6)
     np.testing.assert_array_equal(out[1].cpu().numpy(), 0.0)
 
 
@@ -370,7 +372,10 @@ def test_nan_poisoned_workspace_live_states_written_dead_states_untouched():
     NaN poison) and never read (the output is finite and matches the oracle).
     This batch fills the device, so its workgroups combine their quarters: the
     slots of the folded quarters get the empty state (statistics written,
-    l == 0) and their numerators, which no merge weights, stay untouched.
+    l == 0) and their numerators, which no merge weights, stay untouched. Its
+    grid is also large enough for the call to run over coarser partitions
+    than the plan's (kernel_split): their states fill the workspace's leading
+    part, laid out by that split, and the rest keeps the poison.
     """
     w = make_workload("ragged_shared_b16")
     layout = w.layout
@@ -379,15 +384,21 @@ def test_nan_poisoned_workspace_live_states_written_dead_states_untouched():
         plan = DecodePlan(layout, w.table, w.lengths, split_tokens=w.split_tokens, merge=merge)
         for t in (plan._numerator, plan._stats, plan._out):
             t.fill_(float("nan"))
-        announce(f"nan-poison ragged_shared_b16 merge={merge}")
+        splits, split_tokens = plan.kernel_split(q.dtype)
+        announce(f"nan-poison ragged_shared_b16 merge={merge}, kernel split {splits} x {split_tokens}")
         out = plan.run(q, k, v)
         torch.cuda.synchronize()
         assert torch.isfinite(out).all()
         assert_parity(out.cpu().numpy(), oracle(q, k, v, w.table, w.lengths), torch.float16)
-        num, st = plan._numerator.cpu().numpy(), plan._stats.cpu().numpy()
+        shape = (layout.batch, layout.query_heads, 4 * splits)
+        used = int(np.prod(shape))
+        num = plan._numerator.view(-1)[:used * layout.head_dim].view(*shape, layout.head_dim).cpu().numpy()
+        st = plan._stats.view(-1)[:used * 2].view(*shape, 2).cpu().numpy()
+        assert torch.isnan(plan._numerator.view(-1)[used * layout.head_dim:]).all()
+        assert torch.isnan(plan._stats.view(-1)[used * 2:]).all()
         empty_slots = 0
         for b, length in enumerate(w.lengths):
-            live = 4 * -(-int(length) // w.split_tokens)
+            live = 4 * -(-int(length) // split_tokens)
             assert np.isfinite(st[b, :, :live]).all()
             holds = st[b, :, :live, 1] > 0                          # states with tokens
             assert np.isfinite(num[b, :, :live][holds]).all()

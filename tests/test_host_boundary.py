@@ -82,7 +82,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 13
+    assert lib.pd_abi_version() == 14
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
@@ -110,13 +110,71 @@ def test_launch_count_query():
         cabi.launch_count(lib, f32, fp8, 8, 32, 8, 64, 16, 16, 128, 1, 256)
 
 
+
+def test_kernel_split_query():
+    """Full calls on grids of many waves per CU run over coarser partitions (a
+    power of two times split_tokens, at most 128 KB of K and V per wave, at
+    least 8 waves per CU); single-round grids, whole-row calls and FP32 keep
+    the caller's split."""
+    from paged_decode.workload import make_workload
+
+    lib = cabi.load()
+    f32, f16, fp8 = cabi.PD_DTYPE_F32, cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E4M3
+
+    def split(q, kv, b, hq, hkv, d, t, w, p, s, st, bounds=None, cus=256):
+        return cabi.kernel_split(lib, q, kv, b, hq, hkv, d, t, w, p, s, st, bounds, cus)
+
+    # Llama-3-8B B4 L4096 (FP16 and FP8 K/V) and MQA B128 L1024: eight waves per CU at most, kept.
+    assert split(f16, f16, 4, 32, 8, 128, 16, 256, 1024, 16, 256, [4096] * 4) == (16, 256)
+    assert split(f16, fp8, 4, 32, 8, 128, 16, 256, 1024, 16, 256, [4096] * 4) == (16, 256)
+    assert split(f16, f16, 128, 16, 1, 64, 16, 64, 8192, 4, 256, [1024] * 128) == (4, 256)
+    # Uniform B16 L4096: 32 waves per CU at split 256; 128 KB per wave caps it at 1024 tokens.
+    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256, [4096] * 16) == (4, 1024)
+    # FP8 K/V and D64 MQA reach 1024 tokens at 64 KB per wave, where eight waves per CU remain.
+    assert split(f16, fp8, 16, 32, 8, 128, 16, 256, 4096, 16, 256, [4096] * 16) == (4, 1024)
+    assert split(f16, f16, 512, 16, 1, 64, 16, 64, 32768, 4, 256, [1024] * 512) == (1, 1024)
+    # 32K-context MHA at split 128: 128 waves per CU -> 1024-token partitions.
+    assert split(f16, f16, 1, 32, 32, 128, 16, 2048, 2048, 256, 128, [32768]) == (32, 1024)
+    # The ragged + shared-prefix batch at split 128 (host lengths as bounds): 512-token partitions.
+    w = make_workload("ragged_shared_b16")
+    lay = w.layout
+    splits = -(-int(w.lengths.max()) // 128)
+    assert split(f16, f16, lay.batch, lay.query_heads, lay.kv_heads, lay.head_dim, lay.page_size, w.table.shape[1],
+                 lay.physical_pages, splits, 128, w.lengths) == (-(-splits // 4), 512)
+    # Bounds that reach few partitions keep the split; without bounds every partition counts as live.
+    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256, [0] * 16) == (16, 256)
+    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256) == (4, 1024)
+    # Twice the CUs need twice the waves.
+    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256, cus=512) == (8, 512)
+    # FP32 inputs and whole-row calls keep the caller's split.
+    assert split(f32, f32, 16, 32, 8, 128, 16, 256, 4096, 16, 256) == (16, 256)
+    assert split(f16, f16, 4096, 32, 8, 64, 16, 8, 32768, 2, 64) == (2, 64)
+    # Whatever the rule picks, fewer partitions cover at least the caller's tokens.
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        b, hkv = int(rng.integers(1, 65)), int(rng.choice([1, 2, 4, 8, 32]))
+        hq = hkv * int(rng.choice([1, 4, 8, 16]))
+        d, t = int(rng.choice([64, 128])), int(rng.choice([16, 32]))
+        width = int(rng.integers(1, 513))
+        st = int(rng.choice([16, 64, 128, 256, 512, 1000]))
+        s = max(1, -(-width * t // st))
+        kv = int(rng.choice([f16, fp8]))
+        bounds = rng.integers(0, width * t + 1, size=b) if rng.random() < 0.5 else None
+        ks, kst = split(f16, kv, b, hq, hkv, d, t, width, b * width, s, st, bounds)
+        c = kst // st
+        assert kst % st == 0 and c & (c - 1) == 0 and ks == -(-s // c) and ks * kst >= s * st
+        assert c == 1 or (kst // 4) * d * (1 if kv == fp8 else 2) * 2 <= 128 * 1024
+    with pytest.raises(ValueError, match="dimension"):
+        split(f16, f16, 8, 32, 8, 96, 16, 16, 128, 1, 256)
+
+
 C_CONSUMER = r"""
 #include <stdio.h>
 #include <string.h>
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 13) return 1;
+    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 14) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
