@@ -483,7 +483,8 @@ def main():
             "workload": w.name, "batch": L.batch, "query_heads": L.query_heads, "kv_heads": L.kv_heads,
             "head_dim": L.head_dim, "page_size": L.page_size, "context": int(w.lengths.max()),
             "split_tokens": w.split_tokens, "splits": plan.splits, "merge": args.merge, "mode": "hipgraph, K calls per replay",
-            "kv_buffer_sets": sets, "launches_per_call": launches, "parallelism": "single GPU",
+            "kv_buffer_sets": sets, "launches_per_call": launches,
+            "kernel_split_tokens": plan.kernel_split(q.dtype, k0.dtype)[1], "parallelism": "single GPU",
         },
         "kv_bytes_per_call": logical,
         "unique_kv_bytes_per_call": unique,
