@@ -615,7 +615,10 @@ inline bool rows_fit_one_launch(int64_t splits, int64_t split_tokens, int64_t ca
 //   grids of at most eight waves per CU keep their split: doubling it made
 //     the Llama-3-8B B4 L4096 FP8 call 14.8 -> 17.9, MQA B128 L1024 14.1 ->
 //     16.3, the reference's B4 batch 14.7 -> 16.2 (FP16 Llama-3-8B: 17.4 ->
-//     17.2).
+//     17.3).
+// Going on to four waves per CU helped some shapes and hurt others badly
+// (FP16 B2 L8192 17.6 -> 17.2; FP8 K/V B16 L4096 32.5 -> 47.2, MQA B256
+// L1024 20.2 -> 25.0, FP16 B6 L4096 22.6 -> 23.0), so the rule stops at eight.
 // Whole-row calls and FP32 inputs keep the caller's split.
 constexpr int64_t kCoarseWaveBytes = 128 * 1024;
 constexpr int kCoarseWavesPerCu = 8;
