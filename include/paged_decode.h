@@ -18,7 +18,8 @@
  * state per query head in the caller's workspace, and a merge combines them:
  *   numerator [batch, query_heads, 4 * splits, head_dim]  float32
  *   stats     [batch, query_heads, 4 * splits, 2]         float32 (max, denominator)
- * (state 4 * split + quarter; the reference's workspace shape, decode.cu:223-231).
+ * (state 4 * split + quarter; the reference's workspace shape, decode.cu:223-231;
+ * a full call with length bounds may lay it out for a coarser split, see pd_decode).
  * Where one workgroup of the partition stage holds several quarters of a
  * partition (few KV heads: 16-head GQA tiles with four quarters per
  * workgroup, or two quarters per workgroup), those quarters are stored
@@ -105,9 +106,10 @@ enum pd_hint { PD_HINT_NONE = 0, PD_HINT_UNSHARED_PAGES = 1, PD_HINT_RAGGED_LENG
  * folds a row's states in LDS and writes out itself, and numerator/stats
  * are left unwritten (they remain required arguments, the workspace of the
  * reference's plan). Results agree with the two-launch path to FP32
- * rounding; pd_decode_launch_count says which a call takes. On grids with
- * many waves per CU the two launches run over coarser partitions, a power
- * of two times split_tokens, whose fewer states the workspace holds
+ * rounding; pd_decode_launch_count says which a call takes. With length
+ * bounds (pd_decode_ex, pd_decode_scratch) on grids with many waves per CU
+ * the two launches run over coarser partitions, a power of two times
+ * split_tokens, whose fewer states the workspace holds
  * (pd_decode_kernel_split says which); the workspace's contents are
  * internal to the call.
  * Replaces the native entry `decode(q, k, v, table, lengths, numerator, stats,
@@ -300,12 +302,13 @@ int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads
 
 /*
  * Partitions the two launches of pd_decode / pd_decode_ex / pd_decode_scratch
- * run over for a call of these formats, shapes and host length bounds (NULL:
- * unknown) on a device of compute_units CUs (<= 0: the current device's):
+ * run over for a call of these formats, shapes and host length bounds on a
+ * device of compute_units CUs (<= 0: the current device's):
  * *kernel_splits partitions of *kernel_split_tokens tokens per row, with
  * kernel_split_tokens = c * split_tokens for a power of two c and
- * kernel_splits = ceil(splits / c) (c = 1 for whole-row calls and FP32
- * inputs). A caller that runs the stages itself (pd_decode_partial_ex, then
+ * kernel_splits = ceil(splits / c). c > 1 only with length bounds (the live
+ * partitions they reach set the waves per CU), never for whole-row calls or
+ * FP32 inputs. A caller that runs the stages itself (pd_decode_partial_ex, then
  * pd_decode_merge) passes these two values to both to match the full call's
  * partitioning. Returns a status (the checks of pd_decode_ex). No
  * counterpart in the reference, whose partition count is the caller's

@@ -600,9 +600,11 @@ inline bool rows_fit_one_launch(int64_t splits, int64_t split_tokens, int64_t ca
 // (page ids and first K/V loads, the last tile, the state stores) and the
 // merge's states weigh less per byte -- while the grid keeps enough waves to
 // cover the device. c doubles while a wave would read at most
-// kCoarseWaveBytes of K and V and the live partitions (as far as the host
-// bounds tell; all of them without bounds) still give kCoarseWavesPerCu
-// waves per CU. Measured on MI355X (decode call, us, graph of 200 calls, K/V
+// kCoarseWaveBytes of K and V and the live partitions, as far as the host
+// bounds tell, still give kCoarseWavesPerCu waves per CU. A call without
+// bounds keeps its split: counting every allocated partition as live
+// over-coarsens plans that reserve context (Llama-3-8B B4 L4096 with 4x
+// reserved: 21.7 -> 28.4 us). Measured on MI355X (decode call, us, graph of 200 calls, K/V
 // rotated over 2 GiB; the split the rule picks in brackets):
 //   ragged + shared-prefix B16, page 32, split 128: 40.8 -> 31.9 [512]
 //     (1024: 32.5, 2048: 37.7);
@@ -630,13 +632,14 @@ struct KernelSplit {
 inline KernelSplit coarse_split(int batch, int kv_heads, int head_tiles, int head_dim, int elem, int page_size,
                                 int table_width, int splits, int split_tokens, const int32_t* length_bounds,
                                 int cus) {
+    if (length_bounds == nullptr) return KernelSplit{splits, split_tokens};
     const int64_t capacity = static_cast<int64_t>(table_width) * page_size;
     // Tokens the caller's partitions reach; no partition of a coarser split goes past them.
     const int64_t reach = lmin(static_cast<int64_t>(splits) * split_tokens, capacity);
     auto waves = [&](int64_t span) {
         int64_t parts = 0;
         for (int b = 0; b < batch; ++b) {
-            const int64_t bound = length_bounds ? lmin(reach, length_bounds[b] < 0 ? 0 : length_bounds[b]) : reach;
+            const int64_t bound = lmin(reach, length_bounds[b] < 0 ? 0 : length_bounds[b]);
             parts += (bound + span - 1) / span;
         }
         return parts * kQuarters * kv_heads * head_tiles;

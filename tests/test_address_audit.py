@@ -50,8 +50,8 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
     # The walk covered the measured workloads and the compacted launches.
     for needle in ("llama3-8b B4 L4096 fp16", "ragged shared B16", "mqa B128", "long mha B1", "compact",
                    "rectangular+tails", "whole rows", "1M context", "pages above 4 GiB", "invalid page ids fp8",
-                   "ragged shared B16 T32 split 128 coarse x8", "bounds=half coarse x4",
-                   "long mha B1 Hq32/32 L32768 split 128 coarse x8"):
+                   "ragged shared B16 T32 split 128 bounds=exact coarse x8", "bounds=half coarse x4",
+                   "long mha B1 Hq32/32 L32768 split 128 bounds=exact coarse x8"):
         assert needle in run.stdout, needle
 
 

@@ -141,14 +141,14 @@ def test_kernel_split_query():
     splits = -(-int(w.lengths.max()) // 128)
     assert split(f16, f16, lay.batch, lay.query_heads, lay.kv_heads, lay.head_dim, lay.page_size, w.table.shape[1],
                  lay.physical_pages, splits, 128, w.lengths) == (-(-splits // 4), 512)
-    # Bounds that reach few partitions keep the split; without bounds every partition counts as live.
+    # Bounds that reach few partitions keep the split, and so does a call without bounds.
     assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256, [0] * 16) == (16, 256)
-    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256) == (4, 1024)
+    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256) == (16, 256)
     # Twice the CUs need twice the waves.
-    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256, cus=512) == (8, 512)
+    assert split(f16, f16, 16, 32, 8, 128, 16, 256, 4096, 16, 256, [4096] * 16, cus=512) == (8, 512)
     # FP32 inputs and whole-row calls keep the caller's split.
-    assert split(f32, f32, 16, 32, 8, 128, 16, 256, 4096, 16, 256) == (16, 256)
-    assert split(f16, f16, 4096, 32, 8, 64, 16, 8, 32768, 2, 64) == (2, 64)
+    assert split(f32, f32, 16, 32, 8, 128, 16, 256, 4096, 16, 256, [4096] * 16) == (16, 256)
+    assert split(f16, f16, 4096, 32, 8, 64, 16, 8, 32768, 2, 64, [128] * 4096) == (2, 64)
     # Whatever the rule picks, fewer partitions cover at least the caller's tokens.
     rng = np.random.default_rng(5)
     for _ in range(200):
