@@ -45,9 +45,12 @@ def dims(layout, width, splits, split_tokens, merge, hints):
             layout.physical_pages, splits, split_tokens, merge, hints)
 
 
-def run_both(lib, layout, dtype, lengths, split_tokens, merge, hints, seed):
-    """(scratch-entry output, workspace-entry output, FP64 oracle) for one problem."""
+def run_both(lib, layout, dtype, lengths, split_tokens, merge, hints, seed, with_bounds=False):
+    """(scratch-entry output, workspace-entry output, FP64 oracle) for one problem;
+    with_bounds passes the lengths as host length bounds to both entries."""
     table, lengths, host = problem(layout, dtype, lengths, seed)
+    bounds = lengths.copy() if with_bounds else None
+    bounds_ptr = None if bounds is None else bounds.ctypes.data
     q, k, v = (torch.from_numpy(x).cuda() for x in host)
     d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
     splits = max(1, -(-int(lengths.max()) // split_tokens))
@@ -55,8 +58,8 @@ def run_both(lib, layout, dtype, lengths, split_tokens, merge, hints, seed):
     args = dims(layout, table.shape[1], splits, split_tokens, merge, hints)
     out_scratch = torch.full((layout.batch, layout.query_heads, layout.head_dim), float("nan"), device="cuda")
     status = lib.pd_decode_scratch(q.data_ptr(), code, k.data_ptr(), v.data_ptr(), code, 1.0, 1.0,
-                                   d_table.data_ptr(), d_lengths.data_ptr(), out_scratch.data_ptr(), *args, None,
-                                   stream())
+                                   d_table.data_ptr(), d_lengths.data_ptr(), out_scratch.data_ptr(), *args,
+                                   bounds_ptr, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     shape = (layout.batch, layout.query_heads, 4 * splits)
     num = torch.full((*shape, layout.head_dim), float("nan"), device="cuda")
@@ -64,7 +67,7 @@ def run_both(lib, layout, dtype, lengths, split_tokens, merge, hints, seed):
     out_ws = torch.full_like(out_scratch, float("nan"))
     status = lib.pd_decode_ex(q.data_ptr(), code, k.data_ptr(), v.data_ptr(), code, 1.0, 1.0, d_table.data_ptr(),
                               d_lengths.data_ptr(), num.data_ptr(), stats.data_ptr(), out_ws.data_ptr(), *args,
-                              None, stream())
+                              bounds_ptr, stream())
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     torch.cuda.synchronize()
     expected = fp64.dense_attention(*host, table, lengths)
@@ -89,6 +92,29 @@ def test_scratch_entry_matches_workspace_entry_twice_then_smaller():
                                       cabi.PD_HINT_NONE, seed=0)
     np.testing.assert_array_equal(b_scratch, b_ws)
     assert_parity(b_scratch, b_ref, np.float32)
+
+
+def test_scratch_entry_over_coarser_partitions_then_smaller():
+    """With length bounds on a grid of many waves per CU, both entries run over
+    coarser partitions than the caller's (pd_decode_kernel_split); the scratch
+    entry still matches the workspace entry bit for bit, then a smaller call
+    with bounds at the caller's split follows on the same scratch."""
+    lib = cabi.load()
+    big = Layout(16, 32, 8, 128, 16, 16 * 128)
+    announce("pd_decode_scratch with bounds, call 1: B16 Hq32 Hkv8 D128 FP16 L2048, split 128, serial")
+    kernel = cabi.kernel_split(lib, cabi.PD_DTYPE_F16, cabi.PD_DTYPE_F16, 16, 32, 8, 128, 16, 128, 16 * 128, 16, 128,
+                               [2048] * 16)
+    assert kernel[1] > 128, kernel
+    a_scratch, a_ws, a_ref = run_both(lib, big, np.float16, [2048] * 16, 128, cabi.PD_MERGE_SERIAL,
+                                      cabi.PD_HINT_UNSHARED_PAGES, seed=21, with_bounds=True)
+    np.testing.assert_array_equal(a_scratch, a_ws)
+    assert_parity(a_scratch, a_ref, np.float16)
+    announce("pd_decode_scratch with bounds, call 2: B4 Hq32 Hkv8 D128 FP16 ragged, split 64, shared")
+    small = Layout(4, 32, 8, 128, 16, 4 * 64)
+    b_scratch, b_ws, b_ref = run_both(lib, small, np.float16, [1024, 0, 517, 1000], 64, cabi.PD_MERGE_SHARED,
+                                      cabi.PD_HINT_NONE, seed=22, with_bounds=True)
+    np.testing.assert_array_equal(b_scratch, b_ws)
+    assert_parity(b_scratch, b_ref, np.float16)
 
 
 def test_scratch_entry_rejects_workspaces_beyond_the_scratch():
