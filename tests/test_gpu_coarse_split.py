@@ -104,22 +104,32 @@ def test_coarse_calls_match_oracle_and_stage_entries(name, q_dtype, kv_dtype, me
     torch.testing.assert_close(plan._out, out, rtol=1e-4, atol=2e-5)
 
 
-def test_captured_coarse_call_with_growth_past_the_captured_bounds():
-    """A graph captured while the bounds give a coarse split (2 x 128 tokens) keeps
-    decoding correctly while captured appends grow every sequence from 1024 to
-    4096 tokens: the partitions past the captured bounds run as tail items of
-    the coarse grid. Every replay is checked against the FP64 oracle."""
-    announce("captured coarse call, appends growing 1024 -> 4096 tokens")
-    batch, heads, kv_heads, dim, page, width = 16, 32, 8, 128, 16, 512
+GROWTH = {
+    # 16 sequences of 1024 tokens, split 128: a rectangular grid with tail slices.
+    "uniform": (16, [1024] * 16, 128, 4096),
+    # 8 long and 24 short sequences, split 64: very ragged, so a work list.
+    "ragged-work-list": (32, [4000] * 8 + [100] * 24, 64, 8192),
+}
+
+
+@pytest.mark.parametrize("name", list(GROWTH))
+def test_captured_coarse_call_with_growth_past_the_captured_bounds(name):
+    """A graph captured while the bounds give a coarse split keeps decoding
+    correctly while captured appends grow the sequences by 3072 tokens: the
+    partitions past the captured bounds run as tail items of the coarse grid,
+    a rectangular one with tail slices or a work list. Every replay is checked
+    against the FP64 oracle."""
+    batch, lengths0, split, max_context = GROWTH[name]
+    announce(f"captured coarse call {name}, appends growing by 6 x 512 tokens")
+    heads, kv_heads, dim, page, width = 32, 8, 128, 16, 512
     layout = Layout(batch, heads, kv_heads, dim, page, batch * width)
     rng = np.random.default_rng(17)
     table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
-    lengths = np.full(batch, 1024, dtype=np.int32)
-    plan = DecodePlan(layout, table, lengths, split_tokens=128, max_context=4096)
-    assert plan.splits == 32
+    lengths = np.array(lengths0, dtype=np.int32)
+    plan = DecodePlan(layout, table, lengths, split_tokens=split, max_context=max_context)
     kernel_splits, kernel_tokens = plan.kernel_split(torch.float16)
-    announce(f"  kernel split at capture {kernel_splits} x {kernel_tokens}")
-    assert kernel_tokens > 128
+    announce(f"  plan split {plan.splits} x {split}, kernel split at capture {kernel_splits} x {kernel_tokens}")
+    assert kernel_tokens > split
     q, k, v = (torch.from_numpy(x).to(torch.float16).cuda() for x in host_tensors(layout, dtype=np.float32, seed=5))
     tokens = 512
     q_step = torch.empty_like(q)
@@ -147,10 +157,10 @@ def test_captured_coarse_call_with_growth_past_the_captured_bounds():
         v_step.copy_(torch.from_numpy(vs))
         graph.replay()
         torch.cuda.synchronize()
-        host_k, _ = fp64.append_advance(host_k, table, host_lengths, ks, max_context=4096)
-        host_v, host_lengths = fp64.append_advance(host_v, table, host_lengths, vs, max_context=4096)
-        announce(f"  replay {step}: lengths {int(host_lengths[0])}")
+        host_k, _ = fp64.append_advance(host_k, table, host_lengths, ks, max_context=max_context)
+        host_v, host_lengths = fp64.append_advance(host_v, table, host_lengths, vs, max_context=max_context)
+        announce(f"  replay {step}: longest {int(host_lengths.max())}")
         assert_parity(out.cpu().numpy(), fp64.dense_attention(qs, host_k, host_v, table, host_lengths),
                       torch.float16)
         np.testing.assert_array_equal(plan._lengths.cpu().numpy(), host_lengths)
-    assert (host_lengths == 4096).all()
+    assert (host_lengths == lengths + 6 * tokens).all()
