@@ -96,6 +96,8 @@ struct MergeParams {
     int query_heads;
     int split_tokens;
     int capacity;            // table_width * page_size
+    int first_states;        // states (read units) loaded before the live count arrives: the host's
+                             // bound on any row's live states, else the whole row
 };
 
 // merge_cols_kernel: a row's D columns are cut into 128-byte chunks and each
@@ -155,11 +157,15 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
             }
         }
     };
-    // The first kOptimisticRounds loads are issued for the allocated row
-    // before the live count arrives (it comes with them) and masked
-    // afterwards; the rest of the round covers live states only, so a ragged
-    // batch does not read the states past its sequences' ends.
-    const int optimistic = min(kOptimisticRounds, rounds_from(0, parts));
+    // The first kOptimisticRounds loads are issued before the live count
+    // arrives (it comes with them) and masked afterwards: for the row's first
+    // first_n states, the host's bound on live states where it has one (a plan
+    // reserving context does not read its unwritten reserve), else the whole
+    // row. The rest of the round covers live states only, so a ragged batch
+    // does not read the states past its sequences' ends, and states past the
+    // bound (lengths grown on the device) are still read.
+    const int first_n = max(1, min(parts, mp.first_states));
+    const int optimistic = min(kOptimisticRounds, rounds_from(0, first_n));
     load_rounds(0, 0, optimistic);
     const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, kQuarters >> shift, parts);
     load_rounds(0, optimistic, rounds_from(0, live));
@@ -180,10 +186,13 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
         }
         return m;
     };
+    // The statistics scan's first round covers the same first_n states (whole
+    // kScan blocks of them); later rounds start where it ended.
+    const int scan_end = min(kScanRound, (first_n + kScan - 1) / kScan * kScan);
     float2 first[SU];
-    scan_round(0, parts, first);
-    float mx = round_max(first, 0, parts, kNoToken);
-    for (int base = kScanRound; base < live; base += kScanRound) {
+    scan_round(0, first_n, first);
+    float mx = round_max(first, 0, first_n, kNoToken);
+    for (int base = scan_end; base < live; base += kScanRound) {
         float2 sv[SU];
         scan_round(base, live, sv);
         mx = round_max(sv, base, live, mx);
@@ -212,8 +221,8 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
             }
         }
     };
-    accumulate_den(first, 0, parts);
-    for (int base = kScanRound; base < live; base += kScanRound) {
+    accumulate_den(first, 0, first_n);
+    for (int base = scan_end; base < live; base += kScanRound) {
         float2 sv[SU];
         scan_round(base, live, sv);
         accumulate_den(sv, base, live);
@@ -614,9 +623,11 @@ int check_merge(const float* numerator, const float* stats, const float* out, co
     return PD_OK;
 }
 
+// length_bounds (host, or null): upper bounds on the device lengths, which
+// bound the states the merge loads before it knows a row's live count.
 int run_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
               int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
-              int merge_mode, int stride, hipStream_t stream) {
+              int merge_mode, int stride, hipStream_t stream, const int32_t* length_bounds = nullptr) {
     MergeParams mp{};
     mp.numerator = numerator;
     mp.stats = stats;
@@ -627,6 +638,15 @@ int run_merge(const float* numerator, const float* stats, float* out, const int3
     mp.query_heads = query_heads;
     mp.split_tokens = split_tokens;
     mp.capacity = table_width * page_size;
+    mp.first_states = mp.parts >> mp.stride_shift;
+    if (length_bounds != nullptr) {
+        const int64_t reach = lmin(static_cast<int64_t>(splits) * split_tokens, mp.capacity);
+        int64_t longest = 0;
+        for (int b = 0; b < batch; ++b)
+            longest = std::max<int64_t>(longest, lmin(reach, length_bounds[b] < 0 ? 0 : length_bounds[b]));
+        const int64_t live = (kQuarters >> mp.stride_shift) * ((longest + split_tokens - 1) / split_tokens);
+        mp.first_states = static_cast<int>(lmin(mp.first_states, live));
+    }
     return head_dim == 64 ? launch_merge<64>(mp, batch, merge_mode, stream)
                           : launch_merge<128>(mp, batch, merge_mode, stream);
 }
@@ -770,7 +790,7 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
                          ks.split_tokens, hints, length_bounds, s, out, &stride);
     if (status != PD_OK || stride == 0) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, ks.splits,
-                     ks.split_tokens, merge_mode, stride, s);
+                     ks.split_tokens, merge_mode, stride, s, length_bounds);
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
