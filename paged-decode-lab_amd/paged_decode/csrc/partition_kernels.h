@@ -770,6 +770,14 @@ constexpr int kFp32RowBlockChunks = 4;
 // faster per Llama-3-8B-shape call than eight-tile blocks, same loads).
 constexpr int kMfmaPrefetch = 2;
 constexpr int kMfmaBlock = 2;
+// FP8 K/V tiles are half the bytes: a 64-token quarter's four tiles are all
+// requested at once, in one block. Measured on MI355X (decode call, us), 2 and
+// 2 -> 4 and 4: B1 L4096 10.7 -> 10.2, B16 L4096 32.5 -> 32.1, MQA B128 L1024
+// D64 12.03 -> 11.90, Llama-3-8B B4 L4096 14.7 -> 14.7. Whole-row launches
+// keep 2 and 2: at 1024 lanes their kernel has 128 VGPRs, and four tiles in
+// flight spilled.
+constexpr int kMfmaPrefetchFp8 = 4;
+constexpr int kMfmaBlockFp8 = 4;
 
 // Compute units of the current device, read once per device.
 inline int device_compute_units() {
@@ -796,13 +804,14 @@ int launch_mfma(const PartialParams& prm, int kv_heads, hipStream_t stream) {
     const dim3 block(partial_threads(prm));
     const size_t lds = static_cast<size_t>(mfma_lds_bytes(prm, D, KVF == kKvNative ? 2 : 1));
     const int kind = grid_kind(prm);
-    constexpr int kPD = kMfmaPrefetch, kNC = kMfmaBlock;
+    constexpr int kPD = KVF == kKvNative ? kMfmaPrefetch : kMfmaPrefetchFp8;
+    constexpr int kNC = KVF == kKvNative ? kMfmaBlock : kMfmaBlockFp8;
     // Whole-row launches are rectangular (one workgroup per row).
 #define PD_LAUNCH_MFMA(MODE, FOLD)                                                                                \
     do {                                                                                                          \
         if constexpr (FOLD == 2)                                                                                  \
-            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, 2, kGridRect>), grid, block,  \
-                               lds, stream, prm);                                                                 \
+            hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kMfmaPrefetch, kMfmaBlock, MODE, 2, kGridRect>), \
+                               grid, block, lds, stream, prm);                                                    \
         else if (kind == kGridList)                                                                               \
             hipLaunchKernelGGL((partial_mfma_kernel<QT, KVF, D, GT, kPD, kNC, MODE, FOLD, kGridList>), grid,      \
                                block, lds, stream, prm);                                                          \

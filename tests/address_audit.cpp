@@ -8,8 +8,9 @@
 // partition_range, wave_work, speculative_page, window_entry, tile_span,
 // tile_live, tile_page_offset, token_offset, numerator_offset, stats_offset),
 // following the kernels' loop structure (page-id windows of 64 entries, load
-// groups issued two ahead in blocks of two for the matrix-core kernel, four
-// ahead in blocks of sixteen for the FP32 kernel). Every global load is
+// groups issued two ahead in blocks of two for the matrix-core kernel -- four
+// and four with FP8 K/V outside whole rows -- and four ahead in blocks of sixteen for the FP32
+// kernel). Every global load is
 // checked to lie inside q, k, v, table or lengths (parked loads of dead
 // groups inside q), every store inside numerator or stats, every LDS access
 // inside the launch's dynamic LDS; every live token is read from the page its
@@ -220,9 +221,12 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
     AUDIT(waves >= 1 && waves <= (p.row_mode ? kRowMaxWaves : 8), "workgroup of %d waves", waves);
     if (mfma) AUDIT(mfma_lds_bytes(p, D, pr.kv_elem) <= 160 * 1024, "LDS %d bytes", mfma_lds_bytes(p, D, pr.kv_elem));
     const int align = mfma ? kTileTokens : kWave / (D / 4);
-    // Load groups per straight-line block and issued ahead: matrix-core 2 and
-    // 2; FP32 16 and 4, whole-row FP32 launches 4 and 4.
-    const int block = mfma ? 2 : p.row_mode ? 4 : 16, ahead = mfma ? 2 : 4, group_tokens = align;
+    // Load groups per straight-line block and issued ahead, as the kernels'
+    // constants: matrix-core 2 and 2 (FP8 K/V outside whole rows: 4 and 4);
+    // FP32 16 and 4, whole-row FP32 launches 4 and 4.
+    const bool fp8_deep = mfma && pr.kv_elem == 1 && !p.row_mode;
+    const int block = mfma ? (fp8_deep ? 4 : 2) : p.row_mode ? 4 : 16;
+    const int ahead = mfma ? (fp8_deep ? 4 : 2) : 4, group_tokens = align;
     const int qw = p.quarters_per_wg;
     for (uint32_t bz = 0; bz < grid.z; ++bz) {
         for (uint32_t by = 0; by < grid.y; ++by) {
