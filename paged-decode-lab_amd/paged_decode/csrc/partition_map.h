@@ -775,8 +775,25 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     // smaller tiles were 0.3-0.7 us slower per call. A grid smaller than the
     // CUs leaves the fold's tail exposed (B1 L4096: 12.05 us without, 12.43
     // with), so such launches keep four states per partition.
+    //
+    // Smaller tiles do fold four quarters where the quarters are long: grids
+    // of more than two 8-wave workgroups per CU over partitions of at least
+    // 1024 tokens (the coarser partitions of a large grid), with at most 8 KV
+    // heads, 16-bit K/V and lengths not flagged ragged, run one KV head x four quarters per
+    // 4-wave workgroup (`long_quarters`; the streaming mode stays that of
+    // the default shape). The fold's tail is then short against a 256-token
+    // quarter, and the merge reads a quarter of the states. Measured on
+    // MI355X (decode call, us, two quarters -> four): uniform B16 / B32
+    // L4096 48.3 -> 47.5 / 90.8 -> 88.4, B64 L2048 91.4 -> 88.4, B16 L8192
+    // with 64 / 8 heads 94.7 -> 92.6; FP8 K/V B16 L4096 32.1 -> 34.0, a
+    // ragged B32 L8192 batch 100.1 -> 103.0 and 32K-context MHA (32 KV heads,
+    // whose default workgroups read four heads of each token row) 86.7 ->
+    // 87.1, hence the conditions.
     const bool fills_device = shape_workgroups(prm, kv_heads) >= cus;
     prm.combine = fills_device && (prm.quarters_per_wg == 2 || (prm.quarters_per_wg == 4 && gt == 16));
+    const bool long_quarters = fills_device && wg8 * 2 > cus && gt <= 8 && kv_heads <= 8 && elem == 2 &&
+                               !prm.ragged_lengths && prm.split_tokens >= 1024;
+    const int default_groups = kv_heads / prm.heads_per_wg;
     // When the KV heads need several workgroups (kv_heads > heads_per_wg),
     // each workgroup reads one head group's slice of every token row, and
     // some 16-byte loads may be issued non-temporal. That is faster when
@@ -798,9 +815,14 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     // V (4+ groups) or V (2 groups, or one in a mid-size grid); pages that may
     // be shared stream V (4+ groups) or nothing. FP8 V loads are 8-byte, so
     // FP8 streams its 16-byte K row loads wherever 16-bit K/V would stream V.
-    const int groups = kv_heads / prm.heads_per_wg;
+    const int groups = default_groups;
     prm.stream_mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
                       : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+    if (long_quarters) {
+        choose_workgroup(prm, kv_heads, 1, 4);
+        prm.mid_grid = 0;
+        prm.combine = prm.quarters_per_wg == 4;
+    }
     plan_rows(prm, head_dim, elem, combine_slot_bytes(head_dim), mfma_stage_bytes(head_dim, elem));
     const Grid grid = partial_grid(prm, kv_heads);
     prm.grid_x = grid.x;
