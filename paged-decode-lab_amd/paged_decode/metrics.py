@@ -4,33 +4,46 @@ import statistics
 
 
 def percentile(values, quantile):
-    """Linearly interpolated percentile (the 'linear' method of numpy)."""
-    if not values or not 0 <= quantile <= 1:
-        raise ValueError("nonempty values and quantile in [0,1] required")
-    ordered = sorted(values)
-    position = (len(ordered) - 1) * quantile
-    lower = math.floor(position)
-    upper = math.ceil(position)
-    return ordered[lower] + (ordered[upper] - ordered[lower]) * (position - lower)
+    """Percentile by linear interpolation between closest ranks.
+
+    For ``n`` sorted samples the rank is ``quantile * (n - 1)``; a fractional
+    rank blends its two neighbours (numpy's default 'linear' method).
+    """
+    samples = sorted(values)
+    if len(samples) == 0:
+        raise ValueError("percentile of an empty sample set")
+    if quantile < 0 or quantile > 1:
+        raise ValueError(f"quantile {quantile} lies outside [0, 1]")
+    rank = quantile * (len(samples) - 1)
+    below = int(math.floor(rank))
+    frac = rank - below
+    if frac == 0:
+        return samples[below]
+    return samples[below] * (1 - frac) + samples[below + 1] * frac
 
 
 def summarize(device_ms, wall_ms, batch):
     """p50/p95/min of paired device and wall samples, plus decode rates.
 
-    One decode call advances every sequence of the batch by one token, so the
-    sequence-token rate is ``batch`` times the call rate.
+    The keys are the reference report's schema. One decode call advances every
+    sequence of the batch by one token, so the sequence-token rate is ``batch``
+    times the call rate.
     """
-    if len(device_ms) != len(wall_ms) or not device_ms or min(list(device_ms) + list(wall_ms)) <= 0:
-        raise ValueError("paired positive timing samples required")
-    median = statistics.median(device_ms)
+    device, wall = list(device_ms), list(wall_ms)
+    if not device or len(device) != len(wall):
+        raise ValueError(f"need equally many device and wall samples, got {len(device)} and {len(wall)}")
+    if any(x <= 0 for x in device + wall):
+        raise ValueError("timing samples must be positive")
+    p50 = statistics.median(device)
+    calls_per_second = 1000.0 / p50
     return {
-        "sample_count": len(device_ms),
-        "device_ms_p50": median,
-        "device_ms_p95": percentile(list(device_ms), 0.95),
-        "device_ms_min": min(device_ms),
-        "wall_ms_p50": statistics.median(wall_ms),
-        "decode_steps_per_second": 1000.0 / median,
-        "sequence_tokens_per_second": batch * 1000.0 / median,
+        "sample_count": len(device),
+        "device_ms_p50": p50,
+        "device_ms_p95": percentile(device, 0.95),
+        "device_ms_min": min(device),
+        "wall_ms_p50": statistics.median(wall),
+        "decode_steps_per_second": calls_per_second,
+        "sequence_tokens_per_second": batch * calls_per_second,
     }
 
 

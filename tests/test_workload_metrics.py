@@ -81,6 +81,19 @@ def test_percentiles_are_interpolated():
     assert percentile([3, 1, 2], 0.5) == 2
 
 
+def test_percentiles_match_numpy_linear_method():
+    rng = np.random.default_rng(7)
+    for n in (1, 2, 3, 10, 31):
+        sample = rng.standard_normal(n).tolist()
+        for quantile in (0.0, 0.05, 0.5, 0.95, 1.0, 1 / 3):
+            assert percentile(sample, quantile) == pytest.approx(np.percentile(sample, 100 * quantile), abs=1e-12)
+    for bad in (-0.01, 1.01):
+        with pytest.raises(ValueError):
+            percentile([1.0], bad)
+    with pytest.raises(ValueError):
+        percentile([], 0.5)
+
+
 def test_throughput_uses_sequences_per_decode_step():
     summary = summarize([1., 2., 3.], [2., 3., 4.], batch=8)
     assert summary["device_ms_p50"] == 2
