@@ -98,6 +98,8 @@ struct MergeParams {
     int capacity;            // table_width * page_size
     int first_states;        // states (read units) loaded before the live count arrives: the host's
                              // bound on any row's live states, else the whole row
+    int xcd_rows;            // rows per row group of an XCD-grouped partition grid (merge_xcd_row), 0: plain
+    int xcd_shift;           // log2 of that grid's head groups per sequence
 };
 
 // merge_cols_kernel: a row's D columns are cut into 128-byte chunks and each
@@ -127,8 +129,16 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     extern __shared__ float weight[];  // [parts], shared variant only
     __shared__ f32x4 column_sum[PG][TPR];
     __shared__ float wave_partial[2][kWaves];
-    const int b = blockIdx.y;
-    const int64_t row = static_cast<int64_t>(b) * mp.query_heads + blockIdx.x;
+    int b;
+    int64_t row;
+    if (mp.xcd_rows > 0) {
+        const MergeRow mr = merge_xcd_row(blockIdx.x, blockIdx.y, mp.xcd_rows, mp.xcd_shift, 1, 0);
+        b = mr.b;
+        row = mr.row;
+    } else {
+        b = blockIdx.y;
+        row = static_cast<int64_t>(b) * mp.query_heads + blockIdx.x;
+    }
     const int chunk = blockIdx.z;
     const int shift = mp.stride_shift;
     const int parts = mp.parts >> shift;  // states read: j <-> allocated state j << shift
@@ -292,10 +302,18 @@ __global__ void __launch_bounds__(kWave * RPG) merge_rows_kernel(const MergePara
     static_assert(merge_wave_max_parts<D, NB>() <= kWave, "one state per lane for the statistics");
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const int h = blockIdx.x * RPG + wave;
-    if (h >= mp.query_heads) return;  // whole wave; nothing below synchronises across waves
-    const int b = blockIdx.y;
-    const int64_t row = static_cast<int64_t>(b) * mp.query_heads + h;
+    int b;
+    int64_t row;
+    if (mp.xcd_rows > 0) {
+        const MergeRow mr = merge_xcd_row(blockIdx.x, blockIdx.y, mp.xcd_rows, mp.xcd_shift, RPG, wave);
+        b = mr.b;
+        row = mr.row;
+    } else {
+        const int h = blockIdx.x * RPG + wave;
+        if (h >= mp.query_heads) return;  // whole wave; nothing below synchronises across waves
+        b = blockIdx.y;
+        row = static_cast<int64_t>(b) * mp.query_heads + h;
+    }
     const int shift = mp.stride_shift;
     const int parts = mp.parts >> shift;  // states read: j <-> allocated state j << shift
     const int col = lane % TPR;
@@ -553,19 +571,25 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
                 const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
                 int splits, int split_tokens, int hints, const int32_t* length_bounds, hipStream_t stream,
-                float* out = nullptr, int* state_stride = nullptr) {
+                float* out = nullptr, int* state_stride = nullptr, int* xcd_rows = nullptr,
+                int* xcd_shift = nullptr) {
     PartialParams prm = partial_params(q, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, out,
                                        batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
                                        splits, split_tokens, hints, length_bounds);
     const int status = dispatch_partial(prm, q_dtype, kv_dtype, kv_heads, head_dim, stream);
     if (state_stride) *state_stride = prm.row_mode ? 0 : prm.combine ? prm.quarters_per_wg : 1;
+    if (xcd_rows) *xcd_rows = xcd_row_group_rows(prm);
+    if (xcd_shift) *xcd_shift = prm.xcd_shift;
     return status;
 }
 
 
 template <int D>
-int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t stream) {
+int launch_merge(MergeParams mp, int batch, int merge_mode, hipStream_t stream) {
     const bool shared = merge_mode == PD_MERGE_SHARED;
+    // Row groups of an XCD-grouped partition grid (merge_xcd_row).
+    const uint32_t row_groups = mp.xcd_rows > 0
+        ? static_cast<uint32_t>(static_cast<int64_t>(batch) * mp.query_heads / mp.xcd_rows / 8) : 0u;
     const int states = mp.parts >> mp.stride_shift;
     // merge_rows keeps a row in one wave, loading (states / PGW) 16-byte
     // columns per lane; with few rows of many states, merge_cols (D / 32
@@ -573,7 +597,10 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
     const int rounds = (states + kWave / (D / 4) - 1) / (kWave / (D / 4));
     const bool many_rows = static_cast<int64_t>(batch) * mp.query_heads >= kMergeRowsMin;
     if (states <= merge_wave_max_parts<D>() && (many_rows || rounds <= 2)) {
-        const dim3 grid((mp.query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
+        if (mp.xcd_rows % kMergeRowsPerGroup != 0) mp.xcd_rows = 0;
+        const dim3 grid = mp.xcd_rows > 0
+            ? dim3(8 * mp.xcd_rows / kMergeRowsPerGroup, row_groups)
+            : dim3((mp.query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
         if (shared) {
             hipLaunchKernelGGL((merge_rows_kernel<D, true, kMergeWaveBatch, kMergeRowsPerGroup>), grid,
                                dim3(kWave * kMergeRowsPerGroup), 0, stream, mp);
@@ -583,7 +610,8 @@ int launch_merge(const MergeParams& mp, int batch, int merge_mode, hipStream_t s
         }
         return launch_status();
     }
-    const dim3 grid(mp.query_heads, batch, D / kMergeChunk);
+    const dim3 grid = mp.xcd_rows > 0 ? dim3(8 * mp.xcd_rows, row_groups, D / kMergeChunk)
+                                      : dim3(mp.query_heads, batch, D / kMergeChunk);
     const dim3 block(kMergeThreads);
     const size_t lds = shared ? states * sizeof(float) : 0;
     // The long-row variant issues 1024 states' loads per round but holds one
@@ -627,7 +655,8 @@ int check_merge(const float* numerator, const float* stats, const float* out, co
 // bound the states the merge loads before it knows a row's live count.
 int run_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
               int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
-              int merge_mode, int stride, hipStream_t stream, const int32_t* length_bounds = nullptr) {
+              int merge_mode, int stride, hipStream_t stream, const int32_t* length_bounds = nullptr,
+              int xcd_rows = 0, int xcd_shift = 0) {
     MergeParams mp{};
     mp.numerator = numerator;
     mp.stats = stats;
@@ -639,6 +668,8 @@ int run_merge(const float* numerator, const float* stats, float* out, const int3
     mp.split_tokens = split_tokens;
     mp.capacity = table_width * page_size;
     mp.first_states = mp.parts >> mp.stride_shift;
+    mp.xcd_rows = xcd_rows;
+    mp.xcd_shift = xcd_shift;
     if (length_bounds != nullptr) {
         const int64_t reach = lmin(static_cast<int64_t>(splits) * split_tokens, mp.capacity);
         int64_t longest = 0;
@@ -784,13 +815,13 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
     // per row, so the states fit the caller's workspace.
     const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
                                       table_width, splits, split_tokens, length_bounds, device_compute_units());
-    int stride = 1;
+    int stride = 1, xcd_rows = 0, xcd_shift = 0;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, ks.splits,
-                         ks.split_tokens, hints, length_bounds, s, out, &stride);
+                         ks.split_tokens, hints, length_bounds, s, out, &stride, &xcd_rows, &xcd_shift);
     if (status != PD_OK || stride == 0) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, ks.splits,
-                     ks.split_tokens, merge_mode, stride, s, length_bounds);
+                     ks.split_tokens, merge_mode, stride, s, length_bounds, xcd_rows, xcd_shift);
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,

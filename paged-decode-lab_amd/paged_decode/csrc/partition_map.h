@@ -67,6 +67,11 @@ struct PartialParams {
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
     float v_scale;         // multiplies every stored numerator
+    // XCD-grouped rectangular grid (xcd_shift >= 0, see block_coords): all
+    // workgroups of a row group (one sequence's head group, every partition)
+    // run on one XCD, so the merge can read those states from that XCD's L2.
+    // xcd_shift is log2 of the head groups per sequence; -1: the plain grid.
+    int xcd_shift;
     // Rectangular grid (compact == 0): sequence b's partitions 0 ..
     // main_splits - 1 are items of z-slice b; when main_splits < splits (host
     // bounds reach fewer partitions than reserved), z-slices batch, batch + 1,
@@ -103,23 +108,41 @@ struct PartialParams {
     int shape_splits;      // partitions per sequence the bounds reach: the workgroup shape's grid (plan_items)
     int live_items;        // items holding tokens as far as the bounds tell (plan_items)
     int head_tile;         // GT: query heads per wave's tile (the GQA group padded to 1/2/4/8/16)
+    int uniform_live;      // host bounds given, and every sequence reaches the same partitions (plan_items)
 };
 
 // ---------------------------------------------------------------------------
 // Device-side map (also evaluated on the host by the address audit).
 
-// Workgroup coordinates (token group, head group) in dispatch order: the
-// linear dispatch index x + gx * y is read with the head group varying
-// fastest, so consecutively dispatched (and co-resident) workgroups cover all
-// KV-head groups of the same tokens -- whole token rows -- rather than one head
-// group's slice of many rows.
+// Workgroup coordinates (token group, head group) in dispatch order.
+//
+// Plain grid (xcd_shift < 0): the linear dispatch index x + gx * y is read
+// with the head group varying fastest, so consecutively dispatched (and
+// co-resident) workgroups cover all KV-head groups of the same tokens -- whole
+// token rows -- rather than one head group's slice of many rows.
+//
+// XCD-grouped grid (xcd_shift >= 0; grid 8 * token groups x row groups / 8,
+// z = 1): the dispatcher deals workgroups to the eight XCDs round robin by
+// linear index, so x % 8 is the workgroup's XCD. Row group r = 8 * y + x % 8
+// (sequence r >> xcd_shift, head group r % 2^xcd_shift) takes every token
+// group x / 8 on XCD r % 8, in token order. Each XCD holds its own L2, which
+// keeps the states the row group's workgroups stored after the launch ends;
+// the merge reads a row's states on that same XCD (merge_cols_kernel,
+// merge_rows_kernel). Measured on MI355X: a kernel reading 2-17 MB that the
+// previous kernel wrote takes 6.1-6.4 us when each workgroup reads its own
+// XCD's writes and 7.5-8.2 us when it reads another XCD's.
 struct BlockCoords {
     int tokens;  // item * (4 / qw) + quarter group
     int heads;   // KV heads [hg * hw, hg * hw + hw), head tiles [tg * tw, tg * tw + tw)
     int z;       // sequence of a rectangular grid
 };
 
-PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t gx, uint32_t gy) {
+PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t gx, uint32_t gy, int xcd_shift) {
+    if (xcd_shift >= 0) {
+        const uint32_t r = by * 8u + (bx & 7u);
+        return BlockCoords{static_cast<int>(bx >> 3), static_cast<int>(r & ((1u << xcd_shift) - 1u)),
+                           static_cast<int>(r >> xcd_shift)};
+    }
     // Every path reads gx and gy, so the kernel loads them with its other
     // arguments instead of after a branch.
     const uint64_t lin = bx + static_cast<uint64_t>(gx) * by;
@@ -448,6 +471,7 @@ inline int tail_span_for(int reserved) {
 }
 
 inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
+    prm.xcd_shift = -1;  // plain grid until plan_xcd, once the workgroup shape is known
     prm.compact = 0;
     prm.items = prm.batch * prm.splits;
     prm.main_splits = prm.splits;
@@ -455,6 +479,7 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.tail_span = kTailSpan;
     prm.shape_splits = prm.splits;
     prm.live_items = prm.items;
+    prm.uniform_live = 0;
     if (length_bounds == nullptr) return;
     const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
     auto live_of = [&](int b) {
@@ -463,11 +488,14 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     };
     int64_t live_total = 0;
     int longest = 1;
+    int fewest = prm.splits;
     for (int b = 0; b < prm.batch; ++b) {
         const int live = live_of(b);
         live_total += live;
         longest = imax(longest, live);
+        fewest = imin(fewest, live);
     }
+    prm.uniform_live = fewest == longest;
     prm.shape_splits = longest;
     prm.live_items = static_cast<int>(lmin(live_total > 0 ? live_total : 1, prm.items));
     if (prm.batch <= kCompactMaxBatch && live_total * 2 <= static_cast<int64_t>(prm.batch) * longest) {
@@ -515,6 +543,8 @@ inline Grid partial_grid(const PartialParams& prm, int kv_heads) {
     const uint32_t heads = static_cast<uint32_t>((kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg));
     if (prm.compact) return Grid{static_cast<uint32_t>(prm.items) * groups, heads, 1};
     if (prm.row_mode) return Grid{1, heads, static_cast<uint32_t>(prm.batch)};
+    if (prm.xcd_shift >= 0)
+        return Grid{8u * static_cast<uint32_t>(prm.main_splits) * groups, static_cast<uint32_t>(prm.batch) * heads / 8u, 1};
     const uint32_t tail_slices = prm.main_splits < prm.splits
         ? static_cast<uint32_t>(((static_cast<int64_t>(prm.batch) << prm.tail_shift) + prm.main_splits - 1) /
                                 prm.main_splits)
@@ -707,6 +737,52 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
 // Launch shape of the matrix-core kernel on a device of `cus` compute units,
 // for head_dim and K/V elements of elem bytes: head tile, workgroup shape,
 // quarter combine or whole rows, and streaming mode.
+// The XCD-grouped grid (block_coords) for a plain rectangular launch whose
+// row groups all carry the same work: host bounds that give every sequence
+// the same partitions, no tail items, no work list, no whole-row launch. With
+// the dispatcher dealing workgroups round robin, each XCD then gets the same
+// number of row groups; ragged batches keep the plain grid, which spreads
+// every sequence over all XCDs. A row group must cover whole query heads
+// [hg * hw * group, (hg + 1) * hw * group), so the merge can find it from a
+// row index: one head-tile group per KV head. Head groups per sequence must
+// be a power of two (shifts in the kernels) and sequences x head groups a
+// multiple of 8.
+inline void plan_xcd(PartialParams& prm, int kv_heads) {
+    prm.xcd_shift = -1;
+    if (!prm.uniform_live || prm.compact || prm.row_mode || prm.main_splits < prm.splits) return;
+    if (prm.head_tiles != prm.tiles_per_wg) return;
+    const int groups = kv_heads / prm.heads_per_wg;
+    if ((groups & (groups - 1)) != 0) return;
+    const int64_t row_groups = static_cast<int64_t>(prm.batch) * groups;
+    if (row_groups % 8 != 0 || row_groups / 8 > 65535) return;
+    if (8ll * prm.main_splits * (kQuarters / prm.quarters_per_wg) > 0x7FFFFFFFll) return;
+    int shift = 0;
+    while ((1 << shift) < groups) ++shift;
+    prm.xcd_shift = shift;
+}
+
+// Query-head rows of one XCD row group (merge side of plan_xcd), or 0 for the
+// plain grid.
+inline int xcd_row_group_rows(const PartialParams& prm) {
+    return prm.xcd_shift >= 0 ? prm.heads_per_wg * prm.group : 0;
+}
+
+// The merge's side of the XCD-grouped grid: merge workgroup (bx, by) of a
+// grid 8 * (group_rows / unit) x row groups / 8 takes `unit` consecutive rows
+// of row group r = 8 * by + bx % 8, on XCD r % 8 like the partition
+// workgroups that stored them; lane group `sub` of the workgroup takes row
+// r * group_rows + (bx / 8) * unit + sub, of sequence r >> xcd_shift.
+struct MergeRow {
+    int b;
+    int64_t row;  // b * query_heads + query head
+};
+
+PD_HD MergeRow merge_xcd_row(uint32_t bx, uint32_t by, int group_rows, int xcd_shift, int unit, int sub) {
+    const uint32_t r = by * 8u + (bx & 7u);
+    return MergeRow{static_cast<int>(r >> xcd_shift),
+                    static_cast<int64_t>(r) * group_rows + static_cast<int64_t>(bx >> 3) * unit + sub};
+}
+
 inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, int elem) {
     const int gt = head_tile(prm.group, 16);
     prm.head_tile = gt;
@@ -824,6 +900,7 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
         prm.combine = prm.quarters_per_wg == 4;
     }
     plan_rows(prm, head_dim, elem, combine_slot_bytes(head_dim), mfma_stage_bytes(head_dim, elem));
+    plan_xcd(prm, kv_heads);
     const Grid grid = partial_grid(prm, kv_heads);
     prm.grid_x = grid.x;
     prm.grid_y = grid.y;
@@ -837,6 +914,7 @@ inline void plan_fp32(PartialParams& prm, int kv_heads, int head_dim) {
     prm.head_tiles = (prm.group + gt - 1) / gt;
     choose_workgroup(prm, kv_heads, 8);
     plan_rows(prm, head_dim, 4, row_slot_bytes_fp32(head_dim), 0, fp32_row_max_waves(gt));
+    plan_xcd(prm, kv_heads);
     const Grid grid = partial_grid(prm, kv_heads);
     prm.grid_x = grid.x;
     prm.grid_y = grid.y;

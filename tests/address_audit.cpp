@@ -94,12 +94,19 @@ PartialParams params(const Problem& pr, int cus, bool mfma, bool rows) {
 }
 
 // Writers of each state slot, to check that every live slot is written once.
+// Also the XCD (linear dispatch index % 8) of the workgroups storing each
+// row's states: -1 none yet, -2 more than one.
 struct Coverage {
     std::vector<uint8_t> writes;
-    explicit Coverage(uint64_t states) : writes(states, 0) {}
-    void store(uint64_t slot) {
+    std::vector<int8_t> row_xcd;
+    Coverage(uint64_t states, uint64_t rows) : writes(states, 0), row_xcd(rows, -1) {}
+    void store(uint64_t slot, int64_t row, int xcd) {
         AUDIT(slot < writes.size(), "state slot %" PRIu64 " past the workspace", slot);
         if (slot < writes.size() && writes[slot] < 255) ++writes[slot];
+        if (row >= 0 && static_cast<uint64_t>(row) < row_xcd.size()) {
+            int8_t& x = row_xcd[row];
+            x = x == -1 ? static_cast<int8_t>(xcd) : x == xcd ? x : -2;
+        }
     }
 };
 
@@ -126,6 +133,44 @@ void check_coverage(const Problem& pr, const Coverage& cov) {
                       part, cov.writes[slot], expected);
             }
         }
+    }
+}
+
+// The merge's side of an XCD-grouped grid (merge_xcd_row), for both merge
+// kernels (one row per workgroup, and kMergeRowsPerGroup = 4 rows of one wave
+// each): every row is taken exactly once, by a workgroup of its own sequence
+// on the XCD whose workgroups stored all of the row's states.
+void check_merge_xcd(const Problem& pr, const PartialParams& p, const Coverage& cov) {
+    const int group_rows = xcd_row_group_rows(p);
+    const int64_t rows = static_cast<int64_t>(pr.batch) * pr.q_heads;
+    AUDIT(group_rows > 0 && rows % (8 * group_rows) == 0, "row groups of %d rows over %" PRId64 " rows", group_rows,
+          rows);
+    if (group_rows <= 0 || rows % (8 * group_rows) != 0) return;
+    for (int64_t r = 0; r < rows; ++r) {
+        const int len = imax(0, imin(pr.lengths[r / pr.q_heads], pr.width * pr.page_size));
+        if (len > 0) AUDIT(cov.row_xcd[r] >= 0, "row %" PRId64 " states stored from XCDs %d", r, cov.row_xcd[r]);
+    }
+    for (int unit : {1, 4}) {
+        if (group_rows % unit != 0) continue;
+        const uint32_t gx = static_cast<uint32_t>(8 * group_rows / unit);
+        const uint32_t gy = static_cast<uint32_t>(rows / group_rows / 8);
+        std::vector<uint8_t> taken(rows, 0);
+        for (uint32_t by = 0; by < gy; ++by) {
+            for (uint32_t bx = 0; bx < gx; ++bx) {
+                const int xcd = static_cast<int>((bx + static_cast<uint64_t>(gx) * by) % 8);
+                for (int sub = 0; sub < unit; ++sub) {
+                    const MergeRow m = merge_xcd_row(bx, by, group_rows, p.xcd_shift, unit, sub);
+                    AUDIT(m.row >= 0 && m.row < rows, "merge row %" PRId64, m.row);
+                    if (m.row < 0 || m.row >= rows) continue;
+                    AUDIT(m.b == m.row / pr.q_heads, "merge row %" PRId64 " given sequence %d", m.row, m.b);
+                    ++taken[m.row];
+                    const int stored = cov.row_xcd[m.row];
+                    if (stored >= 0)
+                        AUDIT(stored == xcd, "merge row %" PRId64 " on XCD %d, states on XCD %d", m.row, xcd, stored);
+                }
+            }
+        }
+        for (int64_t r = 0; r < rows; ++r) AUDIT(taken[r] == 1, "merge row %" PRId64 " taken %d times", r, taken[r]);
     }
 }
 
@@ -231,7 +276,8 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
     for (uint32_t bz = 0; bz < grid.z; ++bz) {
         for (uint32_t by = 0; by < grid.y; ++by) {
             for (uint32_t bx = 0; bx < grid.x; ++bx) {
-                const BlockCoords bc = block_coords(bx, by, bz, p.grid_x, p.grid_y);
+                const BlockCoords bc = block_coords(bx, by, bz, p.grid_x, p.grid_y, p.xcd_shift);
+                const int xcd = static_cast<int>((bx + static_cast<uint64_t>(grid.x) * (by + static_cast<uint64_t>(grid.y) * bz)) % 8);
                 const int kind = grid_kind(p);
                 const PartitionRange r = kind == kGridList        ? partition_range<kGridList>(p, bc)
                                          : kind == kGridRectTails ? partition_range<kGridRectTails>(p, bc)
@@ -353,14 +399,14 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                             AUDIT(numerator_offset(p, row, part, D) + D <= static_cast<int64_t>(buf.numerator_elems),
                                   "numerator store");
                             AUDIT(stats_offset(p, row, part) + 2 <= static_cast<int64_t>(buf.stats_elems), "stats store");
-                            cov.store(static_cast<uint64_t>(row) * kQuarters * pr.splits + part);
+                            cov.store(static_cast<uint64_t>(row) * kQuarters * pr.splits + part, row, xcd);
                             // Empty states of the span's other live partitions.
                             const int extra = extra_live_partitions(p, split, r.count, len_raw);
                             for (int e = 1; e <= extra; ++e) {
                                 const int ep = (split + e) * kQuarters + w.quarter;
                                 AUDIT(stats_offset(p, row, ep) + 2 <= static_cast<int64_t>(buf.stats_elems),
                                       "empty-state store");
-                                cov.store(static_cast<uint64_t>(row) * kQuarters * pr.splits + ep);
+                                cov.store(static_cast<uint64_t>(row) * kQuarters * pr.splits + ep, row, xcd);
                             }
                         }
                         if (mfma && p.combine) {
@@ -416,7 +462,8 @@ bool audit(const Problem& pr, bool rows) {
     const uint64_t checks_before = g_checks;
     const bool mfma = pr.q_elem == 2;
     const PartialParams p = params(pr, 256, mfma, rows);
-    Coverage cov(static_cast<uint64_t>(pr.batch) * pr.q_heads * kQuarters * pr.splits);
+    Coverage cov(static_cast<uint64_t>(pr.batch) * pr.q_heads * kQuarters * pr.splits,
+                 static_cast<uint64_t>(pr.batch) * pr.q_heads);
     OutCoverage out(static_cast<uint64_t>(pr.batch) * pr.q_heads * pr.head_dim);
     if (pr.head_dim == 64) audit_gt<64>(pr, p, mfma, cov, out);
     else audit_gt<128>(pr, p, mfma, cov, out);
@@ -426,14 +473,15 @@ bool audit(const Problem& pr, bool rows) {
             AUDIT(out.writes[e] == 1, "output element %zu written %d times", e, out.writes[e]);
     } else {
         check_coverage(pr, cov);
+        if (p.xcd_shift >= 0) check_merge_xcd(pr, p, cov);
     }
     const Grid grid = partial_grid(p, pr.kv_heads);
-    std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s, %" PRIu64 " checks: %s\n",
+    std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s%s, %" PRIu64 " checks: %s\n",
                 (pr.name + (rows ? " [call]" : "")).c_str(), mfma ? "mfma" : "fp32", grid.x, grid.y, grid.z,
                 partial_threads(p) / kWave, p.head_tile, p.quarters_per_wg,
                 p.row_mode ? "whole rows" : p.compact ? "compact" : p.main_splits < p.splits ? "rectangular+tails"
                                                                                               : "rectangular",
-                p.combine ? ", combined" : "",
+                p.combine ? ", combined" : "", p.xcd_shift >= 0 ? ", xcd-grouped" : "",
                 g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
     std::fflush(stdout);
     return g_failures == before;
@@ -539,6 +587,13 @@ int main(int argc, char** argv) {
         add(make("long mha B1 Hq32/32 L32768 split " + std::to_string(split), 1, 32, 32, 128, 16, 2048,
                  uniform(1, 32768), split, 2, 2, 5),
             !quick && split == 128);
+    // XCD-grouped grids (plan_xcd) under exact bounds, the shapes of
+    // tests/test_gpu_xcd_grid.py: both merge kernels' row maps are walked too.
+    add(make("xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp16", 8, 32, 8, 128, 16, 64, uniform(8, 1024), 128, 2, 2, 71));
+    add(make("xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp8", 8, 32, 8, 128, 16, 64, uniform(8, 1024), 128, 2, 1, 71));
+    add(make("xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16", 64, 16, 1, 64, 16, 64, uniform(64, 1024), 256, 2, 2, 73));
+    add(make("xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", 2, 16, 16, 128, 16, 128, uniform(2, 2048), 256, 2, 2, 75));
+    add(make("xcd fp32 B8 Hq16/8 D64 L1024 split 128", 8, 16, 8, 64, 16, 64, uniform(8, 1024), 128, 4, 4, 77));
     // Edge lengths around page and partition boundaries, both page sizes.
     for (int page : {16, 32}) {
         add(make("edges fp16 page " + std::to_string(page), 8, 8, 2, 128, page, 8,

@@ -53,6 +53,16 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
                    "ragged shared B16 T32 split 128 bounds=exact coarse x8", "bounds=half coarse x4",
                    "long mha B1 Hq32/32 L32768 split 128 bounds=exact coarse x8"):
         assert needle in run.stdout, needle
+    # The XCD-grouped grid is chosen for the measured uniform workloads and the
+    # shapes of tests/test_gpu_xcd_grid.py, under exact bounds, and not without.
+    lines = run.stdout.splitlines()
+    for name in ("llama3-8b B4 L4096 fp16", "llama3-8b B4 L4096 fp8", "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp16",
+                 "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp8", "xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16",
+                 "xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", "xcd fp32 B8 Hq16/8 D64 L1024 split 128"):
+        exact = [line for line in lines if line.startswith(name + " bounds=exact ")]
+        plain = [line for line in lines if line.startswith(name + " ") and "bounds=" not in line]
+        assert exact and all("xcd-grouped" in line for line in exact), name
+        assert plain and not any("xcd-grouped" in line for line in plain), name
 
 
 CPU_DRIVER = r"""
