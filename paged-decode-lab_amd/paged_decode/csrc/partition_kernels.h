@@ -89,7 +89,8 @@ __global__ void __launch_bounds__(kRow ? kWave * fp32_row_max_waves(GT) : kWave 
     const int lane = threadIdx.x % kWave;
     const int row = lane / LPT;
     const int col = lane % LPT;
-    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y, p.xcd_shift);
+    const BlockCoords bc = block_coords<kList>(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y, p.xcd_shift,
+                                                     p.xcd_main_rows, p.xcd_tail_shift);
     const PartitionRange pr = partition_range<kList>(p, bc);
     const int waves_wg = blockDim.x / kWave;
     const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
@@ -488,7 +489,8 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
     const int lane = threadIdx.x % kWave;
     const int n = lane % 16;  // head (q.K^T, P) / column (P.V)
     const int g = lane / 16;  // lane group: tokens g + 4 e
-    const BlockCoords bc = block_coords(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y, p.xcd_shift);
+    const BlockCoords bc = block_coords<kList>(blockIdx.x, blockIdx.y, blockIdx.z, p.grid_x, p.grid_y, p.xcd_shift,
+                                                     p.xcd_main_rows, p.xcd_tail_shift);
     const PartitionRange pr = partition_range<kList>(p, bc);
     // A whole-row workgroup's wave runs slice `wave` of its row (one KV head,
     // one head tile); otherwise the wave index splits into (head, tile,

@@ -71,7 +71,12 @@ struct PartialParams {
     // workgroups of a row group (one sequence's head group, every partition)
     // run on one XCD, so the merge can read those states from that XCD's L2.
     // xcd_shift is log2 of the head groups per sequence; -1: the plain grid.
+    // The first xcd_main_rows grid rows hold the main items; tail items (a
+    // grid with tails) follow in rows of their own, 2^xcd_tail_shift token
+    // groups per row group.
     int xcd_shift;
+    uint32_t xcd_main_rows;
+    int xcd_tail_shift;
     // Rectangular grid (compact == 0): sequence b's partitions 0 ..
     // main_splits - 1 are items of z-slice b; when main_splits < splits (host
     // bounds reach fewer partitions than reserved), z-slices batch, batch + 1,
@@ -114,6 +119,15 @@ struct PartialParams {
 // ---------------------------------------------------------------------------
 // Device-side map (also evaluated on the host by the address audit).
 
+// Kinds of grid, fixed at compile time per kernel (kList): a kernel built for
+// plain rectangular grids carries neither the tail arithmetic nor the
+// work-list lookup. The lookup's control flow kept the compiler from loading
+// the kernel arguments in one batch before the first page-id load (measured
+// on MI355X: 0.5 us per launch), and the tail arithmetic took the 8-wave
+// kernel from 128 to 131 VGPRs, one wave per SIMD fewer (ragged + shared B16
+// partition kernel 36 -> 48 us).
+enum GridKind { kGridRect = 0, kGridRectTails = 1, kGridList = 2 };
+
 // Workgroup coordinates (token group, head group) in dispatch order.
 //
 // Plain grid (xcd_shift < 0): the linear dispatch index x + gx * y is read
@@ -121,13 +135,18 @@ struct PartialParams {
 // co-resident) workgroups cover all KV-head groups of the same tokens -- whole
 // token rows -- rather than one head group's slice of many rows.
 //
-// XCD-grouped grid (xcd_shift >= 0; grid 8 * token groups x row groups / 8,
-// z = 1): the dispatcher deals workgroups to the eight XCDs round robin by
-// linear index, so x % 8 is the workgroup's XCD. Row group r = 8 * y + x % 8
-// (sequence r >> xcd_shift, head group r % 2^xcd_shift) takes every token
-// group x / 8 on XCD r % 8, in token order. Each XCD holds its own L2, which
-// keeps the states the row group's workgroups stored after the launch ends;
-// the merge reads a row's states on that same XCD (merge_cols_kernel,
+// XCD-grouped grid (xcd_shift >= 0; grid 8 * main token groups x row groups
+// / 8, z = 1, plus rows for the tail items of a grid with tails): the
+// dispatcher deals workgroups to the eight XCDs round robin by linear index,
+// so x % 8 is the workgroup's XCD. In the first xcd_main_rows rows, row group
+// r = 8 * y + x % 8 (sequence r >> xcd_shift, head group r % 2^xcd_shift)
+// takes main token group x / 8 on XCD r % 8. The tail rows after them hold,
+// per XCD, the row groups' tail token groups in row-group order (2^
+// xcd_tail_shift per row group; slots past the last row group are empty
+// items), so tail items are dispatched after every main item, as on the plain
+// grid, and on their row group's XCD. Each XCD holds its own L2, which keeps
+// the states the row group's workgroups stored after the launch ends; the
+// merge reads a row's states on that same XCD (merge_cols_kernel,
 // merge_rows_kernel). Measured on MI355X: a kernel reading 2-17 MB that the
 // previous kernel wrote takes 6.1-6.4 us when each workgroup reads its own
 // XCD's writes and 7.5-8.2 us when it reads another XCD's.
@@ -137,10 +156,19 @@ struct BlockCoords {
     int z;       // sequence of a rectangular grid
 };
 
-PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t gx, uint32_t gy, int xcd_shift) {
+template <int kList>
+PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t gx, uint32_t gy, int xcd_shift,
+                               uint32_t xcd_main_rows, int xcd_tail_shift) {
     if (xcd_shift >= 0) {
-        const uint32_t r = by * 8u + (bx & 7u);
-        return BlockCoords{static_cast<int>(bx >> 3), static_cast<int>(r & ((1u << xcd_shift) - 1u)),
+        const uint32_t x = bx & 7u;
+        uint32_t r = by * 8u + x, tokens = bx >> 3;
+        if (kList == kGridRectTails && by >= xcd_main_rows) {
+            const uint32_t main_tokens = gx >> 3;
+            const uint32_t slot = (by - xcd_main_rows) * main_tokens + tokens;
+            r = (slot >> xcd_tail_shift) * 8u + x;
+            tokens = main_tokens + (slot & ((1u << xcd_tail_shift) - 1u));
+        }
+        return BlockCoords{static_cast<int>(tokens), static_cast<int>(r & ((1u << xcd_shift) - 1u)),
                            static_cast<int>(r >> xcd_shift)};
     }
     // Every path reads gx and gy, so the kernel loads them with its other
@@ -162,15 +190,6 @@ struct PartitionRange {
     int b, first, count, qgroup;
 };
 
-// Kinds of grid, fixed at compile time per kernel (kList): a kernel built for
-// plain rectangular grids carries neither the tail arithmetic nor the
-// work-list lookup. The lookup's control flow kept the compiler from loading
-// the kernel arguments in one batch before the first page-id load (measured
-// on MI355X: 0.5 us per launch), and the tail arithmetic took the 8-wave
-// kernel from 128 to 131 VGPRs, one wave per SIMD fewer (ragged + shared B16
-// partition kernel 36 -> 48 us).
-enum GridKind { kGridRect = 0, kGridRectTails = 1, kGridList = 2 };
-
 inline int grid_kind(const PartialParams& prm) {
     return prm.compact ? kGridList : prm.main_splits < prm.splits ? kGridRectTails : kGridRect;
 }
@@ -185,6 +204,19 @@ PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& 
         r.b = bc.z;
         r.first = item;
         r.count = 1;
+        return r;
+    }
+    if (kList == kGridRectTails && p.xcd_shift >= 0) {
+        // XCD-grouped grid: tail item j of a row group covers tail_span
+        // partitions from main_splits + j * tail_span (none past the last
+        // partition, nor in the slots past the last row group).
+        const int j = item - p.main_splits;  // negative for main items
+        const int tfirst = p.main_splits + j * p.tail_span;
+        const bool tail = j >= 0;
+        const bool none = (tail && tfirst >= p.splits) || bc.z >= p.batch;
+        r.b = imin(bc.z, p.batch - 1);
+        r.first = tail ? imin(tfirst, p.splits - 1) : item;
+        r.count = none ? 0 : tail ? imin(p.tail_span, p.splits - tfirst) : 1;
         return r;
     }
     if (kList == kGridRectTails) {
@@ -538,13 +570,20 @@ struct Grid {
     uint32_t x, y, z;
 };
 
+// Grid rows of the XCD-grouped grid: xcd_main_rows, then the tail rows.
+inline uint32_t xcd_rows(const PartialParams& prm) {
+    if (prm.main_splits >= prm.splits) return prm.xcd_main_rows;
+    const int64_t main_tokens = static_cast<int64_t>(prm.main_splits) * (kQuarters / prm.quarters_per_wg);
+    const int64_t tail_slots = static_cast<int64_t>(prm.xcd_main_rows) << prm.xcd_tail_shift;
+    return prm.xcd_main_rows + static_cast<uint32_t>((tail_slots + main_tokens - 1) / main_tokens);
+}
+
 inline Grid partial_grid(const PartialParams& prm, int kv_heads) {
     const uint32_t groups = static_cast<uint32_t>(kQuarters / prm.quarters_per_wg);
     const uint32_t heads = static_cast<uint32_t>((kv_heads / prm.heads_per_wg) * (prm.head_tiles / prm.tiles_per_wg));
     if (prm.compact) return Grid{static_cast<uint32_t>(prm.items) * groups, heads, 1};
     if (prm.row_mode) return Grid{1, heads, static_cast<uint32_t>(prm.batch)};
-    if (prm.xcd_shift >= 0)
-        return Grid{8u * static_cast<uint32_t>(prm.main_splits) * groups, static_cast<uint32_t>(prm.batch) * heads / 8u, 1};
+    if (prm.xcd_shift >= 0) return Grid{8u * static_cast<uint32_t>(prm.main_splits) * groups, xcd_rows(prm), 1};
     const uint32_t tail_slices = prm.main_splits < prm.splits
         ? static_cast<uint32_t>(((static_cast<int64_t>(prm.batch) << prm.tail_shift) + prm.main_splits - 1) /
                                 prm.main_splits)
@@ -737,9 +776,10 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
 // Launch shape of the matrix-core kernel on a device of `cus` compute units,
 // for head_dim and K/V elements of elem bytes: head tile, workgroup shape,
 // quarter combine or whole rows, and streaming mode.
-// The XCD-grouped grid (block_coords) for a plain rectangular launch whose
-// row groups all carry the same work: host bounds that give every sequence
-// the same partitions, no tail items, no work list, no whole-row launch. With
+// The XCD-grouped grid (block_coords) for a rectangular launch whose row
+// groups all carry the same work: host bounds that give every sequence the
+// same partitions (and so the same tail items), no work list, no whole-row
+// launch. With
 // the dispatcher dealing workgroups round robin, each XCD then gets the same
 // number of row groups; ragged batches keep the plain grid, which spreads
 // every sequence over all XCDs. A row group must cover whole query heads
@@ -749,16 +789,22 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
 // multiple of 8.
 inline void plan_xcd(PartialParams& prm, int kv_heads) {
     prm.xcd_shift = -1;
-    if (!prm.uniform_live || prm.compact || prm.row_mode || prm.main_splits < prm.splits) return;
+    if (!prm.uniform_live || prm.compact || prm.row_mode) return;
     if (prm.head_tiles != prm.tiles_per_wg) return;
     const int groups = kv_heads / prm.heads_per_wg;
     if ((groups & (groups - 1)) != 0) return;
     const int64_t row_groups = static_cast<int64_t>(prm.batch) * groups;
     if (row_groups % 8 != 0 || row_groups / 8 > 65535) return;
-    if (8ll * prm.main_splits * (kQuarters / prm.quarters_per_wg) > 0x7FFFFFFFll) return;
+    const int quarter_groups = kQuarters / prm.quarters_per_wg;
+    if (8ll * prm.main_splits * quarter_groups > 0x7FFFFFFFll) return;
     int shift = 0;
     while ((1 << shift) < groups) ++shift;
+    int tail_shift = prm.tail_shift;  // tail token groups per row group: 2^tail_shift items x quarter groups
+    while ((1 << (tail_shift - prm.tail_shift)) < quarter_groups) ++tail_shift;
+    prm.xcd_main_rows = static_cast<uint32_t>(row_groups / 8);
+    prm.xcd_tail_shift = tail_shift;
     prm.xcd_shift = shift;
+    if (xcd_rows(prm) > 65535u) prm.xcd_shift = -1;
 }
 
 // Query-head rows of one XCD row group (merge side of plan_xcd), or 0 for the

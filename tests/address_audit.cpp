@@ -276,9 +276,14 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
     for (uint32_t bz = 0; bz < grid.z; ++bz) {
         for (uint32_t by = 0; by < grid.y; ++by) {
             for (uint32_t bx = 0; bx < grid.x; ++bx) {
-                const BlockCoords bc = block_coords(bx, by, bz, p.grid_x, p.grid_y, p.xcd_shift);
-                const int xcd = static_cast<int>((bx + static_cast<uint64_t>(grid.x) * (by + static_cast<uint64_t>(grid.y) * bz)) % 8);
                 const int kind = grid_kind(p);
+                const BlockCoords bc =
+                    kind == kGridRectTails
+                        ? block_coords<kGridRectTails>(bx, by, bz, p.grid_x, p.grid_y, p.xcd_shift, p.xcd_main_rows,
+                                                       p.xcd_tail_shift)
+                        : block_coords<kGridRect>(bx, by, bz, p.grid_x, p.grid_y, p.xcd_shift, p.xcd_main_rows,
+                                                  p.xcd_tail_shift);
+                const int xcd = static_cast<int>((bx + static_cast<uint64_t>(grid.x) * (by + static_cast<uint64_t>(grid.y) * bz)) % 8);
                 const PartitionRange r = kind == kGridList        ? partition_range<kGridList>(p, bc)
                                          : kind == kGridRectTails ? partition_range<kGridRectTails>(p, bc)
                                                                   : partition_range<kGridRect>(p, bc);
@@ -594,6 +599,10 @@ int main(int argc, char** argv) {
     add(make("xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16", 64, 16, 1, 64, 16, 64, uniform(64, 1024), 256, 2, 2, 73));
     add(make("xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", 2, 16, 16, 128, 16, 128, uniform(2, 2048), 256, 2, 2, 75));
     add(make("xcd fp32 B8 Hq16/8 D64 L1024 split 128", 8, 16, 8, 64, 16, 64, uniform(8, 1024), 128, 4, 4, 77));
+    // Reserved context over uniform lengths: tail rows, partly empty slots.
+    add(make("xcd llama3-8b B4 L4096 reserve x4", 4, 32, 8, 128, 16, 1024, uniform(4, 4096), 256, 2, 2, 79, 4));
+    add(make("xcd mqa B128 Hq16/1 D64 L1024 reserve x2", 128, 16, 1, 64, 16, 128, uniform(128, 1024), 256, 2, 2, 81,
+             2));
     // Edge lengths around page and partition boundaries, both page sizes.
     for (int page : {16, 32}) {
         add(make("edges fp16 page " + std::to_string(page), 8, 8, 2, 128, page, 8,

@@ -58,10 +58,11 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
     lines = run.stdout.splitlines()
     for name in ("llama3-8b B4 L4096 fp16", "llama3-8b B4 L4096 fp8", "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp16",
                  "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp8", "xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16",
-                 "xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", "xcd fp32 B8 Hq16/8 D64 L1024 split 128"):
-        exact = [line for line in lines if line.startswith(name + " bounds=exact ")]
+                 "xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", "xcd fp32 B8 Hq16/8 D64 L1024 split 128",
+                 "xcd llama3-8b B4 L4096 reserve x4", "xcd mqa B128 Hq16/1 D64 L1024 reserve x2"):
+        exact = [line for line in lines if line.startswith((name + " bounds=exact ", name + " bounds=half "))]
         plain = [line for line in lines if line.startswith(name + " ") and "bounds=" not in line]
-        assert exact and all("xcd-grouped" in line for line in exact), name
+        assert len(exact) >= 2 and all("xcd-grouped" in line for line in exact), name
         assert plain and not any("xcd-grouped" in line for line in plain), name
 
 

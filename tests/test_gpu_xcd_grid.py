@@ -89,3 +89,31 @@ def test_xcd_grouped_calls_match_oracle_and_plain_grids(name, fmt, merge):
     plan._extension.decode(q, k, v, plan._table, plan._lengths, plan._numerator, plan._stats, out, split,
                            int(plan.merge_implementation == "shared"), k_scale, v_scale)
     torch.testing.assert_close(out, outs[0], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("merge", ["serial", "shared"])
+@pytest.mark.parametrize("name,fmt", [("gqa4 B8 Hq32/8 D128 L1024 split 128", "f16"),
+                                      ("mqa B64 Hq16/1 D64 L1024 split 256", "e4m3"),
+                                      ("fp32 B8 Hq16/8 D64 L1024 split 128", "f32")])
+def test_xcd_grouped_calls_with_tail_items(name, fmt, merge):
+    """Reserved context: the plan's bounds (its host lengths) reach half of
+    max_context, so the grid carries tail items, which follow each row group's
+    main items on its XCD. The device lengths then grow past the bounds to the
+    whole reserve, as appends on the device would, and the tail items cover
+    the growth."""
+    batch, heads, kv_heads, dim, page, length, split, _ = SHAPES[name]
+    q_dtype, kv_dtype = DTYPES[fmt]
+    announce(f"xcd-grouped call with tail items {name} {fmt} merge={merge}")
+    width = length // page
+    rng = np.random.default_rng(batch + heads + 1)
+    layout = Layout(batch, heads, kv_heads, dim, page, batch * width)
+    table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+    lengths = np.full(batch, length // 2, dtype=np.int32)
+    (q, k, v), (k_scale, v_scale), exact = device_inputs(layout, q_dtype, kv_dtype, seed=batch + 1)
+    plan = DecodePlan(layout, table, lengths, split_tokens=split, merge=merge, max_context=length)
+    for live in (length // 2, length - 1, length):
+        plan._lengths.fill_(live)  # as device-side appends would; the host bounds stay at length // 2
+        out = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).clone()
+        torch.cuda.synchronize()
+        grown = np.full(batch, live, dtype=np.int32)
+        assert_parity(out.cpu().numpy(), fp64.dense_attention(*exact, table, grown), q_dtype)
