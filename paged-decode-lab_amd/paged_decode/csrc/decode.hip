@@ -579,7 +579,7 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
     const int status = dispatch_partial(prm, q_dtype, kv_dtype, kv_heads, head_dim, stream);
     if (state_stride) *state_stride = prm.row_mode ? 0 : prm.combine ? prm.quarters_per_wg : 1;
     if (xcd_rows) *xcd_rows = xcd_row_group_rows(prm);
-    if (xcd_shift) *xcd_shift = prm.xcd_shift;
+    if (xcd_shift) *xcd_shift = prm.merge_xcd_shift;
     return status;
 }
 

@@ -114,6 +114,8 @@ struct PartialParams {
     int live_items;        // items holding tokens as far as the bounds tell (plan_items)
     int head_tile;         // GT: query heads per wave's tile (the GQA group padded to 1/2/4/8/16)
     int uniform_live;      // host bounds given, and every sequence reaches the same partitions (plan_items)
+    int merge_xcd_rows;    // rows per row group for an XCD-grouped merge (merge_xcd_row), 0: plain (plan_xcd)
+    int merge_xcd_shift;   // log2 of the head groups per sequence, for that merge
 };
 
 // ---------------------------------------------------------------------------
@@ -779,39 +781,55 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
 // The XCD-grouped grid (block_coords) for a rectangular launch whose row
 // groups all carry the same work: host bounds that give every sequence the
 // same partitions (and so the same tail items), no work list, no whole-row
-// launch. With
-// the dispatcher dealing workgroups round robin, each XCD then gets the same
-// number of row groups; ragged batches keep the plain grid, which spreads
-// every sequence over all XCDs. A row group must cover whole query heads
-// [hg * hw * group, (hg + 1) * hw * group), so the merge can find it from a
-// row index: one head-tile group per KV head. Head groups per sequence must
-// be a power of two (shifts in the kernels) and sequences x head groups a
-// multiple of 8.
+// launch. With the dispatcher dealing workgroups round robin, each XCD then
+// gets the same number of row groups; ragged batches keep the plain grid,
+// which spreads every sequence over all XCDs. A row group must cover whole
+// query heads [hg * hw * group, (hg + 1) * hw * group), so the merge can find
+// it from a row index: one head-tile group per KV head. Head groups per
+// sequence must be a power of two (shifts in the kernels) and sequences x
+// head groups a multiple of 8.
+//
+// With a multiple of 8 head groups per sequence the plain grids (rectangular,
+// with tail slices, or a work list) already keep each row group on one XCD:
+// their linear dispatch index is (token group) * head groups + head group (+
+// a multiple of 8 for later z-slices), so head group hg runs on XCD hg % 8,
+// whatever the lengths. Such launches keep their grid and only the merge is
+// XCD-grouped.
 inline void plan_xcd(PartialParams& prm, int kv_heads) {
     prm.xcd_shift = -1;
-    if (!prm.uniform_live || prm.compact || prm.row_mode) return;
-    if (prm.head_tiles != prm.tiles_per_wg) return;
+    prm.merge_xcd_rows = 0;
+    prm.merge_xcd_shift = 0;
+    if (prm.row_mode || prm.head_tiles != prm.tiles_per_wg) return;
     const int groups = kv_heads / prm.heads_per_wg;
     if ((groups & (groups - 1)) != 0) return;
     const int64_t row_groups = static_cast<int64_t>(prm.batch) * groups;
     if (row_groups % 8 != 0 || row_groups / 8 > 65535) return;
-    const int quarter_groups = kQuarters / prm.quarters_per_wg;
-    if (8ll * prm.main_splits * quarter_groups > 0x7FFFFFFFll) return;
     int shift = 0;
     while ((1 << shift) < groups) ++shift;
+    if (groups % 8 == 0) {
+        prm.merge_xcd_rows = prm.heads_per_wg * prm.group;
+        prm.merge_xcd_shift = shift;
+        return;
+    }
+    if (!prm.uniform_live || prm.compact) return;
+    const int quarter_groups = kQuarters / prm.quarters_per_wg;
+    if (8ll * prm.main_splits * quarter_groups > 0x7FFFFFFFll) return;
     int tail_shift = prm.tail_shift;  // tail token groups per row group: 2^tail_shift items x quarter groups
     while ((1 << (tail_shift - prm.tail_shift)) < quarter_groups) ++tail_shift;
     prm.xcd_main_rows = static_cast<uint32_t>(row_groups / 8);
     prm.xcd_tail_shift = tail_shift;
     prm.xcd_shift = shift;
-    if (xcd_rows(prm) > 65535u) prm.xcd_shift = -1;
+    if (xcd_rows(prm) > 65535u) {
+        prm.xcd_shift = -1;
+        return;
+    }
+    prm.merge_xcd_rows = prm.heads_per_wg * prm.group;
+    prm.merge_xcd_shift = shift;
 }
 
-// Query-head rows of one XCD row group (merge side of plan_xcd), or 0 for the
-// plain grid.
-inline int xcd_row_group_rows(const PartialParams& prm) {
-    return prm.xcd_shift >= 0 ? prm.heads_per_wg * prm.group : 0;
-}
+// Query-head rows of one XCD row group for the merge (plan_xcd), or 0 for
+// the plain merge grid.
+inline int xcd_row_group_rows(const PartialParams& prm) { return prm.merge_xcd_rows; }
 
 // The merge's side of the XCD-grouped grid: merge workgroup (bx, by) of a
 // grid 8 * (group_rows / unit) x row groups / 8 takes `unit` consecutive rows

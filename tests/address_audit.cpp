@@ -159,7 +159,7 @@ void check_merge_xcd(const Problem& pr, const PartialParams& p, const Coverage& 
             for (uint32_t bx = 0; bx < gx; ++bx) {
                 const int xcd = static_cast<int>((bx + static_cast<uint64_t>(gx) * by) % 8);
                 for (int sub = 0; sub < unit; ++sub) {
-                    const MergeRow m = merge_xcd_row(bx, by, group_rows, p.xcd_shift, unit, sub);
+                    const MergeRow m = merge_xcd_row(bx, by, group_rows, p.merge_xcd_shift, unit, sub);
                     AUDIT(m.row >= 0 && m.row < rows, "merge row %" PRId64, m.row);
                     if (m.row < 0 || m.row >= rows) continue;
                     AUDIT(m.b == m.row / pr.q_heads, "merge row %" PRId64 " given sequence %d", m.row, m.b);
@@ -478,7 +478,7 @@ bool audit(const Problem& pr, bool rows) {
             AUDIT(out.writes[e] == 1, "output element %zu written %d times", e, out.writes[e]);
     } else {
         check_coverage(pr, cov);
-        if (p.xcd_shift >= 0) check_merge_xcd(pr, p, cov);
+        if (p.merge_xcd_rows > 0) check_merge_xcd(pr, p, cov);
     }
     const Grid grid = partial_grid(p, pr.kv_heads);
     std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s%s, %" PRIu64 " checks: %s\n",
@@ -486,7 +486,8 @@ bool audit(const Problem& pr, bool rows) {
                 partial_threads(p) / kWave, p.head_tile, p.quarters_per_wg,
                 p.row_mode ? "whole rows" : p.compact ? "compact" : p.main_splits < p.splits ? "rectangular+tails"
                                                                                               : "rectangular",
-                p.combine ? ", combined" : "", p.xcd_shift >= 0 ? ", xcd-grouped" : "",
+                p.combine ? ", combined" : "",
+                p.xcd_shift >= 0 ? ", xcd-grouped" : p.merge_xcd_rows > 0 ? ", xcd merge" : "",
                 g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
     std::fflush(stdout);
     return g_failures == before;
@@ -599,6 +600,11 @@ int main(int argc, char** argv) {
     add(make("xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16", 64, 16, 1, 64, 16, 64, uniform(64, 1024), 256, 2, 2, 73));
     add(make("xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", 2, 16, 16, 128, 16, 128, uniform(2, 2048), 256, 2, 2, 75));
     add(make("xcd fp32 B8 Hq16/8 D64 L1024 split 128", 8, 16, 8, 64, 16, 64, uniform(8, 1024), 128, 4, 4, 77));
+    // Eight head groups per sequence: the plain grids (rectangular, with
+    // tails, or a work list) already keep a row group on one XCD, and only
+    // the merge is XCD-grouped, whatever the lengths.
+    add(make("xcd merge ragged mha B16 Hq32/32 D128 split 128", 16, 32, 32, 128, 16, 64, ragged(16, 1024, 83), 128, 2,
+             2, 83));
     // Reserved context over uniform lengths: tail rows, partly empty slots.
     add(make("xcd llama3-8b B4 L4096 reserve x4", 4, 32, 8, 128, 16, 1024, uniform(4, 4096), 256, 2, 2, 79, 4));
     add(make("xcd mqa B128 Hq16/1 D64 L1024 reserve x2", 128, 16, 1, 64, 16, 128, uniform(128, 1024), 256, 2, 2, 81,

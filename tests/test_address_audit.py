@@ -54,7 +54,11 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
                    "long mha B1 Hq32/32 L32768 split 128 bounds=exact coarse x8"):
         assert needle in run.stdout, needle
     # The XCD-grouped grid is chosen for the measured uniform workloads and the
-    # shapes of tests/test_gpu_xcd_grid.py, under exact bounds, and not without.
+    # shapes of tests/test_gpu_xcd_grid.py under bounds, and not without them;
+    # with eight head groups per sequence only the merge is XCD-grouped (the
+    # plain grids already are), bounds or not.
+    assert "xcd merge" in "\n".join(line for line in run.stdout.splitlines()
+                                     if line.startswith("long mha B1 Hq32/32 L32768 split 1024 "))
     lines = run.stdout.splitlines()
     for name in ("llama3-8b B4 L4096 fp16", "llama3-8b B4 L4096 fp8", "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp16",
                  "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp8", "xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16",
@@ -62,7 +66,7 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
                  "xcd llama3-8b B4 L4096 reserve x4", "xcd mqa B128 Hq16/1 D64 L1024 reserve x2"):
         exact = [line for line in lines if line.startswith((name + " bounds=exact ", name + " bounds=half "))]
         plain = [line for line in lines if line.startswith(name + " ") and "bounds=" not in line]
-        assert len(exact) >= 2 and all("xcd-grouped" in line for line in exact), name
+        assert len(exact) >= 2 and all("xcd-grouped" in line or "xcd merge" in line for line in exact), name
         assert plain and not any("xcd-grouped" in line for line in plain), name
 
 

@@ -4,7 +4,9 @@ A plain rectangular call whose host bounds give every sequence the same
 partitions runs its partition workgroups so that each row group (a
 sequence's head group) stays on one XCD, and its merge workgroups so that
 each row is merged on that same XCD (``plan_xcd``, ``block_coords``,
-``merge_xcd_row``). The planner's choice for these shapes, and that both
+``merge_xcd_row``). With eight head groups per sequence (the MHA shape here)
+the plain grids already keep row groups on one XCD, and only the merge is
+XCD-grouped. The planner's choice for these shapes, and that both
 mappings cover every state and row exactly once on matching XCDs, is checked
 on the CPU by the address audit (``tests/address_audit.cpp``, problems named
 ``xcd ...``). Here the calls are checked against the FP64 oracle on exactly the
@@ -84,7 +86,8 @@ def test_xcd_grouped_calls_match_oracle_and_plain_grids(name, fmt, merge):
     torch.testing.assert_close(outs[1], outs[0], rtol=0, atol=0)
     actual = outs[0].cpu().numpy()
     assert_parity(actual, fp64.dense_attention(*exact, table, lengths), q_dtype)
-    # Without bounds the same entry plans plain partition and merge grids.
+    # Without bounds the same entry plans plain partition grids (and, but for
+    # the MHA shape, plain merge grids).
     out = torch.empty_like(outs[0])
     plan._extension.decode(q, k, v, plan._table, plan._lengths, plan._numerator, plan._stats, out, split,
                            int(plan.merge_implementation == "shared"), k_scale, v_scale)
