@@ -775,9 +775,6 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
     prm.tail_shift = 0;
 }
 
-// Launch shape of the matrix-core kernel on a device of `cus` compute units,
-// for head_dim and K/V elements of elem bytes: head tile, workgroup shape,
-// quarter combine or whole rows, and streaming mode.
 // The XCD-grouped grid (block_coords) for a rectangular launch whose row
 // groups all carry the same work: host bounds that give every sequence the
 // same partitions (and so the same tail items), no work list, no whole-row
@@ -847,6 +844,9 @@ PD_HD MergeRow merge_xcd_row(uint32_t bx, uint32_t by, int group_rows, int xcd_s
                     static_cast<int64_t>(r) * group_rows + static_cast<int64_t>(bx >> 3) * unit + sub};
 }
 
+// Launch shape of the matrix-core kernel on a device of `cus` compute units,
+// for head_dim and K/V elements of elem bytes: head tile, workgroup shape,
+// quarter combine or whole rows, and streaming mode.
 inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, int elem) {
     const int gt = head_tile(prm.group, 16);
     prm.head_tile = gt;
@@ -965,6 +965,17 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     }
     plan_rows(prm, head_dim, elem, combine_slot_bytes(head_dim), mfma_stage_bytes(head_dim, elem));
     plan_xcd(prm, kv_heads);
+    // Where the merge reads its states from the XCD's L2 (plan_xcd), the fold
+    // of the mid-size grids' two quarters no longer pays for its tail: their
+    // states are few per KV byte (GQA groups of up to 8). Measured on MI355X
+    // (decode call, us, combined -> not): Llama-3-8B B4 L4096 16.85-16.87 ->
+    // 16.64-16.66, its FP8 form 14.31-14.38 -> 13.94-13.96, FP8 B8 L2048
+    // 15.28-15.30 -> 14.27-14.30, B8 L4096 27.61 -> 27.43, Llama-3-8B with
+    // twice the context reserved 17.39-17.47 -> 17.26-17.32. The same for
+    // every XCD-merged launch was slower where states are many per KV byte or
+    // the quarters long: MQA B128 13.8 -> 15.15, uniform B32 L4096 (four
+    // quarters) 88.5 -> 92.2.
+    if (prm.mid_grid && prm.merge_xcd_rows > 0) prm.combine = 0;
     const Grid grid = partial_grid(prm, kv_heads);
     prm.grid_x = grid.x;
     prm.grid_y = grid.y;

@@ -493,7 +493,10 @@ def test_partial_then_merge_equals_decode():
 
 
 def test_raw_c_abi_matches_extension():
-    """Calls the C ABI through ctypes with device pointers; same bits as DecodePlan."""
+    """Calls the C ABI through ctypes with device pointers. ``pd_decode_ex`` given
+    the plan's host bounds and hints plans the same launches as DecodePlan and
+    gives the same bits; ``pd_decode`` (no bounds: plain grids, whose states
+    may be combined differently) the same attention to FP32 rounding."""
     lib = cabi.load()
     w = make_workload("llama3_8b_b4_l4096")
     q, k, v = (torch.from_numpy(x).cuda() for x in w.host_tensors())
@@ -506,18 +509,31 @@ def test_raw_c_abi_matches_extension():
     out = torch.full_like(plan._out, float("nan"))
     L = w.layout
     stream = torch.cuda.current_stream().cuda_stream
-    announce("raw C ABI pd_decode")
+    announce("raw C ABI pd_decode_ex with the plan's bounds and hints, then pd_decode")
+    bounds = np.ascontiguousarray(w.lengths, dtype=np.int32)
+    hints = (cabi.PD_HINT_UNSHARED_PAGES if plan._unshared_pages else 0) | \
+        (cabi.PD_HINT_RAGGED_LENGTHS if plan._ragged_lengths else 0)
     for merge in (cabi.PD_MERGE_SERIAL, cabi.PD_MERGE_SHARED):
-        status = lib.pd_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16, table.data_ptr(),
-                               lengths.data_ptr(), numerator.data_ptr(), stats.data_ptr(), out.data_ptr(),
-                               L.batch, L.query_heads, L.kv_heads, L.head_dim, L.page_size, w.table.shape[1],
-                               L.physical_pages, plan.splits, w.split_tokens, merge, ctypes.c_void_p(stream))
+        out.fill_(float("nan"))
+        status = lib.pd_decode_ex(q.data_ptr(), cabi.PD_DTYPE_F16, k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16,
+                                  1.0, 1.0, table.data_ptr(), lengths.data_ptr(), numerator.data_ptr(),
+                                  stats.data_ptr(), out.data_ptr(), L.batch, L.query_heads, L.kv_heads,
+                                  L.head_dim, L.page_size, w.table.shape[1], L.physical_pages, plan.splits,
+                                  w.split_tokens, merge, hints, bounds.ctypes.data, ctypes.c_void_p(stream))
         assert status == cabi.PD_OK, cabi.status_string(lib, status)
         torch.cuda.synchronize()
         if merge == cabi.PD_MERGE_SERIAL:
             torch.testing.assert_close(out, expected, rtol=0, atol=0)
         else:
             torch.testing.assert_close(out, expected, rtol=0, atol=1e-6)
+        out.fill_(float("nan"))
+        status = lib.pd_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), cabi.PD_DTYPE_F16, table.data_ptr(),
+                               lengths.data_ptr(), numerator.data_ptr(), stats.data_ptr(), out.data_ptr(),
+                               L.batch, L.query_heads, L.kv_heads, L.head_dim, L.page_size, w.table.shape[1],
+                               L.physical_pages, plan.splits, w.split_tokens, merge, ctypes.c_void_p(stream))
+        assert status == cabi.PD_OK, cabi.status_string(lib, status)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, expected, rtol=1e-5, atol=1e-6)
 
 
 def test_device_page_guard_skips_invalid_ids():
