@@ -120,3 +120,41 @@ def test_xcd_grouped_calls_with_tail_items(name, fmt, merge):
         torch.cuda.synchronize()
         grown = np.full(batch, live, dtype=np.int32)
         assert_parity(out.cpu().numpy(), fp64.dense_attention(*exact, table, grown), q_dtype)
+
+
+def stress_cases(count=32, seed=2026):
+    """Seeded shapes for the stress below (kept small enough for the FP64 oracle)."""
+    rng = np.random.default_rng(seed)
+    layouts = [(32, 8), (16, 8), (32, 4), (16, 2), (16, 1), (32, 32), (8, 8), (64, 8), (24, 8)]
+    formats = ["f16", "bf16", "e4m3", "f32"]
+    cases = []
+    for _ in range(count):
+        heads, kv_heads = layouts[rng.integers(len(layouts))]
+        batch = int(rng.choice([1, 2, 3, 4, 6, 8, 16] if kv_heads < 32 else [1, 2]))
+        cases.append(dict(heads=heads, kv_heads=kv_heads, batch=batch, fmt=formats[rng.integers(len(formats))],
+                          dim=int(rng.choice([64, 128])), page=int(rng.choice([16, 32])),
+                          split=int(rng.choice([64, 128, 256])), length=int(rng.integers(1, 1025)),
+                          reserve=int(rng.choice([1, 2])), merge="shared" if rng.random() < 0.5 else "serial"))
+    return cases
+
+
+def test_randomized_uniform_calls():
+    """A seeded stress over uniform batches with host bounds: batch sizes and
+    head layouts that do and do not make the XCD-grouped grid (sequences x head
+    groups a multiple of 8 or not, eight head groups per sequence or fewer),
+    reserved context (tail rows) or none, page 16 / 32, D 64 / 128, FP16, BF16,
+    FP8 and FP32, both merges; every call against the FP64 oracle."""
+    for case, c in enumerate(stress_cases()):
+        announce(f"xcd stress {case}: {c}")
+        q_dtype, kv_dtype = DTYPES[c["fmt"]]
+        batch, length, page = c["batch"], c["length"], c["page"]
+        width = -(-length * c["reserve"] // page)
+        layout = Layout(batch, c["heads"], c["kv_heads"], c["dim"], page, batch * width)
+        table = np.random.default_rng(case).permutation(batch * width).reshape(batch, width).astype(np.int32)
+        lengths = np.full(batch, length, dtype=np.int32)
+        (q, k, v), (k_scale, v_scale), exact = device_inputs(layout, q_dtype, kv_dtype, seed=case)
+        plan = DecodePlan(layout, table, lengths, split_tokens=c["split"], merge=c["merge"],
+                          max_context=length * c["reserve"])
+        out = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).clone()
+        torch.cuda.synchronize()
+        assert_parity(out.cpu().numpy(), fp64.dense_attention(*exact, table, lengths), q_dtype)
