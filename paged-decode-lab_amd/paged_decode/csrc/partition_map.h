@@ -451,7 +451,8 @@ inline int largest_divisor(int n, int cap) {
 // batch of the reference's benchmark 50.7 -> 40.2 us, B64 L2048 122.3 ->
 // 103.8 us; with 32 KV heads, 32K-context MHA 97.2 -> 89.8 us at split 256.
 // Grids that would leave most CUs idle take smaller workgroups instead, and
-// grids smaller than the device skip the combine (see plan_mfma).
+// grids smaller than the device skip the combine, as do mid-size grids whose
+// merge is XCD-grouped (see plan_mfma).
 inline void choose_workgroup(PartialParams& prm, int kv_heads, int max_heads, int waves = 8) {
     prm.heads_per_wg = largest_divisor(kv_heads, imin(max_heads, waves));
     if (prm.heads_per_wg == 1 && kv_heads <= waves) prm.heads_per_wg = kv_heads;
@@ -866,7 +867,8 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     //
     // Grids of one to two 8-wave workgroups per CU with 2, 4 or 8 KV heads and
     // GQA groups of up to 8 take workgroups of 2 KV heads x 2 quarters instead
-    // (4 waves, quarters combined). Measured on MI355X by graph replay of 200
+    // (4 waves; quarters combined where the merge is not XCD-grouped, see the
+    // end of this function). Measured on MI355X by graph replay of 200
     // calls, N(0,1) data, K/V sets rotated past the Infinity Cache (decode
     // call, us): Llama-3-8B B4 L4096 18.0-18.4 -> 17.4-17.6, B8 L4096 29.45
     // -> 28.54, B16 L4096 with 2 KV heads (GQA 8) 20.2-20.9 -> 18.5-18.8, B8
