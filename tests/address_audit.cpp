@@ -605,6 +605,39 @@ int main(int argc, char** argv) {
     // the merge is XCD-grouped, whatever the lengths.
     add(make("xcd merge ragged mha B16 Hq32/32 D128 split 128", 16, 32, 32, 128, 16, 64, ragged(16, 1024, 83), 128, 2,
              2, 83));
+    // Seeded random problems (small sizes), each with every kind of bounds:
+    // batch sizes and head layouts that do and do not make the XCD-grouped
+    // grids, uniform and ragged lengths, reserved context, both page sizes,
+    // head dimensions and element sizes.
+    {
+        Lcg rng{2026};
+        const int kv_choices[] = {1, 2, 4, 8, 16, 32};
+        const int group_choices[] = {1, 2, 3, 4, 8, 16};
+        const int batch_choices[] = {1, 2, 3, 4, 6, 8, 12, 16};
+        const int split_choices[] = {16, 32, 64, 128, 256};
+        for (int i = 0; i < (quick ? 8 : 40); ++i) {
+            const int kv = kv_choices[rng.below(6)];
+            const int group = group_choices[rng.below(6)];
+            const int batch = batch_choices[rng.below(8)];
+            const int dim = rng.below(2) ? 128 : 64;
+            const int page = rng.below(2) ? 32 : 16;
+            const int split = split_choices[rng.below(5)];
+            const int len = 1 + rng.below(1024);
+            const bool uni = rng.below(2) != 0;
+            const int reserve = 1 + rng.below(2);
+            const int elems = rng.below(3);  // 0: FP16, 1: FP8 K/V, 2: FP32
+            const int q_elem = elems == 2 ? 4 : 2, kv_elem = elems == 0 ? 2 : elems == 1 ? 1 : 4;
+            const int width = (len * reserve + page - 1) / page;
+            const std::string name = "random " + std::to_string(i) + " B" + std::to_string(batch) + " Hq" +
+                                     std::to_string(kv * group) + "/" + std::to_string(kv) + " D" +
+                                     std::to_string(dim) + " T" + std::to_string(page) + (uni ? " L" : " ragged L") +
+                                     std::to_string(len) + " x" + std::to_string(reserve) + " split " +
+                                     std::to_string(split) + (elems == 2 ? " fp32" : elems == 1 ? " fp8" : " fp16");
+            add(make(name, batch, kv * group, kv, dim, page, width,
+                     uni ? uniform(batch, len) : ragged(batch, len, 100 + i), split, q_elem, kv_elem, 100 + i,
+                     reserve));
+        }
+    }
     // Reserved context over uniform lengths: tail rows, partly empty slots.
     add(make("xcd llama3-8b B4 L4096 reserve x4", 4, 32, 8, 128, 16, 1024, uniform(4, 4096), 256, 2, 2, 79, 4));
     add(make("xcd mqa B128 Hq16/1 D64 L1024 reserve x2", 128, 16, 1, 64, 16, 128, uniform(128, 1024), 256, 2, 2, 81,
