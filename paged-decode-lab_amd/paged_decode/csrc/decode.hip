@@ -102,30 +102,38 @@ struct MergeParams {
     int xcd_shift;           // log2 of that grid's head groups per sequence
 };
 
-// merge_cols_kernel: a row's D columns are cut into 128-byte chunks and each
-// (row, chunk) is one 256-lane workgroup, so D / 32 workgroups read a row's
-// states together. Lane t owns the 16-byte column t % 8 of the chunk for the
-// states j == t / 8 (mod 32) and issues up to NB of those loads in one round
-// (NB = 8 or 32: 256 or 1024 states), together with the first round of the
-// statistics scan, which is kept in registers for the denominator. Longer rows
-// repeat both rounds. All loads use clamped indexes and are masked afterwards,
-// so they issue back to back.
-constexpr int kMergeChunk = 32;                                   // floats per column chunk
-constexpr int kMergeColLanes = kMergeChunk / 4;                   // lanes per state slice
-constexpr int kMergeColGroups = kMergeThreads / kMergeColLanes;  // state groups per workgroup
+// merge_cols_kernel: a row's D columns are cut into chunks of CH floats and
+// each (row, chunk) is one 256-lane workgroup, so D / CH workgroups read a
+// row's states together. Lane t owns the 16-byte column t % (CH / 4) of the
+// chunk for the states j == t / (CH / 4) (mod 1024 / CH) and issues up to NB
+// of those loads in one round (NB = 8 or 32), together with the first round
+// of the statistics scan, which is kept in registers for the denominator.
+// Longer rows repeat both rounds. All loads use clamped indexes and are masked
+// afterwards, so they issue back to back.
+//
+// Every workgroup of a row scans the row's statistics, so wider chunks scan
+// them fewer times per row. That pays where the states come from other XCDs'
+// writes; an XCD-grouped merge (states in its own L2) keeps the narrower
+// chunk and twice the workgroups. Measured on MI355X (decode call, us, 32 ->
+// 64 floats): ragged + shared B16 (plain grids, 512 rows of 28 states) 32.24-
+// 32.28 -> 30.48-30.73, the reference's B4 / B16 batches 14.60 -> 14.51 /
+// 41.11 -> 41.07; XCD-grouped 32K-context MHA 86.05 -> 86.17 and B1 L4096
+// 9.60 -> 9.68, Llama-3-8B B4 L4096 unchanged.
+constexpr int kMergeChunkLocal = 32;  // floats per column chunk, XCD-grouped merge
+constexpr int kMergeChunkWide = 64;   // floats per column chunk, otherwise
 constexpr int kMergeColBatchShort = 8;                            // numerator loads per lane per round
 constexpr int kMergeColBatchLong = 32;
 constexpr int kOptimisticRounds = 2;  // first-round loads issued before the live count (64 states)
 
-template <int D, bool kSharedWeights, int NB>
+template <int D, bool kSharedWeights, int NB, int CH>
 __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergeParams mp) {
-    constexpr int TPR = kMergeColLanes;
-    constexpr int PG = kMergeColGroups;
+    constexpr int TPR = CH / 4;              // lanes per state slice
+    constexpr int PG = kMergeThreads / TPR;  // state groups per workgroup
     constexpr int SU = NB / 2;  // (m, l) loads per scanning lane per round: a serial wave scans NB * PG states
     constexpr int kWaves = kMergeThreads / kWave;
     constexpr int kScan = kSharedWeights ? kMergeThreads : kWave;  // lanes sharing the state scan
     constexpr int kScanRound = SU * kScan;
-    static_assert(D % kMergeChunk == 0, "whole chunks");
+    static_assert(D % CH == 0, "whole chunks");
     extern __shared__ float weight[];  // [parts], shared variant only
     __shared__ f32x4 column_sum[PG][TPR];
     __shared__ float wave_partial[2][kWaves];
@@ -150,7 +158,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int scan0 = kSharedWeights ? t : lane;
     const int last = parts - 1;
     const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * mp.parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D + chunk * kMergeChunk) + col;
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D + chunk * CH) + col;
     const int64_t num_step = static_cast<int64_t>(D / 4) << shift;
 
     auto rounds_from = [&](int base, int limit) { return min(NB, (limit - base + PG - 1) / PG); };
@@ -269,11 +277,11 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     }
     column_sum[pg][col] = acc;
     __syncthreads();
-    if (t < kMergeChunk) {
+    if (t < CH) {
         float sum = 0.0f;
 #pragma unroll
         for (int g = 0; g < PG; ++g) sum += reinterpret_cast<const float*>(column_sum[g])[t];
-        mp.out[row * D + chunk * kMergeChunk + t] = den > 0.0f ? sum / den : 0.0f;
+        mp.out[row * D + chunk * CH + t] = den > 0.0f ? sum / den : 0.0f;
     }
 }
 
@@ -584,6 +592,32 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
 }
 
 
+template <int D, int CH>
+int launch_merge_cols(const MergeParams& mp, int batch, uint32_t row_groups, int states, bool shared,
+                      hipStream_t stream) {
+    const dim3 grid = mp.xcd_rows > 0 ? dim3(8 * mp.xcd_rows, row_groups, D / CH) : dim3(mp.query_heads, batch, D / CH);
+    const dim3 block(kMergeThreads);
+    const size_t lds = shared ? states * sizeof(float) : 0;
+    // The long-row variant issues 1024 states' loads per round but holds one
+    // (serial) or two (shared) workgroups per CU: it pays only while the grid
+    // fits the device in one round. Larger grids take 256-state rounds at full
+    // occupancy (rows of a plan whose reserved context exceeds the live one
+    // among them: the variant follows the allocated states).
+    constexpr int kGroups = kMergeThreads / (CH / 4);
+    const int64_t workgroups = static_cast<int64_t>(grid.x) * grid.y * grid.z;
+    const bool long_rows = states > kMergeColBatchShort * kGroups && workgroups <= device_compute_units();
+    if (shared && long_rows) {
+        hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchLong, CH>), grid, block, lds, stream, mp);
+    } else if (shared) {
+        hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchShort, CH>), grid, block, lds, stream, mp);
+    } else if (long_rows) {
+        hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchLong, CH>), grid, block, lds, stream, mp);
+    } else {
+        hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchShort, CH>), grid, block, lds, stream, mp);
+    }
+    return launch_status();
+}
+
 template <int D>
 int launch_merge(MergeParams mp, int batch, int merge_mode, hipStream_t stream) {
     const bool shared = merge_mode == PD_MERGE_SHARED;
@@ -592,8 +626,8 @@ int launch_merge(MergeParams mp, int batch, int merge_mode, hipStream_t stream) 
         ? static_cast<uint32_t>(static_cast<int64_t>(batch) * mp.query_heads / mp.xcd_rows / 8) : 0u;
     const int states = mp.parts >> mp.stride_shift;
     // merge_rows keeps a row in one wave, loading (states / PGW) 16-byte
-    // columns per lane; with few rows of many states, merge_cols (D / 32
-    // workgroups per row) finishes sooner.
+    // columns per lane; with few rows of many states, merge_cols (D / 32 or
+    // D / 64 workgroups per row) finishes sooner.
     const int rounds = (states + kWave / (D / 4) - 1) / (kWave / (D / 4));
     const bool many_rows = static_cast<int64_t>(batch) * mp.query_heads >= kMergeRowsMin;
     if (states <= merge_wave_max_parts<D>() && (many_rows || rounds <= 2)) {
@@ -610,27 +644,8 @@ int launch_merge(MergeParams mp, int batch, int merge_mode, hipStream_t stream) 
         }
         return launch_status();
     }
-    const dim3 grid = mp.xcd_rows > 0 ? dim3(8 * mp.xcd_rows, row_groups, D / kMergeChunk)
-                                      : dim3(mp.query_heads, batch, D / kMergeChunk);
-    const dim3 block(kMergeThreads);
-    const size_t lds = shared ? states * sizeof(float) : 0;
-    // The long-row variant issues 1024 states' loads per round but holds one
-    // (serial) or two (shared) workgroups per CU: it pays only while the grid
-    // fits the device in one round. Larger grids take 256-state rounds at full
-    // occupancy (rows of a plan whose reserved context exceeds the live one
-    // among them: the variant follows the allocated states).
-    const int64_t workgroups = static_cast<int64_t>(grid.x) * grid.y * grid.z;
-    const bool long_rows = states > kMergeColBatchShort * kMergeColGroups && workgroups <= device_compute_units();
-    if (shared && long_rows) {
-        hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchLong>), grid, block, lds, stream, mp);
-    } else if (shared) {
-        hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchShort>), grid, block, lds, stream, mp);
-    } else if (long_rows) {
-        hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchLong>), grid, block, lds, stream, mp);
-    } else {
-        hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchShort>), grid, block, lds, stream, mp);
-    }
-    return launch_status();
+    return mp.xcd_rows > 0 ? launch_merge_cols<D, kMergeChunkLocal>(mp, batch, row_groups, states, shared, stream)
+                           : launch_merge_cols<D, kMergeChunkWide>(mp, batch, row_groups, states, shared, stream);
 }
 
 int check_hints(int hints) {
