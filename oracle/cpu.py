@@ -6,6 +6,7 @@ and returns the FP32 ``[B, Hq, D]`` output. Built by ``make -C oracle``.
 import ctypes
 import os
 import subprocess
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -15,8 +16,18 @@ LIBRARY = _HERE / "libpd_cpu.so"
 _lib = None
 
 
+def _gpu_initialised():
+    torch = sys.modules.get("torch")
+    return torch is not None and torch.cuda.is_initialized()
+
+
 def build(verbose=False):
-    """Compile ``libpd_cpu.so`` next to its source."""
+    """Compile ``libpd_cpu.so`` next to its source. Refused (RuntimeError) in a
+    process that has initialised the GPU, which must not start a child
+    process (here ``make`` and the compiler): build it beforehand."""
+    if _gpu_initialised():
+        raise RuntimeError("building oracle/libpd_cpu.so would start make from a process that has initialised the "
+                           "GPU; build it first (make -C oracle) and restart")
     result = subprocess.run(["make", "-B", "-C", str(_HERE), "libpd_cpu.so"],
                             capture_output=not verbose, text=True)
     if result.returncode != 0:

@@ -47,7 +47,24 @@ def source_digest():
     return h.hexdigest()[:16]
 
 
+def gpu_initialised():
+    """Whether this process has initialised the GPU runtime (as torch sees it)."""
+    torch = sys.modules.get("torch")
+    return torch is not None and torch.cuda.is_initialized()
+
+
+def refuse_after_gpu_init(what):
+    """Raise instead of starting a child process from a process that has
+    initialised the GPU: on this stack a program started from such a process
+    (a compiler, git) can take the GPU runtime down with it. Build first, in
+    a process that has not touched the GPU."""
+    if gpu_initialised():
+        raise RuntimeError(f"{what} would start a child process from a process that has initialised the GPU; "
+                           f"build the native libraries first (python -m paged_decode._build) and restart")
+
+
 def _run(cmd, verbose):
+    refuse_after_gpu_init(f"running {Path(str(cmd[0])).name}")
     if verbose:
         print(" ".join(str(c) for c in cmd), flush=True)
     result = subprocess.run([str(c) for c in cmd], capture_output=True, text=True)
@@ -132,7 +149,10 @@ def git_head(repo=REPO):
 
 
 def git_dirty(repo=REPO):
-    """True when tracked files differ from HEAD, None when git cannot tell."""
+    """True when tracked files differ from HEAD, None when git cannot tell
+    (also in a process that has initialised the GPU, which starts no git)."""
+    if gpu_initialised():
+        return None
     try:
         status = subprocess.check_output(["git", "status", "--porcelain", "--untracked-files=no"], cwd=repo,
                                          text=True, stderr=subprocess.DEVNULL, timeout=10)

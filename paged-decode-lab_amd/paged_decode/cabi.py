@@ -9,6 +9,11 @@ from pathlib import Path
 
 LIBRARY = Path(__file__).resolve().parent / "libpaged_decode_hip.so"
 
+# The header's PD_ABI_VERSION these prototypes follow; load() refuses a
+# library that reports another (a stale build would read arguments added
+# since then, such as length_bounds or max_context, as its stream).
+PD_ABI_VERSION = 14
+
 PD_OK = 0
 PD_ERR_NULL_POINTER = 1
 PD_ERR_SHAPE = 2
@@ -53,8 +58,15 @@ PROTOTYPES = {
 
 
 def load(path=LIBRARY):
-    """Load the library and attach the prototypes (raises OSError if absent)."""
+    """Load the library and attach the prototypes. Raises OSError if it is
+    absent or reports an ABI version other than ``PD_ABI_VERSION``."""
     lib = ctypes.CDLL(str(path))
+    lib.pd_abi_version.restype = ctypes.c_int
+    lib.pd_abi_version.argtypes = []
+    version = lib.pd_abi_version()
+    if version != PD_ABI_VERSION:
+        raise OSError(f"{path} implements paged_decode ABI {version}, these prototypes follow ABI "
+                      f"{PD_ABI_VERSION}: rebuild the library (python -m paged_decode._build)")
     for name, (restype, argtypes) in PROTOTYPES.items():
         fn = getattr(lib, name)
         fn.restype = restype

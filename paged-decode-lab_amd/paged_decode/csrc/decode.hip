@@ -79,9 +79,10 @@ constexpr int kMergeThreads = 256;
 // States of row b to merge: per_part per partition up to the last one
 // holding a token of the sequence (none for an empty sequence), capped at the
 // row's states. Partitions past the end are never written and never read.
-__device__ __forceinline__ int live_parts(const int32_t* lengths, int b, int split_tokens, int capacity,
+// reach: the tokens the call may read (PartialParams::reach).
+__device__ __forceinline__ int live_parts(const int32_t* lengths, int b, int split_tokens, int reach,
                                           int per_part, int states) {
-    const int len = max(0, min(lengths[b], capacity));  // decode.cu:42-44
+    const int len = max(0, min(lengths[b], reach));  // decode.cu:42-44
     const int64_t live = (static_cast<int64_t>(len) + split_tokens - 1) / split_tokens;
     return static_cast<int>(min<int64_t>(per_part * live, states));
 }
@@ -95,7 +96,7 @@ struct MergeParams {
     int stride_shift;        // read every (1 << stride_shift)-th state: 0, or log2 of the combined quarters
     int query_heads;
     int split_tokens;
-    int capacity;            // table_width * page_size
+    int reach;               // tokens a row may hold: min(caller's splits * split_tokens, table_width * page_size)
     int first_states;        // states (read units) loaded before the live count arrives: the host's
                              // bound on any row's live states, else the whole row
     int xcd_rows;            // rows per row group of an XCD-grouped partition grid (merge_xcd_row), 0: plain
@@ -185,7 +186,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int first_n = max(1, min(parts, mp.first_states));
     const int optimistic = min(kOptimisticRounds, rounds_from(0, first_n));
     load_rounds(0, 0, optimistic);
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, kQuarters >> shift, parts);
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.reach, kQuarters >> shift, parts);
     load_rounds(0, optimistic, rounds_from(0, live));
 
     auto scan_round = [&](int base, int limit, float2 (&sv)[SU]) {
@@ -330,7 +331,7 @@ __global__ void __launch_bounds__(kWave * RPG) merge_rows_kernel(const MergePara
     const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * mp.parts;
     const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D) + col;
     const int rounds = (parts + PGW - 1) / PGW;  // uniform, <= NB
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.capacity, kQuarters >> shift, parts);
+    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.reach, kQuarters >> shift, parts);
 
     f32x4 buf[NB];
     float2 own[NB];
@@ -544,7 +545,7 @@ PartialParams partial_params(const void* q, const void* k, const void* v, int kv
                              float v_scale, const int32_t* table, const int32_t* lengths, float* numerator,
                              float* stats, float* out, int batch, int query_heads, int kv_heads, int head_dim,
                              int page_size, int table_width, int physical_pages, int splits, int split_tokens,
-                             int hints, const int32_t* length_bounds) {
+                             int hints, const int32_t* length_bounds, int reach) {
     PartialParams prm{};
     prm.batch = batch;
     prm.unshared_pages = (hints & PD_HINT_UNSHARED_PAGES) != 0;
@@ -565,6 +566,7 @@ PartialParams partial_params(const void* q, const void* k, const void* v, int kv
     prm.physical_pages = physical_pages;
     prm.splits = splits;
     prm.split_tokens = split_tokens;
+    prm.reach = reach;
     prm.token_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * element_size(kv_dtype));
     prm.page_bytes = static_cast<uint64_t>(page_size) * prm.token_bytes;
     prm.scale_log2 = kLog2e * k_scale / sqrtf(static_cast<float>(head_dim));
@@ -573,17 +575,28 @@ PartialParams partial_params(const void* q, const void* k, const void* v, int kv
     return prm;
 }
 
+// Tokens of a row that `splits` partitions of `split_tokens` reach in a table
+// of `table_width` pages: the reference's grid of splits partitions reads no
+// further (decode.cu:42-44, :176).
+int call_reach(int splits, int split_tokens, int table_width, int page_size) {
+    return static_cast<int>(lmin(static_cast<int64_t>(splits) * split_tokens,
+                                 static_cast<int64_t>(table_width) * page_size));
+}
+
 // state_stride (if given) receives the merge's stride over the states: 1,
 // the quarters combined per state, or 0 after a whole-row launch (no merge).
+// reach: the caller's call_reach, when the launch runs over a coarser split
+// than the caller's (else taken from splits and split_tokens).
 int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale, float v_scale,
                 const int32_t* table, const int32_t* lengths, float* numerator, float* stats, int batch,
                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
                 int splits, int split_tokens, int hints, const int32_t* length_bounds, hipStream_t stream,
                 float* out = nullptr, int* state_stride = nullptr, int* xcd_rows = nullptr,
-                int* xcd_shift = nullptr) {
+                int* xcd_shift = nullptr, int reach = -1) {
+    if (reach < 0) reach = call_reach(splits, split_tokens, table_width, page_size);
     PartialParams prm = partial_params(q, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, out,
                                        batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
-                                       splits, split_tokens, hints, length_bounds);
+                                       splits, split_tokens, hints, length_bounds, reach);
     const int status = dispatch_partial(prm, q_dtype, kv_dtype, kv_heads, head_dim, stream);
     if (state_stride) *state_stride = prm.row_mode ? 0 : prm.combine ? prm.quarters_per_wg : 1;
     if (xcd_rows) *xcd_rows = xcd_row_group_rows(prm);
@@ -668,10 +681,11 @@ int check_merge(const float* numerator, const float* stats, const float* out, co
 
 // length_bounds (host, or null): upper bounds on the device lengths, which
 // bound the states the merge loads before it knows a row's live count.
+// reach: as run_partial's.
 int run_merge(const float* numerator, const float* stats, float* out, const int32_t* lengths, int batch,
               int query_heads, int head_dim, int page_size, int table_width, int splits, int split_tokens,
               int merge_mode, int stride, hipStream_t stream, const int32_t* length_bounds = nullptr,
-              int xcd_rows = 0, int xcd_shift = 0) {
+              int xcd_rows = 0, int xcd_shift = 0, int reach = -1) {
     MergeParams mp{};
     mp.numerator = numerator;
     mp.stats = stats;
@@ -681,15 +695,14 @@ int run_merge(const float* numerator, const float* stats, float* out, const int3
     mp.stride_shift = stride == 4 ? 2 : stride == 2 ? 1 : 0;
     mp.query_heads = query_heads;
     mp.split_tokens = split_tokens;
-    mp.capacity = table_width * page_size;
+    mp.reach = reach < 0 ? call_reach(splits, split_tokens, table_width, page_size) : reach;
     mp.first_states = mp.parts >> mp.stride_shift;
     mp.xcd_rows = xcd_rows;
     mp.xcd_shift = xcd_shift;
     if (length_bounds != nullptr) {
-        const int64_t reach = lmin(static_cast<int64_t>(splits) * split_tokens, mp.capacity);
         int64_t longest = 0;
         for (int b = 0; b < batch; ++b)
-            longest = std::max<int64_t>(longest, lmin(reach, length_bounds[b] < 0 ? 0 : length_bounds[b]));
+            longest = std::max<int64_t>(longest, lmin(mp.reach, length_bounds[b] < 0 ? 0 : length_bounds[b]));
         const int64_t live = (kQuarters >> mp.stride_shift) * ((longest + split_tokens - 1) / split_tokens);
         mp.first_states = static_cast<int>(lmin(mp.first_states, live));
     }
@@ -827,16 +840,18 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     // Both launches run over the same partitions, at most `splits` of them
-    // per row, so the states fit the caller's workspace.
+    // per row, so the states fit the caller's workspace, and read no token
+    // past the caller's partitions (reach).
     const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
                                       table_width, splits, split_tokens, length_bounds, device_compute_units());
+    const int reach = call_reach(splits, split_tokens, table_width, page_size);
     int stride = 1, xcd_rows = 0, xcd_shift = 0;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, ks.splits,
-                         ks.split_tokens, hints, length_bounds, s, out, &stride, &xcd_rows, &xcd_shift);
+                         ks.split_tokens, hints, length_bounds, s, out, &stride, &xcd_rows, &xcd_shift, reach);
     if (status != PD_OK || stride == 0) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, ks.splits,
-                     ks.split_tokens, merge_mode, stride, s, length_bounds, xcd_rows, xcd_shift);
+                     ks.split_tokens, merge_mode, stride, s, length_bounds, xcd_rows, xcd_shift, reach);
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -931,7 +946,8 @@ int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads
     if (status != PD_OK) return status;
     PartialParams prm = partial_params(nullptr, nullptr, nullptr, kv_dtype, 1.0f, 1.0f, nullptr, nullptr, nullptr,
                                        nullptr, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size,
-                                       table_width, physical_pages, splits, split_tokens, hints, nullptr);
+                                       table_width, physical_pages, splits, split_tokens, hints, nullptr,
+                                       call_reach(splits, split_tokens, table_width, page_size));
     if (q_dtype == PD_DTYPE_F32) plan_fp32(prm, kv_heads, head_dim);
     else plan_mfma(prm, kv_heads, device_compute_units(), head_dim, element_size(kv_dtype));
     *launches = prm.row_mode ? 1 : 2;

@@ -63,6 +63,12 @@ struct PartialParams {
     int physical_pages;
     int splits;
     int split_tokens;
+    // Tokens of a sequence the call may read: min(caller's splits *
+    // split_tokens, table capacity). Lengths are clamped to it, so a full call
+    // over coarser partitions (full_call_split) reads exactly the tokens the
+    // caller's partitions cover, as the reference's grid of `splits`
+    // partitions does (decode.cu:42-44, grid z = splits at :176).
+    int reach;
     uint32_t token_bytes;  // bytes between consecutive tokens of a page (kv_heads * D * elem)
     uint64_t page_bytes;   // page_size * token_bytes
     float scale_log2;      // log2(e) * k_scale / sqrt(D)
@@ -299,8 +305,7 @@ PD_HD WaveWork wave_work(const PartialParams& p, int b, int split, int count, in
     w.quarter = qgroup * qw + qq;
     w.kv_head = (heads / tile_groups) * p.heads_per_wg + hh;
     w.tile = (heads % tile_groups) * p.tiles_per_wg + tt;
-    const int capacity = p.table_width << p.page_shift;
-    const int len = imax(0, imin(len_raw, capacity));  // decode.cu:42-44
+    const int len = imax(0, imin(len_raw, p.reach));  // decode.cu:42-44
     const int64_t first = static_cast<int64_t>(split) * p.split_tokens;
     w.dead = first >= len || count <= 0;  // count 0: an empty item of the grid
     const int tb = static_cast<int>(lmin(first, len));
@@ -340,9 +345,7 @@ PD_HD WaveWork row_wave_work(const PartialParams& p, int b, int heads, int wave,
     w.quarter = wave;
     w.kv_head = heads / p.head_tiles;
     w.tile = heads % p.head_tiles;
-    const int capacity = p.table_width << p.page_shift;
-    const int len = imax(0, imin(len_raw, capacity));  // decode.cu:42-44
-    const int te = static_cast<int>(lmin(static_cast<int64_t>(p.splits) * p.split_tokens, len));
+    const int te = imax(0, imin(len_raw, p.reach));  // decode.cu:42-44
     int per = (te + waves - 1) / waves;
     per = (per + ALIGN - 1) / ALIGN * ALIGN;
     w.wb = imin(wave * per, te);
@@ -413,8 +416,7 @@ PD_HD int k_token_of_row(int r) { return (r >> 2) + 4 * (r & 3); }
 // sequence: their state slots take the empty state (the span's tokens are all
 // in the first partition's states). Zero for a single-partition item.
 PD_HD int extra_live_partitions(const PartialParams& p, int split, int count, int len_raw) {
-    const int capacity = p.table_width << p.page_shift;
-    const int64_t len = imax(0, imin(len_raw, capacity));
+    const int64_t len = imax(0, imin(len_raw, p.reach));
     const int64_t live = (len + p.split_tokens - 1) / p.split_tokens;  // partitions holding tokens
     return static_cast<int>(lmin(split + count, live) - lmin(split + 1, live));
 }
@@ -516,9 +518,8 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.live_items = prm.items;
     prm.uniform_live = 0;
     if (length_bounds == nullptr) return;
-    const int64_t capacity = static_cast<int64_t>(prm.table_width) << prm.page_shift;
     auto live_of = [&](int b) {
-        const int64_t bound = lmin(capacity, length_bounds[b] < 0 ? 0 : length_bounds[b]);
+        const int64_t bound = lmin(prm.reach, length_bounds[b] < 0 ? 0 : length_bounds[b]);
         return static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
     };
     int64_t live_total = 0;

@@ -30,11 +30,14 @@ def load_extension():
 
     Never called on import: plan construction is where native code is first
     touched (reference ``runtime.py:9-20``), so compilation and loading stay
-    out of timed regions and graph capture.
+    out of timed regions and graph capture. A process that has already
+    initialised the GPU gets a RuntimeError instead of a build: compilers
+    are child processes, which such a process must not start.
     """
     from . import _build
 
     if not _build.built():
+        _build.refuse_after_gpu_init("building the missing paged_decode native libraries")
         _build.build()
     try:
         extension = importlib.import_module(f"{__package__}._C")

@@ -36,12 +36,23 @@ struct Problem {
     int batch, q_heads, kv_heads, head_dim, page_size, width, pages;
     int q_elem, kv_elem;  // bytes: 4 (FP32), 2 (FP16/BF16), 1 (FP8 K/V)
     int split_tokens, splits;
+    // The caller's partitions: a full call over coarser partitions keeps them
+    // here (split_tokens and splits are then the coarser ones), and no token
+    // at or past caller_splits * caller_split_tokens may be read.
+    int caller_split_tokens, caller_splits;
     std::vector<int32_t> table, lengths, bounds;  // bounds empty: none
     bool unshared = true, ragged = false;
 };
 
 uint64_t g_checks = 0;
 int g_failures = 0;
+bool g_plant_reach = false;  // --plant-reach: launch params that ignore the caller's partitions (negative control)
+
+// Tokens of a row the caller's partitions cover, clamped to the table.
+int reach_of(const Problem& pr) {
+    return static_cast<int>(lmin(static_cast<int64_t>(pr.caller_splits) * pr.caller_split_tokens,
+                                 static_cast<int64_t>(pr.width) * pr.page_size));
+}
 
 #define AUDIT(cond, ...)                                                    \
     do {                                                                    \
@@ -83,6 +94,7 @@ PartialParams params(const Problem& pr, int cus, bool mfma, bool rows) {
     p.physical_pages = pr.pages;
     p.splits = pr.splits;
     p.split_tokens = pr.split_tokens;
+    p.reach = g_plant_reach ? pr.width * pr.page_size : reach_of(pr);
     p.token_bytes = static_cast<uint32_t>(pr.kv_heads * pr.head_dim * pr.kv_elem);
     p.page_bytes = static_cast<uint64_t>(pr.page_size) * p.token_bytes;
     p.unshared_pages = pr.unshared;
@@ -121,9 +133,8 @@ struct OutCoverage {
 };
 
 void check_coverage(const Problem& pr, const Coverage& cov) {
-    const int capacity = pr.width * pr.page_size;
     for (int b = 0; b < pr.batch; ++b) {
-        const int len = imax(0, imin(pr.lengths[b], capacity));
+        const int len = imax(0, imin(pr.lengths[b], reach_of(pr)));
         const int live_parts = (len + pr.split_tokens - 1) / pr.split_tokens;
         for (int h = 0; h < pr.q_heads; ++h) {
             for (int part = 0; part < kQuarters * pr.splits; ++part) {
@@ -294,7 +305,9 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                 if (r.b < 0 || r.b >= pr.batch) continue;
                 const int b = r.b;
                 const int len_raw = pr.lengths[b];
-                const int len = imax(0, imin(len_raw, pr.width * pr.page_size));
+                // Live tokens: the length clamped to the table and to the
+                // caller's partitions; every read below is checked against it.
+                const int len = imax(0, imin(len_raw, reach_of(pr)));
                 const bool rows = p.row_mode != 0;
                 const int row_limit = mfma ? kRowMaxWaves : fp32_row_max_waves(GT);
                 if (rows) {
@@ -520,12 +533,14 @@ Problem make(const std::string& name, int batch, int q_heads, int kv_heads, int 
     pr.q_elem = q_elem;
     pr.kv_elem = kv_elem;
     pr.split_tokens = split_tokens;
+    pr.caller_split_tokens = split_tokens;
     pr.lengths = lengths;
     int longest = 0;
     for (int v : lengths) longest = imax(longest, v);
     const int capacity = width * page_size;
     const int reserved = imin(capacity, imax(1, longest) * reserve);
     pr.splits = imax(1, (reserved + split_tokens - 1) / split_tokens);
+    pr.caller_splits = pr.splits;
     std::vector<int32_t> perm(pr.pages);
     for (int i = 0; i < pr.pages; ++i) perm[i] = i;
     Lcg rng{seed};
@@ -564,7 +579,8 @@ std::vector<Problem> with_bounds(const Problem& base) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    const bool quick = argc > 1 && std::string(argv[1]) == "--quick";
+    const std::string mode = argc > 1 ? argv[1] : "";
+    const bool quick = mode == "--quick";
     std::vector<Problem> problems;
     auto add = [&](const Problem& pr, bool bounds = true) {
         if (bounds) for (const auto& x : with_bounds(pr)) problems.push_back(x);
@@ -642,6 +658,25 @@ int main(int argc, char** argv) {
     add(make("xcd llama3-8b B4 L4096 reserve x4", 4, 32, 8, 128, 16, 1024, uniform(4, 4096), 256, 2, 2, 79, 4));
     add(make("xcd mqa B128 Hq16/1 D64 L1024 reserve x2", 128, 16, 1, 64, 16, 128, uniform(128, 1024), 256, 2, 2, 81,
              2));
+    // Device lengths past the caller's partitions (splits * split_tokens <
+    // length <= table capacity): a full call over coarser partitions must
+    // still read only the first splits * split_tokens tokens. B64, 3
+    // partitions of 256 tokens, lengths 1000 in a 1024-token table: the
+    // coarse split is 2 x 512, whose second partition would reach token 999.
+    {
+        Problem pr = make("past reach B64 Hq32/8 D128 splits 3x256 L1000", 64, 32, 8, 128, 16, 64, uniform(64, 1000),
+                          256, 2, 2, 19);
+        pr.splits = pr.caller_splits = 3;
+        add(pr);
+        Problem ragged_past = make("past reach B16 Hq8/2 D64 splits 5x64 ragged", 16, 8, 2, 64, 16, 32,
+                                   ragged(16, 512, 23), 64, 2, 2, 23);
+        ragged_past.splits = ragged_past.caller_splits = 5;
+        add(ragged_past);
+        Problem fp8_past = make("past reach B32 Hq16/4 D128 fp8 splits 6x128 L900", 32, 16, 4, 128, 32, 32,
+                                uniform(32, 900), 128, 2, 1, 29);
+        fp8_past.splits = fp8_past.caller_splits = 6;
+        add(fp8_past);
+    }
     // Edge lengths around page and partition boundaries, both page sizes.
     for (int page : {16, 32}) {
         add(make("edges fp16 page " + std::to_string(page), 8, 8, 2, 128, page, 8,
@@ -703,6 +738,16 @@ int main(int argc, char** argv) {
         big.pages = 163840;  // 5 GiB per K/V tensor at 32 KB per page
         for (int i = 0; i < 128; ++i) big.table[i] = 163840 - 1 - i;
         add(big);
+    }
+    if (mode == "--plant-reach") {
+        // Negative control: the same problems with launch params that clamp
+        // lengths to the table only. The walk must report reads past the
+        // caller's partitions.
+        g_plant_reach = true;
+        std::vector<Problem> planted;
+        for (const auto& pr : problems)
+            if (pr.name.rfind("past reach", 0) == 0) planted.push_back(pr);
+        problems = planted;
     }
     int failed = 0;
     for (const auto& pr : problems) {

@@ -22,6 +22,15 @@ def require_gpu():
         pytest.skip("needs a GPU", allow_module_level=True)
 
 
+def no_child_processes_after_gpu_init():
+    """Skip a CPU test that starts a child process (a compiler, python) when
+    this process has initialised the GPU: a program started from such a
+    process can take the GPU runtime down with it."""
+    torch_module = sys.modules.get("torch")
+    if torch_module is not None and torch_module.cuda.is_initialized():
+        pytest.skip("the GPU was initialised in this process; no child processes are started")
+
+
 def announce(message):
     print(message, flush=True)
     sys.stdout.flush()

@@ -26,6 +26,8 @@ from pathlib import Path
 
 import pytest
 
+from gpu_util import no_child_processes_after_gpu_init
+
 REPO = Path(__file__).resolve().parent.parent
 CSRC = REPO / "paged-decode-lab_amd" / "paged_decode" / "csrc"
 SANITIZE = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer"]
@@ -33,6 +35,7 @@ ENV = {**os.environ, "ASAN_OPTIONS": "detect_leaks=0:abort_on_error=1", "UBSAN_O
 
 
 def compiler(name):
+    no_child_processes_after_gpu_init()
     path = shutil.which(name)
     if path is None:
         pytest.skip(f"{name} not available")
@@ -51,7 +54,8 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
     for needle in ("llama3-8b B4 L4096 fp16", "ragged shared B16", "mqa B128", "long mha B1", "compact",
                    "rectangular+tails", "whole rows", "1M context", "pages above 4 GiB", "invalid page ids fp8",
                    "ragged shared B16 T32 split 128 bounds=exact coarse x8", "bounds=half coarse x4",
-                   "long mha B1 Hq32/32 L32768 split 128 bounds=exact coarse x8"):
+                   "long mha B1 Hq32/32 L32768 split 128 bounds=exact coarse x8",
+                   "past reach B64 Hq32/8 D128 splits 3x256 L1000 bounds=exact coarse x2"):
         assert needle in run.stdout, needle
     # The XCD-grouped grid is chosen for the measured uniform workloads and the
     # shapes of tests/test_gpu_xcd_grid.py under bounds, and not without them;
@@ -68,6 +72,20 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
         plain = [line for line in lines if line.startswith(name + " ") and "bounds=" not in line]
         assert len(exact) >= 2 and all("xcd-grouped" in line or "xcd merge" in line for line in exact), name
         assert plain and not any("xcd-grouped" in line for line in plain), name
+
+
+def test_address_audit_flags_reads_past_the_callers_partitions(tmp_path):
+    """Negative control of the check above: with launch params that clamp
+    lengths to the table only (not to the caller's splits * split_tokens), a
+    full call over coarser partitions reads tokens the caller's partitions
+    exclude, and the walk must report them."""
+    exe = tmp_path / "address_audit"
+    subprocess.run([compiler("g++"), "-std=c++17", "-O1", "-g", "-Wall", "-Wno-unknown-pragmas", *SANITIZE,
+                    f"-I{CSRC}", str(REPO / "tests" / "address_audit.cpp"), "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    run = subprocess.run([str(exe), "--plant-reach"], capture_output=True, text=True, timeout=300, env=ENV)
+    assert run.returncode == 1, run.stdout[-4000:] + run.stderr[-4000:]
+    assert "FAIL" in run.stderr and "wave range [768, 896)" in run.stderr
 
 
 CPU_DRIVER = r"""

@@ -3,10 +3,13 @@ import subprocess
 import sys
 from pathlib import Path
 
+from gpu_util import no_child_processes_after_gpu_init
+
 REPO = Path(__file__).resolve().parent.parent
 
 
 def run_bench(*args):
+    no_child_processes_after_gpu_init()
     return subprocess.run([sys.executable, str(REPO / "bench.py"), *args], capture_output=True, text=True,
                           timeout=120)
 

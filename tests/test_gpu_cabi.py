@@ -424,3 +424,48 @@ def test_length_bounds_partition_stage_writes_every_live_state():
         assert np.isfinite(st[b, :, :live_states]).all()
         assert np.isnan(st[b, :, live_states:]).all()
     assert_parity(out.cpu().numpy(), fp64.dense_attention(*host, table, lengths), np.float16)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float16, torch.float8_e4m3fn])
+def test_lengths_past_the_callers_partitions_are_not_read(kv_dtype):
+    """Device lengths above splits * split_tokens (but inside the table): the
+    caller's partitions end there, and so does the attention, as in the
+    reference's grid of `splits` partitions (decode.cu:42-44, :176). With
+    host bounds the full call runs over a coarser split (2 x 512 for the
+    caller's 3 x 256) whose last partition would reach further; it must give
+    the same result as the call without bounds and as the FP64 oracle over
+    the first 768 tokens of every sequence."""
+    announce(f"lengths past the caller's partitions, {kv_dtype}")
+    lib = cabi.load()
+    batch, per_seq, split_tokens, splits = 64, 64, 256, 3
+    layout = Layout(batch, 32, 8, 128, 16, batch * per_seq)
+    rng = np.random.default_rng(19)
+    table = rng.permutation(layout.physical_pages).reshape(batch, per_seq).astype(np.int32)
+    lengths = int32_array(np.full(batch, 1000))
+    lengths[::7] = rng.integers(700, 1025, size=len(lengths[::7]))
+    bounds = int32_array(lengths)
+    assert cabi.kernel_split(lib, cabi.PD_DTYPE_F16, KV_CODES[kv_dtype], batch, 32, 8, 128, 16, per_seq,
+                             layout.physical_pages, splits, split_tokens, bounds, 256) == (2, 512)
+    if kv_dtype == torch.float16:
+        host = host_tensors(layout, dtype=np.float16, seed=12)
+        q, k, v = (torch.from_numpy(x).cuda() for x in host)
+        codes, scales = (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_F16), (1.0, 1.0)
+    else:
+        (q, k, v), scales, host = quantize(layout, kv_dtype, 12)
+        codes = (cabi.PD_DTYPE_BF16, KV_CODES[kv_dtype])
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    outs = []
+    for bound_ptr in (None, bounds.ctypes.data_as(ctypes.c_void_p)):
+        num, stats, out = workspace(layout, splits)
+        status = lib.pd_decode_ex(q.data_ptr(), codes[0], k.data_ptr(), v.data_ptr(), codes[1], *scales,
+                                  d_table.data_ptr(), d_lengths.data_ptr(), num.data_ptr(), stats.data_ptr(),
+                                  out.data_ptr(), batch, 32, 8, 128, 16, per_seq, layout.physical_pages, splits,
+                                  split_tokens, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_UNSHARED_PAGES, bound_ptr,
+                                  stream())
+        assert status == cabi.PD_OK, cabi.status_string(lib, status)
+        outs.append(out)
+    torch.cuda.synchronize()
+    expected = fp64.dense_attention(*host, table, np.minimum(lengths, splits * split_tokens))
+    for out in outs:
+        assert_parity(out.cpu().numpy(), expected, np.float16)
+    torch.testing.assert_close(outs[1], outs[0], rtol=1e-5, atol=1e-6)

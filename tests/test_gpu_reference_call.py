@@ -8,7 +8,11 @@ longest sequence, ``runtime.py:46-49``) and calls ``decode`` with exactly ten
 positional arguments (``runtime.py:88-89``, ``bindings.cpp:3-9``): no scales,
 no hints. These tests make that call, on the FP32 oracle case and the
 Llama-3-8B decode shape, for both merge modes, and the reference's
-shared-merge bound (``decode.cu:234-235``) as a ``RuntimeError``.
+shared-merge bound (``decode.cu:234-235``) as a ``RuntimeError``. The
+extension is reached two ways: through this package's ``load_extension``,
+and through the replacement ``load_extension()`` INTEGRATION.md gives for
+the reference's ``runtime.py`` (loaded by file location, as it must be
+inside a package that owns the name ``paged_decode``).
 """
 import math
 
@@ -21,6 +25,7 @@ require_gpu()
 
 import torch  # noqa: E402
 
+import rebinding  # noqa: E402
 from oracle.fp64 import dense_attention  # noqa: E402
 from paged_decode.runtime import load_extension  # noqa: E402
 from paged_decode.workload import make_workload  # noqa: E402
@@ -39,10 +44,14 @@ def reference_buffers(layout, lengths, split_tokens, device):
     return numerator, stats, out
 
 
+BINDINGS = {"package": load_extension, "documented": rebinding.load_as_documented}
+
+
+@pytest.mark.parametrize("binding", sorted(BINDINGS))
 @pytest.mark.parametrize("name", ["fp32_b2_ragged", "llama3_8b_b4_l4096"])
 @pytest.mark.parametrize("merge_mode", [0, 1])
-def test_reference_ten_argument_call(name, merge_mode):
-    announce(f"reference decode(...) call: workload {name} merge_mode={merge_mode}")
+def test_reference_ten_argument_call(name, merge_mode, binding):
+    announce(f"reference decode(...) call: workload {name} merge_mode={merge_mode} binding={binding}")
     w = make_workload(name)
     device = torch.device("cuda", torch.cuda.current_device())
     host = w.host_tensors()
@@ -50,7 +59,9 @@ def test_reference_ten_argument_call(name, merge_mode):
     table = torch.tensor(w.table, device=device)
     lengths = torch.tensor(w.lengths, device=device)
     numerator, stats, out = reference_buffers(w.layout, w.lengths, w.split_tokens, device)
-    extension = load_extension()
+    extension = BINDINGS[binding]()
+    if binding == "documented":
+        assert extension.__name__ == "paged_decode_amd._C" and extension.header_abi_version() == 14
     result = extension.decode(q, k, v, table, lengths, numerator, stats, out, w.split_tokens, merge_mode)
     assert result is None
     expected = dense_attention(*host, w.table, w.lengths)

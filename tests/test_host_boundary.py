@@ -13,6 +13,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+from gpu_util import no_child_processes_after_gpu_init
 from paged_decode import cabi
 from paged_decode.layout import Layout
 from paged_decode.runtime import DecodePlan
@@ -82,11 +83,21 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == 14
+    assert lib.pd_abi_version() == cabi.PD_ABI_VERSION == 14
+    assert re.search(r"#define\s+PD_ABI_VERSION\s+(\d+)", HEADER.read_text()).group(1) == str(cabi.PD_ABI_VERSION)
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
     assert "success" in cabi.status_string(lib, cabi.PD_OK)
     assert cabi.status_string(lib, 99) == "unknown status"
+
+
+def test_ctypes_binding_refuses_another_abi_version(monkeypatch):
+    """cabi.load compares pd_abi_version() with the version its prototypes
+    follow before attaching them: against a library of another ABI the
+    widened entries would read their new arguments as the stream."""
+    monkeypatch.setattr(cabi, "PD_ABI_VERSION", cabi.PD_ABI_VERSION - 1)
+    with pytest.raises(OSError, match="ABI"):
+        cabi.load()
 
 
 def test_launch_count_query():
@@ -196,6 +207,7 @@ def test_header_is_plain_c_and_library_links_from_c(tmp_path):
     import shutil
     import subprocess
 
+    no_child_processes_after_gpu_init()
     gcc = shutil.which("gcc")
     if gcc is None:
         pytest.skip("gcc not available")
@@ -419,3 +431,54 @@ def test_scratch_entry_rejects_before_touching_a_device():
     assert call(batch=1, heads=32, splits=505) == cabi.PD_ERR_SCRATCH
     assert "scratch" in cabi.status_string(lib, cabi.PD_ERR_SCRATCH)
     assert cabi.PD_SCRATCH_BYTES == 32 << 20
+
+
+# ---------------------------------------------------------------------------
+# No child process after GPU initialisation. A program started from a process
+# that has initialised the GPU can take the GPU runtime down with it, so every
+# path that would start one (a compiler for a missing build, make for the C
+# restatement, git for the build record) refuses or skips instead. The GPU
+# state is simulated by patching torch.cuda.is_initialized.
+
+
+@pytest.fixture
+def gpu_initialised(monkeypatch):
+    import torch
+
+    monkeypatch.setattr(torch.cuda, "is_initialized", lambda: True)
+
+
+def test_missing_build_is_refused_after_gpu_init(gpu_initialised, monkeypatch):
+    from paged_decode import _build, runtime
+
+    def no_build(*args, **kwargs):
+        raise AssertionError("a build was started")
+
+    monkeypatch.setattr(_build, "built", lambda: False)
+    monkeypatch.setattr(_build, "build", no_build)
+    runtime.load_extension.cache_clear()
+    try:
+        with pytest.raises(RuntimeError, match="child process"):
+            runtime.load_extension()
+    finally:
+        runtime.load_extension.cache_clear()
+
+
+def test_compiler_runs_are_refused_after_gpu_init(gpu_initialised):
+    from paged_decode import _build
+
+    with pytest.raises(RuntimeError, match="child process"):
+        _build._run(["hipcc", "--version"], verbose=False)
+    assert _build.git_dirty() is None  # no git process either
+
+
+def test_oracle_build_is_refused_after_gpu_init(gpu_initialised):
+    from oracle import cpu
+
+    with pytest.raises(RuntimeError, match="GPU"):
+        cpu.build()
+
+
+def test_spawning_cpu_tests_skip_after_gpu_init(gpu_initialised):
+    with pytest.raises(pytest.skip.Exception):
+        no_child_processes_after_gpu_init()

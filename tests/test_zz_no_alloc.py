@@ -141,3 +141,53 @@ def test_scratch_entry_rejects_workspaces_beyond_the_scratch():
     assert status == cabi.PD_OK, cabi.status_string(lib, status)
     torch.cuda.synchronize()
     assert_parity(out.cpu().numpy(), fp64.dense_attention(*host, table, lengths), np.float16)
+
+
+def test_scratch_entry_allocates_nothing_and_replays_in_a_graph():
+    """What the entry exists for: after one uncaptured call on a device (which
+    looks up the scratch's address), a call changes no device allocation
+    (hipMemGetInfo's free bytes are unchanged), and a call captured in a
+    hipGraph on a side stream replays bit for bit like the eager call, with
+    the program's own eager work between the replays."""
+    lib = cabi.load()
+    layout = Layout(8, 32, 8, 128, 16, 8 * 128)
+    lengths = np.array([2048, 1999, 0, 2048, 1024, 77, 2048, 1500], dtype=np.int32)
+    table, lengths, host = problem(layout, np.float16, lengths, seed=31)
+    bounds = lengths.copy()
+    q, k, v = (torch.from_numpy(x).cuda() for x in host)
+    d_table, d_lengths = torch.from_numpy(table).cuda(), torch.from_numpy(lengths).cuda()
+    args = dims(layout, table.shape[1], 16, 128, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_UNSHARED_PAGES)
+    eager = torch.full((8, 32, 128), float("nan"), device="cuda")
+    graph_out = torch.full_like(eager, float("nan"))
+
+    def call(out):
+        status = lib.pd_decode_scratch(q.data_ptr(), cabi.PD_DTYPE_F16, k.data_ptr(), v.data_ptr(),
+                                       cabi.PD_DTYPE_F16, 1.0, 1.0, d_table.data_ptr(), d_lengths.data_ptr(),
+                                       out.data_ptr(), *args, bounds.ctypes.data, stream())
+        assert status == cabi.PD_OK, cabi.status_string(lib, status)
+
+    announce("pd_decode_scratch: warm-up call, then a call between two hipMemGetInfo readings")
+    call(eager)
+    torch.cuda.synchronize()
+    free_before, _ = torch.cuda.mem_get_info()
+    call(eager)
+    torch.cuda.synchronize()
+    free_after, _ = torch.cuda.mem_get_info()
+    assert free_after == free_before
+    assert_parity(eager.cpu().numpy(), fp64.dense_attention(*host, table, lengths), np.float16)
+
+    announce("pd_decode_scratch: captured in a hipGraph on a side stream, replayed 4 times")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            call(graph_out)
+    torch.cuda.synchronize()
+    for replay in range(4):
+        graph_out.fill_(float("nan"))
+        scribble = torch.randn(1 << 20, device="cuda").sum()  # the program's own eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(scribble)
+        assert torch.equal(graph_out, eager), f"replay {replay}"
