@@ -24,6 +24,10 @@ Protocol
 * Roofline: K back-to-back launches of the partition kernel alone (one
   captured graph) give its average launch duration; achieved = logical KV
   bytes / duration.
+* Streaming-read ceiling: K back-to-back launches of a read-only kernel
+  (pd_stream_read) over as many bytes as the call's logical K/V, read from
+  the same rotated K/V sets in the decode's load form: stream_read_us, and
+  frac_vs_stream = stream_read_us / partition-kernel duration (and per call).
 * The reference's sampling protocol (30 repetitions x 20 inner calls, runners
   in randomized order, p50) is reported for both merge kernels, eager and
   hipGraph, cold (rotated K/V sets) and warm (one set, cache-resident).
@@ -377,6 +381,20 @@ def main():
         del partial_graph
     achieved = logical / (partial_us * 1e-6) / 1e9
 
+    # --- streaming-read ceiling: a read-only pass over as many bytes as the
+    # call's logical K/V (half from call i's K set, half from its V set, so the
+    # same rotation), K launches back to back in one graph: what one launch
+    # moving these bytes reaches on this device, next to the partition kernel.
+    sink = torch.zeros(2, dtype=torch.int32, device=device)
+    half = min((logical // 2) // 16 * 16, k0.numel() * k0.element_size())
+    stream_graph = steps_graph(lambda i: plan._extension.stream_read(ks[i % sets], vs[i % sets], half, half, sink),
+                               args.steps)
+    stream_ms, _ = time_region(torch, lambda i: stream_graph.replay(), 1)
+    stream_us = stream_ms * 1e3 / args.steps
+    del stream_graph
+    log(args, f"streaming read of {2 * half} B: {stream_us:.2f} us ({2 * half / (stream_us * 1e-6) / 1e9:.0f} GB/s); "
+              f"partition kernel {partial_us:.2f} us")
+
     # --- reference sampling protocol: p50 over 30 x 20, randomized order ---
     # Runners: {serial, shared} x {graph, eager}, cold (rotated sets); graph warm (set 0 only).
     runners = {}
@@ -494,6 +512,10 @@ def main():
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": recorded_traffic(w.name, digest), "avg_launch_us": round(partial_us, 3),
+            "stream_read_us": round(stream_us, 3), "stream_read_bytes": 2 * half,
+            "stream_read_GBps": round(2 * half / (stream_us * 1e-6) / 1e9, 1),
+            "frac_vs_stream": round(stream_us / partial_us, 4),
+            "call_frac_vs_stream": round(stream_us / us_graph, 4),
         },
         "cpu_baseline": cpu_baseline,
         "protocol_p50": protocol,

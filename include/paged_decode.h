@@ -264,20 +264,21 @@ int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype,
  * Page table and lengths from CSR page-list metadata held on the device, the
  * inverse of the CSR form reference src/paged_decode/competitors.py:8-18
  * builds: for sequence b, n_b = indptr[b + 1] - indptr[b] page ids are taken
- * from indices[indptr[b]] on (indices must hold indptr[batch] entries),
- * table[b, n_b .. table_width) = -1, and lengths[b] = (n_b - 1) * page_size +
- * last_page_len[b], or 0 for an empty list. table is [batch, table_width],
+ * from indices[indptr[b]] on, table[b, n_b .. table_width) = -1, and
+ * lengths[b] = (n_b - 1) * page_size + last_page_len[b], or 0 for an empty
+ * list. indices holds indices_count entries. table is [batch, table_width],
  * lengths [batch], as pd_decode reads them. A sequence that does not fit
- * (n_b < 0, n_b > table_width, last_page_len outside [1, page_size], or a
- * length above max_context -- the context the caller's splits cover) is
+ * (n_b < 0, n_b > table_width, a page list reaching outside
+ * [0, indices_count), last_page_len outside [1, page_size], or a length
+ * above max_context -- the context the caller's splits cover) is
  * written as empty and sets *overflow to 1 if overflow is not NULL (it is
  * never cleared: zero it before the call with a kernel, not a memset, if the
  * call is captured). Page ids are not checked; the decode skips ids outside
  * [0, physical_pages). Lets a caller keeping CSR metadata on the device
  * refresh a plan without a host round trip, inside a captured graph.
  */
-int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len,
-                      int32_t* table, int32_t* lengths, int32_t* overflow,
+int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, int64_t indices_count,
+                      const int32_t* last_page_len, int32_t* table, int32_t* lengths, int32_t* overflow,
                       int batch, int table_width, int page_size, int max_context, void* stream);
 
 /*
@@ -319,6 +320,17 @@ int pd_decode_kernel_split(int q_dtype, int kv_dtype, int batch, int query_heads
                            const int32_t* length_bounds, int compute_units, int* kernel_splits,
                            int* kernel_split_tokens);
 
+/*
+ * Streaming read: reads a_bytes of a and b_bytes of b once each (16-byte
+ * loads, the form of the decode's K/V loads) in one launch and writes at most
+ * 8 bytes to sink, a device buffer of at least 2 uint32. Both sizes and
+ * pointers must be multiples of 16 (else PD_ERR_SHAPE). No counterpart in
+ * the reference: the bandwidth ceiling a decode launch over the same number
+ * of K/V bytes is measured against (the reference profiled its partial
+ * stage's DRAM throughput, results/2026-10-31-final-t4/profiling/ncu-details.csv:6,22).
+ */
+int pd_stream_read(const void* a, size_t a_bytes, const void* b, size_t b_bytes, uint32_t* sink, void* stream);
+
 /* Static description of a status code (never NULL). */
 const char* pd_status_string(int status);
 
@@ -331,9 +343,11 @@ const char* pd_status_string(int status);
  * entries; 11: PD_HINT_RAGGED_LENGTHS; 12: max_context argument of
  * pd_append_kv_advance, length_bounds argument of the _ex entries; 13: whole-row launches of small rows,
  * pd_decode_launch_count; 14: coarser partitions for full calls on large
- * grids, pd_decode_kernel_split). PD_ABI_VERSION is the value this header
- * describes; a binding compares it with what the loaded library returns. */
-#define PD_ABI_VERSION 14
+ * grids, pd_decode_kernel_split; 15: pd_stream_read, indices_count argument
+ * of pd_table_from_csr). PD_ABI_VERSION is the
+ * value this header describes; a binding compares it with what the loaded
+ * library returns. */
+#define PD_ABI_VERSION 15
 int pd_abi_version(void);
 
 #ifdef __cplusplus

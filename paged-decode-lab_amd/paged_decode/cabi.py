@@ -12,7 +12,7 @@ LIBRARY = Path(__file__).resolve().parent / "libpaged_decode_hip.so"
 # The header's PD_ABI_VERSION these prototypes follow; load() refuses a
 # library that reports another (a stale build would read arguments added
 # since then, such as length_bounds or max_context, as its stream).
-PD_ABI_VERSION = 14
+PD_ABI_VERSION = 15
 
 PD_OK = 0
 PD_ERR_NULL_POINTER = 1
@@ -48,10 +48,11 @@ PROTOTYPES = {
     "pd_decode_merge": (_I, [_P, _P, _P, _P] + [_I] * 8 + [_P]),
     "pd_append_kv": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 7 + [_P]),
     "pd_append_kv_advance": (_I, [_P, _P, _I, _P, _P, _P, _P] + [_I] * 8 + [_P]),
-    "pd_table_from_csr": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 4 + [_P]),
+    "pd_table_from_csr": (_I, [_P, _P, ctypes.c_int64, _P, _P, _P, _P] + [_I] * 4 + [_P]),
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
     "pd_decode_launch_count": (_I, [_I] * 12 + [_P]),
     "pd_decode_kernel_split": (_I, [_I] * 11 + [_P, _I, _P, _P]),
+    "pd_stream_read": (_I, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, _P]),
     "pd_status_string": (ctypes.c_char_p, [_I]),
     "pd_abi_version": (_I, []),
 }

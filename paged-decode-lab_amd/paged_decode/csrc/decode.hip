@@ -57,7 +57,9 @@
 // and docs/DESIGN.md:5-76 (workspace of 4 * S states); the decomposition and
 // data paths are this file's own.
 
-#include "device_common.h"
+#include "device_common.h"  // first: the HIP runtime header the maps' __host__ __device__ need
+#include "cache_map.h"
+#include "merge_map.h"
 #include "partition_kernels.h"
 
 namespace {
@@ -74,34 +76,10 @@ using namespace pd;
 //   shared: the workgroup forms each state's weight once, into LDS
 //           (4 bytes per state, hence the PD_SHARED_MERGE_MAX_PARTS bound).
 
-constexpr int kMergeThreads = 256;
-
-// States of row b to merge: per_part per partition up to the last one
-// holding a token of the sequence (none for an empty sequence), capped at the
-// row's states. Partitions past the end are never written and never read.
-// reach: the tokens the call may read (PartialParams::reach).
-__device__ __forceinline__ int live_parts(const int32_t* lengths, int b, int split_tokens, int reach,
-                                          int per_part, int states) {
-    const int len = max(0, min(lengths[b], reach));  // decode.cu:42-44
-    const int64_t live = (static_cast<int64_t>(len) + split_tokens - 1) / split_tokens;
-    return static_cast<int>(min<int64_t>(per_part * live, states));
+// States of row b to merge (merge_map.h: live_states), from its device length.
+__device__ __forceinline__ int live_parts(const MergeParams& mp, int b, int per_part, int states) {
+    return live_states(mp.lengths[b], mp.split_tokens, mp.reach, per_part, states);
 }
-
-struct MergeParams {
-    const float* numerator;  // [B, Hq, parts, D]
-    const float* stats;      // [B, Hq, parts, 2]
-    float* out;              // [B, Hq, D]
-    const int32_t* lengths;  // [B]
-    int parts;               // allocated states per row (4 * splits)
-    int stride_shift;        // read every (1 << stride_shift)-th state: 0, or log2 of the combined quarters
-    int query_heads;
-    int split_tokens;
-    int reach;               // tokens a row may hold: min(caller's splits * split_tokens, table_width * page_size)
-    int first_states;        // states (read units) loaded before the live count arrives: the host's
-                             // bound on any row's live states, else the whole row
-    int xcd_rows;            // rows per row group of an XCD-grouped partition grid (merge_xcd_row), 0: plain
-    int xcd_shift;           // log2 of that grid's head groups per sequence
-};
 
 // merge_cols_kernel: a row's D columns are cut into chunks of CH floats and
 // each (row, chunk) is one 256-lane workgroup, so D / CH workgroups read a
@@ -120,11 +98,6 @@ struct MergeParams {
 // 32.28 -> 30.48-30.73, the reference's B4 / B16 batches 14.60 -> 14.51 /
 // 41.11 -> 41.07; XCD-grouped 32K-context MHA 86.05 -> 86.17 and B1 L4096
 // 9.60 -> 9.68, Llama-3-8B B4 L4096 unchanged.
-constexpr int kMergeChunkLocal = 32;  // floats per column chunk, XCD-grouped merge
-constexpr int kMergeChunkWide = 64;   // floats per column chunk, otherwise
-constexpr int kMergeColBatchShort = 8;                            // numerator loads per lane per round
-constexpr int kMergeColBatchLong = 32;
-constexpr int kOptimisticRounds = 2;  // first-round loads issued before the live count (64 states)
 
 template <int D, bool kSharedWeights, int NB, int CH>
 __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergeParams mp) {
@@ -138,16 +111,9 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     extern __shared__ float weight[];  // [parts], shared variant only
     __shared__ f32x4 column_sum[PG][TPR];
     __shared__ float wave_partial[2][kWaves];
-    int b;
-    int64_t row;
-    if (mp.xcd_rows > 0) {
-        const MergeRow mr = merge_xcd_row(blockIdx.x, blockIdx.y, mp.xcd_rows, mp.xcd_shift, 1, 0);
-        b = mr.b;
-        row = mr.row;
-    } else {
-        b = blockIdx.y;
-        row = static_cast<int64_t>(b) * mp.query_heads + blockIdx.x;
-    }
+    const MergeRow mr = merge_cols_row(mp, blockIdx.x, blockIdx.y);
+    const int b = mr.b;
+    const int64_t row = mr.row;
     const int chunk = blockIdx.z;
     const int shift = mp.stride_shift;
     const int parts = mp.parts >> shift;  // states read: j <-> allocated state j << shift
@@ -158,11 +124,10 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int pg = t / TPR;
     const int scan0 = kSharedWeights ? t : lane;
     const int last = parts - 1;
-    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * mp.parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D + chunk * CH) + col;
-    const int64_t num_step = static_cast<int64_t>(D / 4) << shift;
+    const float2* st = reinterpret_cast<const float2*>(mp.stats) + merge_stats_base(mp, row);
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator) + merge_numerator_base(mp, row, D, chunk, CH, col);
 
-    auto rounds_from = [&](int base, int limit) { return min(NB, (limit - base + PG - 1) / PG); };
+    auto rounds_from = [&](int base, int limit) { return merge_cols_rounds(base, limit, NB, PG); };
     f32x4 buf[NB];
     float2 own[NB];
     // Loads k0 <= k < k1 (uniform bounds) of the round starting at state base.
@@ -170,9 +135,9 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
 #pragma unroll
         for (int k = 0; k < NB; ++k) {
             if (k >= k0 && k < k1) {
-                const int j = min(base + pg + k * PG, last);
-                buf[k] = num[j * num_step];
-                if constexpr (!kSharedWeights) own[k] = read_state(st, j << shift);
+                const int j = merge_load_unit(base, pg, k, PG, last);
+                buf[k] = num[merge_numerator_offset(mp, D, j)];
+                if constexpr (!kSharedWeights) own[k] = read_state(st, merge_stats_offset(mp, j));
             }
         }
     };
@@ -186,13 +151,13 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
     const int first_n = max(1, min(parts, mp.first_states));
     const int optimistic = min(kOptimisticRounds, rounds_from(0, first_n));
     load_rounds(0, 0, optimistic);
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.reach, kQuarters >> shift, parts);
+    const int live = live_parts(mp, b, kQuarters >> shift, parts);
     load_rounds(0, optimistic, rounds_from(0, live));
 
     auto scan_round = [&](int base, int limit, float2 (&sv)[SU]) {
 #pragma unroll
         for (int i = 0; i < SU; ++i) {
-            if (base + i * kScan < limit) sv[i] = read_state(st, min(base + scan0 + i * kScan, last) << shift);
+            if (base + i * kScan < limit) sv[i] = read_state(st, merge_stats_offset(mp, min(base + scan0 + i * kScan, last)));
         }
     };
     auto round_max = [&](const float2 (&sv)[SU], int base, int limit, float m) {
@@ -293,57 +258,41 @@ __global__ void __launch_bounds__(kMergeThreads) merge_cols_kernel(const MergePa
 // state's weight once, in lane j, and broadcasts it with a cross-lane read;
 // the serial variant has every lane recompute the weights it uses. The PGW
 // column sums meet through permlane swaps. Used when a row's allocated states
-// fit in NB loads per lane (NB = 8: 16 states at D = 128, 32 at D = 64; NB =
-// 16: 32 and 64); all loads are issued at once and masked with the live
-// count. RPG rows (waves) per workgroup.
-constexpr int kMergeWaveBatch = 8;
-constexpr int kMergeWaveBatchLong = 16;
-constexpr int kMergeRowsMin = 256;  // rows (sequences x query heads) from which merge_rows takes rows of > 2 rounds
-constexpr int kMergeRowsPerGroup = 4;
-
-template <int D, int NB = kMergeWaveBatch>
-constexpr int merge_wave_max_parts() { return NB * (kWave / (D / 4)); }
-
+// fit in NB loads per lane (NB = kMergeWaveBatch = 8: 16 states at D = 128, 32
+// at D = 64); all loads are issued at once and masked with the live count.
+// RPG rows (waves) per workgroup.
 template <int D, bool kSharedWeights, int NB, int RPG>
 __global__ void __launch_bounds__(kWave * RPG) merge_rows_kernel(const MergeParams mp) {
     constexpr int TPR = D / 4;        // lanes per state row
     constexpr int PGW = kWave / TPR;  // state groups per wave (2 or 4)
-    static_assert(merge_wave_max_parts<D, NB>() <= kWave, "one state per lane for the statistics");
+    static_assert(merge_wave_max_parts(D, NB) <= kWave, "one state per lane for the statistics");
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    int b;
-    int64_t row;
-    if (mp.xcd_rows > 0) {
-        const MergeRow mr = merge_xcd_row(blockIdx.x, blockIdx.y, mp.xcd_rows, mp.xcd_shift, RPG, wave);
-        b = mr.b;
-        row = mr.row;
-    } else {
-        const int h = blockIdx.x * RPG + wave;
-        if (h >= mp.query_heads) return;  // whole wave; nothing below synchronises across waves
-        b = blockIdx.y;
-        row = static_cast<int64_t>(b) * mp.query_heads + h;
-    }
+    const MergeRow mr = merge_rows_row(mp, blockIdx.x, blockIdx.y, wave, RPG);
+    if (mr.row < 0) return;  // whole wave past the last head; nothing below synchronises across waves
+    const int b = mr.b;
+    const int64_t row = mr.row;
     const int shift = mp.stride_shift;
     const int parts = mp.parts >> shift;  // states read: j <-> allocated state j << shift
     const int col = lane % TPR;
     const int pg = lane / TPR;
     const int last = parts - 1;
-    const float2* st = reinterpret_cast<const float2*>(mp.stats) + row * mp.parts;
-    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator + row * mp.parts * D) + col;
+    const float2* st = reinterpret_cast<const float2*>(mp.stats) + merge_stats_base(mp, row);
+    const f32x4* num = reinterpret_cast<const f32x4*>(mp.numerator) + merge_numerator_base(mp, row, D, 0, D, col);
     const int rounds = (parts + PGW - 1) / PGW;  // uniform, <= NB
-    const int live = live_parts(mp.lengths, b, mp.split_tokens, mp.reach, kQuarters >> shift, parts);
+    const int live = live_parts(mp, b, kQuarters >> shift, parts);
 
     f32x4 buf[NB];
     float2 own[NB];
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
         if (k < rounds) {
-            const int j = min(pg + k * PGW, last);
-            buf[k] = num[(static_cast<int64_t>(j) << shift) * TPR];
-            if constexpr (!kSharedWeights) own[k] = read_state(st, j << shift);
+            const int j = merge_load_unit(0, pg, k, PGW, last);
+            buf[k] = num[merge_numerator_offset(mp, D, j)];
+            if constexpr (!kSharedWeights) own[k] = read_state(st, merge_stats_offset(mp, j));
         }
     }
-    const float2 mine = read_state(st, min(lane, last) << shift);
+    const float2 mine = read_state(st, merge_stats_offset(mp, min(lane, last)));
     const bool ok = (lane < live) & (mine.y > 0.0f);
     const float mx = wave_max(ok ? mine.x : kNoToken);
     const float f = ok ? fast_exp2(mine.x - mx) : 0.0f;  // weight of state `lane`
@@ -386,40 +335,22 @@ __global__ void __launch_bounds__(kWave * RPG) merge_rows_kernel(const MergePara
 // [P, T, Hkv, D], so a token is a straight 16-byte-per-lane copy of its K row
 // and its V row. Same addressing as the gather (reference docs/DESIGN.md:10-13).
 
-struct AppendParams {
-    const char* k_new;
-    const char* v_new;
-    const int32_t* table;
-    const int32_t* positions;  // explicit variant: first position per sequence
-    int32_t* lengths;          // advance variant: positions in, advanced lengths out
-    char* k_cache;
-    char* v_cache;
-    int tokens;
-    int table_width;
-    int page_shift;
-    int physical_pages;
-    int64_t capacity;          // positions [0, capacity) may be written: the table's, or less (advance variant)
-    uint32_t row_bytes;        // kv_heads * head_dim * element size
-};
-
-// Physical row of logical position pos, or -1 if pos is outside
-// [0, capacity) or its page id is outside [0, physical_pages).
+// Physical row of logical position pos of the sequence whose page-table row
+// is `pages`, or -1 if pos is outside [0, capacity) or its page id is outside
+// [0, physical_pages) (cache_map.h).
 __device__ __forceinline__ int64_t cache_row(const AppendParams& a, const int32_t* pages, int64_t pos) {
-    if (pos < 0 || pos >= a.capacity) return -1;
-    const int page = pages[pos >> a.page_shift];
-    if (static_cast<uint32_t>(page) >= static_cast<uint32_t>(a.physical_pages)) return -1;
-    return (static_cast<int64_t>(page) << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+    const int64_t entry = append_table_entry(a, pos);
+    if (entry < 0) return -1;
+    return append_cache_row(a, pages[entry], pos);
 }
 
 __device__ __forceinline__ void copy_token_row(const AppendParams& a, int64_t src_row, int64_t dst_row) {
-    const u32x4* ks = reinterpret_cast<const u32x4*>(a.k_new + src_row * a.row_bytes);
-    const u32x4* vs = reinterpret_cast<const u32x4*>(a.v_new + src_row * a.row_bytes);
-    u32x4* kd = reinterpret_cast<u32x4*>(a.k_cache + dst_row * a.row_bytes);
-    u32x4* vd = reinterpret_cast<u32x4*>(a.v_cache + dst_row * a.row_bytes);
     const uint32_t chunks = a.row_bytes / 16u;
     for (uint32_t c = threadIdx.x; c < chunks; c += blockDim.x) {
-        kd[c] = ks[c];
-        vd[c] = vs[c];
+        const int64_t src = append_chunk_offset(a, src_row, c);
+        const int64_t dst = append_chunk_offset(a, dst_row, c);
+        *reinterpret_cast<u32x4*>(a.k_cache + dst) = *reinterpret_cast<const u32x4*>(a.k_new + src);
+        *reinterpret_cast<u32x4*>(a.v_cache + dst) = *reinterpret_cast<const u32x4*>(a.v_new + src);
     }
 }
 
@@ -431,7 +362,7 @@ __global__ void __launch_bounds__(256) append_kv_kernel(const AppendParams a) {
     const int32_t* pages = a.table + static_cast<int64_t>(b) * a.table_width;
     const int64_t dst = cache_row(a, pages, static_cast<int64_t>(a.positions[b]) + j);
     if (dst < 0) return;
-    copy_token_row(a, static_cast<int64_t>(b) * a.tokens + j, dst);
+    copy_token_row(a, append_source_row(a, b, j), dst);
 }
 
 // Positions from lengths, all or nothing per sequence: workgroup b writes its
@@ -447,7 +378,7 @@ __global__ void __launch_bounds__(256) append_kv_advance_kernel(const AppendPara
     bool fits = true;
     for (int j = 0; j < a.tokens; ++j) fits &= cache_row(a, pages, base + j) >= 0;  // uniform
     if (!fits) return;
-    for (int j = 0; j < a.tokens; ++j) copy_token_row(a, static_cast<int64_t>(b) * a.tokens + j, cache_row(a, pages, base + j));
+    for (int j = 0; j < a.tokens; ++j) copy_token_row(a, append_source_row(a, b, j), cache_row(a, pages, base + j));
     __syncthreads();  // every thread has read lengths[b] before it changes
     if (threadIdx.x == 0) a.lengths[b] = static_cast<int32_t>(base + a.tokens);
 }
@@ -459,34 +390,20 @@ __global__ void __launch_bounds__(256) append_kv_advance_kernel(const AppendPara
 // indices[indptr[b]] on and -1 past them; lengths[b] = (n_b - 1) * page_size +
 // last_page_len[b], or 0 for an empty list. A row that does not fit (n_b < 0,
 // n_b > table_width, last_page_len outside [1, page_size], or a length above
-// max_context) is written empty and raises *overflow. Page ids are not
-// checked here: the partition kernel skips ids outside [0, physical_pages).
-struct CsrParams {
-    const int32_t* indptr;
-    const int32_t* indices;
-    const int32_t* last_page_len;
-    int32_t* table;
-    int32_t* lengths;
-    int32_t* overflow;  // may be null
-    int table_width;
-    int page_size;
-    int max_context;
-};
-
+// max_context, or a page list reaching outside [0, indices_count)) is written
+// empty and raises *overflow, so a malformed indptr never reads past indices.
+// Page ids are not checked here: the partition kernel skips ids outside
+// [0, physical_pages).
 __global__ void __launch_bounds__(256) table_from_csr_kernel(const CsrParams c) {
     const int b = blockIdx.x;
     const int64_t begin = c.indptr[b];
-    const int64_t n = static_cast<int64_t>(c.indptr[b + 1]) - begin;
-    const int last = n > 0 ? c.last_page_len[b] : 0;
-    const int64_t length = n > 0 ? (n - 1) * c.page_size + last : 0;
-    const bool fits = n >= 0 && n <= c.table_width && (n == 0 || (last >= 1 && last <= c.page_size)) &&
-                      length <= c.max_context;
-    const int64_t live = fits ? n : 0;
+    const int64_t end = c.indptr[b + 1];
+    const CsrRow r = csr_row(c, begin, end, end > begin ? c.last_page_len[b] : 0);
     int32_t* row = c.table + static_cast<int64_t>(b) * c.table_width;
-    for (int i = threadIdx.x; i < c.table_width; i += blockDim.x) row[i] = i < live ? c.indices[begin + i] : -1;
+    for (int i = threadIdx.x; i < c.table_width; i += blockDim.x) row[i] = i < r.live ? c.indices[r.begin + i] : -1;
     if (threadIdx.x == 0) {
-        c.lengths[b] = fits ? static_cast<int32_t>(length) : 0;
-        if (!fits && c.overflow != nullptr) *c.overflow = 1;
+        c.lengths[b] = r.fits ? static_cast<int32_t>(r.length) : 0;
+        if (!r.fits && c.overflow != nullptr) *c.overflow = 1;
     }
 }
 
@@ -606,59 +523,41 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
 
 
 template <int D, int CH>
-int launch_merge_cols(const MergeParams& mp, int batch, uint32_t row_groups, int states, bool shared,
-                      hipStream_t stream) {
-    const dim3 grid = mp.xcd_rows > 0 ? dim3(8 * mp.xcd_rows, row_groups, D / CH) : dim3(mp.query_heads, batch, D / CH);
-    const dim3 block(kMergeThreads);
-    const size_t lds = shared ? states * sizeof(float) : 0;
-    // The long-row variant issues 1024 states' loads per round but holds one
-    // (serial) or two (shared) workgroups per CU: it pays only while the grid
-    // fits the device in one round. Larger grids take 256-state rounds at full
-    // occupancy (rows of a plan whose reserved context exceeds the live one
-    // among them: the variant follows the allocated states).
-    constexpr int kGroups = kMergeThreads / (CH / 4);
-    const int64_t workgroups = static_cast<int64_t>(grid.x) * grid.y * grid.z;
-    const bool long_rows = states > kMergeColBatchShort * kGroups && workgroups <= device_compute_units();
-    if (shared && long_rows) {
+void launch_merge_cols(const MergeLaunch& ml, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                       const MergeParams& mp) {
+    if (ml.shared && ml.nb == kMergeColBatchLong) {
         hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchLong, CH>), grid, block, lds, stream, mp);
-    } else if (shared) {
+    } else if (ml.shared) {
         hipLaunchKernelGGL((merge_cols_kernel<D, true, kMergeColBatchShort, CH>), grid, block, lds, stream, mp);
-    } else if (long_rows) {
+    } else if (ml.nb == kMergeColBatchLong) {
         hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchLong, CH>), grid, block, lds, stream, mp);
     } else {
         hipLaunchKernelGGL((merge_cols_kernel<D, false, kMergeColBatchShort, CH>), grid, block, lds, stream, mp);
     }
-    return launch_status();
 }
 
+// Launches the merge plan_merge chooses (kernel, variant, grid).
 template <int D>
 int launch_merge(MergeParams mp, int batch, int merge_mode, hipStream_t stream) {
-    const bool shared = merge_mode == PD_MERGE_SHARED;
-    // Row groups of an XCD-grouped partition grid (merge_xcd_row).
-    const uint32_t row_groups = mp.xcd_rows > 0
-        ? static_cast<uint32_t>(static_cast<int64_t>(batch) * mp.query_heads / mp.xcd_rows / 8) : 0u;
-    const int states = mp.parts >> mp.stride_shift;
-    // merge_rows keeps a row in one wave, loading (states / PGW) 16-byte
-    // columns per lane; with few rows of many states, merge_cols (D / 32 or
-    // D / 64 workgroups per row) finishes sooner.
-    const int rounds = (states + kWave / (D / 4) - 1) / (kWave / (D / 4));
-    const bool many_rows = static_cast<int64_t>(batch) * mp.query_heads >= kMergeRowsMin;
-    if (states <= merge_wave_max_parts<D>() && (many_rows || rounds <= 2)) {
-        if (mp.xcd_rows % kMergeRowsPerGroup != 0) mp.xcd_rows = 0;
-        const dim3 grid = mp.xcd_rows > 0
-            ? dim3(8 * mp.xcd_rows / kMergeRowsPerGroup, row_groups)
-            : dim3((mp.query_heads + kMergeRowsPerGroup - 1) / kMergeRowsPerGroup, batch);
-        if (shared) {
-            hipLaunchKernelGGL((merge_rows_kernel<D, true, kMergeWaveBatch, kMergeRowsPerGroup>), grid,
-                               dim3(kWave * kMergeRowsPerGroup), 0, stream, mp);
+    const MergeLaunch ml = plan_merge(mp, batch, D, merge_mode == PD_MERGE_SHARED, device_compute_units());
+    mp.xcd_rows = ml.xcd_rows;
+    const dim3 grid(ml.grid_x, ml.grid_y, ml.grid_z);
+    const dim3 block(ml.threads);
+    const size_t lds = static_cast<size_t>(ml.lds_bytes);
+    if (ml.kind == kMergeRows) {
+        if (ml.shared) {
+            hipLaunchKernelGGL((merge_rows_kernel<D, true, kMergeWaveBatch, kMergeRowsPerGroup>), grid, block, 0,
+                               stream, mp);
         } else {
-            hipLaunchKernelGGL((merge_rows_kernel<D, false, kMergeWaveBatch, kMergeRowsPerGroup>), grid,
-                               dim3(kWave * kMergeRowsPerGroup), 0, stream, mp);
+            hipLaunchKernelGGL((merge_rows_kernel<D, false, kMergeWaveBatch, kMergeRowsPerGroup>), grid, block, 0,
+                               stream, mp);
         }
-        return launch_status();
+    } else if (ml.ch == kMergeChunkLocal) {
+        launch_merge_cols<D, kMergeChunkLocal>(ml, grid, block, lds, stream, mp);
+    } else {
+        launch_merge_cols<D, kMergeChunkWide>(ml, grid, block, lds, stream, mp);
     }
-    return mp.xcd_rows > 0 ? launch_merge_cols<D, kMergeChunkLocal>(mp, batch, row_groups, states, shared, stream)
-                           : launch_merge_cols<D, kMergeChunkWide>(mp, batch, row_groups, states, shared, stream);
+    return launch_status();
 }
 
 int check_hints(int hints) {
@@ -696,16 +595,9 @@ int run_merge(const float* numerator, const float* stats, float* out, const int3
     mp.query_heads = query_heads;
     mp.split_tokens = split_tokens;
     mp.reach = reach < 0 ? call_reach(splits, split_tokens, table_width, page_size) : reach;
-    mp.first_states = mp.parts >> mp.stride_shift;
+    mp.first_states = merge_first_states(mp.parts, mp.stride_shift, split_tokens, mp.reach, length_bounds, batch);
     mp.xcd_rows = xcd_rows;
     mp.xcd_shift = xcd_shift;
-    if (length_bounds != nullptr) {
-        int64_t longest = 0;
-        for (int b = 0; b < batch; ++b)
-            longest = std::max<int64_t>(longest, lmin(mp.reach, length_bounds[b] < 0 ? 0 : length_bounds[b]));
-        const int64_t live = (kQuarters >> mp.stride_shift) * ((longest + split_tokens - 1) / split_tokens);
-        mp.first_states = static_cast<int>(lmin(mp.first_states, live));
-    }
     return head_dim == 64 ? launch_merge<64>(mp, batch, merge_mode, stream)
                           : launch_merge<128>(mp, batch, merge_mode, stream);
 }
@@ -739,6 +631,45 @@ AppendParams append_params(const void* k_new, const void* v_new, int dtype, cons
     a.capacity = static_cast<int64_t>(table_width) << a.page_shift;
     a.row_bytes = static_cast<uint32_t>(static_cast<size_t>(kv_heads) * head_dim * element_size(dtype));
     return a;
+}
+
+// ---------------------------------------------------------------------------
+// Streaming read (pd_stream_read): the bandwidth ceiling a decode launch is
+// measured against. Reads a_bytes of a, then b_bytes of b, once each, with the
+// decode's own load form (16 bytes per lane, plain global loads), each lane
+// keeping kStreamLoads loads in flight. The workgroups of the first ceil(a /
+// block) grid slots read a, the rest b. The loaded words are folded with XOR
+// into a value that is stored only if it equals `magic`, so no load is dead
+// code and the kernel writes (almost always) nothing.
+constexpr int kStreamThreads = 256;
+constexpr int kStreamLoads = 8;
+constexpr uint64_t kStreamBlockVectors = static_cast<uint64_t>(kStreamThreads) * kStreamLoads;
+
+struct StreamParams {
+    const u32x4* a;
+    const u32x4* b;
+    uint64_t a_vectors, b_vectors;  // 16-byte vectors of each buffer to read
+    uint64_t a_blocks;              // workgroups reading a
+    uint32_t magic;
+    uint32_t* sink;
+};
+
+__global__ void __launch_bounds__(kStreamThreads) stream_read_kernel(const StreamParams sp) {
+    const bool in_a = blockIdx.x < sp.a_blocks;
+    const u32x4* base = in_a ? sp.a : sp.b;
+    const uint64_t vectors = in_a ? sp.a_vectors : sp.b_vectors;
+    const uint64_t block = in_a ? blockIdx.x : blockIdx.x - sp.a_blocks;
+    const uint64_t first = block * kStreamBlockVectors + threadIdx.x;
+    u32x4 v[kStreamLoads];
+#pragma unroll
+    for (int i = 0; i < kStreamLoads; ++i) {
+        const uint64_t idx = first + static_cast<uint64_t>(i) * kStreamThreads;
+        v[i] = idx < vectors ? base[idx] : u32x4{0u, 0u, 0u, 0u};
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < kStreamLoads; ++i) acc ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+    if (acc == sp.magic) sp.sink[threadIdx.x & 1] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -919,14 +850,37 @@ int pd_append_kv_advance(const void* k_new, const void* v_new, int dtype, const 
     return launch_status();
 }
 
-int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, const int32_t* last_page_len, int32_t* table,
-                      int32_t* lengths, int32_t* overflow, int batch, int table_width, int page_size,
-                      int max_context, void* stream) {
-    if (!indptr || !indices || !last_page_len || !table || !lengths) return PD_ERR_NULL_POINTER;
-    if (batch < 1 || batch > 65535 || table_width < 1 || table_width > 65536) return PD_ERR_SHAPE;
+int pd_stream_read(const void* a, size_t a_bytes, const void* b, size_t b_bytes, uint32_t* sink, void* stream) {
+    if (!sink || (a_bytes && !a) || (b_bytes && !b)) return PD_ERR_NULL_POINTER;
+    if (a_bytes % 16 != 0 || b_bytes % 16 != 0 || reinterpret_cast<uintptr_t>(a) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(b) % 16 != 0)
+        return PD_ERR_SHAPE;
+    StreamParams sp{};
+    sp.a = static_cast<const u32x4*>(a);
+    sp.b = static_cast<const u32x4*>(b);
+    sp.a_vectors = a_bytes / 16;
+    sp.b_vectors = b_bytes / 16;
+    sp.a_blocks = (sp.a_vectors + kStreamBlockVectors - 1) / kStreamBlockVectors;
+    const uint64_t blocks = sp.a_blocks + (sp.b_vectors + kStreamBlockVectors - 1) / kStreamBlockVectors;
+    if (blocks == 0) return PD_OK;
+    if (blocks > 0x7FFFFFFFull) return PD_ERR_SHAPE;
+    sp.magic = 0x9E3779B9u;
+    sp.sink = sink;
+    hipLaunchKernelGGL(stream_read_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kStreamThreads), 0,
+                       static_cast<hipStream_t>(stream), sp);
+    return launch_status();
+}
+
+int pd_table_from_csr(const int32_t* indptr, const int32_t* indices, int64_t indices_count,
+                      const int32_t* last_page_len, int32_t* table, int32_t* lengths, int32_t* overflow, int batch,
+                      int table_width, int page_size, int max_context, void* stream) {
+    if (!indptr || !last_page_len || !table || !lengths || (!indices && indices_count > 0)) return PD_ERR_NULL_POINTER;
+    if (batch < 1 || batch > 65535 || table_width < 1 || table_width > 65536 || indices_count < 0)
+        return PD_ERR_SHAPE;
     if (page_size != 16 && page_size != 32) return PD_ERR_SHAPE;
     if (max_context < 0 || max_context > (1 << 20)) return PD_ERR_SHAPE;
-    CsrParams c{indptr, indices, last_page_len, table, lengths, overflow, table_width, page_size, max_context};
+    CsrParams c{indptr, indices, last_page_len, table, lengths, overflow, indices_count, table_width, page_size,
+                max_context};
     hipLaunchKernelGGL(table_from_csr_kernel, dim3(batch), dim3(256), 0, static_cast<hipStream_t>(stream), c);
     return launch_status();
 }

@@ -255,7 +255,7 @@ void table_from_csr(torch::Tensor indptr, torch::Tensor indices, torch::Tensor l
         flag = o.data_ptr<int32_t>();
     }
     c10::hip::HIPGuardMasqueradingAsCUDA guard(table.device());
-    check_status(pd_table_from_csr(indptr.data_ptr<int32_t>(), indices.data_ptr<int32_t>(),
+    check_status(pd_table_from_csr(indptr.data_ptr<int32_t>(), indices.data_ptr<int32_t>(), indices.numel(),
                                    last_page_len.data_ptr<int32_t>(), table.data_ptr<int32_t>(),
                                    lengths.data_ptr<int32_t>(), flag, static_cast<int>(table.size(0)),
                                    static_cast<int>(table.size(1)), static_cast<int>(page_size),
@@ -297,6 +297,22 @@ std::tuple<int64_t, int64_t> kernel_split(at::ScalarType q_dtype, at::ScalarType
     return {kernel_splits, kernel_split_tokens};
 }
 
+// One streaming read of the leading a_bytes of a and b_bytes of b (the
+// bandwidth ceiling of a decode launch over as many K/V bytes).
+void stream_read(torch::Tensor a, torch::Tensor b, int64_t a_bytes, int64_t b_bytes, torch::Tensor sink) {
+    for (const auto& t : {a, b, sink}) {
+        TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.device() == a.device(),
+                    "stream_read: contiguous tensors on one GPU");
+    }
+    TORCH_CHECK(a_bytes >= 0 && b_bytes >= 0 && a_bytes <= a.numel() * a.element_size() &&
+                    b_bytes <= b.numel() * b.element_size(),
+                "stream_read: byte counts must fit the tensors");
+    TORCH_CHECK(sink.numel() * sink.element_size() >= 8, "stream_read: sink needs 8 bytes");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+    check_status(pd_stream_read(a.data_ptr(), static_cast<size_t>(a_bytes), b.data_ptr(), static_cast<size_t>(b_bytes),
+                                static_cast<uint32_t*>(sink.data_ptr()), current_stream(a)));
+}
+
 PYBIND11_MODULE(_C, m) {
     m.doc() = "Split-K paged GQA decode for gfx950 (calls libpaged_decode_hip.so)";
     m.def("decode", &decode, "Paged split-K GQA decode (partition + merge)", py::arg("q"), py::arg("k"), py::arg("v"),
@@ -325,6 +341,8 @@ PYBIND11_MODULE(_C, m) {
           py::arg("head_dim"), py::arg("page_size"), py::arg("table_width"), py::arg("physical_pages"),
           py::arg("splits"), py::arg("split_tokens"), py::arg("length_bounds") = py::none(),
           py::arg("compute_units") = 0);
+    m.def("stream_read", &stream_read, "One streaming read of the leading bytes of two tensors", py::arg("a"),
+          py::arg("b"), py::arg("a_bytes"), py::arg("b_bytes"), py::arg("sink"));
     m.def("abi_version", &pd_abi_version, "ABI version the loaded HIP library reports");
     m.def("header_abi_version", [] { return PD_ABI_VERSION; }, "ABI version of the header this module was built with");
     m.def("build_digest", [] { return std::string(PD_BUILD_DIGEST); }, "Digest of the sources this module was built from");

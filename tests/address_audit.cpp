@@ -25,6 +25,8 @@
 #include <string>
 #include <vector>
 
+#include "cache_map.h"
+#include "merge_map.h"
 #include "partition_map.h"
 
 using namespace pd;
@@ -111,6 +113,7 @@ PartialParams params(const Problem& pr, int cus, bool mfma, bool rows) {
 struct Coverage {
     std::vector<uint8_t> writes;
     std::vector<int8_t> row_xcd;
+    Coverage() = default;
     Coverage(uint64_t states, uint64_t rows) : writes(states, 0), row_xcd(rows, -1) {}
     void store(uint64_t slot, int64_t row, int xcd) {
         AUDIT(slot < writes.size(), "state slot %" PRIu64 " past the workspace", slot);
@@ -474,14 +477,15 @@ void audit_gt(const Problem& pr, const PartialParams& p, bool mfma, Coverage& co
 }
 
 // Audits the launch planned for a partition-only call (states), and for a
-// full decode call (rows: the planner may choose a whole-row launch).
-bool audit(const Problem& pr, bool rows) {
+// full decode call (rows: the planner may choose a whole-row launch); leaves
+// the launch's params and which state slots it wrote in p and cov.
+bool audit(const Problem& pr, bool rows, PartialParams& p, Coverage& cov) {
     const int before = g_failures;
     const uint64_t checks_before = g_checks;
     const bool mfma = pr.q_elem == 2;
-    const PartialParams p = params(pr, 256, mfma, rows);
-    Coverage cov(static_cast<uint64_t>(pr.batch) * pr.q_heads * kQuarters * pr.splits,
-                 static_cast<uint64_t>(pr.batch) * pr.q_heads);
+    p = params(pr, 256, mfma, rows);
+    cov = Coverage(static_cast<uint64_t>(pr.batch) * pr.q_heads * kQuarters * pr.splits,
+                   static_cast<uint64_t>(pr.batch) * pr.q_heads);
     OutCoverage out(static_cast<uint64_t>(pr.batch) * pr.q_heads * pr.head_dim);
     if (pr.head_dim == 64) audit_gt<64>(pr, p, mfma, cov, out);
     else audit_gt<128>(pr, p, mfma, cov, out);
@@ -502,6 +506,335 @@ bool audit(const Problem& pr, bool rows) {
                 p.combine ? ", combined" : "",
                 p.xcd_shift >= 0 ? ", xcd-grouped" : p.merge_xcd_rows > 0 ? ", xcd merge" : "",
                 g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
+    std::fflush(stdout);
+    return g_failures == before;
+}
+
+
+// ---------------------------------------------------------------------------
+// Merge launches (merge_map.h): every workgroup, wave and lane of the merge a
+// call runs after its partition launch, following the kernels' loop
+// structure (decode.hip: merge_cols_kernel's optimistic first round, its two
+// statistics scans and its accumulation rounds; merge_rows_kernel's single
+// round). Every numerator and statistics load is checked against the
+// workspace, every LDS weight against the launch's dynamic LDS, every output
+// store against out (each element written exactly once), and every state the
+// merge counts as live must have been written by the partition launch.
+
+uint64_t g_merge_launches = 0;
+bool g_plant_merge_live = false;  // --plant-merge-live: merge params that count one partition too many
+
+struct MergeWalk {
+    const Problem& pr;
+    const MergeParams& mp;
+    const MergeLaunch& ml;
+    const Coverage& written;  // state slots the partition launch wrote
+    uint64_t numerator_elems, stats_elems;
+    OutCoverage out;
+
+    MergeWalk(const Problem& p, const MergeParams& m, const MergeLaunch& l, const Coverage& w)
+        : pr(p), mp(m), ml(l), written(w), out(static_cast<uint64_t>(p.batch) * p.q_heads * p.head_dim) {
+        const Buffers buf = buffers(p);
+        numerator_elems = buf.numerator_elems;
+        stats_elems = buf.stats_elems;
+    }
+    int parts() const { return mp.parts >> mp.stride_shift; }
+    int live(int b) const {
+        const int per_part = (kQuarters >> mp.stride_shift) + (g_plant_merge_live ? kQuarters : 0);
+        return live_states(pr.lengths[b], mp.split_tokens, mp.reach, per_part, parts());
+    }
+    void numerator_load(int64_t base, int j) {
+        AUDIT(j >= 0 && j < parts(), "merge read unit %d of %d", j, parts());
+        const int64_t idx = base + merge_numerator_offset(mp, pr.head_dim, j);
+        AUDIT(idx >= 0 && static_cast<uint64_t>(idx + 1) * 4 <= numerator_elems, "numerator load %" PRId64, idx);
+    }
+    void stats_load(int64_t base, int j) {
+        AUDIT(j >= 0 && j < parts(), "merge stats unit %d of %d", j, parts());
+        const int64_t idx = base + merge_stats_offset(mp, j);
+        AUDIT(idx >= 0 && static_cast<uint64_t>(idx + 1) * 2 <= stats_elems, "stats load %" PRId64, idx);
+    }
+    // A state the merge weighs in (j < live) holds what the partition launch wrote.
+    void used(int64_t row, int j) {
+        const uint64_t slot = static_cast<uint64_t>(row) * kQuarters * pr.splits + merge_stats_offset(mp, j);
+        AUDIT(slot < written.writes.size() && written.writes[slot] == 1, "merge uses state %d of row %" PRId64
+              " that the partition launch did not write", j, row);
+    }
+    void check_row(const MergeRow& mr) {
+        AUDIT(mr.row >= 0 && mr.row < static_cast<int64_t>(pr.batch) * pr.q_heads && mr.b == mr.row / pr.q_heads,
+              "merge row %" PRId64 " of sequence %d", mr.row, mr.b);
+    }
+};
+
+void walk_merge_cols(MergeWalk& mw) {
+    const MergeParams& mp = mw.mp;
+    const MergeLaunch& ml = mw.ml;
+    const int D = mw.pr.head_dim, CH = ml.ch, TPR = CH / 4, PG = kMergeThreads / TPR, NB = ml.nb, SU = NB / 2;
+    const int scan = ml.shared ? kMergeThreads : kWave, scan_round = SU * scan;
+    const int parts = mw.parts(), last = parts - 1;
+    AUDIT(D % CH == 0 && ml.grid_z == static_cast<uint32_t>(D / CH) && ml.threads == kMergeThreads, "merge_cols launch");
+    if (ml.shared) AUDIT(ml.lds_bytes == parts * 4 && ml.lds_bytes <= 160 * 1024, "shared merge LDS %d", ml.lds_bytes);
+    for (uint32_t bz = 0; bz < ml.grid_z; ++bz)
+        for (uint32_t by = 0; by < ml.grid_y; ++by)
+            for (uint32_t bx = 0; bx < ml.grid_x; ++bx) {
+                const MergeRow mr = merge_cols_row(mp, bx, by);
+                mw.check_row(mr);
+                if (mr.row < 0 || mr.b < 0 || mr.b >= mw.pr.batch) continue;
+                const int chunk = static_cast<int>(bz);
+                const int live = mw.live(mr.b);
+                const int first_n = imax(1, imin(parts, mp.first_states));
+                const int64_t sbase = merge_stats_base(mp, mr.row);
+                for (int t = 0; t < kMergeThreads; ++t) {
+                    const int lane = t % kWave, col = t % TPR, pg = t / TPR, scan0 = ml.shared ? t : lane;
+                    const int64_t nbase = merge_numerator_base(mp, mr.row, D, chunk, CH, col);
+                    auto load_round = [&](int base, int k0, int k1) {
+                        for (int k = k0; k < k1 && k < NB; ++k) {
+                            const int j = merge_load_unit(base, pg, k, PG, last);
+                            mw.numerator_load(nbase, j);
+                            if (!ml.shared) mw.stats_load(sbase, j);
+                        }
+                    };
+                    const int optimistic = imin(kOptimisticRounds, merge_cols_rounds(0, first_n, NB, PG));
+                    load_round(0, 0, optimistic);
+                    load_round(0, optimistic, merge_cols_rounds(0, live, NB, PG));
+                    const int scan_end = imin(scan_round, (first_n + scan - 1) / scan * scan);
+                    for (int pass = 0; pass < 2; ++pass) {  // maximum, then denominator (and weights)
+                        auto scan_at = [&](int base, int limit, bool load) {
+                            for (int i = 0; i < SU; ++i) {
+                                if (base + i * scan >= limit) continue;
+                                if (load) mw.stats_load(sbase, imin(base + scan0 + i * scan, last));
+                                const int j = base + scan0 + i * scan;
+                                if (pass == 1 && ml.shared && j < live)
+                                    AUDIT((j + 1) * 4 <= ml.lds_bytes, "weight[%d] write past %d B", j, ml.lds_bytes);
+                            }
+                        };
+                        scan_at(0, first_n, pass == 0);  // the first round stays in registers for pass 1
+                        for (int base = scan_end; base < live; base += scan_round) scan_at(base, live, true);
+                    }
+                    for (int base = 0;;) {
+                        const int rounds = merge_cols_rounds(base, live, NB, PG);
+                        for (int k = 0; k < rounds && k < NB; ++k) {
+                            const int j = base + pg + k * PG;
+                            if (j < live) {
+                                mw.used(mr.row, j);
+                                if (ml.shared) AUDIT((j + 1) * 4 <= ml.lds_bytes, "weight[%d] read", j);
+                            }
+                        }
+                        base += NB * PG;
+                        if (base >= live) break;
+                        load_round(base, 0, merge_cols_rounds(base, live, NB, PG));
+                    }
+                    AUDIT(pg < PG && col < TPR, "column_sum[%d][%d]", pg, col);
+                    if (t < CH) mw.out.store(mr.row * D + chunk * CH + t);
+                }
+            }
+}
+
+void walk_merge_rows(MergeWalk& mw) {
+    const MergeParams& mp = mw.mp;
+    const MergeLaunch& ml = mw.ml;
+    const int D = mw.pr.head_dim, TPR = D / 4, PGW = kWave / TPR, NB = ml.nb, RPG = kMergeRowsPerGroup;
+    const int parts = mw.parts(), last = parts - 1, rounds = (parts + PGW - 1) / PGW;
+    AUDIT(rounds <= NB && parts <= kWave && ml.threads == kWave * RPG, "merge_rows launch of %d states", parts);
+    for (uint32_t by = 0; by < ml.grid_y; ++by)
+        for (uint32_t bx = 0; bx < ml.grid_x; ++bx)
+            for (int wave = 0; wave < RPG; ++wave) {
+                const MergeRow mr = merge_rows_row(mp, bx, by, wave, RPG);
+                if (mr.row < 0) {
+                    AUDIT(mp.xcd_rows == 0 && static_cast<int>(bx) * RPG + wave >= mp.query_heads, "wave skipped");
+                    continue;
+                }
+                mw.check_row(mr);
+                if (mr.b < 0 || mr.b >= mw.pr.batch) continue;
+                const int live = mw.live(mr.b);
+                const int64_t sbase = merge_stats_base(mp, mr.row);
+                for (int lane = 0; lane < kWave; ++lane) {
+                    const int col = lane % TPR, pg = lane / TPR;
+                    const int64_t nbase = merge_numerator_base(mp, mr.row, D, 0, D, col);
+                    for (int k = 0; k < NB && k < rounds; ++k) {
+                        const int j = merge_load_unit(0, pg, k, PGW, last);
+                        mw.numerator_load(nbase, j);
+                        if (!ml.shared) mw.stats_load(sbase, j);
+                        const int jj = pg + k * PGW;
+                        if (jj < live) {
+                            mw.used(mr.row, jj);
+                            AUDIT(jj < kWave, "state %d's weight is outside the wave", jj);
+                        }
+                    }
+                    mw.stats_load(sbase, imin(lane, last));  // lane j holds state j's (m, l)
+                    if (pg == 0)
+                        for (int e = 0; e < 4; ++e) mw.out.store(mr.row * D + col * 4 + e);
+                }
+            }
+}
+
+// The merge a call runs over the states of partition launch p: the staged
+// entry's (pd_decode_merge: every state, plain rows, no bounds) or the full
+// call's (combined quarters, XCD-grouped rows, bounds), for both merge modes.
+bool audit_merges(const Problem& pr, const PartialParams& p, const Coverage& cov, bool full_call) {
+    const int before = g_failures;
+    const uint64_t checks_before = g_checks;
+    std::string kinds;
+    for (int shared = 0; shared < 2; ++shared) {
+        if (shared && kQuarters * pr.splits > 4096) continue;  // PD_SHARED_MERGE_MAX_PARTS
+        MergeParams mp{};
+        mp.parts = kQuarters * pr.splits;
+        const int stride = full_call && p.combine ? p.quarters_per_wg : 1;
+        mp.stride_shift = stride == 4 ? 2 : stride == 2 ? 1 : 0;
+        mp.query_heads = pr.q_heads;
+        mp.split_tokens = pr.split_tokens;
+        mp.reach = reach_of(pr);
+        mp.first_states = merge_first_states(mp.parts, mp.stride_shift, mp.split_tokens, mp.reach,
+                                             full_call && !pr.bounds.empty() ? pr.bounds.data() : nullptr, pr.batch);
+        mp.xcd_rows = full_call ? p.merge_xcd_rows : 0;
+        mp.xcd_shift = full_call ? p.merge_xcd_shift : 0;
+        const MergeLaunch ml = plan_merge(mp, pr.batch, pr.head_dim, shared != 0, 256);
+        mp.xcd_rows = ml.xcd_rows;
+        MergeWalk mw(pr, mp, ml, cov);
+        if (ml.kind == kMergeRows) walk_merge_rows(mw);
+        else walk_merge_cols(mw);
+        for (size_t e = 0; e < mw.out.writes.size(); ++e)
+            AUDIT(mw.out.writes[e] == 1, "merge output element %zu written %d times", e, mw.out.writes[e]);
+        ++g_merge_launches;
+        kinds += std::string(shared ? " shared:" : " serial:") + (ml.kind == kMergeRows ? "rows" : "cols") +
+                 (ml.kind == kMergeCols ? "/NB" + std::to_string(ml.nb) + "/CH" + std::to_string(ml.ch) : "") +
+                 (ml.xcd_rows > 0 ? "/xcd" : "") + (mp.stride_shift ? "/stride" + std::to_string(stride) : "");
+    }
+    std::printf("%-44s merge%s%s, %" PRIu64 " checks: %s\n", (pr.name + (full_call ? " [call]" : " [stage]")).c_str(),
+                kinds.c_str(), "", g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
+    std::fflush(stdout);
+    return g_failures == before;
+}
+
+
+// ---------------------------------------------------------------------------
+// KV-cache append (cache_map.h; decode.hip: append_kv_kernel with explicit
+// positions, grid tokens x batch, and append_kv_advance_kernel, grid batch,
+// all or nothing per sequence), 256 threads each copying 16-byte chunks of
+// a token's K and V rows. Every table read, new-token read and cache write is
+// checked against its buffer, and every written row is the one the decode
+// reads the token from (page table[b, pos / T], slot pos % T).
+
+bool g_plant_append_capacity = false;  // --plant-append: capacity one page past the table (negative control)
+bool g_plant_csr_count = false;        // --plant-csr: no bound on the indices read (negative control)
+
+struct AppendProblem {
+    std::string name;
+    int batch, tokens, kv_heads, head_dim, elem, page_size, width, pages, max_context;
+    std::vector<int32_t> table, starts;  // starts: positions (explicit) or lengths (advance)
+    bool advance;
+};
+
+bool audit_append(const AppendProblem& ap) {
+    const int before = g_failures;
+    const uint64_t checks_before = g_checks;
+    AppendParams a{};
+    a.tokens = ap.tokens;
+    a.table_width = ap.width;
+    a.page_shift = ap.page_size == 16 ? 4 : 5;
+    a.physical_pages = ap.pages;
+    a.capacity = static_cast<int64_t>(ap.width) << a.page_shift;
+    if (ap.advance) a.capacity = lmin(a.capacity, ap.max_context);
+    if (g_plant_append_capacity) a.capacity = static_cast<int64_t>(ap.width + 1) << a.page_shift;
+    a.row_bytes = static_cast<uint32_t>(ap.kv_heads * ap.head_dim * ap.elem);
+    const int64_t new_bytes = static_cast<int64_t>(ap.batch) * ap.tokens * a.row_bytes;
+    const int64_t cache_bytes = static_cast<int64_t>(ap.pages) * ap.page_size * a.row_bytes;
+    const uint32_t chunks = a.row_bytes / 16u;
+    AUDIT(a.row_bytes % 16 == 0, "row of %u bytes", a.row_bytes);
+    std::vector<uint8_t> row_writes(static_cast<size_t>(ap.pages) * ap.page_size, 0);
+    int written = 0;
+    // Cache row of (b, pos) through the kernel's map, its table read checked.
+    auto row_of = [&](int b, int64_t pos) -> int64_t {
+        const int64_t entry = append_table_entry(a, pos);
+        if (entry < 0) return -1;
+        AUDIT(entry < ap.width, "append reads table entry %" PRId64 " of a %d-wide row", entry, ap.width);
+        if (entry >= ap.width) return -1;
+        const int page = ap.table[static_cast<size_t>(b) * ap.width + entry];
+        const int64_t row = append_cache_row(a, page, pos);
+        if (row >= 0) {
+            AUDIT(pos < static_cast<int64_t>(ap.width) * ap.page_size && page >= 0 && page < ap.pages &&
+                      row == static_cast<int64_t>(page) * ap.page_size + pos % ap.page_size,
+                  "append row %" PRId64 " for position %" PRId64, row, pos);
+            if (ap.advance) AUDIT(pos < ap.max_context, "append past max_context at %" PRId64, pos);
+        }
+        return row;
+    };
+    auto copy = [&](int b, int j, int64_t dst) {
+        const int64_t src = append_source_row(a, b, j);
+        AUDIT(src >= 0 && src < static_cast<int64_t>(ap.batch) * ap.tokens, "source row %" PRId64, src);
+        for (int t = 0; t < 256; ++t)
+            for (uint32_t c = static_cast<uint32_t>(t); c < chunks; c += 256) {
+                const int64_t so = append_chunk_offset(a, src, c), d = append_chunk_offset(a, dst, c);
+                AUDIT(so >= 0 && so + 16 <= new_bytes, "new-token read at %" PRId64, so);
+                AUDIT(d >= 0 && d + 16 <= cache_bytes, "cache write at %" PRId64, d);
+            }
+        if (dst >= 0 && static_cast<size_t>(dst) < row_writes.size()) ++row_writes[dst];
+        ++written;
+    };
+    for (int b = 0; b < ap.batch; ++b) {
+        if (ap.advance) {  // workgroup b
+            const int64_t base = ap.starts[b];
+            bool fits = true;
+            for (int j = 0; j < ap.tokens; ++j) fits &= row_of(b, base + j) >= 0;
+            if (fits)
+                for (int j = 0; j < ap.tokens; ++j) copy(b, j, row_of(b, base + j));
+        } else {  // workgroups (j, b)
+            for (int j = 0; j < ap.tokens; ++j) {
+                const int64_t dst = row_of(b, static_cast<int64_t>(ap.starts[b]) + j);
+                if (dst >= 0) copy(b, j, dst);
+            }
+        }
+    }
+    std::printf("%-44s %s %d tokens x %d sequences, %d rows written, %" PRIu64 " checks: %s\n", ap.name.c_str(),
+                ap.advance ? "append+advance" : "append", ap.tokens, ap.batch, written, g_checks - checks_before,
+                g_failures == before ? "ok" : "FAILED");
+    std::fflush(stdout);
+    return g_failures == before;
+}
+
+// CSR page lists -> page table (cache_map.h; decode.hip: table_from_csr_kernel,
+// grid batch x 256 threads). Every indptr, last-page-length and indices read
+// and every table and lengths write is checked against its buffer.
+struct CsrProblem {
+    std::string name;
+    int batch, width, page_size, max_context;
+    std::vector<int32_t> indptr, indices, last;
+};
+
+bool audit_csr(const CsrProblem& cp) {
+    const int before = g_failures;
+    const uint64_t checks_before = g_checks;
+    CsrParams c{};
+    c.indices_count = g_plant_csr_count ? (int64_t{1} << 40) : static_cast<int64_t>(cp.indices.size());
+    c.table_width = cp.width;
+    c.page_size = cp.page_size;
+    c.max_context = cp.max_context;
+    std::vector<uint8_t> table_writes(static_cast<size_t>(cp.batch) * cp.width, 0);
+    int rejected = 0;
+    for (int b = 0; b < cp.batch; ++b) {
+        AUDIT(b + 1 < static_cast<int>(cp.indptr.size()), "indptr read %d", b + 1);
+        const int64_t begin = cp.indptr[b], end = cp.indptr[b + 1];
+        int last = 0;
+        if (end > begin) {
+            AUDIT(b < static_cast<int>(cp.last.size()), "last_page_len read %d", b);
+            last = cp.last[b];
+        }
+        const CsrRow r = csr_row(c, begin, end, last);
+        rejected += r.fits ? 0 : 1;
+        for (int t = 0; t < 256; ++t)
+            for (int i = t; i < cp.width; i += 256) {
+                const int64_t e = static_cast<int64_t>(b) * cp.width + i;
+                AUDIT(e < static_cast<int64_t>(table_writes.size()), "table write %" PRId64, e);
+                if (e < static_cast<int64_t>(table_writes.size())) ++table_writes[e];
+                if (i < r.live)
+                    AUDIT(r.begin + i >= 0 && r.begin + i < static_cast<int64_t>(cp.indices.size()),
+                          "indices read %" PRId64 " of %zu", r.begin + i, cp.indices.size());
+            }
+        if (r.fits) AUDIT(r.length <= cp.max_context && r.live <= cp.width, "row %d length %" PRId64, b, r.length);
+    }
+    for (size_t e = 0; e < table_writes.size(); ++e)
+        AUDIT(table_writes[e] == 1, "table entry %zu written %d times", e, table_writes[e]);
+    std::printf("%-44s csr -> table, %d of %d rows rejected, %" PRIu64 " checks: %s\n", cp.name.c_str(), rejected,
+                cp.batch, g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
     std::fflush(stdout);
     return g_failures == before;
 }
@@ -739,6 +1072,90 @@ int main(int argc, char** argv) {
         for (int i = 0; i < 128; ++i) big.table[i] = 163840 - 1 - i;
         add(big);
     }
+    // KV-cache appends: explicit positions inside, at and past the table's end
+    // and negative; invalid page ids (-1, physical_pages, INT_MAX); several
+    // tokens per sequence; both page sizes; FP8, 16-bit and FP32 rows of D 64
+    // and 128; the advance variant below, at and past max_context.
+    std::vector<AppendProblem> appends;
+    {
+        Lcg rng{909};
+        for (int i = 0; i < (quick ? 6 : 32); ++i) {
+            AppendProblem ap;
+            ap.batch = 1 + rng.below(8);
+            ap.tokens = 1 + rng.below(40);
+            ap.kv_heads = 1 << rng.below(4);
+            ap.head_dim = rng.below(2) ? 128 : 64;
+            ap.elem = 1 << rng.below(3);
+            ap.page_size = rng.below(2) ? 32 : 16;
+            ap.width = 1 + rng.below(12);
+            ap.pages = ap.batch * ap.width + rng.below(3);
+            ap.advance = rng.below(2) != 0;
+            const int cap = ap.width * ap.page_size;
+            ap.max_context = rng.below(cap + 1);
+            ap.table.resize(static_cast<size_t>(ap.batch) * ap.width);
+            for (auto& id : ap.table) id = rng.below(ap.pages);
+            const int32_t invalid[] = {-1, ap.pages, 2147483647};
+            for (int k = 0; k < 3; ++k) ap.table[rng.below(static_cast<int>(ap.table.size()))] = invalid[k];
+            ap.starts.resize(ap.batch);
+            for (auto& st : ap.starts) st = rng.below(cap + 12) - 6;
+            ap.starts[0] = cap - ap.tokens;  // exactly up to the table's end
+            ap.name = "append " + std::to_string(i) + (ap.advance ? " advance" : " positions") + " B" +
+                      std::to_string(ap.batch) + " n" + std::to_string(ap.tokens) + " T" + std::to_string(ap.page_size) +
+                      " W" + std::to_string(ap.width) + " row " + std::to_string(ap.kv_heads * ap.head_dim * ap.elem);
+            appends.push_back(ap);
+        }
+        AppendProblem end{"append at the table's end", 2, 4, 8, 128, 2, 16, 4, 8, 64, {}, {60, 61}, false};
+        end.table = {0, 1, 2, 3, 4, 5, 6, 7};
+        appends.push_back(end);
+    }
+    // CSR page lists: valid lists (empty rows included), lists longer than
+    // the table, last-page lengths outside [1, T], lengths past max_context,
+    // negative counts, and lists reaching before or past the indices tensor.
+    std::vector<CsrProblem> csrs;
+    {
+        Lcg rng{4242};
+        for (int i = 0; i < (quick ? 6 : 32); ++i) {
+            CsrProblem cp;
+            cp.batch = 1 + rng.below(10);
+            cp.width = 1 + rng.below(300);
+            cp.page_size = rng.below(2) ? 32 : 16;
+            cp.max_context = rng.below(cp.width * cp.page_size + 1);
+            cp.indptr.assign(1, 0);
+            for (int b = 0; b < cp.batch; ++b) cp.indptr.push_back(cp.indptr.back() + rng.below(cp.width + 3));
+            cp.indices.resize(cp.indptr.back());
+            for (auto& x : cp.indices) x = rng.below(1000);
+            cp.last.resize(cp.batch);
+            for (auto& l : cp.last) l = rng.below(cp.page_size + 2);  // 0 and T + 1 are invalid
+            const int kind = rng.below(4);  // 0: as drawn; 1: a negative count; 2: past the end; 3: before the start
+            const int b = rng.below(cp.batch);
+            if (kind == 1) cp.indptr[b + 1] = cp.indptr[b] - 1;
+            if (kind == 2) cp.indptr[b + 1] = static_cast<int32_t>(cp.indices.size()) + 1 + rng.below(5);
+            if (kind == 3) cp.indptr[b] = -1 - rng.below(5);
+            cp.name = "csr " + std::to_string(i) + " B" + std::to_string(cp.batch) + " W" + std::to_string(cp.width) +
+                      " T" + std::to_string(cp.page_size) + (kind == 1 ? " negative count" : kind == 2 ? " past end"
+                                                             : kind == 3 ? " before start" : "");
+            csrs.push_back(cp);
+        }
+        // A list that meets every other rule but reaches past the indices
+        // tensor (5 pages from entry 4 of 6): only the indices bound rejects it.
+        csrs.push_back(CsrProblem{"csr list past the indices end", 2, 8, 16, 128, {0, 4, 9}, {0, 1, 2, 3, 4, 5}, {16, 16}});
+    }
+    if (mode == "--plant-merge-live" || mode == "--plant-append" || mode == "--plant-csr") {
+        // Negative controls: merge params that count one partition too many
+        // as live, an append capacity one page past the table, a CSR
+        // conversion without its indices bound. Each walk must report it.
+        g_plant_merge_live = mode == "--plant-merge-live";
+        g_plant_append_capacity = mode == "--plant-append";
+        g_plant_csr_count = mode == "--plant-csr";
+        std::vector<Problem> kept;
+        if (g_plant_merge_live)
+            for (const auto& pr : problems)
+                if (pr.name.rfind("llama3-8b B4 L4096 fp16", 0) == 0 || pr.name.rfind("edges fp16", 0) == 0)
+                    kept.push_back(pr);
+        problems = kept;
+        if (!g_plant_append_capacity) appends.clear();
+        if (!g_plant_csr_count) csrs.clear();
+    }
     if (mode == "--plant-reach") {
         // Negative control: the same problems with launch params that clamp
         // lengths to the table only. The walk must report reads past the
@@ -751,27 +1168,49 @@ int main(int argc, char** argv) {
     }
     int failed = 0;
     for (const auto& pr : problems) {
-        failed += audit(pr, false) ? 0 : 1;
-        // The plan for a full decode call, when it is a whole-row launch.
-        if (params(pr, 256, pr.q_elem == 2, true).row_mode) failed += audit(pr, true) ? 0 : 1;
-        // A full call over coarser partitions: fewer of them, covering at
-        // least the caller's, their states inside the caller's workspace
-        // (the audited buffers are those of the coarser split, a prefix).
+        // The staged entries: the partition launch, then pd_decode_merge over
+        // every state slot it left.
+        PartialParams stage;
+        Coverage stage_cov;
+        failed += audit(pr, false, stage, stage_cov) ? 0 : 1;
+        failed += audit_merges(pr, stage, stage_cov, false) ? 0 : 1;
+        // The full decode call: over coarser partitions (fewer of them,
+        // covering at least the caller's, their states inside the caller's
+        // workspace: the audited buffers are those of the coarser split, a
+        // prefix), or one whole-row launch, or the staged partition launch
+        // with the full call's merge.
         const KernelSplit ks = full_call_split(pr.q_elem == 4, pr.kv_elem, pr.batch, pr.q_heads, pr.kv_heads,
                                                pr.head_dim, pr.page_size, pr.width, pr.splits, pr.split_tokens,
                                                pr.bounds.empty() ? nullptr : pr.bounds.data(), 256);
-        if (ks.splits != pr.splits || ks.split_tokens != pr.split_tokens) {
+        Problem call = pr;
+        const bool coarse = ks.splits != pr.splits || ks.split_tokens != pr.split_tokens;
+        if (coarse) {
             AUDIT(ks.splits < pr.splits && ks.split_tokens % pr.split_tokens == 0 &&
                       static_cast<int64_t>(ks.splits) * ks.split_tokens >=
                           static_cast<int64_t>(pr.splits) * pr.split_tokens,
                   "coarse split %d x %d for %d x %d", ks.splits, ks.split_tokens, pr.splits, pr.split_tokens);
-            Problem coarse = pr;
-            coarse.name += " coarse x" + std::to_string(ks.split_tokens / pr.split_tokens);
-            coarse.splits = ks.splits;
-            coarse.split_tokens = ks.split_tokens;
-            failed += audit(coarse, true) ? 0 : 1;
+            call.name += " coarse x" + std::to_string(ks.split_tokens / pr.split_tokens);
+            call.splits = ks.splits;
+            call.split_tokens = ks.split_tokens;
+        }
+        const PartialParams planned = params(call, 256, call.q_elem == 2, true);
+        const bool same_launch = !coarse && !planned.row_mode && planned.grid_x == stage.grid_x &&
+                                 planned.grid_y == stage.grid_y && planned.combine == stage.combine &&
+                                 planned.quarters_per_wg == stage.quarters_per_wg &&
+                                 planned.heads_per_wg == stage.heads_per_wg && planned.xcd_shift == stage.xcd_shift;
+        if (same_launch) {
+            failed += audit_merges(call, planned, stage_cov, true) ? 0 : 1;
+        } else {
+            PartialParams p;
+            Coverage cov;
+            failed += audit(call, true, p, cov) ? 0 : 1;
+            if (!p.row_mode) failed += audit_merges(call, p, cov, true) ? 0 : 1;
         }
     }
-    std::printf("%zu problems, %" PRIu64 " checks, %d failures\n", problems.size(), g_checks, g_failures);
+    for (const auto& ap : appends) failed += audit_append(ap) ? 0 : 1;
+    for (const auto& cp : csrs) failed += audit_csr(cp) ? 0 : 1;
+    std::printf("%zu problems, %" PRIu64 " merge launches, %zu appends, %zu csr conversions, %" PRIu64
+                " checks, %d failures\n", problems.size(), g_merge_launches, appends.size(), csrs.size(), g_checks,
+                g_failures);
     return failed == 0 ? 0 : 1;
 }

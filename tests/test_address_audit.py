@@ -5,7 +5,10 @@ The reference ran compute-sanitizer memcheck over its GPU tests
 leave its buffer? -- is answered on the CPU:
 
 * ``tests/address_audit.cpp`` walks every workgroup, wave, lane and load group
-  of the partition launches for the measured workloads and the edge cases
+  of the partition launches, and every workgroup and lane of the merge
+  launches that follow them (both merge kernels in every variant: serial and
+  shared, plain and XCD-grouped rows, combined-quarter strides, short and
+  long rounds, both column-chunk widths), for the measured workloads and the edge cases
   (lengths around page and partition boundaries, invalid page ids, uncommon
   head layouts, a 1M-token context in a 65536-wide table, pages above 4 GiB,
   work lists and rectangular grids with tail items under exact, low and zero
@@ -14,7 +17,14 @@ leave its buffer? -- is answered on the CPU:
   same ``partition_map.h`` functions the kernels call, and checks every load,
   store and LDS access against its buffer, every live token against the page
   its table entry names, and that every live state slot is written exactly
-  once. It is compiled with AddressSanitizer and UndefinedBehaviorSanitizer.
+  once; that every merge load, LDS weight and output store stays in its buffer,
+  every output element is written once and every state a merge counts as
+  live was written by its partition launch. It also walks the KV-cache append
+  (explicit positions and the advancing variant) and the device CSR -> page
+  table conversion over valid and malformed metadata. Each kernel family has
+  a planted-mistake negative control (wrong reach, merge live count, append
+  capacity, missing CSR indices bound) that the walk must report. It is
+  compiled with AddressSanitizer and UndefinedBehaviorSanitizer.
 * ``oracle/cpu_decode.c`` (the FP32 restatement the bench times) runs under
   the same sanitizers on ragged, empty-row, invalid-page-id and both-format
   cases through a small C driver.
@@ -42,12 +52,17 @@ def compiler(name):
     return path
 
 
-def test_partition_address_map_stays_in_bounds(tmp_path):
-    exe = tmp_path / "address_audit"
+@pytest.fixture(scope="module")
+def audit_exe(tmp_path_factory):
+    exe = tmp_path_factory.mktemp("audit") / "address_audit"
     subprocess.run([compiler("g++"), "-std=c++17", "-O1", "-g", "-Wall", "-Wno-unknown-pragmas", *SANITIZE,
                     f"-I{CSRC}", str(REPO / "tests" / "address_audit.cpp"), "-o", str(exe)],
                    check=True, capture_output=True, text=True)
-    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600, env=ENV)
+    return exe
+
+
+def test_partition_address_map_stays_in_bounds(audit_exe):
+    run = subprocess.run([str(audit_exe)], capture_output=True, text=True, timeout=600, env=ENV)
     assert run.returncode == 0, run.stdout[-4000:] + run.stderr[-4000:]
     assert ", 0 failures" in run.stdout
     # The walk covered the measured workloads and the compacted launches.
@@ -64,28 +79,42 @@ def test_partition_address_map_stays_in_bounds(tmp_path):
     assert "xcd merge" in "\n".join(line for line in run.stdout.splitlines()
                                      if line.startswith("long mha B1 Hq32/32 L32768 split 1024 "))
     lines = run.stdout.splitlines()
+    launches = [line for line in lines if " grid " in line]  # partition launches (merge lines say "merge")
     for name in ("llama3-8b B4 L4096 fp16", "llama3-8b B4 L4096 fp8", "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp16",
                  "xcd gqa4 B8 Hq32/8 D128 L1024 split 128 fp8", "xcd mqa B64 Hq16/1 D64 L1024 split 256 fp16",
                  "xcd mha B2 Hq16/16 D128 L2048 split 256 fp16", "xcd fp32 B8 Hq16/8 D64 L1024 split 128",
                  "xcd llama3-8b B4 L4096 reserve x4", "xcd mqa B128 Hq16/1 D64 L1024 reserve x2"):
-        exact = [line for line in lines if line.startswith((name + " bounds=exact ", name + " bounds=half "))]
-        plain = [line for line in lines if line.startswith(name + " ") and "bounds=" not in line]
+        exact = [line for line in launches if line.startswith((name + " bounds=exact ", name + " bounds=half "))]
+        plain = [line for line in launches if line.startswith(name + " ") and "bounds=" not in line]
         assert len(exact) >= 2 and all("xcd-grouped" in line or "xcd merge" in line for line in exact), name
         assert plain and not any("xcd-grouped" in line for line in plain), name
+    # Every merge kernel variant was walked, for staged and full calls.
+    merges = [line for line in lines if " merge " in line and line.rstrip().endswith("ok")]
+    for variant in ("serial:rows", "shared:rows", "rows/xcd", "cols/NB8/CH64", "cols/NB32/CH64", "cols/NB8/CH32/xcd",
+                    "cols/NB32/CH32/xcd", "shared:cols/NB32", "stride2", "stride4"):
+        assert any(variant in line for line in merges), variant
+    assert any("[stage]" in line for line in merges) and any("[call]" in line for line in merges)
+    summary = lines[-1]
+    assert " merge launches, " in summary and " appends, " in summary and " csr conversions, " in summary
+    assert any(line.startswith("append") and "append+advance" in line for line in lines)
+    assert any(line.startswith("csr list past the indices end") and "1 of 2 rows rejected" in line for line in lines)
 
 
-def test_address_audit_flags_reads_past_the_callers_partitions(tmp_path):
-    """Negative control of the check above: with launch params that clamp
-    lengths to the table only (not to the caller's splits * split_tokens), a
-    full call over coarser partitions reads tokens the caller's partitions
-    exclude, and the walk must report them."""
-    exe = tmp_path / "address_audit"
-    subprocess.run([compiler("g++"), "-std=c++17", "-O1", "-g", "-Wall", "-Wno-unknown-pragmas", *SANITIZE,
-                    f"-I{CSRC}", str(REPO / "tests" / "address_audit.cpp"), "-o", str(exe)],
-                   check=True, capture_output=True, text=True)
-    run = subprocess.run([str(exe), "--plant-reach"], capture_output=True, text=True, timeout=300, env=ENV)
+@pytest.mark.parametrize("plant,message", [
+    ("--plant-reach", "wave range [768, 896)"),
+    ("--plant-merge-live", "that the partition launch did not write"),
+    ("--plant-append", "append reads table entry"),
+    ("--plant-csr", "indices read 6 of 6"),
+])
+def test_address_audit_flags_planted_mistakes(audit_exe, plant, message):
+    """Negative controls: launch parameters with one mistake planted (lengths
+    clamped to the table instead of the caller's partitions; a merge live
+    count one partition too long; an append capacity one page past the table;
+    a CSR conversion without its bound on the indices read). Each walk must
+    report the accesses the mistake causes."""
+    run = subprocess.run([str(audit_exe), plant], capture_output=True, text=True, timeout=300, env=ENV)
     assert run.returncode == 1, run.stdout[-4000:] + run.stderr[-4000:]
-    assert "FAIL" in run.stderr and "wave range [768, 896)" in run.stderr
+    assert "FAIL" in run.stderr and message in run.stderr
 
 
 CPU_DRIVER = r"""

@@ -469,3 +469,31 @@ def test_lengths_past_the_callers_partitions_are_not_read(kv_dtype):
     for out in outs:
         assert_parity(out.cpu().numpy(), expected, np.float16)
     torch.testing.assert_close(outs[1], outs[0], rtol=1e-5, atol=1e-6)
+
+
+def test_stream_read_reads_without_writing():
+    """The streaming-read ceiling kernel reads whole and partial blocks of both
+    buffers and leaves its sink untouched (zeros fold to zero, never the magic
+    value), also inside a captured graph."""
+    announce("pd_stream_read")
+    lib = cabi.load()
+    a = torch.zeros(3 * 2048 * 4 + 4, dtype=torch.int32, device="cuda")   # 3 blocks + one vector
+    b = torch.zeros(5 * 4, dtype=torch.int32, device="cuda")             # less than a block
+    sink = torch.full((2,), 7, dtype=torch.int32, device="cuda")
+    status = lib.pd_stream_read(a.data_ptr(), a.numel() * 4, b.data_ptr(), b.numel() * 4, sink.data_ptr(), stream())
+    assert status == cabi.PD_OK, cabi.status_string(lib, status)
+    from paged_decode.runtime import load_extension
+
+    ext = load_extension()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            ext.stream_read(a, b, a.numel() * 4, 64, sink)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert sink.tolist() == [7, 7]
+    with pytest.raises(RuntimeError, match="fit"):
+        ext.stream_read(a, b, a.numel() * 4 + 16, 0, sink)

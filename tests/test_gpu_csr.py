@@ -94,6 +94,31 @@ def test_device_csr_empty_rows_and_overflow():
     assert int(flag.item()) == 1 and small._lengths.cpu().numpy().tolist() == [0] * 6
 
 
+def test_device_csr_page_lists_reaching_past_indices_are_not_read():
+    """A malformed indptr whose page list reaches past the indices tensor (or
+    starts before it) gives an empty row and raises the overflow flag instead
+    of reading outside indices; well-formed rows convert normally."""
+    announce("device csr: page lists outside the indices tensor")
+    layout = Layout(4, 8, 2, 64, 16, 4 * 8)
+    table = np.arange(4 * 8, dtype=np.int32).reshape(4, 8)
+    lengths = np.array([128, 64, 16, 128], dtype=np.int32)
+    for b, n in enumerate(lengths):
+        table[b, (n + 15) // 16:] = -1
+    indptr, indices, last = csr_with_empty_rows(layout, table, lengths)
+    plan = DecodePlan(layout, table, lengths, max_context=128)
+    bad = indptr.copy()
+    bad[3] = -5                     # row 2: a negative page count; row 3: starts before indices ...
+    bad[4] = indices.size + 5       # ... and ends past its last entry. Both rows are rejected.
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    plan.refresh_csr(*device(bad, indices, last), overflow=flag)
+    torch.cuda.synchronize()
+    got_t, got_l = plan._table.cpu().numpy(), plan._lengths.cpu().numpy()
+    assert int(flag.item()) == 1
+    assert got_l.tolist() == [128, 64, 0, 0]
+    np.testing.assert_array_equal(got_t[:2], table[:2])
+    assert np.all(got_t[2:] == -1)
+
+
 @pytest.mark.parametrize("merge", ["serial", "shared"])
 def test_captured_csr_refresh_then_decode(merge):
     """One graph = load this step's CSR page lists, then decode; replayed after the lists change."""

@@ -27,6 +27,7 @@ import torch  # noqa: E402
 
 import rebinding  # noqa: E402
 from oracle.fp64 import dense_attention  # noqa: E402
+from paged_decode import cabi  # noqa: E402
 from paged_decode.runtime import load_extension  # noqa: E402
 from paged_decode.workload import make_workload  # noqa: E402
 
@@ -61,7 +62,7 @@ def test_reference_ten_argument_call(name, merge_mode, binding):
     numerator, stats, out = reference_buffers(w.layout, w.lengths, w.split_tokens, device)
     extension = BINDINGS[binding]()
     if binding == "documented":
-        assert extension.__name__ == "paged_decode_amd._C" and extension.header_abi_version() == 14
+        assert extension.__name__ == "paged_decode_amd._C" and extension.header_abi_version() == cabi.PD_ABI_VERSION
     result = extension.decode(q, k, v, table, lengths, numerator, stats, out, w.split_tokens, merge_mode)
     assert result is None
     expected = dense_attention(*host, w.table, w.lengths)

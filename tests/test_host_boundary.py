@@ -83,7 +83,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == cabi.PD_ABI_VERSION == 14
+    assert lib.pd_abi_version() == cabi.PD_ABI_VERSION == 15
     assert re.search(r"#define\s+PD_ABI_VERSION\s+(\d+)", HEADER.read_text()).group(1) == str(cabi.PD_ABI_VERSION)
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
@@ -185,7 +185,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 14) return 1;
+    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 15) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
@@ -193,9 +193,10 @@ int main(void) {
     if (pd_append_kv(NULL, NULL, PD_DTYPE_FP8_E4M3, NULL, NULL, NULL, NULL,
                      4, 1, 8, 128, 16, 256, 1024, NULL) != PD_ERR_NULL_POINTER) return 4;
     if (strstr(pd_status_string(PD_ERR_SHAPE), "dimension") == NULL) return 5;
-    if (pd_table_from_csr(NULL, NULL, NULL, NULL, NULL, NULL, 4, 256, 16, 4096, NULL) != PD_ERR_NULL_POINTER) return 6;
+    if (pd_table_from_csr(NULL, NULL, 0, NULL, NULL, NULL, NULL, 4, 256, 16, 4096, NULL) != PD_ERR_NULL_POINTER) return 6;
     if (strstr(pd_status_string(PD_ERR_HINT), "hint") == NULL || PD_HINT_UNSHARED_PAGES != 1 ||
         PD_HINT_RAGGED_LENGTHS != 2) return 7;
+    if (pd_stream_read(NULL, 16, NULL, 0, NULL, NULL) != PD_ERR_NULL_POINTER) return 8;
     puts("ok");
     return 0;
 }
@@ -393,12 +394,14 @@ def test_page_sharing_hint_follows_the_table():
 
 
 def test_table_from_csr_rejects_invalid_arguments():
-    """pd_table_from_csr: null pointers (overflow may be NULL) and dimensions, before any launch."""
+    """pd_table_from_csr: null pointers (overflow may be NULL; indices too when it holds no entry) and
+    dimensions, before any launch."""
     lib = cabi.load()
     ptrs, _keep = fake(6)
 
-    def call(indptr, indices, last, table, lengths, overflow, batch=4, width=256, page=16, max_context=4096):
-        return lib.pd_table_from_csr(indptr, indices, last, table, lengths, overflow, batch, width, page,
+    def call(indptr, indices, last, table, lengths, overflow, batch=4, width=256, page=16, max_context=4096,
+             count=100):
+        return lib.pd_table_from_csr(indptr, indices, count, last, table, lengths, overflow, batch, width, page,
                                      max_context, None)
 
     for i in range(5):
@@ -406,7 +409,7 @@ def test_table_from_csr_rejects_invalid_arguments():
         broken[i] = None
         assert call(*broken, ptrs[5]) == cabi.PD_ERR_NULL_POINTER
     for over in (dict(batch=0), dict(batch=65536), dict(width=0), dict(width=65537), dict(page=8),
-                 dict(max_context=-1), dict(max_context=(1 << 20) + 1)):
+                 dict(max_context=-1), dict(max_context=(1 << 20) + 1), dict(count=-1)):
         assert call(*ptrs, **over) == cabi.PD_ERR_SHAPE, over
 
 
@@ -482,3 +485,14 @@ def test_oracle_build_is_refused_after_gpu_init(gpu_initialised):
 def test_spawning_cpu_tests_skip_after_gpu_init(gpu_initialised):
     with pytest.raises(pytest.skip.Exception):
         no_child_processes_after_gpu_init()
+
+
+def test_stream_read_rejects_bad_arguments_before_any_launch():
+    """pd_stream_read checks pointers and 16-byte granularity on the host."""
+    lib = cabi.load()
+    ptrs, _keep = fake(3)
+    assert lib.pd_stream_read(ptrs[0], 32, ptrs[1], 32, None, None) == cabi.PD_ERR_NULL_POINTER
+    assert lib.pd_stream_read(None, 32, ptrs[1], 32, ptrs[2], None) == cabi.PD_ERR_NULL_POINTER
+    assert lib.pd_stream_read(ptrs[0], 24, ptrs[1], 32, ptrs[2], None) == cabi.PD_ERR_SHAPE
+    assert lib.pd_stream_read(ptrs[0] + 8, 32, ptrs[1], 32, ptrs[2], None) == cabi.PD_ERR_SHAPE
+    assert lib.pd_stream_read(None, 0, None, 0, ptrs[2], None) == cabi.PD_OK  # nothing to read: no launch

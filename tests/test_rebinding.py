@@ -19,7 +19,7 @@ import pytest
 
 import rebinding
 from gpu_util import no_child_processes_after_gpu_init
-from paged_decode import _build
+from paged_decode import _build, cabi
 
 STAND_IN_RUNTIME = '''"""Stand-in for the reference's runtime module: its imports, then the rebinding."""
 from functools import lru_cache
@@ -63,7 +63,7 @@ def test_documented_rebinding_loads_inside_a_package_named_paged_decode(tmp_path
     assert run.returncode == 0, run.stdout[-3000:] + run.stderr[-3000:]
     result = json.loads(run.stdout.strip().splitlines()[-1])
     assert result["package"] == str(package / "__init__.py") and result["version"] == "0.2.0"
-    assert result["abi"] == result["library_abi"] == 14
+    assert result["abi"] == result["library_abi"] == cabi.PD_ABI_VERSION
     assert result["has_decode"] and result["cached"]
     assert result["module"] == "paged_decode_amd._C"
 
