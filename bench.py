@@ -25,8 +25,9 @@ Protocol
   captured graph) give its average launch duration; achieved = logical KV
   bytes / duration.
 * Streaming-read ceiling: K back-to-back launches of a read-only kernel
-  (pd_stream_read) over as many bytes as the call's logical K/V, read from
-  the same rotated K/V sets in the decode's load form: stream_read_us, and
+  (pd_stream_read: 16-byte non-temporal loads, the fastest read shape
+  measured) over as many bytes as the call's logical K/V, read from the same
+  rotated K/V sets: stream_read_us, and
   frac_vs_stream = stream_read_us / partition-kernel duration (and per call).
 * The reference's sampling protocol (30 repetitions x 20 inner calls, runners
   in randomized order, p50) is reported for both merge kernels, eager and
@@ -53,6 +54,12 @@ from .git's files; the dirty flag needs a git process and is computed only
 before the GPU is touched and only when no profiler is loaded.
 --output PATH also writes the record, indented, to a new file (an existing
 file is never overwritten).
+
+--sweep NAMES replaces the benchmark with the launch planner's shape sweeps
+(paged_decode/sweep.py): for every shape a planner rule was decided on, the
+full call, the partition launch alone and the staged path at forced kernel
+splits, each as a graph of --steps calls over K/V rotated across >= 2 GiB,
+with the launch plan the library chose; one JSON line per shape.
 """
 import argparse
 import datetime
@@ -92,6 +99,11 @@ def parse_args():
     p.add_argument("--quiet", action="store_true", help="suppress progress lines on stderr")
     p.add_argument("--output", type=Path, default=None,
                    help="also write the record to this new file (refuses to overwrite)")
+    p.add_argument("--sweep", default=None,
+                   help="instead of the benchmark: time the named shape sweeps of the launch planner "
+                        "(comma-separated: coarse, reserved, small, mid, xcd, rows, or all), one JSON line per shape "
+                        "with us per call, the partition launch alone, staged calls at forced kernel splits and the "
+                        "launch plan; --steps calls per graph")
     return p.parse_args()
 
 
@@ -250,6 +262,11 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.sweep is not None:
+        from paged_decode import sweep
+
+        sweep.run(args.sweep.split(","), steps=args.steps, merge=args.merge, log=lambda m: log(args, m))
+        return 0
     from paged_decode.metrics import kv_bytes, summarize, unique_token_bytes
     from paged_decode.runtime import DecodePlan
     from paged_decode.traffic import partition_kernel_name, source_digest

@@ -321,8 +321,40 @@ int pd_decode_kernel_split(int q_dtype, int kv_dtype, int batch, int query_heads
                            int* kernel_split_tokens);
 
 /*
+ * The launches a full decode call (pd_decode_ex / pd_decode_scratch) of these
+ * formats, shapes, merge mode, hints and host length bounds makes on a device
+ * of compute_units CUs (<= 0: the current device's). No counterpart in the
+ * reference, whose launch shape is fixed (decode.cu:170-194); for callers and
+ * benchmarks that record which plan a measurement ran.
+ */
+typedef struct pd_launch_plan {
+    int launches;                 /* 1: one whole-row launch, 2: partition + merge */
+    int kernel_splits;            /* partitions per row the launches run over ... */
+    int kernel_split_tokens;      /* ... of this many tokens (pd_decode_kernel_split) */
+    unsigned grid_x, grid_y, grid_z;  /* partition launch grid */
+    int waves_per_workgroup;
+    int kv_heads_per_workgroup;
+    int quarters_per_workgroup;
+    int head_tile;                /* query heads per wave's tile */
+    int grid_kind;                /* 0 rectangular, 1 rectangular + tail items, 2 work list, 3 whole rows */
+    int xcd_grouped;              /* 1: each row group's partition workgroups on one XCD */
+    int combined;                 /* 1: a workgroup's quarters stored as one state */
+    int stream_mode;              /* non-temporal K/V loads: 0 none, 1 V (FP8: K), 2 K and V */
+    int merge_kernel;             /* -1 none (whole rows), 0 one wave per row, 1 column chunks */
+    int merge_loads;              /* numerator loads per lane per round */
+    int merge_chunk_floats;       /* column chunk width (head_dim for one wave per row) */
+    int merge_xcd_grouped;        /* 1: each row merged on the XCD that wrote its states */
+    int merge_state_stride;       /* states per read state (combined quarters) */
+} pd_launch_plan;
+
+int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                          int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                          int merge_mode, int hints, const int32_t* length_bounds, int compute_units,
+                          pd_launch_plan* plan);
+
+/*
  * Streaming read: reads a_bytes of a and b_bytes of b once each (16-byte
- * loads, the form of the decode's K/V loads) in one launch and writes at most
+ * non-temporal loads, the fastest read form measured here) in one launch and writes at most
  * 8 bytes to sink, a device buffer of at least 2 uint32. Both sizes and
  * pointers must be multiples of 16 (else PD_ERR_SHAPE). No counterpart in
  * the reference: the bandwidth ceiling a decode launch over the same number
@@ -344,7 +376,7 @@ const char* pd_status_string(int status);
  * pd_append_kv_advance, length_bounds argument of the _ex entries; 13: whole-row launches of small rows,
  * pd_decode_launch_count; 14: coarser partitions for full calls on large
  * grids, pd_decode_kernel_split; 15: pd_stream_read, indices_count argument
- * of pd_table_from_csr). PD_ABI_VERSION is the
+ * of pd_table_from_csr, pd_decode_launch_plan). PD_ABI_VERSION is the
  * value this header describes; a binding compares it with what the loaded
  * library returns. */
 #define PD_ABI_VERSION 15

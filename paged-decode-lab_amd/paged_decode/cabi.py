@@ -39,6 +39,17 @@ PD_SCRATCH_BYTES = 32 << 20
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+
+
+class LaunchPlan(ctypes.Structure):
+    """``pd_launch_plan`` of the header."""
+    _fields_ = [(name, ctypes.c_uint if name.startswith("grid_") and name != "grid_kind" else ctypes.c_int)
+                for name in ("launches", "kernel_splits", "kernel_split_tokens", "grid_x", "grid_y", "grid_z",
+                             "waves_per_workgroup", "kv_heads_per_workgroup", "quarters_per_workgroup", "head_tile",
+                             "grid_kind", "xcd_grouped", "combined", "stream_mode", "merge_kernel", "merge_loads",
+                             "merge_chunk_floats", "merge_xcd_grouped", "merge_state_stride")]
+
+
 PROTOTYPES = {
     "pd_decode": (_I, [_P, _P, _P, _I, _P, _P, _P, _P, _P] + [_I] * 10 + [_P]),
     "pd_decode_ex": (_I, [_P, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _P] + [_I] * 11 + [_P, _P]),
@@ -52,6 +63,7 @@ PROTOTYPES = {
     "pd_workspace_bytes": (ctypes.c_size_t, [_I] * 4),
     "pd_decode_launch_count": (_I, [_I] * 12 + [_P]),
     "pd_decode_kernel_split": (_I, [_I] * 11 + [_P, _I, _P, _P]),
+    "pd_decode_launch_plan": (_I, [_I] * 13 + [_P, _I, ctypes.POINTER(LaunchPlan)]),
     "pd_stream_read": (_I, [_P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, _P]),
     "pd_status_string": (ctypes.c_char_p, [_I]),
     "pd_abi_version": (_I, []),
@@ -112,3 +124,22 @@ def kernel_split(lib, q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim,
     if status != PD_OK:
         raise ValueError(status_string(lib, status))
     return splits_out.value, tokens_out.value
+
+
+def launch_plan(lib, q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size, table_width,
+                physical_pages, splits, split_tokens, merge_mode=PD_MERGE_SERIAL, hints=PD_HINT_NONE,
+                length_bounds=None, compute_units=0):
+    """The launches of a full decode call (``pd_decode_launch_plan``) as a dict of
+    the header's fields. Raises ValueError with the library's message for
+    shapes it rejects."""
+    import numpy as np
+
+    bounds = None if length_bounds is None else np.ascontiguousarray(length_bounds, dtype=np.int32)
+    plan = LaunchPlan()
+    status = lib.pd_decode_launch_plan(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
+                                       table_width, physical_pages, splits, split_tokens, merge_mode, hints,
+                                       None if bounds is None else bounds.ctypes.data, compute_units,
+                                       ctypes.byref(plan))
+    if status != PD_OK:
+        raise ValueError(status_string(lib, status))
+    return {name: getattr(plan, name) for name, _ in LaunchPlan._fields_}

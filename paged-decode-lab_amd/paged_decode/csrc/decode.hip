@@ -635,12 +635,17 @@ AppendParams append_params(const void* k_new, const void* v_new, int dtype, cons
 
 // ---------------------------------------------------------------------------
 // Streaming read (pd_stream_read): the bandwidth ceiling a decode launch is
-// measured against. Reads a_bytes of a, then b_bytes of b, once each, with the
-// decode's own load form (16 bytes per lane, plain global loads), each lane
-// keeping kStreamLoads loads in flight. The workgroups of the first ceil(a /
-// block) grid slots read a, the rest b. The loaded words are folded with XOR
-// into a value that is stored only if it equals `magic`, so no load is dead
-// code and the kernel writes (almost always) nothing.
+// measured against. Reads a_bytes of a, then b_bytes of b, once each, in
+// 16-byte non-temporal loads, each lane keeping kStreamLoads loads in flight.
+// The workgroups of the first ceil(a / block) grid slots read a, the rest b.
+// The loaded words are folded with XOR into a value that is stored only if it
+// equals `magic`, so no load is dead code and the kernel writes (almost
+// always) nothing. The shape is the fastest of those measured on MI355X
+// (graph of 200 launches over a 2.3 GB rotation; 2, 4, 8 or 16 loads per lane,
+// 256, 512 or 1024 threads, plain or non-temporal loads): 8 non-temporal loads
+// per lane in 256-thread workgroups read 33.5 / 67 / 201 / 537 MB in 6.13 /
+// 10.69 / 29.8 / 77.9 us, against 6.41 / 11.33 / 32.0 / 83.5 us for the best
+// plain-load shape.
 constexpr int kStreamThreads = 256;
 constexpr int kStreamLoads = 8;
 constexpr uint64_t kStreamBlockVectors = static_cast<uint64_t>(kStreamThreads) * kStreamLoads;
@@ -664,7 +669,7 @@ __global__ void __launch_bounds__(kStreamThreads) stream_read_kernel(const Strea
 #pragma unroll
     for (int i = 0; i < kStreamLoads; ++i) {
         const uint64_t idx = first + static_cast<uint64_t>(i) * kStreamThreads;
-        v[i] = idx < vectors ? base[idx] : u32x4{0u, 0u, 0u, 0u};
+        v[i] = idx < vectors ? __builtin_nontemporal_load(base + idx) : u32x4{0u, 0u, 0u, 0u};
     }
     uint32_t acc = 0;
 #pragma unroll
@@ -926,6 +931,72 @@ int pd_decode_kernel_split(int q_dtype, int kv_dtype, int batch, int query_heads
                                       compute_units > 0 ? compute_units : device_compute_units());
     *kernel_splits = ks.splits;
     *kernel_split_tokens = ks.split_tokens;
+    return PD_OK;
+}
+
+int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
+                          int page_size, int table_width, int physical_pages, int splits, int split_tokens,
+                          int merge_mode, int hints, const int32_t* length_bounds, int compute_units,
+                          pd_launch_plan* plan) {
+    if (!plan) return PD_ERR_NULL_POINTER;
+    const char* const stand_in = reinterpret_cast<const char*>(alignof(float));
+    float* const f_stand_in = reinterpret_cast<float*>(alignof(float));
+    int status = check_common(stand_in, q_dtype, stand_in, stand_in, kv_dtype, 1.0f, 1.0f,
+                              reinterpret_cast<const int32_t*>(stand_in), reinterpret_cast<const int32_t*>(stand_in),
+                              f_stand_in, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size, table_width,
+                              physical_pages, splits, split_tokens);
+    if (status == PD_OK)
+        status = check_merge(f_stand_in, f_stand_in, f_stand_in, reinterpret_cast<const int32_t*>(stand_in), batch,
+                             query_heads, head_dim, page_size, table_width, splits, split_tokens, merge_mode);
+    if (status == PD_OK) status = check_hints(hints);
+    if (status != PD_OK) return status;
+    const int cus = compute_units > 0 ? compute_units : device_compute_units();
+    // The planning of pd_decode_ex, without its launches.
+    const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
+                                      table_width, splits, split_tokens, length_bounds, cus);
+    const int reach = call_reach(splits, split_tokens, table_width, page_size);
+    PartialParams prm = partial_params(nullptr, nullptr, nullptr, kv_dtype, 1.0f, 1.0f, nullptr, nullptr, nullptr,
+                                       nullptr, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size,
+                                       table_width, physical_pages, ks.splits, ks.split_tokens, hints, length_bounds,
+                                       reach);
+    if (q_dtype == PD_DTYPE_F32) plan_fp32(prm, kv_heads, head_dim);
+    else plan_mfma(prm, kv_heads, cus, head_dim, static_cast<int>(element_size(kv_dtype)));
+    const Grid grid = partial_grid(prm, kv_heads);
+    pd_launch_plan p{};
+    p.launches = prm.row_mode ? 1 : 2;
+    p.kernel_splits = ks.splits;
+    p.kernel_split_tokens = ks.split_tokens;
+    p.grid_x = grid.x;
+    p.grid_y = grid.y;
+    p.grid_z = grid.z;
+    p.waves_per_workgroup = partial_threads(prm) / kWave;
+    p.kv_heads_per_workgroup = prm.heads_per_wg;
+    p.quarters_per_workgroup = prm.quarters_per_wg;
+    p.head_tile = prm.head_tile;
+    p.grid_kind = prm.row_mode ? 3 : grid_kind(prm);
+    p.xcd_grouped = prm.xcd_shift >= 0;
+    p.combined = prm.combine;
+    p.stream_mode = prm.stream_mode;
+    p.merge_kernel = -1;
+    if (!prm.row_mode) {
+        const int stride = prm.combine ? prm.quarters_per_wg : 1;
+        MergeParams mp{};
+        mp.parts = kQuarters * ks.splits;
+        mp.stride_shift = stride == 4 ? 2 : stride == 2 ? 1 : 0;
+        mp.query_heads = query_heads;
+        mp.split_tokens = ks.split_tokens;
+        mp.reach = reach;
+        mp.first_states = merge_first_states(mp.parts, mp.stride_shift, ks.split_tokens, reach, length_bounds, batch);
+        mp.xcd_rows = xcd_row_group_rows(prm);
+        mp.xcd_shift = prm.merge_xcd_shift;
+        const MergeLaunch ml = plan_merge(mp, batch, head_dim, merge_mode == PD_MERGE_SHARED, cus);
+        p.merge_kernel = ml.kind == kMergeRows ? 0 : 1;
+        p.merge_loads = ml.nb;
+        p.merge_chunk_floats = ml.ch;
+        p.merge_xcd_grouped = ml.xcd_rows > 0;
+        p.merge_state_stride = stride;
+    }
+    *plan = p;
     return PD_OK;
 }
 

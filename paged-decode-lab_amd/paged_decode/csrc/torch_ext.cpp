@@ -297,6 +297,44 @@ std::tuple<int64_t, int64_t> kernel_split(at::ScalarType q_dtype, at::ScalarType
     return {kernel_splits, kernel_split_tokens};
 }
 
+// The launches decode makes for these formats, shapes, merge mode, hints and
+// optional host length bounds (pd_decode_launch_plan), as a dict.
+py::dict launch_plan(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t batch, int64_t query_heads,
+                     int64_t kv_heads, int64_t head_dim, int64_t page_size, int64_t table_width,
+                     int64_t physical_pages, int64_t splits, int64_t split_tokens, int64_t merge_mode,
+                     bool unshared_pages, bool ragged_lengths, c10::optional<torch::Tensor> length_bounds,
+                     int64_t compute_units) {
+    const int32_t* bounds = bounds_pointer(length_bounds, batch);
+    pd_launch_plan p{};
+    check_status(pd_decode_launch_plan(dtype_code(q_dtype), dtype_code(kv_dtype), static_cast<int>(batch),
+                                       static_cast<int>(query_heads), static_cast<int>(kv_heads),
+                                       static_cast<int>(head_dim), static_cast<int>(page_size),
+                                       static_cast<int>(table_width), static_cast<int>(physical_pages),
+                                       static_cast<int>(splits), static_cast<int>(split_tokens),
+                                       static_cast<int>(merge_mode), hints(unshared_pages, ragged_lengths), bounds,
+                                       static_cast<int>(compute_units), &p));
+    static const char* kinds[] = {"rectangular", "rectangular+tails", "work list", "whole rows"};
+    py::dict d;
+    d["launches"] = p.launches;
+    d["kernel_split"] = py::make_tuple(p.kernel_splits, p.kernel_split_tokens);
+    d["grid"] = py::make_tuple(p.grid_x, p.grid_y, p.grid_z);
+    d["waves_per_workgroup"] = p.waves_per_workgroup;
+    d["kv_heads_per_workgroup"] = p.kv_heads_per_workgroup;
+    d["quarters_per_workgroup"] = p.quarters_per_workgroup;
+    d["head_tile"] = p.head_tile;
+    d["grid_kind"] = kinds[std::min(std::max(p.grid_kind, 0), 3)];
+    d["xcd_grouped"] = p.xcd_grouped != 0;
+    d["combined"] = p.combined != 0;
+    d["stream_mode"] = p.stream_mode;
+    if (p.merge_kernel >= 0) {
+        d["merge"] = py::make_tuple(p.merge_kernel == 0 ? "rows" : "cols", p.merge_loads, p.merge_chunk_floats,
+                                    p.merge_xcd_grouped != 0, p.merge_state_stride);
+    } else {
+        d["merge"] = py::none();
+    }
+    return d;
+}
+
 // One streaming read of the leading a_bytes of a and b_bytes of b (the
 // bandwidth ceiling of a decode launch over as many K/V bytes).
 void stream_read(torch::Tensor a, torch::Tensor b, int64_t a_bytes, int64_t b_bytes, torch::Tensor sink) {
@@ -341,6 +379,11 @@ PYBIND11_MODULE(_C, m) {
           py::arg("head_dim"), py::arg("page_size"), py::arg("table_width"), py::arg("physical_pages"),
           py::arg("splits"), py::arg("split_tokens"), py::arg("length_bounds") = py::none(),
           py::arg("compute_units") = 0);
+    m.def("launch_plan", &launch_plan, "The launches a decode call makes (pd_decode_launch_plan)", py::arg("q_dtype"),
+          py::arg("kv_dtype"), py::arg("batch"), py::arg("query_heads"), py::arg("kv_heads"), py::arg("head_dim"),
+          py::arg("page_size"), py::arg("table_width"), py::arg("physical_pages"), py::arg("splits"),
+          py::arg("split_tokens"), py::arg("merge_mode"), py::arg("unshared_pages") = false,
+          py::arg("ragged_lengths") = false, py::arg("length_bounds") = py::none(), py::arg("compute_units") = 0);
     m.def("stream_read", &stream_read, "One streaming read of the leading bytes of two tensors", py::arg("a"),
           py::arg("b"), py::arg("a_bytes"), py::arg("b_bytes"), py::arg("sink"));
     m.def("abi_version", &pd_abi_version, "ABI version the loaded HIP library reports");

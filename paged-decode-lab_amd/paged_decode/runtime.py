@@ -278,6 +278,20 @@ class DecodePlan:
                                             self._table.shape[1], layout.physical_pages, self.splits,
                                             self.split_tokens, self._length_bounds())
 
+    def launch_plan(self, q_dtype, kv_dtype=None, compute_units=0):
+        """The launches ``run`` makes for q (and K/V) of these dtypes at the current
+        host length bounds and hints: a dict with the launch count, the kernel
+        split, the partition grid and workgroup shape, the grid kind, XCD
+        grouping, quarter combine, streaming loads and the merge kernel
+        variant (``pd_decode_launch_plan``). ``compute_units`` <= 0 means the
+        current device's."""
+        layout = self.layout
+        return self._extension.launch_plan(q_dtype, q_dtype if kv_dtype is None else kv_dtype, layout.batch,
+                                           layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size,
+                                           self._table.shape[1], layout.physical_pages, self.splits,
+                                           self.split_tokens, self._merge_mode, self._unshared_pages,
+                                           self._ragged_lengths, self._length_bounds(), compute_units)
+
     def _stage_workspace(self, splits):
         """Numerator and stats views for ``splits`` partitions per row: the leading
         part of the workspace buffers, as the full call uses them."""

@@ -1,5 +1,7 @@
 """bench.py's command-line contract, on the CPU (no GPU work is started)."""
 import subprocess
+
+import pytest
 import sys
 from pathlib import Path
 
@@ -72,3 +74,25 @@ def test_build_record_names_this_checkout(monkeypatch, tmp_path):
     assert info["sha"] == _build.git_head() and info["source_digest"] == _build.source_digest()
     if info["sha"] is not None:
         assert len(info["sha"]) == 40 and info["dirty"] in (True, False, None)
+
+
+def test_sweep_shapes_are_well_formed():
+    """Every named sweep shape builds valid metadata: lengths within the
+    table, page ids in range, the reserve and the shared prefix respected."""
+    from paged_decode import sweep
+    from paged_decode.layout import validate_metadata
+
+    listed = sweep.shapes(["all"])
+    assert {name for name, _ in listed} == set(sweep.SWEEPS)
+    assert len({shape for _, shape in listed}) == len(listed)
+    for _, shape in listed:
+        layout, table, lengths, max_context = sweep.metadata(shape)
+        validate_metadata(layout, table, lengths)
+        assert max_context <= table.shape[1] * layout.page_size
+        assert int(lengths.max()) * shape.reserve <= table.shape[1] * layout.page_size
+        if shape.shared_prefix:
+            shared = int(-(-int(lengths.max()) // layout.page_size) * shape.shared_prefix)
+            live = lengths >= shared * layout.page_size
+            assert (table[live, :shared] == table[live][0, :shared]).all()
+    with pytest.raises(ValueError):
+        sweep.shapes(["nonesuch"])

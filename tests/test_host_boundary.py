@@ -496,3 +496,33 @@ def test_stream_read_rejects_bad_arguments_before_any_launch():
     assert lib.pd_stream_read(ptrs[0], 24, ptrs[1], 32, ptrs[2], None) == cabi.PD_ERR_SHAPE
     assert lib.pd_stream_read(ptrs[0] + 8, 32, ptrs[1], 32, ptrs[2], None) == cabi.PD_ERR_SHAPE
     assert lib.pd_stream_read(None, 0, None, 0, ptrs[2], None) == cabi.PD_OK  # nothing to read: no launch
+
+
+def test_launch_plan_query_agrees_with_the_other_queries():
+    """pd_decode_launch_plan describes the launches pd_decode_ex makes: its launch
+    count and kernel split equal pd_decode_launch_count's and
+    pd_decode_kernel_split's, and the Llama-3-8B shape with host bounds on 256
+    CUs is the XCD-grouped mid-size grid (2 KV heads x 2 quarters per 4-wave
+    workgroup, 512 workgroups) merged by XCD-grouped column chunks."""
+    lib = cabi.load()
+    f32, f16, fp8 = cabi.PD_DTYPE_F32, cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E4M3
+    cases = [(f16, f16, 4, 32, 8, 128, 16, 256, 1024, 16, 256, [4096] * 4),
+             (f16, f16, 4, 32, 8, 128, 16, 256, 1024, 16, 256, None),
+             (f16, fp8, 128, 16, 1, 64, 16, 64, 8192, 4, 256, [1024] * 128),
+             (f32, f32, 2, 8, 2, 64, 16, 16, 32, 1, 256, [100, 256]),
+             (f16, f16, 16, 32, 8, 128, 32, 256, 4096, 64, 128, list(range(0, 8192, 512)))]
+    for q, kv, b, hq, hkv, d, t, w, p, s, st, bounds in cases:
+        plan = cabi.launch_plan(lib, q, kv, b, hq, hkv, d, t, w, p, s, st, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_NONE,
+                                bounds, 256)
+        assert plan["launches"] == cabi.launch_count(lib, q, kv, b, hq, hkv, d, t, w, p, s, st)
+        assert (plan["kernel_splits"], plan["kernel_split_tokens"]) == cabi.kernel_split(
+            lib, q, kv, b, hq, hkv, d, t, w, p, s, st, bounds, 256)
+        assert (plan["merge_kernel"] == -1) == (plan["launches"] == 1)
+        assert plan["grid_x"] * plan["grid_y"] * plan["grid_z"] >= 1 and 1 <= plan["waves_per_workgroup"] <= 16
+    llama = cabi.launch_plan(lib, f16, f16, 4, 32, 8, 128, 16, 256, 1024, 16, 256, cabi.PD_MERGE_SERIAL,
+                             cabi.PD_HINT_UNSHARED_PAGES, [4096] * 4, 256)
+    assert llama["xcd_grouped"] == 1 and llama["kv_heads_per_workgroup"] == 2 and llama["quarters_per_workgroup"] == 2
+    assert llama["waves_per_workgroup"] == 4 and llama["grid_x"] * llama["grid_y"] * llama["grid_z"] == 512
+    assert llama["merge_kernel"] == 1 and llama["merge_xcd_grouped"] == 1 and llama["merge_chunk_floats"] == 32
+    with pytest.raises(ValueError):
+        cabi.launch_plan(lib, f16, f16, 4, 32, 8, 96, 16, 256, 1024, 16, 256)
