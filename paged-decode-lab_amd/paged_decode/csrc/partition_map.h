@@ -953,14 +953,26 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     //     50.3, V only 52.0, K and V 59.3.
     //   - The 2-head x 2-quarter workgroups of mid-size grids: with 2 KV
     //     heads, one head group, streaming V anyway took B16 L4096 (GQA 8)
-    //     from 19.75 to 18.81 us per call.
+    //     from 19.75 to 18.81 us per call. Streaming K as well, on every
+    //     mid-size grid with unshared pages, took it to 17.78, and (us per
+    //     call, V only -> K and V, graph of 200 calls, best of two) B8 L4096
+    //     with 4 KV heads 19.64 -> 17.98, B6 L4096 22.82 -> 22.11, B2 L4096
+    //     11.99 -> 11.65, a ragged B8 L4096 batch 23.36 -> 22.36, B4 L4096
+    //     with 4 KV heads / 64 query heads 13.92 -> 13.61 (Llama-3-8B B4
+    //     L4096, whose 8 KV heads already count 4 head groups there, was
+    //     unchanged). No shape of the coarse, small, mid or XCD sweeps got
+    //     slower beyond noise.
     // So the mode follows the page-sharing hint: unshared pages stream K and
-    // V (4+ groups) or V (2 groups, or one in a mid-size grid); pages that may
+    // V (4+ groups, or any mid-size grid) or V (2 groups); pages that may
     // be shared stream V (4+ groups) or nothing. FP8 V loads are 8-byte, so
     // FP8 streams its 16-byte K row loads wherever 16-bit K/V would stream V.
     const int groups = default_groups;
-    prm.stream_mode = groups == 1 ? (prm.mid_grid && prm.unshared_pages ? 1 : 0)
-                      : prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+    if (prm.mid_grid && prm.unshared_pages) {
+        prm.stream_mode = 2;
+    } else {
+        prm.stream_mode = prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
+        if (groups == 1) prm.stream_mode = 0;
+    }
     if (long_quarters) {
         choose_workgroup(prm, kv_heads, 1, 4);
         prm.mid_grid = 0;

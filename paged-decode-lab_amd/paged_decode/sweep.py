@@ -200,8 +200,10 @@ def _tensors(torch, layout, fmt, device, seed):
     k = torch.randn(cache, generator=g, device=device)
     v = torch.randn(cache, generator=g, device=device)
     if fmt == "fp8":
-        scale = 4.0 / float(torch.finfo(torch.float8_e4m3fn).max)
-        return q, (k / scale).to(torch.float8_e4m3fn), (v / scale).to(torch.float8_e4m3fn), scale, scale
+        largest = float(torch.finfo(torch.float8_e4m3fn).max)
+        scale = 6.0 / largest  # codes of |x| / scale, clamped into range (e4m3fn has no infinity)
+        k, v = ((x / scale).clamp(-largest, largest).to(torch.float8_e4m3fn) for x in (k, v))
+        return q, k, v, scale, scale
     return q, k.to(q_dtype), v.to(q_dtype), 1.0, 1.0
 
 
