@@ -962,16 +962,25 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     //     L4096, whose 8 KV heads already count 4 head groups there, was
     //     unchanged). No shape of the coarse, small, mid or XCD sweeps got
     //     slower beyond noise.
+    //   - One head group (a single KV head, or all KV heads in one
+    //     workgroup) on a grid that fills the device, no shared pages:
+    //     streaming K and V took (us per call) MQA B512 L1024 D64 from 32.65
+    //     to 31.13, B8 L4096 with 2 KV heads (GQA 16) 14.54 -> 12.99, B16
+    //     L2048 with 1 KV head 11.10 -> 10.40, MQA B128 L1024 13.84 -> 13.46;
+    //     on the small MQA B4 grid it cost 8.29 -> 8.94, so small grids keep
+    //     their loads cached.
     // So the mode follows the page-sharing hint: unshared pages stream K and
-    // V (4+ groups, or any mid-size grid) or V (2 groups); pages that may
-    // be shared stream V (4+ groups) or nothing. FP8 V loads are 8-byte, so
-    // FP8 streams its 16-byte K row loads wherever 16-bit K/V would stream V.
+    // V (4+ groups, any mid-size grid, or one head group on a grid that fills
+    // the device) or V (2 groups); pages that may be shared stream V (4+
+    // groups) or nothing. FP8 V loads are 8-byte, so FP8 streams its 16-byte
+    // K row loads wherever 16-bit K/V would stream V.
     const int groups = default_groups;
     if (prm.mid_grid && prm.unshared_pages) {
         prm.stream_mode = 2;
+    } else if (groups == 1) {
+        prm.stream_mode = prm.unshared_pages && fills_device ? 2 : 0;
     } else {
         prm.stream_mode = prm.unshared_pages ? (groups >= 4 ? 2 : 1) : (groups >= 4 ? 1 : 0);
-        if (groups == 1) prm.stream_mode = 0;
     }
     if (long_quarters) {
         choose_workgroup(prm, kv_heads, 1, 4);

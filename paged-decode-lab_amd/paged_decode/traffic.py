@@ -19,6 +19,11 @@ digest of the kernel source the counters were taken on.
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT/write -- \\
         python3 paged-decode-lab_amd/paged_decode/traffic.py run
     python3 paged-decode-lab_amd/paged_decode/traffic.py summarize OUT/fetch OUT/write
+
+``--private-pages`` (both steps) maps every live table entry of the workload to
+a page of its own, with the same lengths and layout: the same workload without
+shared pages, so a shared-prefix workload's counter bytes can be compared with
+what its reads cost when nothing is shared (profiles/traffic_<workload>_private.json).
 """
 import argparse
 import csv
@@ -52,14 +57,37 @@ def partition_kernel_name(dtype_is_half, whole_rows=False):
     return name + " (whole rows)" if whole_rows else name
 
 
+def private_table(table, lengths, page_size, physical_pages):
+    """The table with every live entry mapped to a distinct physical page (in
+    entry order), entries past each sequence's end left as they are."""
+    import numpy as np
+
+    out = np.array(table, dtype=np.int32, copy=True)
+    live = [(b, i) for b, n in enumerate(lengths) for i in range(-(-int(n) // page_size))]
+    if len(live) > physical_pages:
+        raise ValueError("more live pages than the cache holds")
+    for page, (b, i) in enumerate(live):
+        out[b, i] = page
+    return out
+
+
+def workload(args):
+    from paged_decode.workload import make_workload
+
+    w = make_workload(args.workload)
+    if args.private_pages:
+        w.table = private_table(w.table, w.lengths, w.layout.page_size, w.layout.physical_pages)
+        w.name += "_private"
+    return w
+
+
 def run(args):
     import numpy as np
     import torch
 
     from paged_decode.runtime import DecodePlan
-    from paged_decode.workload import make_workload
 
-    w = make_workload(args.workload)
+    w = workload(args)
     dev = torch.device("cuda", 0)
     q, k0, v0, k_scale, v_scale = w.tensors(dev)  # K/V in the workload's storage format (FP8 with scales)
     sets = max(1, math.ceil(ROTATION_BYTES / (2 * k0.numel() * k0.element_size())))
@@ -105,10 +133,9 @@ def pick(per_kernel, needle):
 
 def summarize(args):
     from paged_decode.metrics import kv_bytes, unique_token_bytes
-    from paged_decode.workload import make_workload
     import numpy as np
 
-    w = make_workload(args.workload)
+    w = workload(args)
     L = w.layout
     logical = kv_bytes(w.lengths, L.kv_heads, L.head_dim, w.element_size)
     unique = unique_token_bytes(w.table, w.lengths, L.page_size, L.kv_heads, L.head_dim, w.element_size)
@@ -138,13 +165,14 @@ def summarize(args):
     record["traffic_over_unique_pages"] = round(total / unique, 4)
     record["copy_bytes"] = COPY_BYTES
     record["source_digest"] = source_digest()
+    flag = " --private-pages" if args.private_pages else ""
     record["commands"] = [
         "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/pmc_fetch -- "
-        f"python3 paged-decode-lab_amd/paged_decode/traffic.py run --workload {w.name}",
+        f"python3 paged-decode-lab_amd/paged_decode/traffic.py run --workload {args.workload}{flag}",
         "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/pmc_write -- "
-        f"python3 paged-decode-lab_amd/paged_decode/traffic.py run --workload {w.name}",
+        f"python3 paged-decode-lab_amd/paged_decode/traffic.py run --workload {args.workload}{flag}",
         f"python3 paged-decode-lab_amd/paged_decode/traffic.py summarize gpurun_out/pmc_fetch gpurun_out/pmc_write "
-        f"--workload {w.name}",
+        f"--workload {args.workload}{flag}",
     ]
     out = REPO / "profiles" / f"traffic_{w.name}.json"
     out.parent.mkdir(exist_ok=True)
@@ -163,10 +191,12 @@ def main(argv=None):
     r.add_argument("--workload", default="llama3_8b_b4_l4096")
     r.add_argument("--launches", type=int, default=24)
     r.add_argument("--copies", type=int, default=4)
+    r.add_argument("--private-pages", action="store_true")
     s = sub.add_parser("summarize")
     s.add_argument("fetch_dir")
     s.add_argument("write_dir")
     s.add_argument("--workload", default="llama3_8b_b4_l4096")
+    s.add_argument("--private-pages", action="store_true")
     args = p.parse_args(argv)
     return run(args) if args.cmd == "run" else summarize(args)
 
