@@ -60,7 +60,8 @@ enum pd_status {
     PD_ERR_MERGE = 5,         /* unknown merge mode or shared-merge bound exceeded */
     PD_ERR_LAUNCH = 6,        /* the HIP runtime rejected a kernel launch */
     PD_ERR_HINT = 7,          /* unknown bits in the hints argument */
-    PD_ERR_SCRATCH = 8        /* pd_decode_scratch: the workspace does not fit PD_SCRATCH_BYTES */
+    PD_ERR_SCRATCH = 8,       /* pd_decode_scratch: the workspace does not fit PD_SCRATCH_BYTES */
+    PD_ERR_PREFIX = 9         /* malformed shared-prefix runs (pd_decode_prefix) */
 };
 
 /* Storage formats. q, k and v share F32, F16 or BF16 in pd_decode; the _ex
@@ -165,6 +166,49 @@ int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* 
                          int batch, int query_heads, int kv_heads, int head_dim, int page_size,
                          int table_width, int physical_pages, int splits, int split_tokens,
                          int hints, const int32_t* length_bounds, void* stream);
+
+/*
+ * Shared prefixes. pd_prefix_runs describes which sequences of a HOST page
+ * table [batch, table_width] share leading pages: runs[2 b] is sequence b's
+ * leader -- the first sequence whose row starts with the same page id (b
+ * itself if none before it does), or -1 if b's first entry is negative -- and
+ * runs[2 b + 1] is the number of leading entries b's row has in common with
+ * its leader's (up to the first difference or negative entry). runs is a
+ * HOST array [2 * batch]. Returns a status.
+ *
+ * pd_decode_prefix and pd_decode_partial_prefix are pd_decode_ex and
+ * pd_decode_partial_ex with such runs (a HOST array read during the call, or
+ * NULL). With runs and length bounds, a work-list launch (batches of up to 64
+ * sequences, F16 or BF16 q, GQA groups of up to 8) scores each partition
+ * that lies inside the common prefix of several sequences once for up to
+ * 16 / GT of them (GT: the GQA group padded to a power of two), reading its
+ * K and V once instead of once per sequence. The runs are a promise about the
+ * device table: on the leading entries they cover, the rows of one leader's
+ * sequences must hold the same page ids, or those sequences get wrong
+ * results (runs computed from the table uploaded to the device keep it).
+ * Runs with a leader outside [-1, batch) or a count outside [0, table_width]
+ * return PD_ERR_PREFIX. Results equal those without runs up to the last
+ * bits. No counterpart in the reference, whose kernel reads a shared page
+ * once per sequence that maps it (its workload has no sharing,
+ * src/paged_decode/workload.py:12-13; reuse across readers is left open,
+ * docs/DESIGN.md:24-26).
+ */
+int pd_prefix_runs(const int32_t* table, int batch, int table_width, int32_t* runs);
+int pd_decode_prefix(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
+                     float k_scale, float v_scale,
+                     const int32_t* table, const int32_t* lengths,
+                     float* numerator, float* stats, float* out,
+                     int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                     int table_width, int physical_pages, int splits, int split_tokens,
+                     int merge_mode, int hints, const int32_t* length_bounds, const int32_t* prefix_runs,
+                     void* stream);
+int pd_decode_partial_prefix(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype,
+                             float k_scale, float v_scale,
+                             const int32_t* table, const int32_t* lengths,
+                             float* numerator, float* stats,
+                             int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                             int table_width, int physical_pages, int splits, int split_tokens,
+                             int hints, const int32_t* length_bounds, const int32_t* prefix_runs, void* stream);
 
 /*
  * Partition stage only (the first launch of pd_decode): fills numerator and
@@ -345,12 +389,14 @@ typedef struct pd_launch_plan {
     int merge_chunk_floats;       /* column chunk width (head_dim for one wave per row) */
     int merge_xcd_grouped;        /* 1: each row merged on the XCD that wrote its states */
     int merge_state_stride;       /* states per read state (combined quarters) */
+    int shared_prefix_items;      /* work-list items that score one partition for several sequences */
 } pd_launch_plan;
 
+/* prefix_runs: as pd_decode_prefix (NULL: the plan of pd_decode_ex). */
 int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
                           int page_size, int table_width, int physical_pages, int splits, int split_tokens,
-                          int merge_mode, int hints, const int32_t* length_bounds, int compute_units,
-                          pd_launch_plan* plan);
+                          int merge_mode, int hints, const int32_t* length_bounds, const int32_t* prefix_runs,
+                          int compute_units, pd_launch_plan* plan);
 
 /*
  * Streaming read: reads a_bytes of a and b_bytes of b once each (16-byte
@@ -376,10 +422,12 @@ const char* pd_status_string(int status);
  * pd_append_kv_advance, length_bounds argument of the _ex entries; 13: whole-row launches of small rows,
  * pd_decode_launch_count; 14: coarser partitions for full calls on large
  * grids, pd_decode_kernel_split; 15: pd_stream_read, indices_count argument
- * of pd_table_from_csr, pd_decode_launch_plan). PD_ABI_VERSION is the
+ * of pd_table_from_csr, pd_decode_launch_plan; 16: shared-prefix items,
+ * pd_prefix_runs, pd_decode_prefix, pd_decode_partial_prefix, the
+ * prefix_runs argument of pd_decode_launch_plan). PD_ABI_VERSION is the
  * value this header describes; a binding compares it with what the loaded
  * library returns. */
-#define PD_ABI_VERSION 15
+#define PD_ABI_VERSION 16
 int pd_abi_version(void);
 
 #ifdef __cplusplus

@@ -462,9 +462,12 @@ PartialParams partial_params(const void* q, const void* k, const void* v, int kv
                              float v_scale, const int32_t* table, const int32_t* lengths, float* numerator,
                              float* stats, float* out, int batch, int query_heads, int kv_heads, int head_dim,
                              int page_size, int table_width, int physical_pages, int splits, int split_tokens,
-                             int hints, const int32_t* length_bounds, int reach) {
+                             int hints, const int32_t* length_bounds, int reach,
+                             const int32_t* prefix_runs = nullptr) {
     PartialParams prm{};
     prm.batch = batch;
+    prm.host_bounds = length_bounds;
+    prm.host_prefix_runs = prefix_runs;
     prm.unshared_pages = (hints & PD_HINT_UNSHARED_PAGES) != 0;
     prm.ragged_lengths = (hints & PD_HINT_RAGGED_LENGTHS) != 0;
     prm.q = q;
@@ -509,11 +512,11 @@ int run_partial(const void* q, int q_dtype, const void* k, const void* v, int kv
                 int query_heads, int kv_heads, int head_dim, int page_size, int table_width, int physical_pages,
                 int splits, int split_tokens, int hints, const int32_t* length_bounds, hipStream_t stream,
                 float* out = nullptr, int* state_stride = nullptr, int* xcd_rows = nullptr,
-                int* xcd_shift = nullptr, int reach = -1) {
+                int* xcd_shift = nullptr, int reach = -1, const int32_t* prefix_runs = nullptr) {
     if (reach < 0) reach = call_reach(splits, split_tokens, table_width, page_size);
     PartialParams prm = partial_params(q, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, out,
                                        batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
-                                       splits, split_tokens, hints, length_bounds, reach);
+                                       splits, split_tokens, hints, length_bounds, reach, prefix_runs);
     const int status = dispatch_partial(prm, q_dtype, kv_dtype, kv_heads, head_dim, stream);
     if (state_stride) *state_stride = prm.row_mode ? 0 : prm.combine ? prm.quarters_per_wg : 1;
     if (xcd_rows) *xcd_rows = xcd_row_group_rows(prm);
@@ -562,6 +565,10 @@ int launch_merge(MergeParams mp, int batch, int merge_mode, hipStream_t stream) 
 
 int check_hints(int hints) {
     return (hints & ~(PD_HINT_UNSHARED_PAGES | PD_HINT_RAGGED_LENGTHS)) == 0 ? PD_OK : PD_ERR_HINT;
+}
+
+int check_prefix_runs(const int32_t* prefix_runs, int batch, int table_width) {
+    return prefix_runs == nullptr || prefix_runs_valid(prefix_runs, batch, table_width) ? PD_OK : PD_ERR_PREFIX;
 }
 
 int check_merge(const float* numerator, const float* stats, const float* out, const int32_t* lengths, int batch,
@@ -727,19 +734,31 @@ size_t scratch_stats_offset(int batch, int query_heads, int head_dim, int splits
 
 extern "C" {
 
+int pd_decode_partial_prefix(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
+                             float v_scale, const int32_t* table, const int32_t* lengths, float* numerator,
+                             float* stats, int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                             int table_width, int physical_pages, int splits, int split_tokens, int hints,
+                             const int32_t* length_bounds, const int32_t* prefix_runs, void* stream) {
+    int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
+                              query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                              split_tokens);
+    if (status == PD_OK) status = check_hints(hints);
+    if (status == PD_OK) status = check_prefix_runs(prefix_runs, batch, table_width);
+    if (status != PD_OK) return status;
+    return run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
+                       query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
+                       hints, length_bounds, static_cast<hipStream_t>(stream), nullptr, nullptr, nullptr, nullptr, -1,
+                       prefix_runs);
+}
+
 int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
                          float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
                          int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
                          int physical_pages, int splits, int split_tokens, int hints, const int32_t* length_bounds,
                          void* stream) {
-    int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
-                              query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
-                              split_tokens);
-    if (status == PD_OK) status = check_hints(hints);
-    if (status != PD_OK) return status;
-    return run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
-                       query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits, split_tokens,
-                       hints, length_bounds, static_cast<hipStream_t>(stream));
+    return pd_decode_partial_prefix(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats,
+                                    batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages,
+                                    splits, split_tokens, hints, length_bounds, nullptr, stream);
 }
 
 int pd_decode_partial(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -761,11 +780,11 @@ int pd_decode_merge(const float* numerator, const float* stats, float* out, cons
                      split_tokens, merge_mode, 1, static_cast<hipStream_t>(stream));
 }
 
-int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
-                 float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
-                 float* out, int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
-                 int physical_pages, int splits, int split_tokens, int merge_mode, int hints,
-                 const int32_t* length_bounds, void* stream) {
+int pd_decode_prefix(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
+                     float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
+                     float* out, int batch, int query_heads, int kv_heads, int head_dim, int page_size,
+                     int table_width, int physical_pages, int splits, int split_tokens, int merge_mode, int hints,
+                     const int32_t* length_bounds, const int32_t* prefix_runs, void* stream) {
     int status = check_common(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                               query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
                               split_tokens);
@@ -773,6 +792,7 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
         status = check_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width,
                              splits, split_tokens, merge_mode);
     if (status == PD_OK) status = check_hints(hints);
+    if (status == PD_OK) status = check_prefix_runs(prefix_runs, batch, table_width);
     if (status != PD_OK) return status;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     // Both launches run over the same partitions, at most `splits` of them
@@ -784,10 +804,28 @@ int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int k
     int stride = 1, xcd_rows = 0, xcd_shift = 0;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
                          query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, ks.splits,
-                         ks.split_tokens, hints, length_bounds, s, out, &stride, &xcd_rows, &xcd_shift, reach);
+                         ks.split_tokens, hints, length_bounds, s, out, &stride, &xcd_rows, &xcd_shift, reach,
+                         prefix_runs);
     if (status != PD_OK || stride == 0) return status;
     return run_merge(numerator, stats, out, lengths, batch, query_heads, head_dim, page_size, table_width, ks.splits,
                      ks.split_tokens, merge_mode, stride, s, length_bounds, xcd_rows, xcd_shift, reach);
+}
+
+int pd_decode_ex(const void* q, int q_dtype, const void* k, const void* v, int kv_dtype, float k_scale,
+                 float v_scale, const int32_t* table, const int32_t* lengths, float* numerator, float* stats,
+                 float* out, int batch, int query_heads, int kv_heads, int head_dim, int page_size, int table_width,
+                 int physical_pages, int splits, int split_tokens, int merge_mode, int hints,
+                 const int32_t* length_bounds, void* stream) {
+    return pd_decode_prefix(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, out,
+                            batch, query_heads, kv_heads, head_dim, page_size, table_width, physical_pages, splits,
+                            split_tokens, merge_mode, hints, length_bounds, nullptr, stream);
+}
+
+int pd_prefix_runs(const int32_t* table, int batch, int table_width, int32_t* runs) {
+    if (!table || !runs) return PD_ERR_NULL_POINTER;
+    if (batch < 1 || batch > 65535 || table_width < 1 || table_width > 65536) return PD_ERR_SHAPE;
+    prefix_runs_of_table(table, batch, table_width, runs);
+    return PD_OK;
 }
 
 int pd_decode(const void* q, const void* k, const void* v, int dtype, const int32_t* table,
@@ -936,8 +974,8 @@ int pd_decode_kernel_split(int q_dtype, int kv_dtype, int batch, int query_heads
 
 int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
                           int page_size, int table_width, int physical_pages, int splits, int split_tokens,
-                          int merge_mode, int hints, const int32_t* length_bounds, int compute_units,
-                          pd_launch_plan* plan) {
+                          int merge_mode, int hints, const int32_t* length_bounds, const int32_t* prefix_runs,
+                          int compute_units, pd_launch_plan* plan) {
     if (!plan) return PD_ERR_NULL_POINTER;
     const char* const stand_in = reinterpret_cast<const char*>(alignof(float));
     float* const f_stand_in = reinterpret_cast<float*>(alignof(float));
@@ -949,6 +987,7 @@ int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads,
         status = check_merge(f_stand_in, f_stand_in, f_stand_in, reinterpret_cast<const int32_t*>(stand_in), batch,
                              query_heads, head_dim, page_size, table_width, splits, split_tokens, merge_mode);
     if (status == PD_OK) status = check_hints(hints);
+    if (status == PD_OK) status = check_prefix_runs(prefix_runs, batch, table_width);
     if (status != PD_OK) return status;
     const int cus = compute_units > 0 ? compute_units : device_compute_units();
     // The planning of pd_decode_ex, without its launches.
@@ -958,7 +997,7 @@ int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads,
     PartialParams prm = partial_params(nullptr, nullptr, nullptr, kv_dtype, 1.0f, 1.0f, nullptr, nullptr, nullptr,
                                        nullptr, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size,
                                        table_width, physical_pages, ks.splits, ks.split_tokens, hints, length_bounds,
-                                       reach);
+                                       reach, prefix_runs);
     if (q_dtype == PD_DTYPE_F32) plan_fp32(prm, kv_heads, head_dim);
     else plan_mfma(prm, kv_heads, cus, head_dim, static_cast<int>(element_size(kv_dtype)));
     const Grid grid = partial_grid(prm, kv_heads);
@@ -977,6 +1016,7 @@ int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads,
     p.xcd_grouped = prm.xcd_shift >= 0;
     p.combined = prm.combine;
     p.stream_mode = prm.stream_mode;
+    p.shared_prefix_items = prm.group_items;
     p.merge_kernel = -1;
     if (!prm.row_mode) {
         const int stride = prm.combine ? prm.quarters_per_wg : 1;
@@ -1018,6 +1058,7 @@ const char* pd_status_string(int status) {
         case PD_ERR_SCRATCH:
             return "the workspace does not fit the library's static scratch (PD_SCRATCH_BYTES), or its device "
                    "address could not be obtained";
+        case PD_ERR_PREFIX: return "malformed shared-prefix runs (a leader outside [-1, batch) or a count outside [0, table_width])";
         default: return "unknown status";
     }
 }

@@ -496,11 +496,31 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
     // one head tile); otherwise the wave index splits into (head, tile,
     // quarter) within the workgroup's partition.
     const int waves_wg = blockDim.x / kWave;
-    const int32_t* pages = p.table + static_cast<int64_t>(pr.b) * p.table_width;
+    // The item's page-table row (a shared-prefix item's: its members' leader,
+    // which its shared pass reads for every member that maps the same pages).
+    const int32_t* pages = p.table + static_cast<int64_t>(pr.row) * p.table_width;
     int window = kFold == 2 ? row_speculative_page<kTileTokens>(p, wave, waves_wg)
                             : speculative_page<kTileTokens>(p, pr.first, pr.count, pr.qgroup, wave);
     int window_ids = pages[window_entry(p, window, lane)];
-    const int len_raw = p.lengths[pr.b];
+    // Members of a shared-prefix item (work lists only): lane m < members
+    // holds member m's sequence and length; the wave covers the longest
+    // member's tokens, and tile column n belongs to member n / GT, which
+    // masks it at its own length. Any other item is one member, all columns.
+    const bool grouped = kList == kGridList && pr.members > 1;
+    int member_b = pr.b;
+    int member_len = 0;
+    int len_raw;
+    if (grouped) {
+        const bool is_member = lane < pr.members;
+        member_b = p.prefix_order[pr.member0 + (is_member ? lane : 0)];
+        member_len = is_member ? p.lengths[member_b] : 0;
+        int longest = member_len;
+#pragma unroll
+        for (int offset = 8; offset > 0; offset >>= 1) longest = max(longest, __shfl_xor(longest, offset));
+        len_raw = __builtin_amdgcn_readfirstlane(longest);
+    } else {
+        len_raw = p.lengths[pr.b];
+    }
     const WaveWork w = kFold == 2 ? row_wave_work<GT, kTileTokens>(p, pr.b, bc.heads, wave, waves_wg, len_raw)
                                   : wave_work<GT, kTileTokens>(p, pr.b, pr.first, pr.count, pr.qgroup, bc.heads, wave,
                                                                len_raw);
@@ -515,12 +535,54 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
         return;
     }
     const char* q_row = static_cast<const char*>(p.q) + w.q_row * D * 2;
+    // Column n's member, its query head within the tile, and its first masked
+    // token: for a single-member item, member 0, head n, no mask of its own.
+    const int col_slots = grouped ? GT : 16;
+    const int col_member = n / col_slots;
+    const int col_head = n - col_member * col_slots;
+    const bool col_live = col_member < pr.members && col_head < w.heads_here;
+    const int64_t row_base = static_cast<int64_t>(w.kv_head) * p.group + static_cast<int64_t>(w.tile) * GT;
+    // q row (batch x query-head index) of member m's tile head 0.
+    auto member_row = [&](int m) {
+        return grouped ? static_cast<int64_t>(__shfl(member_b, m)) * p.query_heads + row_base : w.q_row;
+    };
+    const int64_t col_row = member_row(col_member) + col_head;
+    const int col_end = grouped ? min(max(__shfl(member_len, col_member), 0), p.reach) : 0x7FFFFFFF;
+
+    // Page check of a shared-prefix item (prefix_span_pages): bit m of `own`
+    // marks member m, whose table row differs from the leader's on a page
+    // where it has tokens; it reads its own row in a later pass.
+    uint32_t own = 0;
+    if (grouped) {
+        const int span = prefix_span_pages(p, w.wb, w.we);
+        const int pairs = span * pr.members;
+        uint32_t differs = 0;
+        for (int base = 0; base < pairs; base += kWave) {
+            const int pair = base + lane;
+            const int m = pair < pairs ? prefix_pair_member(pair, span) : 0;
+            const int page = prefix_pair_page(p, w.wb, pair < pairs ? pair : 0, span);
+            const int mb = __shfl(member_b, m);
+            const int m_end = min(min(max(__shfl(member_len, m), 0), p.reach), w.we);
+            if (pair < pairs && (page << p.page_shift) < m_end &&
+                p.table[static_cast<int64_t>(mb) * p.table_width + page] != pages[page])
+                differs |= 1u << m;
+        }
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) differs |= __shfl_xor(differs, offset);
+        own = __builtin_amdgcn_readfirstlane(differs);
+    }
 
     u32x4 qb[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         qb[s] = u32x4{0u, 0u, 0u, 0u};
-        if (n < w.heads_here) qb[s] = *reinterpret_cast<const u32x4*>(q_row + (n * D + 32 * s + 8 * g) * 2);
+        if (grouped) {
+            if (col_live)
+                qb[s] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(p.q) +
+                                                        (col_row * D + 32 * s + 8 * g) * 2);
+        } else if (n < w.heads_here) {
+            qb[s] = *reinterpret_cast<const u32x4*>(q_row + (n * D + 32 * s + 8 * g) * 2);
+        }
     }
 
     float m_head = kNoToken;  // running max (log2 units) of head n, equal in all lane groups
@@ -535,6 +597,11 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
     const uint32_t v_lane_bytes = static_cast<uint32_t>(n) * VH * ES;
     const int k_row_token = k_token_of_row(n);
     int rb = w.wb, re = w.wb;
+    // The pass: its page-table row, its token end, and whether this lane's
+    // column takes part (the shared pass: every member but those in `own`).
+    const int32_t* pass_pages = pages;
+    int pass_end = w.we;
+    bool col_on = !grouped || ((own >> col_member) & 1u) == 0;
 
     auto issue = [&](Tile& tl, int t0, int ids, int win) {
         const TileSpan span = tile_span(p, t0, kTileTokens, rb, re, win);
@@ -587,12 +654,12 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int t = t0 + g + 4 * e;
-            const bool valid = (tl.live != 0u) & (t >= rb) & (t < re);
+            const bool valid = (tl.live != 0u) & (t >= rb) & (t < re) & (t < col_end) & col_on;
             x[e] = valid ? sc[e] : -INFINITY;
             mx = fmaxf(mx, x[e]);
         }
         const float tile_max = max_over_lane_groups(mx) * p.scale_log2;
-        if (__any((n < GT) & (tile_max > m_head + kRescaleSlack))) {
+        if (__any((n < GT * pr.members) & (tile_max > m_head + kRescaleSlack))) {
             const float m_new = fmaxf(m_head, tile_max);
             const float alpha = fast_exp2(m_head - m_new);
             m_head = m_new;
@@ -632,23 +699,34 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
         for (int j = 0; j < VH; ++j) acc[j] = C::pv(p_lo, v_operand<VH>(vq, j), acc[j]);
     };
 
-    for (rb = w.wb; rb < w.we; rb = re) {
-        if ((rb >> p.page_shift) != window) {
-            window = rb >> p.page_shift;
-            window_ids = pages[window_entry(p, window, lane)];
-        }
-        re = min(w.we, (window + kWave) << p.page_shift);
-        for (int s0 = rb & ~(kTileTokens - 1); s0 < re; s0 += NC * kTileTokens) {
-            Tile buf[PD + 1];
+    uint32_t pending = own;
+    for (;;) {
+        for (rb = w.wb; rb < pass_end; rb = re) {
+            if ((rb >> p.page_shift) != window) {
+                window = rb >> p.page_shift;
+                window_ids = pass_pages[window_entry(p, window, lane)];
+            }
+            re = min(pass_end, (window + kWave) << p.page_shift);
+            for (int s0 = rb & ~(kTileTokens - 1); s0 < re; s0 += NC * kTileTokens) {
+                Tile buf[PD + 1];
 #pragma unroll
-            for (int n0 = 0; n0 < PD; ++n0) issue(buf[n0], s0 + n0 * kTileTokens, window_ids, window);
+                for (int n0 = 0; n0 < PD; ++n0) issue(buf[n0], s0 + n0 * kTileTokens, window_ids, window);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                if (s0 + c * kTileTokens >= re) break;
-                if (c + PD < NC) issue(buf[(c + PD) % (PD + 1)], s0 + (c + PD) * kTileTokens, window_ids, window);
-                consume(buf[c % (PD + 1)], s0 + c * kTileTokens);
+                for (int c = 0; c < NC; ++c) {
+                    if (s0 + c * kTileTokens >= re) break;
+                    if (c + PD < NC) issue(buf[(c + PD) % (PD + 1)], s0 + (c + PD) * kTileTokens, window_ids, window);
+                    consume(buf[c % (PD + 1)], s0 + c * kTileTokens);
+                }
             }
         }
+        if (!grouped || pending == 0) break;
+        // Next member with a row of its own: its row, up to its own end.
+        const int m = __builtin_ctz(pending);
+        pending &= pending - 1;
+        pass_pages = p.table + static_cast<int64_t>(__builtin_amdgcn_readlane(member_b, m)) * p.table_width;
+        pass_end = min(w.we, min(max(__builtin_amdgcn_readlane(member_len, m), 0), p.reach));
+        col_on = col_member == m;
+        window = -1;
     }
 
     // Lane (g, n) holds heads 4 g + i of dims n VH .. n VH + VH - 1; the
@@ -691,7 +769,12 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
         return;
     }
     const int part = w.split * kQuarters + w.quarter;
-    store_empty_states(p, w, lane, extra_live_partitions(p, pr.first, pr.count, len_raw));
+    if (!grouped) store_empty_states(p, w, lane, extra_live_partitions(p, pr.first, pr.count, len_raw));
+    // A member whose own length ends before the partition (shorter on the
+    // device than its host bound) stores nothing, like a dead item: no state
+    // past a sequence's end is written. Column h's end lives in lane h.
+    const int64_t part_first = static_cast<int64_t>(w.split) * p.split_tokens;
+    auto column_alive = [&](int h) { return !grouped || part_first < __shfl(col_end, h); };
     if constexpr (kFold == 1) {
         // The workgroup's qw quarters of one (KV head, head tile) -- waves
         // wave - wave % qw onwards, all of one partition, so all live or all
@@ -712,9 +795,8 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
             }
 #pragma unroll
             for (int j = 0; j < VH; ++j) slot->acc[j][lane] = acc[j];
-            if (lane < w.heads_here)
-                *reinterpret_cast<float2*>(p.stats + stats_offset(p, w.q_row + lane, part)) =
-                    make_float2(kNoToken, 0.0f);
+            if (lane < 16 && col_live && part_first < col_end)
+                *reinterpret_cast<float2*>(p.stats + stats_offset(p, col_row, part)) = make_float2(kNoToken, 0.0f);
         }
         __syncthreads();
         if (qq != 0) return;
@@ -738,18 +820,23 @@ __global__ void __launch_bounds__(kFold == 2 ? kWave * kRowMaxWaves : kWave * 8)
             }
         }
     }
+    // acc[.][i] is tile column h = 4 g + i: member h / col_slots, head h % col_slots.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int h = 4 * g + i;
-        if (h < w.heads_here) {
-            f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + numerator_offset(p, w.q_row + h, part, D) + n * VH);
+        const int m = h / col_slots;
+        const int hm = h - m * col_slots;
+        const int64_t row = member_row(m) + hm;
+        const bool alive = column_alive(h);
+        if (m < pr.members && hm < w.heads_here && alive) {
+            f32x4* dst = reinterpret_cast<f32x4*>(p.numerator + numerator_offset(p, row, part, D) + n * VH);
 #pragma unroll
             for (int j = 0; j < VH; j += 4)
                 dst[j / 4] = f32x4{acc[j][i], acc[j + 1][i], acc[j + 2][i], acc[j + 3][i]} * p.v_scale;
         }
     }
-    if (lane < w.heads_here) {
-        float2* st = reinterpret_cast<float2*>(p.stats + stats_offset(p, w.q_row + lane, part));
+    if (lane < 16 && col_live && part_first < col_end) {
+        float2* st = reinterpret_cast<float2*>(p.stats + stats_offset(p, col_row, part));
         *st = make_float2(l_head > 0.0f ? m_head : kNoToken, l_head);
     }
 }

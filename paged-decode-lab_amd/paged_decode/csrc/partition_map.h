@@ -35,6 +35,7 @@ constexpr int kTileTokens = 16;  // tokens per matrix-core tile
 constexpr int kCompactMaxBatch = 64;
 constexpr int kTailSpan = 8;      // partitions per tail item, at least
 constexpr int kMaxTailItems = 4;  // tail items per sequence, at most (wider spans above that)
+constexpr int kMaxGroupItems = 128;  // shared-prefix items of a work list, at most (plan_prefix_items)
 
 PD_HD int imin(int a, int b) { return a < b ? a : b; }
 PD_HD int imax(int a, int b) { return a > b ? a : b; }
@@ -93,10 +94,11 @@ struct PartialParams {
     int main_splits;
     int tail_shift;
     int tail_span;
-    // Compacted work list (compact != 0): the grid's items are first the main
-    // items of every sequence, in sequence order -- sequence b has
-    // main_first[b + 1] - main_first[b] of them, partitions 0, 1, ... one
-    // each -- and then the tail items, again in sequence order: sequence b's
+    // Compacted work list (compact != 0): the grid's items are first the
+    // shared-prefix items (below), then the main items of every sequence, in
+    // sequence order -- sequence b has main_first[b + 1] - main_first[b] of
+    // them, partitions main_skip[b], main_skip[b] + 1, ... one each -- and
+    // then the tail items, again in sequence order: sequence b's
     // tail_first[b + 1] - tail_first[b] tail items, tail item j covering the
     // tail_span partitions after its main ones from j * tail_span on (fewer
     // at the end), which a sequence reaches only if it grew on the device
@@ -108,7 +110,24 @@ struct PartialParams {
     int items;             // grid items (compact), else batch * splits
     int32_t main_first[kCompactMaxBatch + 1];
     int32_t tail_first[kCompactMaxBatch + 1];
+    // Shared-prefix items (plan_prefix_items; work lists of the matrix-core
+    // kernel): the list's first group_items items each cover one partition of
+    // several sequences whose page-table rows name the same pages there, so
+    // the partition's K and V are read once for all of them. Item i covers
+    // partition group_item[i] >> 16 of the sequences prefix_order[s], ...,
+    // prefix_order[s + n - 1], with s = (group_item[i] >> 8) & 0xFF and n =
+    // group_item[i] & 0xFF (2 <= n <= 16 / GT): member m takes the tile's
+    // columns [m GT, (m + 1) GT). It reads the page ids of row group_row[i],
+    // the members' leader, whose row each member's run is measured against.
+    // Sequence b's main items then start at partition main_skip[b], not 0.
+    int group_items;
+    uint32_t group_item[kMaxGroupItems];
+    int8_t group_row[kMaxGroupItems];
+    int8_t prefix_order[kCompactMaxBatch];
+    int16_t main_skip[kCompactMaxBatch];
     // Host only (launch choices, not read by the kernels).
+    const int32_t* host_bounds;       // the caller's host length bounds, or null
+    const int32_t* host_prefix_runs;  // the caller's shared-prefix runs [2 * batch] (pd_prefix_runs), or null
     int combine;           // the launch stores a workgroup's qw quarters as one state (kFold 1)
     int row_allowed;       // the caller takes the output from the partition launch when row_mode is chosen
     int row_mode;          // whole-row workgroups fold every state of a row into out (kFold 2): no merge launch
@@ -196,6 +215,10 @@ PD_HD BlockCoords block_coords(uint32_t bx, uint32_t by, uint32_t bz, uint32_t g
 // partition's slots (the span's other live partitions get the empty state).
 struct PartitionRange {
     int b, first, count, qgroup;
+    // A shared-prefix item's sequences: prefix_order[member0 .. member0 +
+    // members), b the first of them, row the leader whose page ids it reads.
+    // For every other item members = 1 and row = b.
+    int member0, members, row;
 };
 
 inline int grid_kind(const PartialParams& prm) {
@@ -208,8 +231,11 @@ PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& 
     const int item = bc.tokens / groups;
     PartitionRange r;
     r.qgroup = bc.tokens - item * groups;
+    r.member0 = 0;
+    r.members = 1;
     if (kList == kGridRect) {
         r.b = bc.z;
+        r.row = r.b;
         r.first = item;
         r.count = 1;
         return r;
@@ -223,6 +249,7 @@ PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& 
         const bool tail = j >= 0;
         const bool none = (tail && tfirst >= p.splits) || bc.z >= p.batch;
         r.b = imin(bc.z, p.batch - 1);
+        r.row = r.b;
         r.first = tail ? imin(tfirst, p.splits - 1) : item;
         r.count = none ? 0 : tail ? imin(p.tail_span, p.splits - tfirst) : 1;
         return r;
@@ -236,30 +263,44 @@ PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& 
         const bool tail = zt >= 0;
         const bool none = tail && (tb >= p.batch || tfirst >= p.splits);
         r.b = tail ? imin(tb, p.batch - 1) : bc.z;
+        r.row = r.b;
         r.first = tail ? imin(tfirst, p.splits - 1) : item;
         r.count = none ? 0 : tail ? imin(p.tail_span, p.splits - tfirst) : 1;
         return r;
     }
+    if (item < p.group_items) {
+        const uint32_t word = p.group_item[item];
+        r.first = static_cast<int>(word >> 16);
+        r.member0 = static_cast<int>((word >> 8) & 0xFFu);
+        r.members = static_cast<int>(word & 0xFFu);
+        r.b = p.prefix_order[r.member0];
+        r.row = p.group_row[item];
+        r.count = 1;
+        return r;
+    }
+    const int listed = item - p.group_items;
     const int mains = p.main_first[p.batch];
-    const bool tail = item >= mains;
-    const int index = tail ? item - mains : item;
+    const bool tail = listed >= mains;
+    const int index = tail ? listed - mains : listed;
     // Sequence of the item: the last b with first[b] <= index (a sequence
     // without items of this kind repeats its predecessor's entry), i.e. the
     // number of sequences b < batch with first[b] <= index, minus one (first
     // is non-decreasing and first[0] = 0). On the device lane l loads both
     // arrays' entry l at once (batch <= kCompactMaxBatch = one wave) and a
     // ballot counts: one round of loads, where a search would chain several.
-    int b, first_b, next_main, main_b;
+    int b, first_b, next_main, main_b, skip_b;
 #if defined(__HIP_DEVICE_COMPILE__)
     static_assert(kCompactMaxBatch <= kWave, "one lane per sequence");
     const int lane = __lane_id();
     const bool in_batch = lane < p.batch;
     const int mf = in_batch ? p.main_first[lane] : 0x7FFFFFFF;
     const int tf = in_batch ? p.tail_first[lane] : 0x7FFFFFFF;
+    const int sk = in_batch ? p.main_skip[lane] : 0;
     const int f = tail ? tf : mf;
     b = static_cast<int>(__popcll(__ballot(f <= index))) - 1;
     first_b = __builtin_amdgcn_readlane(f, b);
     main_b = __builtin_amdgcn_readlane(mf, b);
+    skip_b = __builtin_amdgcn_readlane(sk, b);
     next_main = b + 1 < p.batch ? __builtin_amdgcn_readlane(mf, b + 1) : mains;
 #else
     const int32_t* first = tail ? p.tail_first : p.main_first;
@@ -268,17 +309,39 @@ PD_HD PartitionRange partition_range(const PartialParams& p, const BlockCoords& 
     b = count - 1;
     first_b = first[b];
     main_b = p.main_first[b];
+    skip_b = p.main_skip[b];
     next_main = p.main_first[b + 1];
 #endif
     r.b = b;
+    r.row = b;
+    // Sequence b's main items are its partitions skip_b, skip_b + 1, ...
+    // (those before skip_b are in shared-prefix items), then its tail items.
     if (!tail) {
-        r.first = index - first_b;
+        r.first = skip_b + index - first_b;
         r.count = 1;
     } else {
-        r.first = next_main - main_b + (index - first_b) * p.tail_span;
+        r.first = skip_b + next_main - main_b + (index - first_b) * p.tail_span;
         r.count = imin(p.tail_span, p.splits - r.first);
     }
     return r;
+}
+
+// The page check of a shared-prefix item's wave. The runs that formed the
+// item are the caller's description of the table; the kernel does not rely
+// on them. Before its loop, a wave compares each member's table entries with
+// the leader row's over the pages its tokens [wb, we) touch: pair i of the
+// check is member prefix_pair_member(i) on logical page prefix_pair_page(i),
+// checked when the member has tokens there (page * page_size < the member's
+// end). Members with a differing entry are left out of the shared pass and
+// read their own rows in a pass of their own, so results do not depend on
+// the runs being right (a plan refreshed after a graph was captured, or runs
+// that claim too much, only cost passes).
+PD_HD int prefix_span_pages(const PartialParams& p, int wb, int we) {
+    return wb < we ? ((we - 1) >> p.page_shift) - (wb >> p.page_shift) + 1 : 0;
+}
+PD_HD int prefix_pair_member(int pair, int span_pages) { return pair / span_pages; }
+PD_HD int prefix_pair_page(const PartialParams& p, int wb, int pair, int span_pages) {
+    return (wb >> p.page_shift) + pair % span_pages;
 }
 
 // Which KV head, head tile and token range a wave owns in the `count`
@@ -510,6 +573,11 @@ inline int tail_span_for(int reserved) {
 inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.xcd_shift = -1;  // plain grid until plan_xcd, once the workgroup shape is known
     prm.compact = 0;
+    prm.group_items = 0;
+    for (int b = 0; b < kCompactMaxBatch; ++b) {
+        prm.main_skip[b] = 0;
+        prm.prefix_order[b] = 0;
+    }
     prm.items = prm.batch * prm.splits;
     prm.main_splits = prm.splits;
     prm.tail_shift = 0;
@@ -777,6 +845,139 @@ inline void plan_rows(PartialParams& prm, int head_dim, int elem, int slot_bytes
     prm.tail_shift = 0;
 }
 
+// ---------------------------------------------------------------------------
+// Shared prefixes.
+//
+// Sequences that share a prefix of physical pages (one prompt, several
+// continuations) would each read that prefix's K and V. The matrix-core
+// tile scores 16 query-head columns per MFMA, and a GQA group fills only GT
+// of them, so one wave can score a K/V tile for 16 / GT sequences at the cost
+// of one: a shared-prefix item gives each member sequence GT columns (its own
+// q rows, its own length mask, its own states) and reads the tile once.
+//
+// The caller describes the sharing with prefix runs (pd_prefix_runs): for
+// each sequence b, runs[2 b] is its leader (the first sequence whose row
+// starts with the same page, or -1 when its first entry is not a page) and
+// runs[2 b + 1] the number of leading table entries b has in common with the
+// leader's row. Two sequences of one leader then share their first
+// min(run, run') entries. The device table must hold the rows the runs were
+// taken from; DecodePlan keeps the two in step (its table is the host copy it
+// uploads, and it drops the runs when the device rewrites the table).
+
+// Prefix runs of a host page table [batch, width] (pd_prefix_runs). A
+// sequence's leader is the first sequence whose row starts with the same page
+// (found among the leaders so far: the batch is small next to the table).
+inline void prefix_runs_of_table(const int32_t* table, int batch, int width, int32_t* runs) {
+    for (int b = 0; b < batch; ++b) {
+        const int32_t* row = table + static_cast<int64_t>(b) * width;
+        int leader = -1;
+        if (row[0] >= 0) {
+            for (int c = 0; c < b && leader < 0; ++c)
+                if (runs[2 * c] == c && table[static_cast<int64_t>(c) * width] == row[0]) leader = c;
+            if (leader < 0) leader = b;
+        }
+        int run = 0;
+        if (leader >= 0) {
+            const int32_t* lrow = table + static_cast<int64_t>(leader) * width;
+            while (run < width && row[run] >= 0 && row[run] == lrow[run]) ++run;
+        }
+        runs[2 * b] = leader;
+        runs[2 * b + 1] = run;
+    }
+}
+
+// Whether a runs array is well formed for the batch and table width.
+inline bool prefix_runs_valid(const int32_t* runs, int batch, int width) {
+    for (int b = 0; b < batch; ++b) {
+        const int leader = runs[2 * b], run = runs[2 * b + 1];
+        if (leader < -1 || leader >= batch || run < 0 || run > width) return false;
+    }
+    return true;
+}
+
+// Shared-prefix items of a work list (compact), for a matrix-core launch
+// whose tile holds `slots` = 16 / GT member sequences. Sequence b's leading
+// kernel partitions whose tokens below its host bound all lie inside its run
+// may be shared, lead_b of them: every partition that holds tokens when the
+// bound ends inside the run (a short sequence whose whole context is the
+// prefix), else the partitions that end inside it. A length that grows past
+// the bound onto pages of its own is caught by the kernel's page check.
+// Per leader, the members with lead >= 1 are sorted
+// by lead (longest first, then by sequence) into prefix_order; partition j's
+// members -- those with lead_b > j, a prefix of that order -- are cut into
+// chunks of `slots` in that order, and each chunk of at least two is one
+// item. A sequence's shared partitions are then a prefix [0, main_skip[b]):
+// its chunk only shrinks as j grows. Items past kMaxGroupItems are not
+// formed; the partitions from the first one left out are main items again.
+// Batches above kCompactMaxBatch, rectangular grids, whole-row launches and
+// calls without host bounds or runs keep one sequence per item.
+inline void plan_prefix_items(PartialParams& prm, int slots) {
+    prm.group_items = 0;
+    for (int b = 0; b < kCompactMaxBatch; ++b) prm.main_skip[b] = 0;
+    const int32_t* runs = prm.host_prefix_runs;
+    const int32_t* bounds = prm.host_bounds;
+    if (!prm.compact || prm.row_mode || runs == nullptr || bounds == nullptr || slots < 2) return;
+    const int batch = prm.batch;
+    int lead[kCompactMaxBatch], live[kCompactMaxBatch], skip[kCompactMaxBatch];
+    for (int b = 0; b < batch; ++b) {
+        live[b] = prm.main_first[b + 1] - prm.main_first[b];
+        skip[b] = 0;
+        const int leader = runs[2 * b];
+        const int64_t shared = static_cast<int64_t>(runs[2 * b + 1]) << prm.page_shift;
+        const int64_t bound = lmin(prm.reach, bounds[b] < 0 ? 0 : bounds[b]);
+        const int64_t parts = bound <= shared ? (bound + prm.split_tokens - 1) / prm.split_tokens
+                                              : shared / prm.split_tokens;
+        lead[b] = leader < 0 || leader >= batch ? 0 : static_cast<int>(lmin(parts, live[b]));
+    }
+    bool placed[kCompactMaxBatch] = {};
+    int order = 0;
+    bool capped = false;
+    for (int b0 = 0; b0 < batch && !capped; ++b0) {
+        if (placed[b0] || lead[b0] < 1) continue;
+        // The class of b0's leader, sorted by lead (descending), then sequence.
+        int members[kCompactMaxBatch];
+        int n = 0;
+        for (int b = b0; b < batch; ++b) {
+            if (placed[b] || lead[b] < 1 || runs[2 * b] != runs[2 * b0]) continue;
+            placed[b] = true;
+            int k = n++;
+            while (k > 0 && lead[members[k - 1]] < lead[b]) {
+                members[k] = members[k - 1];
+                --k;
+            }
+            members[k] = b;
+        }
+        if (n < 2) continue;
+        const int start = order;
+        for (int k = 0; k < n; ++k) prm.prefix_order[order++] = static_cast<int8_t>(members[k]);
+        for (int j = 0; j < lead[members[0]] && !capped; ++j) {
+            int covering = 0;
+            while (covering < n && lead[members[covering]] > j) ++covering;
+            for (int c = 0; c + 1 < covering && !capped; c += slots) {  // chunks of two or more
+                const int size = imin(slots, covering - c);
+                if (prm.group_items == kMaxGroupItems) {
+                    capped = true;
+                    break;
+                }
+                prm.group_row[prm.group_items] = static_cast<int8_t>(runs[2 * b0]);
+                prm.group_item[prm.group_items++] = (static_cast<uint32_t>(j) << 16) |
+                                                    (static_cast<uint32_t>(start + c) << 8) |
+                                                    static_cast<uint32_t>(size);
+                for (int k = c; k < c + size; ++k) skip[members[k]] = j + 1;
+            }
+        }
+    }
+    if (prm.group_items == 0) return;
+    int mains = 0;
+    for (int b = 0; b < batch; ++b) {
+        prm.main_first[b] = mains;
+        prm.main_skip[b] = static_cast<int16_t>(skip[b]);
+        mains += live[b] - skip[b];
+    }
+    prm.main_first[batch] = mains;
+    prm.items = prm.group_items + mains + prm.tail_first[batch];
+}
+
 // The XCD-grouped grid (block_coords) for a rectangular launch whose row
 // groups all carry the same work: host bounds that give every sequence the
 // same partitions (and so the same tail items), no work list, no whole-row
@@ -988,6 +1189,7 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
         prm.combine = prm.quarters_per_wg == 4;
     }
     plan_rows(prm, head_dim, elem, combine_slot_bytes(head_dim), mfma_stage_bytes(head_dim, elem));
+    plan_prefix_items(prm, prm.head_tiles == 1 ? 16 / gt : 1);
     plan_xcd(prm, kv_heads);
     // Where the merge reads its states from the XCD's L2 (plan_xcd), the fold
     // of the mid-size grids' two quarters no longer pays for its tail: their

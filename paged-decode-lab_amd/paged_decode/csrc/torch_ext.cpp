@@ -129,40 +129,66 @@ const int32_t* bounds_pointer(const c10::optional<torch::Tensor>& bounds, int64_
     return t.data_ptr<int32_t>();
 }
 
+// Host pointer of the optional shared-prefix runs (a CPU int32 tensor
+// [2 * batch], see pd_prefix_runs), or null.
+const int32_t* runs_pointer(const c10::optional<torch::Tensor>& runs, int64_t batch) {
+    if (!runs.has_value()) return nullptr;
+    const auto& t = *runs;
+    TORCH_CHECK(t.device().is_cpu() && t.scalar_type() == at::kInt && t.is_contiguous() && t.dim() == 1 &&
+                    t.size(0) == 2 * batch,
+                "prefix_runs must be a contiguous CPU int32 tensor [2 * batch]");
+    return t.data_ptr<int32_t>();
+}
+
 }  // namespace
 
 void decode(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
             torch::Tensor numerator, torch::Tensor stats, torch::Tensor out, int64_t split_tokens,
             int64_t merge_mode, double k_scale, double v_scale, bool unshared_pages, bool ragged_lengths,
-            c10::optional<torch::Tensor> length_bounds) {
+            c10::optional<torch::Tensor> length_bounds, c10::optional<torch::Tensor> prefix_runs) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     check_output(q, out, merge_mode, s.splits);
     const int32_t* bounds = bounds_pointer(length_bounds, s.batch);
+    const int32_t* runs = runs_pointer(prefix_runs, s.batch);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    check_status(pd_decode_ex(q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k),
+    check_status(pd_decode_prefix(q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k),
                               static_cast<float>(k_scale), static_cast<float>(v_scale), table.data_ptr<int32_t>(),
                               lengths.data_ptr<int32_t>(), numerator.data_ptr<float>(), stats.data_ptr<float>(),
                               out.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
                               static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
                               static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
                               static_cast<int>(split_tokens), static_cast<int>(merge_mode),
-                              hints(unshared_pages, ragged_lengths), bounds, current_stream(q)));
+                              hints(unshared_pages, ragged_lengths), bounds, runs, current_stream(q)));
 }
 
 // Partition stage alone (first launch of decode); used to time that kernel.
 void partial(torch::Tensor q, torch::Tensor k, torch::Tensor v, torch::Tensor table, torch::Tensor lengths,
              torch::Tensor numerator, torch::Tensor stats, int64_t split_tokens, double k_scale, double v_scale,
-             bool unshared_pages, bool ragged_lengths, c10::optional<torch::Tensor> length_bounds) {
+             bool unshared_pages, bool ragged_lengths, c10::optional<torch::Tensor> length_bounds,
+             c10::optional<torch::Tensor> prefix_runs) {
     const Shape s = check_inputs(q, k, v, table, lengths, numerator, stats, split_tokens);
     const int32_t* bounds = bounds_pointer(length_bounds, s.batch);
+    const int32_t* runs = runs_pointer(prefix_runs, s.batch);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(q.device());
-    check_status(pd_decode_partial_ex(
+    check_status(pd_decode_partial_prefix(
         q.data_ptr(), dtype_code(q), k.data_ptr(), v.data_ptr(), dtype_code(k), static_cast<float>(k_scale),
         static_cast<float>(v_scale), table.data_ptr<int32_t>(), lengths.data_ptr<int32_t>(),
         numerator.data_ptr<float>(), stats.data_ptr<float>(), static_cast<int>(s.batch), static_cast<int>(s.heads),
         static_cast<int>(s.kv_heads), static_cast<int>(s.dim), static_cast<int>(s.page_size),
         static_cast<int>(s.width), static_cast<int>(s.pages), static_cast<int>(s.splits),
-        static_cast<int>(split_tokens), hints(unshared_pages, ragged_lengths), bounds, current_stream(q)));
+        static_cast<int>(split_tokens), hints(unshared_pages, ragged_lengths), bounds, runs, current_stream(q)));
+}
+
+// Shared-prefix runs of a host page table [batch, width] (pd_prefix_runs):
+// a CPU int32 tensor [2 * batch] of (leader, leading entries in common).
+torch::Tensor prefix_runs(torch::Tensor table) {
+    TORCH_CHECK(table.device().is_cpu() && table.scalar_type() == at::kInt && table.is_contiguous() &&
+                    table.dim() == 2 && table.size(0) > 0 && table.size(1) > 0,
+                "table must be a contiguous CPU int32 tensor [batch, width]");
+    torch::Tensor runs = torch::empty({2 * table.size(0)}, torch::dtype(torch::kInt32));
+    check_status(pd_prefix_runs(table.data_ptr<int32_t>(), static_cast<int>(table.size(0)),
+                                static_cast<int>(table.size(1)), runs.data_ptr<int32_t>()));
+    return runs;
 }
 
 // Merge stage alone (second launch of decode); lengths, page_size,
@@ -303,8 +329,9 @@ py::dict launch_plan(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t ba
                      int64_t kv_heads, int64_t head_dim, int64_t page_size, int64_t table_width,
                      int64_t physical_pages, int64_t splits, int64_t split_tokens, int64_t merge_mode,
                      bool unshared_pages, bool ragged_lengths, c10::optional<torch::Tensor> length_bounds,
-                     int64_t compute_units) {
+                     int64_t compute_units, c10::optional<torch::Tensor> prefix_runs) {
     const int32_t* bounds = bounds_pointer(length_bounds, batch);
+    const int32_t* runs = runs_pointer(prefix_runs, batch);
     pd_launch_plan p{};
     check_status(pd_decode_launch_plan(dtype_code(q_dtype), dtype_code(kv_dtype), static_cast<int>(batch),
                                        static_cast<int>(query_heads), static_cast<int>(kv_heads),
@@ -312,7 +339,7 @@ py::dict launch_plan(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t ba
                                        static_cast<int>(table_width), static_cast<int>(physical_pages),
                                        static_cast<int>(splits), static_cast<int>(split_tokens),
                                        static_cast<int>(merge_mode), hints(unshared_pages, ragged_lengths), bounds,
-                                       static_cast<int>(compute_units), &p));
+                                       runs, static_cast<int>(compute_units), &p));
     static const char* kinds[] = {"rectangular", "rectangular+tails", "work list", "whole rows"};
     py::dict d;
     d["launches"] = p.launches;
@@ -326,6 +353,7 @@ py::dict launch_plan(at::ScalarType q_dtype, at::ScalarType kv_dtype, int64_t ba
     d["xcd_grouped"] = p.xcd_grouped != 0;
     d["combined"] = p.combined != 0;
     d["stream_mode"] = p.stream_mode;
+    d["shared_prefix_items"] = p.shared_prefix_items;
     if (p.merge_kernel >= 0) {
         d["merge"] = py::make_tuple(p.merge_kernel == 0 ? "rows" : "cols", p.merge_loads, p.merge_chunk_floats,
                                     p.merge_xcd_grouped != 0, p.merge_state_stride);
@@ -357,11 +385,13 @@ PYBIND11_MODULE(_C, m) {
           py::arg("table"), py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("out"),
           py::arg("split_tokens"), py::arg("merge_mode"), py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0,
           py::arg("unshared_pages") = false, py::arg("ragged_lengths") = false,
-          py::arg("length_bounds") = py::none());
+          py::arg("length_bounds") = py::none(), py::arg("prefix_runs") = py::none());
     m.def("partial", &partial, "Partition stage only", py::arg("q"), py::arg("k"), py::arg("v"), py::arg("table"),
           py::arg("lengths"), py::arg("numerator"), py::arg("stats"), py::arg("split_tokens"),
           py::arg("k_scale") = 1.0, py::arg("v_scale") = 1.0, py::arg("unshared_pages") = false,
-          py::arg("ragged_lengths") = false, py::arg("length_bounds") = py::none());
+          py::arg("ragged_lengths") = false, py::arg("length_bounds") = py::none(),
+          py::arg("prefix_runs") = py::none());
+    m.def("prefix_runs", &prefix_runs, "Shared-prefix runs of a host page table (pd_prefix_runs)", py::arg("table"));
     m.def("merge", &merge, "Merge stage only");
     m.def("append_kv", &append_kv, "Paged KV-cache append", py::arg("k_new"), py::arg("v_new"), py::arg("table"),
           py::arg("positions"), py::arg("k_cache"), py::arg("v_cache"), py::arg("advance"),
@@ -383,7 +413,8 @@ PYBIND11_MODULE(_C, m) {
           py::arg("kv_dtype"), py::arg("batch"), py::arg("query_heads"), py::arg("kv_heads"), py::arg("head_dim"),
           py::arg("page_size"), py::arg("table_width"), py::arg("physical_pages"), py::arg("splits"),
           py::arg("split_tokens"), py::arg("merge_mode"), py::arg("unshared_pages") = false,
-          py::arg("ragged_lengths") = false, py::arg("length_bounds") = py::none(), py::arg("compute_units") = 0);
+          py::arg("ragged_lengths") = false, py::arg("length_bounds") = py::none(), py::arg("compute_units") = 0,
+          py::arg("prefix_runs") = py::none());
     m.def("stream_read", &stream_read, "One streaming read of the leading bytes of two tensors", py::arg("a"),
           py::arg("b"), py::arg("a_bytes"), py::arg("b_bytes"), py::arg("sink"));
     m.def("abi_version", &pd_abi_version, "ABI version the loaded HIP library reports");

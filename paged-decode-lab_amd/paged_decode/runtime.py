@@ -127,6 +127,7 @@ class DecodePlan:
         self._stage_views = {}
         self._staged_split = (self.splits, split_tokens)
         self._extension = load_extension()
+        self._prefix_runs = self._shared_prefixes(table)
 
     @classmethod
     def from_csr(cls, layout: Layout, indptr, indices, last_page_len, **kwargs):
@@ -164,6 +165,7 @@ class DecodePlan:
         self._table_cpu, self._lengths_cpu = table, lengths
         self._unshared_pages = unshared_pages(table, self.layout.page_size, self.context_capacity)
         self._ragged_lengths = ragged_lengths(lengths)
+        self._prefix_runs = self._shared_prefixes(table)
         self.max_context = longest
 
     def refresh_csr(self, indptr, indices, last_page_len, overflow=None):
@@ -196,6 +198,7 @@ class DecodePlan:
         self._unshared_pages = False
         self._ragged_lengths = False
         self._bounds_known = False
+        self._prefix_runs = None
 
     def append(self, k_cache, v_cache, k_new, v_new):
         """Append new tokens at the plan's current lengths and advance them on the device.
@@ -253,7 +256,7 @@ class DecodePlan:
         self._check(q, k, v, k_scale, v_scale)
         self._extension.decode(q, k, v, self._table, self._lengths, self._numerator, self._stats,
                                self._out, self.split_tokens, self._merge_mode, float(k_scale), float(v_scale),
-                               self._unshared_pages, self._ragged_lengths, self._length_bounds())
+                               self._unshared_pages, self._ragged_lengths, self._length_bounds(), self._prefix_runs)
         return self._out
 
     def launches(self, q_dtype, kv_dtype=None):
@@ -290,7 +293,8 @@ class DecodePlan:
                                            layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size,
                                            self._table.shape[1], layout.physical_pages, self.splits,
                                            self.split_tokens, self._merge_mode, self._unshared_pages,
-                                           self._ragged_lengths, self._length_bounds(), compute_units)
+                                           self._ragged_lengths, self._length_bounds(), compute_units,
+                                           self._prefix_runs)
 
     def _stage_workspace(self, splits):
         """Numerator and stats views for ``splits`` partitions per row: the leading
@@ -314,12 +318,23 @@ class DecodePlan:
         numerator, stats = self._stage_workspace(splits)
         self._extension.partial(q, k, v, self._table, self._lengths, numerator, stats, split_tokens,
                                 float(k_scale), float(v_scale), self._unshared_pages, self._ragged_lengths,
-                                self._length_bounds())
+                                self._length_bounds(), self._prefix_runs)
         self._staged_split = (splits, split_tokens)
 
     def _length_bounds(self):
         """Host upper bounds on the device lengths, or None after a device-side CSR refresh."""
         return self._bounds if self._bounds_known else None
+
+    def _shared_prefixes(self, table):
+        """Shared-prefix runs of the host table (``pd_prefix_runs``), or None when
+        no page is mapped twice. With them, a work-list launch scores each
+        partition inside several sequences' common prefix once for up to 16 / GT
+        of them (one read of its K and V). The kernel checks the pages itself,
+        so runs that no longer describe the device table (a graph captured
+        before ``refresh``) cost time, never correctness."""
+        if self._unshared_pages:
+            return None
+        return self._extension.prefix_runs(torch.from_numpy(np.ascontiguousarray(table, dtype=np.int32)))
 
     def run_merge(self):
         """Merge stage only, from the states the last ``run_partial`` left in the

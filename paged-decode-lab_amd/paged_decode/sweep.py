@@ -36,14 +36,16 @@ class Shape:
     kv_heads: int
     head_dim: int
     page_size: int
-    lengths: str          # "uniform:L" | "ragged:L" (U[0, L] seeded, one empty) | "reference:L" (make_metadata
-                          # seed 123) | "workload:NAME" (a named workload's own table and lengths)
+    lengths: str          # "uniform:L" | "ragged:L" (U[0, L] seeded, one empty) | "skewed:L" (one at L, the
+                          # rest U[0, L/2]) | "reference:L" (make_metadata seed 123) | "workload:NAME" (a named
+                          # workload's own table and lengths)
     split_tokens: int
     fmt: str = "f16"      # f16 | bf16 | fp8 (e4m3 K/V under an f16 q) | f32
     reserve: int = 1      # max_context = reserve x the longest sequence
     shared_prefix: float = 0.0  # leading fraction of the longest sequence's pages, mapped to one shared set
     coarse: tuple = ()    # kernel split factors c timed through the stage entries
     bounds: bool = True   # False: calls without host length bounds (the library sees device lengths only)
+    runs: bool = True     # False: calls without shared-prefix runs (every sequence reads its own pages)
 
 
 def _s(name, b, hq, hkv, d, t, lengths, split, **kw):
@@ -134,7 +136,27 @@ ROWS = [
     _s("mqa B256 L256 D64", 256, 16, 1, 64, 16, "uniform:256", 256, coarse=(1,)),
 ]
 
-SWEEPS = {"coarse": COARSE, "reserved": RESERVED, "small": SMALL, "mid": MID, "xcd": XCD, "rows": ROWS}
+# Shared prefixes (plan_prefix_items): work lists whose partitions inside
+# several sequences' common prefix are scored once for up to 16 / GT of them,
+# against the same calls without runs (one read per sequence).
+PREFIX = [
+    _s(f"{base}{'' if runs else ' no runs'}", *args, runs=runs, **kw)
+    for base, args, kw in [
+        ("ragged+shared B16 T32 split 128", (16, 32, 8, 128, 32, "workload:ragged_shared_b16", 128), {}),
+        ("skewed B16 L8192 T32 50% shared", (16, 32, 8, 128, 32, "skewed:8192", 128), {"shared_prefix": 0.5}),
+        ("skewed B32 L4096 25% shared", (32, 32, 8, 128, 16, "skewed:4096", 256), {"shared_prefix": 0.25}),
+        ("fp8 skewed B16 L8192 T32 25% shared", (16, 32, 8, 128, 32, "skewed:8192", 128),
+         {"shared_prefix": 0.25, "fmt": "fp8"}),
+        ("mha skewed B16 Hq16/16 L4096 25% shared", (16, 16, 16, 128, 16, "skewed:4096", 256),
+         {"shared_prefix": 0.25}),
+        ("gqa8 skewed B16 Hq32/4 L4096 25% shared", (16, 32, 4, 128, 16, "skewed:4096", 256),
+         {"shared_prefix": 0.25}),
+    ]
+    for runs in (True, False)
+]
+
+SWEEPS = {"coarse": COARSE, "reserved": RESERVED, "small": SMALL, "mid": MID, "xcd": XCD, "rows": ROWS,
+          "prefix": PREFIX}
 
 
 def shapes(names):
@@ -173,6 +195,9 @@ def metadata(shape, seed=7):
         lengths[0] = context
         if shape.batch > 2:
             lengths[rng.integers(1, shape.batch)] = 0
+    elif kind == "skewed":
+        lengths = rng.integers(0, context // 2 + 1, size=shape.batch, dtype=np.int32)
+        lengths[0] = context
     elif kind == "uniform":
         lengths = np.full(shape.batch, context, dtype=np.int32)
     else:
@@ -251,6 +276,8 @@ def run(names, steps=200, merge="serial", out=sys.stdout, log=None):
         vs = [v0] + [v0.clone() for _ in range(sets - 1)]
         plan = DecodePlan(layout, table, lengths, device=device, split_tokens=shape.split_tokens, merge=merge,
                           max_context=int(min(max_context, table.shape[1] * layout.page_size)))
+        if not shape.runs:
+            plan._prefix_runs = None
         scales = {"k_scale": k_scale, "v_scale": v_scale}
         ext = plan._extension
         if shape.bounds:
@@ -263,6 +290,7 @@ def run(names, steps=200, merge="serial", out=sys.stdout, log=None):
                            plan._ragged_lengths, None)
         record = {"sweep": sweep, "shape": shape.name, "lengths": shape.lengths, "fmt": shape.fmt,
                   "split_tokens": shape.split_tokens, "reserve": shape.reserve, "bounds": shape.bounds,
+                  "runs": shape.runs,
                   "kv_bytes_per_call": int(lengths.astype(np.int64).sum()) * layout.kv_heads * layout.head_dim * 2
                   * k0.element_size(), "kv_buffer_sets": sets}
         record["us_per_call"] = round(_graph_us(torch, call, steps), 3)
@@ -279,7 +307,7 @@ def run(names, steps=200, merge="serial", out=sys.stdout, log=None):
             def stage(i, c=c, num=num, stats=stats, bounds=bounds):
                 ext.partial(q, ks[i % sets], vs[i % sets], plan._table, plan._lengths, num, stats,
                             c * shape.split_tokens, k_scale, v_scale, plan._unshared_pages, plan._ragged_lengths,
-                            bounds)
+                            bounds, plan._prefix_runs)
                 ext.merge(num, stats, plan._out, plan._lengths, layout.page_size, table.shape[1],
                           c * shape.split_tokens, plan._merge_mode)
             staged[f"x{c}"] = round(_graph_us(torch, stage, steps), 3)

@@ -43,12 +43,15 @@ struct Problem {
     // at or past caller_splits * caller_split_tokens may be read.
     int caller_split_tokens, caller_splits;
     std::vector<int32_t> table, lengths, bounds;  // bounds empty: none
+    std::vector<int32_t> runs;                    // shared-prefix runs [2 * batch] (pd_prefix_runs); empty: none
     bool unshared = true, ragged = false;
 };
 
 uint64_t g_checks = 0;
 int g_failures = 0;
 bool g_plant_reach = false;  // --plant-reach: launch params that ignore the caller's partitions (negative control)
+bool g_plant_no_check = false;  // --plant-prefix: shared-prefix items that trust the runs (negative control)
+uint64_t g_own_passes = 0;      // shared-prefix members that read their own rows after the page check
 
 // Tokens of a row the caller's partitions cover, clamped to the table.
 int reach_of(const Problem& pr) {
@@ -101,7 +104,9 @@ PartialParams params(const Problem& pr, int cus, bool mfma, bool rows) {
     p.page_bytes = static_cast<uint64_t>(pr.page_size) * p.token_bytes;
     p.unshared_pages = pr.unshared;
     p.ragged_lengths = pr.ragged;
-    plan_items(p, pr.bounds.empty() ? nullptr : pr.bounds.data());
+    p.host_bounds = pr.bounds.empty() ? nullptr : pr.bounds.data();
+    p.host_prefix_runs = pr.runs.empty() ? nullptr : pr.runs.data();
+    plan_items(p, p.host_bounds);
     if (mfma) plan_mfma(p, pr.kv_heads, cus, pr.head_dim, pr.kv_elem);
     else plan_fp32(p, pr.kv_heads, pr.head_dim);
     return p;
@@ -196,7 +201,7 @@ int page_of(const Problem& pr, int b, int window, int slot, const PartialParams&
 // One load group of the matrix-core kernel (a 16-token tile), all 64 lanes.
 template <int D>
 void mfma_tile(const Problem& pr, const PartialParams& p, const Buffers& buf, const WaveWork& w, int b, int t0,
-               int rb, int re, int window, int wave, int waves, int len) {
+               int rb, int re, int window, int wave, int waves, int len, const std::vector<int>& members) {
     const int ES = pr.kv_elem;
     const int VH = D / 16, VW = VH * ES / 4, KR = D * ES / 16, TK = kWave / KR, KL = kTileTokens / TK;
     const int stage_row = mfma_stage_bytes(D, ES) / kTileTokens;
@@ -212,6 +217,18 @@ void mfma_tile(const Problem& pr, const PartialParams& p, const Buffers& buf, co
         AUDIT((span.hi >> p.page_shift) == (span.lo >> p.page_shift), "tile %d straddles a page", t0);
         AUDIT(span.lo >= rb && span.hi < re && span.hi < len, "tile %d span [%d, %d] outside [%d, %d)", t0, span.lo,
               span.hi, rb, re);
+        // A shared-prefix item reads its leader's page for its members: every
+        // reader with live tokens in the tile must name that page.
+        {
+            const int logical = span.lo >> p.page_shift;
+            for (int s : members) {
+                const int member_len = imax(0, imin(pr.lengths[s], reach_of(pr)));
+                if (span.lo < member_len)
+                    AUDIT(pr.table[static_cast<size_t>(s) * pr.width + logical] == page,
+                          "tile %d: member %d maps page %d, the item reads page %d", t0, s,
+                          pr.table[static_cast<size_t>(s) * pr.width + logical], page);
+            }
+        }
     }
     const uint64_t page_off = tile_page_offset(p, ok, page);
     const uint64_t head_off = static_cast<uint64_t>(w.kv_head) * D * ES;
@@ -307,7 +324,29 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                       "partition range %d + %d", r.first, r.count);
                 if (r.b < 0 || r.b >= pr.batch) continue;
                 const int b = r.b;
-                const int len_raw = pr.lengths[b];
+                // A shared-prefix item's member sequences (else the item's
+                // own); the wave covers the longest member's tokens.
+                std::vector<int> members{b};
+                if (r.members == 1) AUDIT(r.row == b, "item of sequence %d reads row %d", b, r.row);
+                if (r.members != 1) {
+                    AUDIT(kind == kGridList && mfma && !p.row_mode, "shared-prefix item outside a matrix-core work list");
+                    AUDIT(r.members >= 2 && r.members <= 16 / GT && r.member0 >= 0 &&
+                              r.member0 + r.members <= kCompactMaxBatch && r.count == 1,
+                          "shared-prefix item of %d members from slot %d, count %d", r.members, r.member0, r.count);
+                    members.clear();
+                    for (int m = 0; m < r.members && r.member0 + m < kCompactMaxBatch; ++m) {
+                        const int s = p.prefix_order[r.member0 + m];
+                        AUDIT(s >= 0 && s < pr.batch, "member sequence %d", s);
+                        for (int other : members) AUDIT(other != s, "sequence %d twice in one item", s);
+                        if (s >= 0 && s < pr.batch) members.push_back(s);
+                    }
+                    AUDIT(!members.empty() && members[0] == b, "item sequence %d is not its first member", b);
+                    AUDIT(r.row >= 0 && r.row < pr.batch && !pr.runs.empty() && pr.runs[2 * members[0]] == r.row,
+                          "item reads row %d, not its members' leader", r.row);
+                    if (members.empty() || r.row < 0 || r.row >= pr.batch) continue;
+                }
+                int len_raw = 0;
+                for (int s : members) len_raw = imax(len_raw, pr.lengths[s]);
                 // Live tokens: the length clamped to the table and to the
                 // caller's partitions; every read below is checked against it.
                 const int len = imax(0, imin(len_raw, reach_of(pr)));
@@ -327,7 +366,7 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                                               : row_speculative_page<TPLV>(p, wave, waves))
                                       : mfma ? speculative_page<kTileTokens>(p, split, r.count, r.qgroup, wave)
                                              : speculative_page<TPLV>(p, split, r.count, r.qgroup, wave);
-                    window_loads(pr, p, buf, b, window);
+                    window_loads(pr, p, buf, r.row, window);
                     {
                         const WaveWork w =
                             rows ? (mfma ? row_wave_work<GT, kTileTokens>(p, b, bc.heads, wave, waves, len_raw)
@@ -374,9 +413,19 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                         const int64_t parts = rows ? pr.splits : r.count;
                         AUDIT(w.wb >= first && w.we <= first + parts * pr.split_tokens && w.wb <= w.we && w.we <= len,
                               "wave range [%d, %d) of partitions %d + %" PRId64, w.wb, w.we, split, parts);
-                        // q loads of the tile's live heads.
+                        // q loads of the tile's live heads (a shared-prefix
+                        // item: column n is member n / GT's head n % GT).
+                        const int64_t row_base = static_cast<int64_t>(w.kv_head) * p.group +
+                                                 static_cast<int64_t>(w.tile) * GT;
                         for (int lane = 0; lane < kWave; ++lane) {
-                            if (mfma) {
+                            if (mfma && members.size() > 1) {
+                                const int n = lane % 16, g = lane / 16, m = n / GT, h = n % GT;
+                                if (m < static_cast<int>(members.size()) && h < w.heads_here)
+                                    for (int s = 0; s < D / 32; ++s)
+                                        AUDIT(static_cast<uint64_t>((members[m] * static_cast<int64_t>(pr.q_heads) +
+                                                                     row_base + h) * D + 32 * s + 8 * g) * 2 + 16 <=
+                                                  buf.q_bytes, "member q load");
+                            } else if (mfma) {
                                 const int n = lane % 16, g = lane / 16;
                                 if (n < w.heads_here)
                                     for (int s = 0; s < D / 32; ++s)
@@ -388,34 +437,89 @@ void audit_launch(const Problem& pr, const PartialParams& p, bool mfma, Coverage
                                               buf.q_bytes, "q load");
                             }
                         }
-                        // The kernels' token loop: page-id windows of 64 pages,
-                        // load groups issued `ahead` in blocks of `block`.
-                        int rb = w.wb, re = w.wb;
-                        for (rb = w.wb; rb < w.we; rb = re) {
-                            if ((rb >> p.page_shift) != window) {
-                                window = rb >> p.page_shift;
-                                window_loads(pr, p, buf, b, window);
+                        // A shared-prefix item's page check (prefix_span_pages):
+                        // the table loads of every pair, and the members whose
+                        // rows differ from the first member's where they have
+                        // tokens, which then read their own rows.
+                        std::vector<int> shared_members = members, own;
+                        if (members.size() > 1) {
+                            const int span = prefix_span_pages(p, w.wb, w.we);
+                            const int pairs = span * static_cast<int>(members.size());
+                            std::vector<bool> differs(members.size(), false);
+                            for (int pair = 0; pair < pairs; ++pair) {
+                                const int m = prefix_pair_member(pair, span);
+                                const int page = prefix_pair_page(p, w.wb, pair, span);
+                                const int m_end = imin(imax(0, imin(pr.lengths[members[m]], reach_of(pr))), w.we);
+                                if ((page << p.page_shift) >= m_end) continue;
+                                AUDIT(page >= 0 && page < pr.width, "page check entry %d", page);
+                                if (page < 0 || page >= pr.width) continue;
+                                if (pr.table[static_cast<size_t>(members[m]) * pr.width + page] !=
+                                    pr.table[static_cast<size_t>(r.row) * pr.width + page])
+                                    differs[m] = true;
                             }
-                            re = imin(w.we, (window + kWave) << p.page_shift);
-                            for (int s0 = rb & ~(group_tokens - 1); s0 < re; s0 += block * group_tokens) {
-                                auto issue = [&](int t0) {
-                                    if (mfma) mfma_tile<D>(pr, p, buf, w, b, t0, rb, re, window, wave, waves, len);
-                                    else fp32_group<D>(pr, p, buf, w, b, t0, rb, re, window, len);
-                                };
-                                for (int n0 = 0; n0 < ahead; ++n0) issue(s0 + n0 * group_tokens);
-                                for (int c = 0; c < block; ++c) {
-                                    if (s0 + c * group_tokens >= re) break;
-                                    if (c + ahead < block) issue(s0 + (c + ahead) * group_tokens);
+                            shared_members.clear();
+                            for (size_t m = 0; m < members.size(); ++m) {
+                                if (differs[m] && !g_plant_no_check) own.push_back(members[m]);
+                                else shared_members.push_back(members[m]);
+                            }
+                            g_own_passes += own.size();
+                        }
+                        // The kernels' token loop: page-id windows of 64 pages,
+                        // load groups issued `ahead` in blocks of `block`; a
+                        // shared-prefix item runs it once over the first
+                        // member's row for the members that share it, then
+                        // once per member with a row of its own.
+                        auto walk = [&](int row_b, int end, const std::vector<int>& readers) {
+                            int rb = w.wb, re = w.wb;
+                            int win = row_b == r.row ? window : -1;
+                            for (rb = w.wb; rb < end; rb = re) {
+                                if ((rb >> p.page_shift) != win) {
+                                    win = rb >> p.page_shift;
+                                    window_loads(pr, p, buf, row_b, win);
+                                }
+                                re = imin(end, (win + kWave) << p.page_shift);
+                                for (int s0 = rb & ~(group_tokens - 1); s0 < re; s0 += block * group_tokens) {
+                                    auto issue = [&](int t0) {
+                                        if (mfma)
+                                            mfma_tile<D>(pr, p, buf, w, row_b, t0, rb, re, win, wave, waves, len,
+                                                         readers);
+                                        else fp32_group<D>(pr, p, buf, w, row_b, t0, rb, re, win, len);
+                                    };
+                                    for (int n0 = 0; n0 < ahead; ++n0) issue(s0 + n0 * group_tokens);
+                                    for (int c = 0; c < block; ++c) {
+                                        if (s0 + c * group_tokens >= re) break;
+                                        if (c + ahead < block) issue(s0 + (c + ahead) * group_tokens);
+                                    }
                                 }
                             }
-                        }
+                        };
+                        walk(r.row, w.we, members.size() > 1 ? shared_members : members);
+                        for (int s : own)
+                            walk(s, imin(w.we, imax(0, imin(pr.lengths[s], reach_of(pr)))), std::vector<int>{s});
                         if (rows) continue;  // no state stores: the fold below writes out
                         // State stores: one state per live head of the tile;
                         // a combining workgroup's later quarters store the empty
                         // state in their own slots.
                         const int part = split * kQuarters + w.quarter;
                         AUDIT(part >= 0 && part < kQuarters * pr.splits, "state %d", part);
-                        for (int h = 0; h < w.heads_here; ++h) {
+                        // A shared-prefix item stores each member's states,
+                        // for members whose own length reaches the partition.
+                        for (size_t m = 1; m < members.size(); ++m) {
+                            const int member_len = imax(0, imin(pr.lengths[members[m]], reach_of(pr)));
+                            if (static_cast<int64_t>(split) * pr.split_tokens >= member_len) continue;
+                            for (int h = 0; h < w.heads_here; ++h) {
+                                const int64_t row = members[m] * static_cast<int64_t>(pr.q_heads) + row_base + h;
+                                AUDIT(numerator_offset(p, row, part, D) + D <= static_cast<int64_t>(buf.numerator_elems),
+                                      "member numerator store");
+                                AUDIT(stats_offset(p, row, part) + 2 <= static_cast<int64_t>(buf.stats_elems),
+                                      "member stats store");
+                                cov.store(static_cast<uint64_t>(row) * kQuarters * pr.splits + part, row, xcd);
+                            }
+                        }
+                        const int lead_len = imax(0, imin(pr.lengths[b], reach_of(pr)));
+                        const bool lead_stores = members.size() == 1 ||
+                                                 static_cast<int64_t>(split) * pr.split_tokens < lead_len;
+                        for (int h = 0; h < (lead_stores ? w.heads_here : 0); ++h) {
                             const int64_t row = w.q_row + h;
                             AUDIT(numerator_offset(p, row, part, D) + D <= static_cast<int64_t>(buf.numerator_elems),
                                   "numerator store");
@@ -482,6 +586,7 @@ void audit_gt(const Problem& pr, const PartialParams& p, bool mfma, Coverage& co
 bool audit(const Problem& pr, bool rows, PartialParams& p, Coverage& cov) {
     const int before = g_failures;
     const uint64_t checks_before = g_checks;
+    const uint64_t own_before = g_own_passes;
     const bool mfma = pr.q_elem == 2;
     p = params(pr, 256, mfma, rows);
     cov = Coverage(static_cast<uint64_t>(pr.batch) * pr.q_heads * kQuarters * pr.splits,
@@ -489,6 +594,7 @@ bool audit(const Problem& pr, bool rows, PartialParams& p, Coverage& cov) {
     OutCoverage out(static_cast<uint64_t>(pr.batch) * pr.q_heads * pr.head_dim);
     if (pr.head_dim == 64) audit_gt<64>(pr, p, mfma, cov, out);
     else audit_gt<128>(pr, p, mfma, cov, out);
+    if (!mfma || p.row_mode) AUDIT(p.group_items == 0, "shared-prefix items in a %s launch", mfma ? "whole-row" : "fp32");
     if (p.row_mode) {
         AUDIT(mfma_lds_bytes(p, pr.head_dim, pr.kv_elem) <= 160 * 1024, "whole-row LDS");
         for (size_t e = 0; e < out.writes.size(); ++e)
@@ -498,13 +604,15 @@ bool audit(const Problem& pr, bool rows, PartialParams& p, Coverage& cov) {
         if (p.merge_xcd_rows > 0) check_merge_xcd(pr, p, cov);
     }
     const Grid grid = partial_grid(p, pr.kv_heads);
-    std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s%s, %" PRIu64 " checks: %s\n",
+    std::string shared = p.group_items > 0 ? ", " + std::to_string(p.group_items) + " shared-prefix items" : "";
+    if (g_own_passes > own_before) shared += " (" + std::to_string(g_own_passes - own_before) + " own passes)";
+    std::printf("%-44s %s grid %ux%ux%u x %d waves, GT %d, qw %d, %s%s%s%s, %" PRIu64 " checks: %s\n",
                 (pr.name + (rows ? " [call]" : "")).c_str(), mfma ? "mfma" : "fp32", grid.x, grid.y, grid.z,
                 partial_threads(p) / kWave, p.head_tile, p.quarters_per_wg,
                 p.row_mode ? "whole rows" : p.compact ? "compact" : p.main_splits < p.splits ? "rectangular+tails"
                                                                                               : "rectangular",
                 p.combine ? ", combined" : "",
-                p.xcd_shift >= 0 ? ", xcd-grouped" : p.merge_xcd_rows > 0 ? ", xcd merge" : "",
+                p.xcd_shift >= 0 ? ", xcd-grouped" : p.merge_xcd_rows > 0 ? ", xcd merge" : "", shared.c_str(),
                 g_checks - checks_before, g_failures == before ? "ok" : "FAILED");
     std::fflush(stdout);
     return g_failures == before;
@@ -895,6 +1003,34 @@ std::vector<int32_t> ragged(int batch, int hi, uint64_t seed) {
     return v;
 }
 
+// Sequences [first, last) of pr map the first `pages` logical pages of
+// sequence `from` (a shared prefix).
+void share_prefix(Problem& pr, int from, int first, int last, int pages) {
+    for (int b = first; b < last; ++b)
+        for (int i = 0; i < pages; ++i)
+            pr.table[static_cast<size_t>(b) * pr.width + i] = pr.table[static_cast<size_t>(from) * pr.width + i];
+    pr.unshared = false;
+}
+
+// The problem with shared-prefix runs taken from its own table (pd_prefix_runs).
+Problem with_runs(Problem pr) {
+    pr.name += " prefix runs";
+    pr.runs.assign(2 * static_cast<size_t>(pr.batch), 0);
+    prefix_runs_of_table(pr.table.data(), pr.batch, pr.width, pr.runs.data());
+    return pr;
+}
+
+// Runs that claim each sequence's whole row in common with its leader: the
+// description of a table the device no longer holds (a plan refreshed after
+// a graph captured it). Items then reach past the shared pages.
+Problem with_stale_runs(Problem pr) {
+    pr = with_runs(pr);
+    pr.name += " stale";
+    for (int b = 0; b < pr.batch; ++b)
+        if (pr.runs[2 * b] >= 0) pr.runs[2 * b + 1] = pr.width;
+    return pr;
+}
+
 // The same problem with host bounds: exact lengths, half, zero, or none.
 std::vector<Problem> with_bounds(const Problem& base) {
     std::vector<Problem> out{base};
@@ -932,9 +1068,89 @@ int main(int argc, char** argv) {
         pr.unshared = false;
         pr.ragged = true;
         add(pr);
+        add(with_runs(pr));
+        Problem fp8 = pr;
+        fp8.name = "ragged shared B16 T32 split 128 fp8";
+        fp8.kv_elem = 1;
+        add(with_runs(fp8));
         Problem reserved = make("ragged B16 T32 split 128 reserve x4", 16, 32, 8, 128, 32, 1024, ragged(16, 8192, 3),
                                 128, 2, 2, 3, 4);
         add(reserved);
+    }
+    // Shared prefixes of other tile widths, several sharing classes, and more
+    // items than kMaxGroupItems (each with runs from its table).
+    {
+        // MHA: 16 members per item. 24 sequences share 32 pages of sequence 0.
+        std::vector<int32_t> lens(24);
+        Lcg rng{601};
+        for (auto& x : lens) x = 520 + rng.below(1000);
+        lens[0] = 4096;
+        Problem mha = make("prefix mha B24 Hq8/8 D64 T16 split 64", 24, 8, 8, 64, 16, 256, lens, 64, 2, 2, 601);
+        share_prefix(mha, 0, 1, 24, 32);
+        add(with_runs(mha));
+        add(with_stale_runs(mha));
+        // Rows padded with -1 past each length, as plans and workloads hold
+        // them: a short member's run ends at its last page, and items still
+        // read every member's pages from the leader's row (no own passes).
+        Problem padded = mha;
+        padded.name = "prefix padded rows B24 Hq8/8 D64 T16 split 64";
+        for (int b = 0; b < padded.batch; ++b)
+            for (int i = (padded.lengths[b] + 15) / 16; i < padded.width; ++i)
+                padded.table[static_cast<size_t>(b) * padded.width + i] = -1;
+        add(with_runs(padded));
+        Problem padded4 = make("prefix padded rows B32 Hq32/8 D128 T16 split 256", 32, 32, 8, 128, 16, 256, [] {
+            std::vector<int32_t> v(32);
+            Lcg r{611};
+            for (auto& x : v) x = r.below(2049);
+            v[0] = 4096;
+            return v;
+        }(), 256, 2, 2, 611);
+        share_prefix(padded4, 0, 1, 32, 64);
+        for (int b = 0; b < padded4.batch; ++b)
+            for (int i = (padded4.lengths[b] + 15) / 16; i < padded4.width; ++i)
+                padded4.table[static_cast<size_t>(b) * padded4.width + i] = -1;
+        add(with_runs(padded4));
+        // GQA 8 (Hq16/Hkv2): 2 members per item.
+        Problem gqa8 = make("prefix gqa8 B6 Hq16/2 D128 T16 split 64", 6, 16, 2, 128, 16, 128,
+                            {2048, 400, 700, 300, 650, 520}, 64, 2, 2, 603);
+        share_prefix(gqa8, 0, 1, 6, 16);
+        add(with_runs(gqa8));
+        // Two classes; one member diverges early, one shares more than the rest.
+        std::vector<int32_t> two(16);
+        for (int b = 0; b < 16; ++b) two[b] = 600 + 97 * b;
+        two[0] = 8192;
+        Problem classes = make("prefix two classes B16 Hq32/8 D128 T32 split 128", 16, 32, 8, 128, 32, 256, two, 128,
+                               2, 2, 605);
+        share_prefix(classes, 0, 1, 8, 48);
+        share_prefix(classes, 8, 9, 16, 24);
+        share_prefix(classes, 8, 12, 13, 40);
+        for (int i = 10; i < 48; ++i) classes.table[3 * 256 + i] = classes.table[15 * 256 + 200 + i];
+        add(with_runs(classes));
+        add(with_stale_runs(classes));
+        // Members shorter on the device than their host bounds: a length of
+        // 0, one inside a shared partition, one at a partition boundary, and
+        // a shorter first member (whose row the items read).
+        Problem shrunk = with_runs(classes);
+        shrunk.name += " lengths below bounds";
+        shrunk.bounds = classes.lengths;
+        shrunk.lengths[1] = 0;
+        shrunk.lengths[2] = 300;
+        shrunk.lengths[4] = 512;
+        shrunk.lengths[9] = 1000;
+        shrunk.lengths[0] = 700;
+        add(shrunk, false);
+        // 64 sequences sharing 40 partitions of 16 tokens: 160 items before the cap.
+        std::vector<int32_t> many(64);
+        Lcg rng2{607};
+        for (auto& x : many) x = 700 + rng2.below(700);
+        many[0] = 4096;
+        Problem cap = make("prefix cap B64 Hq8/8 D64 T16 split 16", 64, 8, 8, 64, 16, 256, many, 16, 2, 2, 607);
+        share_prefix(cap, 0, 1, 64, 40);
+        add(with_runs(cap));
+        // FP32 inputs take no shared-prefix items.
+        Problem f32 = make("prefix fp32 B24 Hq8/8 D64 T16 split 64", 24, 8, 8, 64, 16, 256, lens, 64, 4, 4, 601);
+        share_prefix(f32, 0, 1, 24, 32);
+        add(with_runs(f32));
     }
     add(make("mqa B128 Hq16/1 D64 L1024", 128, 16, 1, 64, 16, 64, uniform(128, 1024), 256, 2, 2, 4), false);
     add(make("mqa B64 Hq16/1 D64 ragged split 64", 64, 16, 1, 64, 16, 64, ragged(64, 1024, 41), 64, 2, 2, 41));
@@ -1156,6 +1372,18 @@ int main(int argc, char** argv) {
         if (!g_plant_append_capacity) appends.clear();
         if (!g_plant_csr_count) csrs.clear();
     }
+    if (mode == "--plant-prefix") {
+        // Negative control: the stale-runs problems walked as a kernel
+        // without the page check would run them (every member in the shared
+        // pass). The walk must report members reading pages they do not map.
+        g_plant_no_check = true;
+        std::vector<Problem> planted;
+        for (const auto& pr : problems)
+            if (pr.name.find(" prefix runs stale") != std::string::npos) planted.push_back(pr);
+        problems = planted;
+        appends.clear();
+        csrs.clear();
+    }
     if (mode == "--plant-reach") {
         // Negative control: the same problems with launch params that clamp
         // lengths to the table only. The walk must report reads past the
@@ -1210,7 +1438,7 @@ int main(int argc, char** argv) {
     for (const auto& ap : appends) failed += audit_append(ap) ? 0 : 1;
     for (const auto& cp : csrs) failed += audit_csr(cp) ? 0 : 1;
     std::printf("%zu problems, %" PRIu64 " merge launches, %zu appends, %zu csr conversions, %" PRIu64
-                " checks, %d failures\n", problems.size(), g_merge_launches, appends.size(), csrs.size(), g_checks,
-                g_failures);
+                " shared-prefix own passes, %" PRIu64 " checks, %d failures\n", problems.size(), g_merge_launches,
+                appends.size(), csrs.size(), g_own_passes, g_checks, g_failures);
     return failed == 0 ? 0 : 1;
 }

@@ -98,6 +98,27 @@ def test_partition_address_map_stays_in_bounds(audit_exe):
     assert " merge launches, " in summary and " appends, " in summary and " csr conversions, " in summary
     assert any(line.startswith("append") and "append+advance" in line for line in lines)
     assert any(line.startswith("csr list past the indices end") and "1 of 2 rows rejected" in line for line in lines)
+    # Shared-prefix items were walked for every tile width that takes them
+    # (MHA: 16 members, GQA 4: 4, GQA 8: 2), with several sharing classes, at
+    # the item cap, with members shorter on the device than their bounds, and
+    # in the full call's coarser partitions; never without bounds or for FP32.
+    shared = [line for line in launches if "shared-prefix items" in line]
+    for name in ("prefix mha B24 Hq8/8 D64 T16 split 64 prefix runs bounds=exact",
+                 "prefix gqa8 B6 Hq16/2 D128 T16 split 64 prefix runs bounds=exact",
+                 "prefix two classes B16 Hq32/8 D128 T32 split 128 prefix runs bounds=exact",
+                 "prefix two classes B16 Hq32/8 D128 T32 split 128 prefix runs lengths below bounds",
+                 "prefix padded rows B24 Hq8/8 D64 T16 split 64 prefix runs bounds=exact",
+                 "prefix padded rows B32 Hq32/8 D128 T16 split 256 prefix runs bounds=exact"):
+        assert any(line.startswith(name + " ") for line in shared), name
+    assert any(line.startswith("prefix cap ") and ", 128 shared-prefix items" in line for line in shared)
+    # Runs that claim more than the table shares (stale runs) stay correct:
+    # the page check sends the differing members to passes of their own.
+    assert any(" prefix runs stale bounds=exact " in line and " own passes)" in line for line in shared)
+    assert not any(" own passes)" in line for line in shared if " stale " not in line)
+    own_passes = int(summary.split(" shared-prefix own passes")[0].rsplit(", ", 1)[1])
+    assert own_passes > 0, summary
+    assert any("coarse x" in line and "[call]" in line for line in shared)
+    assert not any("bounds=zero" in line or " fp32 " in line for line in shared)
 
 
 @pytest.mark.parametrize("plant,message", [
@@ -105,13 +126,15 @@ def test_partition_address_map_stays_in_bounds(audit_exe):
     ("--plant-merge-live", "that the partition launch did not write"),
     ("--plant-append", "append reads table entry"),
     ("--plant-csr", "indices read 6 of 6"),
+    ("--plant-prefix", "the item reads page"),
 ])
 def test_address_audit_flags_planted_mistakes(audit_exe, plant, message):
     """Negative controls: launch parameters with one mistake planted (lengths
     clamped to the table instead of the caller's partitions; a merge live
     count one partition too long; an append capacity one page past the table;
-    a CSR conversion without its bound on the indices read). Each walk must
-    report the accesses the mistake causes."""
+    a CSR conversion without its bound on the indices read; shared-prefix
+    items that trust stale runs, without the kernel's page check). Each walk
+    must report the accesses the mistake causes."""
     run = subprocess.run([str(audit_exe), plant], capture_output=True, text=True, timeout=300, env=ENV)
     assert run.returncode == 1, run.stdout[-4000:] + run.stderr[-4000:]
     assert "FAIL" in run.stderr and message in run.stderr

@@ -83,7 +83,7 @@ def test_library_exports_every_declared_symbol():
     lib = cabi.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.pd_abi_version() == cabi.PD_ABI_VERSION == 15
+    assert lib.pd_abi_version() == cabi.PD_ABI_VERSION == 16
     assert re.search(r"#define\s+PD_ABI_VERSION\s+(\d+)", HEADER.read_text()).group(1) == str(cabi.PD_ABI_VERSION)
     assert lib.pd_workspace_bytes(4, 32, 128, 16) == 4_259_840  # reference docs/DESIGN.md:76
     assert lib.pd_workspace_bytes(0, 32, 128, 16) == 0
@@ -185,7 +185,7 @@ C_CONSUMER = r"""
 #include "paged_decode.h"
 
 int main(void) {
-    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 15) return 1;
+    if (pd_abi_version() != PD_ABI_VERSION || PD_ABI_VERSION != 16) return 1;
     if (pd_workspace_bytes(4, 32, 128, 16) != 4259840u) return 2;
     /* Rejected before any launch: no device is touched. */
     if (pd_decode(NULL, NULL, NULL, PD_DTYPE_F16, NULL, NULL, NULL, NULL, NULL,
@@ -526,3 +526,68 @@ def test_launch_plan_query_agrees_with_the_other_queries():
     assert llama["merge_kernel"] == 1 and llama["merge_xcd_grouped"] == 1 and llama["merge_chunk_floats"] == 32
     with pytest.raises(ValueError):
         cabi.launch_plan(lib, f16, f16, 4, 32, 8, 96, 16, 256, 1024, 16, 256)
+
+
+def test_prefix_runs_of_a_host_table():
+    """pd_prefix_runs: each sequence's leader is the first sequence whose row
+    starts with the same page (-1 when its first entry is not a page) and its
+    run the leading entries it has in common with the leader's row, up to the
+    first difference or negative entry. A hand-worked table, then random tables
+    with shared prefixes against a brute-force longest common prefix."""
+    lib = cabi.load()
+    table = np.array([[5, 6, 7, 8], [5, 6, 9, 10], [1, 2, 3, 4], [5, 6, 7, -1], [-1, -1, -1, -1], [1, 2, 3, 0],
+                      [5, 6, 7, 8]], dtype=np.int32)
+    assert cabi.prefix_runs(lib, table).tolist() == [0, 4, 0, 2, 2, 4, 0, 3, -1, 0, 2, 3, 0, 4]
+    rng = np.random.default_rng(5)
+    for _ in range(50):
+        batch, width = int(rng.integers(1, 20)), int(rng.integers(1, 40))
+        table = rng.integers(-1, 6, size=(batch, width)).astype(np.int32)
+        for b in range(1, batch):  # some rows copy a prefix of an earlier one
+            if rng.random() < 0.6:
+                src, n = int(rng.integers(0, b)), int(rng.integers(0, width + 1))
+                table[b, :n] = table[src, :n]
+        runs = cabi.prefix_runs(lib, table)
+        for b in range(batch):
+            leader, run = int(runs[2 * b]), int(runs[2 * b + 1])
+            if table[b, 0] < 0:
+                assert (leader, run) == (-1, 0)
+                continue
+            assert leader == next(c for c in range(b + 1) if table[c, 0] == table[b, 0])
+            lcp = 0
+            while lcp < width and table[b, lcp] >= 0 and table[b, lcp] == table[leader, lcp]:
+                lcp += 1
+            assert run == lcp
+
+
+def test_shared_prefix_items_in_the_launch_plan():
+    """With prefix runs and host bounds, the work list of the ragged + shared
+    prefix workload scores its shared partitions for several sequences at once
+    (fewer workgroups, shared_prefix_items > 0). Without bounds, with FP32
+    inputs or with unshared rows there are none; malformed runs are refused
+    with PD_ERR_PREFIX."""
+    from paged_decode.workload import make_workload
+
+    lib = cabi.load()
+    w = make_workload("ragged_shared_b16")
+    L = w.layout
+    runs = cabi.prefix_runs(lib, w.table)
+    splits = -(-int(w.lengths.max()) // w.split_tokens)
+    shape = (L.batch, L.query_heads, L.kv_heads, L.head_dim, L.page_size, w.table.shape[1], L.physical_pages, splits,
+             w.split_tokens)
+    f16, f32 = cabi.PD_DTYPE_F16, cabi.PD_DTYPE_F32
+    args = (cabi.PD_MERGE_SERIAL, cabi.PD_HINT_RAGGED_LENGTHS, w.lengths)
+    grouped = cabi.launch_plan(lib, f16, f16, *shape, *args, 256, runs)
+    plain = cabi.launch_plan(lib, f16, f16, *shape, *args, 256)
+    assert plain["shared_prefix_items"] == 0 and plain["grid_kind"] == 2
+    assert 0 < grouped["shared_prefix_items"] <= 128 and grouped["grid_kind"] == 2
+    assert grouped["grid_x"] < plain["grid_x"] and grouped["kernel_split_tokens"] == plain["kernel_split_tokens"]
+    assert cabi.launch_plan(lib, f16, f16, *shape, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_RAGGED_LENGTHS, None, 256,
+                            runs)["shared_prefix_items"] == 0
+    assert cabi.launch_plan(lib, f32, f32, *shape, *args, 256, runs)["shared_prefix_items"] == 0
+    private = np.array([[b, 0] for b in range(L.batch)], dtype=np.int32).reshape(-1)
+    assert cabi.launch_plan(lib, f16, f16, *shape, *args, 256, private)["shared_prefix_items"] == 0
+    for bad in ([L.batch, 1], [-2, 1], [0, w.table.shape[1] + 1], [0, -1]):
+        broken = runs.copy()
+        broken[2:4] = bad
+        with pytest.raises(ValueError, match="shared-prefix runs"):
+            cabi.launch_plan(lib, f16, f16, *shape, *args, 256, broken)
