@@ -570,6 +570,34 @@ inline int tail_span_for(int reserved) {
     return imax(kTailSpan, (reserved + kMaxTailItems - 1) / kMaxTailItems);
 }
 
+// Partitions of sequence b the host bound reaches (at most splits).
+inline int bounded_partitions(const PartialParams& prm, const int32_t* length_bounds, int b) {
+    const int64_t bound = lmin(prm.reach, length_bounds[b] < 0 ? 0 : length_bounds[b]);
+    return static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
+}
+
+// The work list (compact) under host bounds: sequence b's main items are the
+// partitions its bound reaches, its tail items span the rest (plan_items).
+inline void make_work_list(PartialParams& prm, const int32_t* length_bounds) {
+    int shortest = prm.splits;
+    for (int b = 0; b < prm.batch; ++b) shortest = imin(shortest, bounded_partitions(prm, length_bounds, b));
+    prm.tail_span = tail_span_for(prm.splits - shortest);
+    int mains = 0, tails = 0;
+    for (int b = 0; b < prm.batch; ++b) {
+        const int live = bounded_partitions(prm, length_bounds, b);
+        prm.main_first[b] = mains;
+        prm.tail_first[b] = tails;
+        mains += live;
+        tails += (prm.splits - live + prm.tail_span - 1) / prm.tail_span;
+    }
+    prm.main_first[prm.batch] = mains;
+    prm.tail_first[prm.batch] = tails;
+    prm.compact = 1;
+    prm.items = mains + tails;
+    prm.main_splits = prm.splits;
+    prm.tail_shift = 0;
+}
+
 inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.xcd_shift = -1;  // plain grid until plan_xcd, once the workgroup shape is known
     prm.compact = 0;
@@ -586,10 +614,7 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.live_items = prm.items;
     prm.uniform_live = 0;
     if (length_bounds == nullptr) return;
-    auto live_of = [&](int b) {
-        const int64_t bound = lmin(prm.reach, length_bounds[b] < 0 ? 0 : length_bounds[b]);
-        return static_cast<int>(lmin((bound + prm.split_tokens - 1) / prm.split_tokens, prm.splits));
-    };
+    auto live_of = [&](int b) { return bounded_partitions(prm, length_bounds, b); };
     int64_t live_total = 0;
     int longest = 1;
     int fewest = prm.splits;
@@ -603,23 +628,7 @@ inline void plan_items(PartialParams& prm, const int32_t* length_bounds) {
     prm.shape_splits = longest;
     prm.live_items = static_cast<int>(lmin(live_total > 0 ? live_total : 1, prm.items));
     if (prm.batch <= kCompactMaxBatch && live_total * 2 <= static_cast<int64_t>(prm.batch) * longest) {
-        // Very ragged: the work list.
-        int shortest = prm.splits;
-        for (int b = 0; b < prm.batch; ++b) shortest = imin(shortest, live_of(b));
-        prm.tail_span = tail_span_for(prm.splits - shortest);
-        int mains[kCompactMaxBatch + 1], tails[kCompactMaxBatch + 1];
-        mains[0] = tails[0] = 0;
-        for (int b = 0; b < prm.batch; ++b) {
-            const int live = live_of(b);
-            mains[b + 1] = mains[b] + live;
-            tails[b + 1] = tails[b] + (prm.splits - live + prm.tail_span - 1) / prm.tail_span;
-        }
-        prm.compact = 1;
-        prm.items = mains[prm.batch] + tails[prm.batch];
-        for (int b = 0; b <= prm.batch; ++b) {
-            prm.main_first[b] = mains[b];
-            prm.tail_first[b] = tails[b];
-        }
+        make_work_list(prm, length_bounds);  // very ragged
         return;
     }
     if (longest >= prm.splits) return;
@@ -730,6 +739,104 @@ inline bool rows_fit_one_launch(int64_t splits, int64_t split_tokens, int64_t ca
     return span * head_dim * elem * 2 <= kRowMaxBytes;
 }
 
+// The grouping itself, as plain host arithmetic on the runs and bounds (so
+// that coarse_split can count the waves it leaves): the items (partition <<
+// 16 | first slot << 8 | members), their leader rows, the member order, each
+// sequence's shared leading partitions (skip), and the member-partitions the
+// items score (covered).
+struct PrefixGrouping {
+    int items;
+    int64_t covered;
+    uint32_t item[kMaxGroupItems];
+    int8_t row[kMaxGroupItems];
+    int8_t order[kCompactMaxBatch];
+    int skip[kCompactMaxBatch];
+};
+
+inline void group_prefixes(PrefixGrouping& g, const int32_t* runs, const int32_t* bounds, int batch, int64_t reach,
+                           int split_tokens, int splits, int page_shift, int slots) {
+    g.items = 0;
+    g.covered = 0;
+    for (int b = 0; b < kCompactMaxBatch; ++b) {
+        g.skip[b] = 0;
+        g.order[b] = 0;
+    }
+    if (runs == nullptr || bounds == nullptr || batch > kCompactMaxBatch || slots < 2) return;
+    int lead[kCompactMaxBatch];
+    for (int b = 0; b < batch; ++b) {
+        const int leader = runs[2 * b];
+        const int64_t shared = static_cast<int64_t>(runs[2 * b + 1]) << page_shift;
+        const int64_t bound = lmin(reach, bounds[b] < 0 ? 0 : bounds[b]);
+        const int64_t live = lmin((bound + split_tokens - 1) / split_tokens, splits);
+        const int64_t parts = bound <= shared ? live : shared / split_tokens;
+        lead[b] = leader < 0 || leader >= batch ? 0 : static_cast<int>(lmin(parts, live));
+    }
+    bool placed[kCompactMaxBatch] = {};
+    int order = 0;
+    bool capped = false;
+    for (int b0 = 0; b0 < batch && !capped; ++b0) {
+        if (placed[b0] || lead[b0] < 1) continue;
+        // The class of b0's leader, sorted by lead (descending), then sequence.
+        int members[kCompactMaxBatch];
+        int n = 0;
+        for (int b = b0; b < batch; ++b) {
+            if (placed[b] || lead[b] < 1 || runs[2 * b] != runs[2 * b0]) continue;
+            placed[b] = true;
+            int k = n++;
+            while (k > 0 && lead[members[k - 1]] < lead[b]) {
+                members[k] = members[k - 1];
+                --k;
+            }
+            members[k] = b;
+        }
+        if (n < 2) continue;
+        const int start = order;
+        for (int k = 0; k < n; ++k) g.order[order++] = static_cast<int8_t>(members[k]);
+        for (int j = 0; j < lead[members[0]] && !capped; ++j) {
+            int covering = 0;
+            while (covering < n && lead[members[covering]] > j) ++covering;
+            for (int c = 0; c + 1 < covering && !capped; c += slots) {  // chunks of two or more
+                const int size = imin(slots, covering - c);
+                if (g.items == kMaxGroupItems) {
+                    capped = true;
+                    break;
+                }
+                g.row[g.items] = static_cast<int8_t>(runs[2 * b0]);
+                g.item[g.items++] = (static_cast<uint32_t>(j) << 16) | (static_cast<uint32_t>(start + c) << 8) |
+                                    static_cast<uint32_t>(size);
+                g.covered += size;
+                for (int k = c; k < c + size; ++k) g.skip[members[k]] = j + 1;
+            }
+        }
+    }
+}
+
+// Tile slots for shared-prefix members of a matrix-core launch: 16 / GT
+// when a KV head's query heads fit one tile, else 1 (no grouping).
+inline int prefix_slots(int group) {
+    const int gt = head_tile(group, 16);
+    return gt >= group ? 16 / gt : 1;
+}
+
+// Whether a rectangular grid (lengths not ragged enough for a work list) of
+// `live` items should run shared-prefix items: when grouping removes at least
+// 1 / kPrefixListShare of the items and the remaining ones still give
+// kCoarseWavesPerCu waves per CU (the grid then becomes a work list). Work
+// lists always form the items. Measured on MI355X (decode call, us, graph of
+// 200 calls; with runs / without, equal lengths and a shared prompt): B16
+// L4096 50% shared over 512-token partitions 35.7 / 38.9, but over the 1024
+// tokens the coarse split picks for it (5 waves per CU once grouped) 41.9,
+// and B4 L4096 50% (5 waves per CU) 19.2-19.6 / 16.3. coarse_split does not
+// count the items, so those grids keep their rectangular grid; choosing a
+// finer split for them together with the grouping is not built.
+constexpr int kPrefixListShare = 8;
+constexpr int kCoarseWavesPerCu = 8;  // waves per CU a grid keeps (coarse_split)
+
+inline bool rect_prefix_items_pay(int64_t live, int64_t saved, int64_t waves_per_item, int cus) {
+    return saved > 0 && saved * kPrefixListShare >= live &&
+           (live - saved) * waves_per_item >= static_cast<int64_t>(kCoarseWavesPerCu) * cus;
+}
+
 // Coarser partitions for a whole decode call on a large grid. The caller's
 // split_tokens sizes the workspace (four states per partition) and is what
 // the separate partition and merge entries use; a whole call (partition
@@ -764,7 +871,6 @@ inline bool rows_fit_one_launch(int64_t splits, int64_t split_tokens, int64_t ca
 // L1024 20.2 -> 25.0, FP16 B6 L4096 22.6 -> 23.0), so the rule stops at eight.
 // Whole-row calls and FP32 inputs keep the caller's split.
 constexpr int64_t kCoarseWaveBytes = 128 * 1024;
-constexpr int kCoarseWavesPerCu = 8;
 
 struct KernelSplit {
     int splits, split_tokens;
@@ -777,20 +883,25 @@ inline KernelSplit coarse_split(int batch, int kv_heads, int head_tiles, int hea
     const int64_t capacity = static_cast<int64_t>(table_width) * page_size;
     // Tokens the caller's partitions reach; no partition of a coarser split goes past them.
     const int64_t reach = lmin(static_cast<int64_t>(splits) * split_tokens, capacity);
-    auto waves = [&](int64_t span) {
+    // Whether partitions of `span` tokens leave enough waves per CU. Shared-
+    // prefix items are not counted: measured with them, the ragged + shared
+    // B16 workload ran 27.2 us per staged call at the 512-token partitions
+    // this count picks and 32.5 us at 256 tokens, where counting the items'
+    // waves against 8 per CU would have stopped.
+    auto enough = [&](int64_t span) {
         int64_t parts = 0;
         for (int b = 0; b < batch; ++b) {
             const int64_t bound = lmin(reach, length_bounds[b] < 0 ? 0 : length_bounds[b]);
             parts += (bound + span - 1) / span;
         }
-        return parts * kQuarters * kv_heads * head_tiles;
+        return parts * kQuarters * kv_heads * head_tiles >= static_cast<int64_t>(kCoarseWavesPerCu) * cus;
     };
     int c = 1;
     while (2 * c <= splits) {
         const int64_t span = static_cast<int64_t>(split_tokens) * 2 * c;
         if (span > (int64_t{1} << 20)) break;
         if ((span + kQuarters - 1) / kQuarters * head_dim * elem * 2 > kCoarseWaveBytes) break;
-        if (waves(span) < static_cast<int64_t>(kCoarseWavesPerCu) * cus) break;
+        if (!enough(span)) break;
         c *= 2;
     }
     return KernelSplit{(splits + c - 1) / c, split_tokens * c};
@@ -914,68 +1025,42 @@ inline bool prefix_runs_valid(const int32_t* runs, int batch, int width) {
 inline void plan_prefix_items(PartialParams& prm, int slots) {
     prm.group_items = 0;
     for (int b = 0; b < kCompactMaxBatch; ++b) prm.main_skip[b] = 0;
-    const int32_t* runs = prm.host_prefix_runs;
-    const int32_t* bounds = prm.host_bounds;
-    if (!prm.compact || prm.row_mode || runs == nullptr || bounds == nullptr || slots < 2) return;
-    const int batch = prm.batch;
-    int lead[kCompactMaxBatch], live[kCompactMaxBatch], skip[kCompactMaxBatch];
-    for (int b = 0; b < batch; ++b) {
-        live[b] = prm.main_first[b + 1] - prm.main_first[b];
-        skip[b] = 0;
-        const int leader = runs[2 * b];
-        const int64_t shared = static_cast<int64_t>(runs[2 * b + 1]) << prm.page_shift;
-        const int64_t bound = lmin(prm.reach, bounds[b] < 0 ? 0 : bounds[b]);
-        const int64_t parts = bound <= shared ? (bound + prm.split_tokens - 1) / prm.split_tokens
-                                              : shared / prm.split_tokens;
-        lead[b] = leader < 0 || leader >= batch ? 0 : static_cast<int>(lmin(parts, live[b]));
+    if (!prm.compact || prm.row_mode) return;
+    PrefixGrouping g;
+    group_prefixes(g, prm.host_prefix_runs, prm.host_bounds, prm.batch, prm.reach, prm.split_tokens, prm.splits,
+                   prm.page_shift, slots);
+    if (g.items == 0) return;
+    prm.group_items = g.items;
+    for (int i = 0; i < g.items; ++i) {
+        prm.group_item[i] = g.item[i];
+        prm.group_row[i] = g.row[i];
     }
-    bool placed[kCompactMaxBatch] = {};
-    int order = 0;
-    bool capped = false;
-    for (int b0 = 0; b0 < batch && !capped; ++b0) {
-        if (placed[b0] || lead[b0] < 1) continue;
-        // The class of b0's leader, sorted by lead (descending), then sequence.
-        int members[kCompactMaxBatch];
-        int n = 0;
-        for (int b = b0; b < batch; ++b) {
-            if (placed[b] || lead[b] < 1 || runs[2 * b] != runs[2 * b0]) continue;
-            placed[b] = true;
-            int k = n++;
-            while (k > 0 && lead[members[k - 1]] < lead[b]) {
-                members[k] = members[k - 1];
-                --k;
-            }
-            members[k] = b;
-        }
-        if (n < 2) continue;
-        const int start = order;
-        for (int k = 0; k < n; ++k) prm.prefix_order[order++] = static_cast<int8_t>(members[k]);
-        for (int j = 0; j < lead[members[0]] && !capped; ++j) {
-            int covering = 0;
-            while (covering < n && lead[members[covering]] > j) ++covering;
-            for (int c = 0; c + 1 < covering && !capped; c += slots) {  // chunks of two or more
-                const int size = imin(slots, covering - c);
-                if (prm.group_items == kMaxGroupItems) {
-                    capped = true;
-                    break;
-                }
-                prm.group_row[prm.group_items] = static_cast<int8_t>(runs[2 * b0]);
-                prm.group_item[prm.group_items++] = (static_cast<uint32_t>(j) << 16) |
-                                                    (static_cast<uint32_t>(start + c) << 8) |
-                                                    static_cast<uint32_t>(size);
-                for (int k = c; k < c + size; ++k) skip[members[k]] = j + 1;
-            }
-        }
-    }
-    if (prm.group_items == 0) return;
     int mains = 0;
-    for (int b = 0; b < batch; ++b) {
+    for (int b = 0; b < prm.batch; ++b) {
+        const int live = prm.main_first[b + 1] - prm.main_first[b];
+        prm.prefix_order[b] = g.order[b];
         prm.main_first[b] = mains;
-        prm.main_skip[b] = static_cast<int16_t>(skip[b]);
-        mains += live[b] - skip[b];
+        prm.main_skip[b] = static_cast<int16_t>(g.skip[b]);
+        mains += live - g.skip[b];
     }
-    prm.main_first[batch] = mains;
-    prm.items = prm.group_items + mains + prm.tail_first[batch];
+    prm.main_first[prm.batch] = mains;
+    prm.items = prm.group_items + mains + prm.tail_first[prm.batch];
+}
+
+// A rectangular grid whose shared-prefix items pay (rect_prefix_items_pay)
+// becomes a work list; plan_prefix_items then forms them.
+inline void prefer_work_list_for_prefixes(PartialParams& prm, int kv_heads, int slots, int cus) {
+    if (prm.compact || prm.host_prefix_runs == nullptr || prm.host_bounds == nullptr ||
+        prm.batch > kCompactMaxBatch || slots < 2)
+        return;
+    PrefixGrouping g;
+    group_prefixes(g, prm.host_prefix_runs, prm.host_bounds, prm.batch, prm.reach, prm.split_tokens, prm.splits,
+                   prm.page_shift, slots);
+    int64_t live = 0;
+    for (int b = 0; b < prm.batch; ++b) live += bounded_partitions(prm, prm.host_bounds, b);
+    if (rect_prefix_items_pay(live, g.covered - g.items, static_cast<int64_t>(kQuarters) * kv_heads * prm.head_tiles,
+                              cus))
+        make_work_list(prm, prm.host_bounds);
 }
 
 // The XCD-grouped grid (block_coords) for a rectangular launch whose row
@@ -1054,6 +1139,7 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
     const int gt = head_tile(prm.group, 16);
     prm.head_tile = gt;
     prm.head_tiles = (prm.group + gt - 1) / gt;
+    prefer_work_list_for_prefixes(prm, kv_heads, prefix_slots(prm.group), cus);
     choose_workgroup(prm, kv_heads, kMfmaWorkgroupHeads);
     // A grid of at most half as many 8-wave workgroups as CUs leaves most CUs
     // idle, and each busy CU can keep only so many loads in flight. The same
@@ -1189,7 +1275,7 @@ inline void plan_mfma(PartialParams& prm, int kv_heads, int cus, int head_dim, i
         prm.combine = prm.quarters_per_wg == 4;
     }
     plan_rows(prm, head_dim, elem, combine_slot_bytes(head_dim), mfma_stage_bytes(head_dim, elem));
-    plan_prefix_items(prm, prm.head_tiles == 1 ? 16 / gt : 1);
+    plan_prefix_items(prm, prefix_slots(prm.group));
     plan_xcd(prm, kv_heads);
     // Where the merge reads its states from the XCD's L2 (plan_xcd), the fold
     // of the mid-size grids' two quarters no longer pays for its tail: their

@@ -151,6 +151,15 @@ PREFIX = [
          {"shared_prefix": 0.25}),
         ("gqa8 skewed B16 Hq32/4 L4096 25% shared", (16, 32, 4, 128, 16, "skewed:4096", 256),
          {"shared_prefix": 0.25}),
+        # Several samples of one prompt (equal lengths): a rectangular grid that
+        # becomes a work list when the items remove enough of it.
+        ("samples B16 L4096 50% shared", (16, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.5}),
+        ("samples B16 L4096 25% shared", (16, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.25}),
+        ("samples B16 L4096 12.5% shared", (16, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.125}),
+        ("samples B8 L8192 50% shared", (8, 32, 8, 128, 16, "uniform:8192", 256), {"shared_prefix": 0.5}),
+        ("samples B32 L2048 50% shared", (32, 32, 8, 128, 16, "uniform:2048", 256), {"shared_prefix": 0.5}),
+        ("samples B32 L4096 50% shared", (32, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.5}),
+        ("samples B4 L4096 50% shared", (4, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.5}),
     ]
     for runs in (True, False)
 ]

@@ -1147,6 +1147,17 @@ int main(int argc, char** argv) {
         Problem cap = make("prefix cap B64 Hq8/8 D64 T16 split 16", 64, 8, 8, 64, 16, 256, many, 16, 2, 2, 607);
         share_prefix(cap, 0, 1, 64, 40);
         add(with_runs(cap));
+        // Equal lengths (a rectangular grid) with a shared prompt: several
+        // samples of one prompt. The grid becomes a work list when the items
+        // remove enough of it (prefer_work_list_for_prefixes).
+        Problem samples = make("prefix samples B16 Hq32/8 D128 T16 L4096 split 256", 16, 32, 8, 128, 16, 256,
+                               uniform(16, 4096), 256, 2, 2, 613);
+        share_prefix(samples, 0, 1, 16, 128);
+        add(with_runs(samples));
+        Problem few = make("prefix samples B8 Hq32/8 D128 T16 L4096 split 256 6% shared", 8, 32, 8, 128, 16, 256,
+                           uniform(8, 4096), 256, 2, 2, 617);
+        share_prefix(few, 0, 1, 8, 16);
+        add(with_runs(few));
         // FP32 inputs take no shared-prefix items.
         Problem f32 = make("prefix fp32 B24 Hq8/8 D64 T16 split 64", 24, 8, 8, 64, 16, 256, lens, 64, 4, 4, 601);
         share_prefix(f32, 0, 1, 24, 32);

@@ -108,13 +108,17 @@ def test_partition_address_map_stays_in_bounds(audit_exe):
                  "prefix two classes B16 Hq32/8 D128 T32 split 128 prefix runs bounds=exact",
                  "prefix two classes B16 Hq32/8 D128 T32 split 128 prefix runs lengths below bounds",
                  "prefix padded rows B24 Hq8/8 D64 T16 split 64 prefix runs bounds=exact",
-                 "prefix padded rows B32 Hq32/8 D128 T16 split 256 prefix runs bounds=exact"):
+                 "prefix padded rows B32 Hq32/8 D128 T16 split 256 prefix runs bounds=exact",
+                 "prefix samples B16 Hq32/8 D128 T16 L4096 split 256 prefix runs bounds=exact"):
         assert any(line.startswith(name + " ") for line in shared), name
     assert any(line.startswith("prefix cap ") and ", 128 shared-prefix items" in line for line in shared)
     # Runs that claim more than the table shares (stale runs) stay correct:
     # the page check sends the differing members to passes of their own.
     assert any(" prefix runs stale bounds=exact " in line and " own passes)" in line for line in shared)
-    assert not any(" own passes)" in line for line in shared if " stale " not in line)
+    assert not any(" own passes)" in line for line in shared if " stale " not in line and "bounds=half" not in line)
+    # Equal lengths with a shared prompt: the rectangular grid became a work list.
+    assert any(line.startswith("prefix samples B16 Hq32/8 D128 T16 L4096 split 256 prefix runs bounds=exact ")
+               and " compact," in line for line in shared)
     own_passes = int(summary.split(" shared-prefix own passes")[0].rsplit(", ", 1)[1])
     assert own_passes > 0, summary
     assert any("coarse x" in line and "[call]" in line for line in shared)

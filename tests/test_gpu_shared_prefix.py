@@ -84,11 +84,16 @@ def case(name):
         table = shared_table(rng, 16, 256, [(0, range(1, 8), 48), (8, range(9, 16), 24), (8, [12], 40)])
         table[3, 10:48] = rng.permutation(np.arange(16 * 256, 17 * 256))[:38]  # diverges after 10 pages
         return Layout(16, 32, 8, 128, 32, 17 * 256), padded(table, lengths, 32), lengths, 128, torch.float16, None
+    if name == "samples B32 L4096 50% shared (equal lengths)":
+        lengths = np.full(32, 4096, dtype=np.int32)
+        table = shared_table(rng, 32, 256, [(0, range(1, 32), 128)])
+        return Layout(32, 32, 8, 128, 16, 32 * 256), table, lengths, 256, torch.float16, None
     raise KeyError(name)
 
 
 CASES = ["workload ragged+shared B16 GQA4 page 32", "mha B24 D64 (16 members per item)",
-         "gqa8 B6 bf16 (2 members per item)", "gqa4 B16 fp8 e4m3 K/V", "two classes B16 GQA4"]
+         "gqa8 B6 bf16 (2 members per item)", "gqa4 B16 fp8 e4m3 K/V", "two classes B16 GQA4",
+         "samples B32 L4096 50% shared (equal lengths)"]
 
 
 @pytest.mark.parametrize("name", CASES)
