@@ -182,7 +182,11 @@ int pd_decode_partial_ex(const void* q, int q_dtype, const void* k, const void* 
  * sequences, F16 or BF16 q, GQA groups of up to 8) scores each partition
  * that lies inside the common prefix of several sequences once for up to
  * 16 / GT of them (GT: the GQA group padded to a power of two), reading its
- * K and V once instead of once per sequence. The runs are a promise about the
+ * K and V once instead of once per sequence. A rectangular grid (lengths
+ * close to equal) becomes such a work list where the items remove enough of
+ * it and the rest still fill the device; a full call may then run over half
+ * the partition span it takes without runs (pd_decode_kernel_split), where
+ * only the finer span lets the items pay. The runs are a promise about the
  * device table: on the leading entries they cover, the rows of one leader's
  * sequences must hold the same page ids, or those sequences get wrong
  * results (runs computed from the table uploaded to the device keep it).
@@ -355,7 +359,10 @@ int pd_decode_launch_count(int q_dtype, int kv_dtype, int batch, int query_heads
  * partitions they reach set the waves per CU), never for whole-row calls or
  * FP32 inputs. A caller that runs the stages itself (pd_decode_partial_ex, then
  * pd_decode_merge) passes these two values to both to match the full call's
- * partitioning. Returns a status (the checks of pd_decode_ex). No
+ * partitioning. These are the partitions of a call without prefix runs: with
+ * runs, pd_decode_prefix may run over c / 2 where its shared-prefix items pay
+ * only there (pd_decode_launch_plan reports the split it takes). Returns a
+ * status (the checks of pd_decode_ex). No
  * counterpart in the reference, whose partition count is the caller's
  * (decode.cu:170-194).
  */

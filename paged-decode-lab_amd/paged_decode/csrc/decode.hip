@@ -718,9 +718,9 @@ float* scratch_address() {
 // split for FP32 inputs and whole-row calls, else coarse_split's.
 KernelSplit call_split(int q_dtype, int kv_dtype, int batch, int query_heads, int kv_heads, int head_dim,
                        int page_size, int table_width, int splits, int split_tokens, const int32_t* length_bounds,
-                       int cus) {
+                       int cus, const int32_t* prefix_runs = nullptr) {
     return full_call_split(q_dtype == PD_DTYPE_F32, element_size(kv_dtype), batch, query_heads, kv_heads, head_dim,
-                           page_size, table_width, splits, split_tokens, length_bounds, cus);
+                           page_size, table_width, splits, split_tokens, length_bounds, cus, prefix_runs);
 }
 
 // The scratch holds numerator [B, Hq, 4 * splits, D] at offset 0 and stats
@@ -799,7 +799,8 @@ int pd_decode_prefix(const void* q, int q_dtype, const void* k, const void* v, i
     // per row, so the states fit the caller's workspace, and read no token
     // past the caller's partitions (reach).
     const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
-                                      table_width, splits, split_tokens, length_bounds, device_compute_units());
+                                      table_width, splits, split_tokens, length_bounds, device_compute_units(),
+                                      prefix_runs);
     const int reach = call_reach(splits, split_tokens, table_width, page_size);
     int stride = 1, xcd_rows = 0, xcd_shift = 0;
     status = run_partial(q, q_dtype, k, v, kv_dtype, k_scale, v_scale, table, lengths, numerator, stats, batch,
@@ -992,7 +993,7 @@ int pd_decode_launch_plan(int q_dtype, int kv_dtype, int batch, int query_heads,
     const int cus = compute_units > 0 ? compute_units : device_compute_units();
     // The planning of pd_decode_ex, without its launches.
     const KernelSplit ks = call_split(q_dtype, kv_dtype, batch, query_heads, kv_heads, head_dim, page_size,
-                                      table_width, splits, split_tokens, length_bounds, cus);
+                                      table_width, splits, split_tokens, length_bounds, cus, prefix_runs);
     const int reach = call_reach(splits, split_tokens, table_width, page_size);
     PartialParams prm = partial_params(nullptr, nullptr, nullptr, kv_dtype, 1.0f, 1.0f, nullptr, nullptr, nullptr,
                                        nullptr, f_stand_in, batch, query_heads, kv_heads, head_dim, page_size,

@@ -827,14 +827,67 @@ inline int prefix_slots(int group) {
 // L4096 50% shared over 512-token partitions 35.7 / 38.9, but over the 1024
 // tokens the coarse split picks for it (5 waves per CU once grouped) 41.9,
 // and B4 L4096 50% (5 waves per CU) 19.2-19.6 / 16.3. coarse_split does not
-// count the items, so those grids keep their rectangular grid; choosing a
-// finer split for them together with the grouping is not built.
+// count the items; it halves its span instead where they pay only at the
+// finer one (prefix_finer_split).
 constexpr int kPrefixListShare = 8;
 constexpr int kCoarseWavesPerCu = 8;  // waves per CU a grid keeps (coarse_split)
 
 inline bool rect_prefix_items_pay(int64_t live, int64_t saved, int64_t waves_per_item, int cus) {
     return saved > 0 && saved * kPrefixListShare >= live &&
            (live - saved) * waves_per_item >= static_cast<int64_t>(kCoarseWavesPerCu) * cus;
+}
+
+// The partitions of a grid over partitions of `span` tokens: the live ones
+// the bounds reach, those its shared-prefix items save (members scored by
+// an item, less the items), and whether the lengths are ragged enough for a
+// work list (plan_items), which forms the items whether or not they pay.
+struct PrefixSaving {
+    int64_t live, saved;
+    bool work_list;
+};
+
+inline PrefixSaving prefix_saving(const int32_t* runs, const int32_t* bounds, int batch, int64_t reach,
+                                  int64_t span, int splits, int page_shift, int slots) {
+    PrefixSaving s{0, 0, false};
+    int64_t longest = 1;
+    for (int b = 0; b < batch; ++b) {
+        const int64_t bound = lmin(reach, bounds[b] < 0 ? 0 : bounds[b]);
+        const int64_t live = lmin((bound + span - 1) / span, splits);
+        s.live += live;
+        longest = live > longest ? live : longest;
+    }
+    s.work_list = batch <= kCompactMaxBatch && s.live * 2 <= static_cast<int64_t>(batch) * longest;
+    PrefixGrouping g;
+    group_prefixes(g, runs, bounds, batch, reach, static_cast<int>(span), splits, page_shift, slots);
+    s.saved = g.covered - g.items;
+    return s;
+}
+
+// A rectangular grid at coarse_split's factor c whose shared-prefix items do
+// not pay (rect_prefix_items_pay), while at c / 2 they save at least
+// 1 / kPrefixFinerShare of the partitions and pay, runs at c / 2 with them.
+// Measured on MI355X (graph of 200 calls, K/V rotated over 2 GiB, equal
+// lengths, 8 KV heads, GQA 4, page 16, split 256, us; staged call over 512-
+// and 1024-token partitions with runs, and the full call at 1024 before this
+// rule): B16 L4096 50% shared 35.4 / 39.2, 37.7; B8 L8192 50% 36.6 / 38.8,
+// 40.6; B32 L2048 50% 36.0 / 38.0, 38.1; but B16 L4096 25% shared, whose
+// items save 3 / 16 of the 512-token partitions, 46.6 / 45.0, 44.7.
+constexpr int kPrefixFinerShare = 4;
+
+inline int prefix_finer_split(int c, const int32_t* runs, const int32_t* bounds, int batch, int64_t reach,
+                              int splits, int split_tokens, int page_shift, int slots, int64_t waves_per_item,
+                              int cus) {
+    if (c < 2 || runs == nullptr || bounds == nullptr || batch > kCompactMaxBatch || slots < 2) return c;
+    const int64_t span = static_cast<int64_t>(split_tokens) * c;
+    const PrefixSaving at = prefix_saving(runs, bounds, batch, reach, span, (splits + c - 1) / c, page_shift, slots);
+    if (at.work_list || rect_prefix_items_pay(at.live, at.saved, waves_per_item, cus)) return c;
+    const int h = c / 2;
+    const PrefixSaving finer =
+        prefix_saving(runs, bounds, batch, reach, span / 2, (splits + h - 1) / h, page_shift, slots);
+    if (finer.saved * kPrefixFinerShare >= finer.live &&
+        rect_prefix_items_pay(finer.live, finer.saved, waves_per_item, cus))
+        return h;
+    return c;
 }
 
 // Coarser partitions for a whole decode call on a large grid. The caller's
@@ -869,7 +922,9 @@ inline bool rect_prefix_items_pay(int64_t live, int64_t saved, int64_t waves_per
 // Going on to four waves per CU helped some shapes and hurt others badly
 // (FP16 B2 L8192 17.6 -> 17.2; FP8 K/V B16 L4096 32.5 -> 47.2, MQA B256
 // L1024 20.2 -> 25.0, FP16 B6 L4096 22.6 -> 23.0), so the rule stops at eight.
-// Whole-row calls and FP32 inputs keep the caller's split.
+// Whole-row calls and FP32 inputs keep the caller's split. With prefix runs
+// (`slots` members per shared-prefix item, pages of 1 << page_shift tokens)
+// prefix_finer_split may halve c.
 constexpr int64_t kCoarseWaveBytes = 128 * 1024;
 
 struct KernelSplit {
@@ -878,7 +933,7 @@ struct KernelSplit {
 
 inline KernelSplit coarse_split(int batch, int kv_heads, int head_tiles, int head_dim, int elem, int page_size,
                                 int table_width, int splits, int split_tokens, const int32_t* length_bounds,
-                                int cus) {
+                                int cus, const int32_t* prefix_runs = nullptr, int page_shift = 0, int slots = 1) {
     if (length_bounds == nullptr) return KernelSplit{splits, split_tokens};
     const int64_t capacity = static_cast<int64_t>(table_width) * page_size;
     // Tokens the caller's partitions reach; no partition of a coarser split goes past them.
@@ -904,15 +959,18 @@ inline KernelSplit coarse_split(int batch, int kv_heads, int head_tiles, int hea
         if (!enough(span)) break;
         c *= 2;
     }
+    c = prefix_finer_split(c, prefix_runs, length_bounds, batch, reach, splits, split_tokens, page_shift, slots,
+                           static_cast<int64_t>(kQuarters) * kv_heads * head_tiles, cus);
     return KernelSplit{(splits + c - 1) / c, split_tokens * c};
 }
 
 // The partitions of a full decode call's two launches: coarse_split's for a
 // matrix-core call (16-bit q) that is not a whole-row launch, else the
-// caller's. kv_elem: bytes per stored K/V element.
+// caller's. kv_elem: bytes per stored K/V element; prefix_runs: the call's
+// shared-prefix runs, or nullptr.
 inline KernelSplit full_call_split(bool fp32, int kv_elem, int batch, int query_heads, int kv_heads, int head_dim,
                                    int page_size, int table_width, int splits, int split_tokens,
-                                   const int32_t* length_bounds, int cus) {
+                                   const int32_t* length_bounds, int cus, const int32_t* prefix_runs = nullptr) {
     const KernelSplit same{splits, split_tokens};
     if (fp32 || rows_fit_one_launch(splits, split_tokens, static_cast<int64_t>(table_width) * page_size, head_dim,
                                     kv_elem))
@@ -920,7 +978,7 @@ inline KernelSplit full_call_split(bool fp32, int kv_elem, int batch, int query_
     const int group = query_heads / kv_heads;
     const int gt = head_tile(group, 16);
     return coarse_split(batch, kv_heads, (group + gt - 1) / gt, head_dim, kv_elem, page_size, table_width, splits,
-                        split_tokens, length_bounds, cus);
+                        split_tokens, length_bounds, cus, prefix_runs, page_size == 16 ? 4 : 5, prefix_slots(group));
 }
 
 // Bytes of one whole-row LDS slot of the FP32 kernel (per-head max and

@@ -274,8 +274,12 @@ class DecodePlan:
         for q (and K/V) of these dtypes at the current host length bounds: the
         plan's ``(splits, split_tokens)``, or on grids with many waves per CU a
         coarser split (a power of two times ``split_tokens``, with fewer
-        partitions, so the workspace holds their states)."""
+        partitions, so the workspace holds their states). With shared-prefix
+        runs the split can be half the one the same call takes without them,
+        so it comes from the launch plan."""
         layout = self.layout
+        if self._prefix_runs is not None:
+            return tuple(self.launch_plan(q_dtype, kv_dtype)["kernel_split"])
         return self._extension.kernel_split(q_dtype, q_dtype if kv_dtype is None else kv_dtype, layout.batch,
                                             layout.query_heads, layout.kv_heads, layout.head_dim, layout.page_size,
                                             self._table.shape[1], layout.physical_pages, self.splits,

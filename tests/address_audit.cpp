@@ -1420,7 +1420,8 @@ int main(int argc, char** argv) {
         // with the full call's merge.
         const KernelSplit ks = full_call_split(pr.q_elem == 4, pr.kv_elem, pr.batch, pr.q_heads, pr.kv_heads,
                                                pr.head_dim, pr.page_size, pr.width, pr.splits, pr.split_tokens,
-                                               pr.bounds.empty() ? nullptr : pr.bounds.data(), 256);
+                                               pr.bounds.empty() ? nullptr : pr.bounds.data(), 256,
+                                               pr.runs.empty() ? nullptr : pr.runs.data());
         Problem call = pr;
         const bool coarse = ks.splits != pr.splits || ks.split_tokens != pr.split_tokens;
         if (coarse) {

@@ -116,9 +116,13 @@ def test_partition_address_map_stays_in_bounds(audit_exe):
     # the page check sends the differing members to passes of their own.
     assert any(" prefix runs stale bounds=exact " in line and " own passes)" in line for line in shared)
     assert not any(" own passes)" in line for line in shared if " stale " not in line and "bounds=half" not in line)
-    # Equal lengths with a shared prompt: the rectangular grid became a work list.
+    # Equal lengths with a shared prompt: the rectangular grid became a work
+    # list, and the full call took half the coarse split that fills the device
+    # without items (x4 for this batch), where the items pay.
     assert any(line.startswith("prefix samples B16 Hq32/8 D128 T16 L4096 split 256 prefix runs bounds=exact ")
                and " compact," in line for line in shared)
+    assert any(line.startswith("prefix samples B16 Hq32/8 D128 T16 L4096 split 256 prefix runs bounds=exact "
+                               "coarse x2 [call] mfma") and " compact," in line for line in shared)
     own_passes = int(summary.split(" shared-prefix own passes")[0].rsplit(", ", 1)[1])
     assert own_passes > 0, summary
     assert any("coarse x" in line and "[call]" in line for line in shared)

@@ -88,12 +88,21 @@ def case(name):
         lengths = np.full(32, 4096, dtype=np.int32)
         table = shared_table(rng, 32, 256, [(0, range(1, 32), 128)])
         return Layout(32, 32, 8, 128, 16, 32 * 256), table, lengths, 256, torch.float16, None
+    if name == "samples B16 L4096 50% shared (half the coarse split)":
+        lengths = np.full(16, 4096, dtype=np.int32)
+        table = shared_table(rng, 16, 256, [(0, range(1, 16), 128)])
+        return Layout(16, 32, 8, 128, 16, 16 * 256), table, lengths, 256, torch.float16, None
     raise KeyError(name)
+
+
+# Cases whose full call runs over half the partition span it takes without
+# runs (prefix_finer_split): 512 tokens instead of 1024.
+FINER = {"samples B16 L4096 50% shared (half the coarse split)": 512}
 
 
 CASES = ["workload ragged+shared B16 GQA4 page 32", "mha B24 D64 (16 members per item)",
          "gqa8 B6 bf16 (2 members per item)", "gqa4 B16 fp8 e4m3 K/V", "two classes B16 GQA4",
-         "samples B32 L4096 50% shared (equal lengths)"]
+         "samples B32 L4096 50% shared (equal lengths)", "samples B16 L4096 50% shared (half the coarse split)"]
 
 
 @pytest.mark.parametrize("name", CASES)
@@ -106,6 +115,8 @@ def test_shared_prefix_items_match_the_oracle(name, merge):
     announce(f"shared prefix {name} merge={merge}: {launch['shared_prefix_items']} items, "
              f"kernel split {launch['kernel_split']}")
     assert launch["shared_prefix_items"] > 0 and launch["grid_kind"] == "work list"
+    if name in FINER:
+        assert launch["kernel_split"][1] == FINER[name] and plan.kernel_split(q.dtype)[1] == FINER[name]
     out = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).clone()
     expected = fp64.dense_attention(*exact, table, lengths)
     assert_parity(out.cpu().numpy(), expected, torch.float16)

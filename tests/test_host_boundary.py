@@ -591,3 +591,46 @@ def test_shared_prefix_items_in_the_launch_plan():
         broken[2:4] = bad
         with pytest.raises(ValueError, match="shared-prefix runs"):
             cabi.launch_plan(lib, f16, f16, *shape, *args, 256, broken)
+
+
+def _sample_table(batch, width, shared):
+    """Page table of `batch` samples of one prompt: the first `shared`
+    entries of every row are sequence 0's, the rest pages of their own."""
+    table = np.zeros((batch, width), dtype=np.int32)
+    table[0] = np.arange(width)
+    nxt = width
+    for b in range(1, batch):
+        table[b, :shared] = table[0, :shared]
+        table[b, shared:] = np.arange(nxt, nxt + width - shared)
+        nxt += width - shared
+    return table, nxt
+
+
+@pytest.mark.parametrize("batch,context,shared_share,finer", [
+    (16, 4096, 2, True),    # half the prompt shared: items over 512-token partitions
+    (8, 8192, 2, True),
+    (32, 2048, 2, True),
+    (16, 4096, 4, False),   # a quarter shared: items would save too little, 1024 tokens stay
+])
+def test_shared_prompt_samples_take_half_the_coarse_split(batch, context, shared_share, finer):
+    """Equal-length samples of one prompt (8 KV heads, GQA 4, page 16,
+    split 256, 256 CUs): without runs the full call runs over 1024-token
+    partitions; with runs, where grouping over 512-token partitions saves at
+    least a quarter of them and still fills the device, it runs over 512 with
+    shared-prefix items, else it keeps 1024."""
+    lib = cabi.load()
+    width = context // 16
+    table, pages = _sample_table(batch, width, width // shared_share)
+    runs = cabi.prefix_runs(lib, table)
+    lengths = np.full(batch, context, dtype=np.int32)
+    shape = (batch, 32, 8, 128, 16, width, pages, context // 256, 256)
+    f16 = cabi.PD_DTYPE_F16
+    plain = cabi.launch_plan(lib, f16, f16, *shape, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_NONE, lengths, 256)
+    grouped = cabi.launch_plan(lib, f16, f16, *shape, cabi.PD_MERGE_SERIAL, cabi.PD_HINT_NONE, lengths, 256, runs)
+    assert plain["kernel_split_tokens"] == 1024 and plain["shared_prefix_items"] == 0
+    assert cabi.kernel_split(lib, f16, f16, *shape, lengths, 256) == (context // 1024, 1024)
+    if finer:
+        assert grouped["kernel_split_tokens"] == 512 and grouped["kernel_splits"] == context // 512
+        assert grouped["shared_prefix_items"] > 0 and grouped["grid_kind"] == 2
+    else:
+        assert grouped["kernel_split_tokens"] == 1024 and grouped["shared_prefix_items"] == 0
