@@ -23,7 +23,8 @@ Protocol
   K eager (Python-level) calls are timed the same way and reported beside it.
 * Roofline: K back-to-back launches of the partition kernel alone (one
   captured graph) give its average launch duration; achieved = logical KV
-  bytes / duration.
+  bytes / duration. Where sequences share pages, frac_unique prices the
+  same duration on the unique pages' bytes (each shared page counted once).
 * Streaming-read ceiling: K back-to-back launches of a read-only kernel
   (pd_stream_read: 16-byte non-temporal loads, the fastest read shape
   measured) over as many bytes as the call's logical K/V, read from the same
@@ -528,6 +529,7 @@ def main():
             "bound": "hbm", "kernel": partition_kernel_name(w.dtype == np.float16 or not w.native, launches == 1),
             "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
             "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "frac_unique": round(unique / (partial_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
             "traffic": recorded_traffic(w.name, digest), "avg_launch_us": round(partial_us, 3),
             "stream_read_us": round(stream_us, 3), "stream_read_bytes": 2 * half,
             "stream_read_GBps": round(2 * half / (stream_us * 1e-6) / 1e9, 1),
