@@ -1214,6 +1214,62 @@ int main(int argc, char** argv) {
                      reserve));
         }
     }
+    // Seeded random shared-prefix problems: head layouts that form items
+    // (GQA groups up to 8, MHA) and one that does not (GQA 3 pads to 4),
+    // one to three sharing classes with random leaders, members and shared
+    // page counts, some members diverging earlier, rows padded past their
+    // lengths or not, uniform, ragged or skewed lengths, FP16 or FP8 K/V;
+    // runs taken from the table (every kind of bounds), and for every fourth
+    // problem stale runs as well.
+    {
+        Lcg rng{3031};
+        const int kv_choices[] = {1, 2, 4, 8};
+        const int group_choices[] = {1, 2, 3, 4, 8};
+        const int batch_choices[] = {2, 3, 5, 8, 12, 16, 24, 33};
+        const int split_choices[] = {16, 32, 64, 128, 256};
+        for (int i = 0; i < (quick ? 4 : 24); ++i) {
+            const int kv = kv_choices[rng.below(4)];
+            const int group = group_choices[rng.below(5)];
+            const int batch = batch_choices[rng.below(8)];
+            const int dim = rng.below(2) ? 128 : 64;
+            const int page = rng.below(2) ? 32 : 16;
+            const int split = split_choices[rng.below(5)];
+            const int len = 64 + rng.below(2048);
+            const int kind = rng.below(3);  // 0: uniform, 1: ragged, 2: skewed (one at len, the rest up to len / 2)
+            const bool fp8 = rng.below(3) == 0;
+            const bool pad = rng.below(2) != 0;
+            const int width = (len + page - 1) / page;
+            std::vector<int32_t> lens = kind == 0 ? uniform(batch, len) : ragged(batch, len, 300 + i);
+            if (kind == 2)
+                for (int b = 1; b < batch; ++b) lens[b] = rng.below(len / 2 + 1);
+            const std::string name = "prefix random " + std::to_string(i) + " B" + std::to_string(batch) + " Hq" +
+                                     std::to_string(kv * group) + "/" + std::to_string(kv) + " D" +
+                                     std::to_string(dim) + " T" + std::to_string(page) +
+                                     (kind == 0 ? " L" : kind == 1 ? " ragged L" : " skewed L") +
+                                     std::to_string(len) + " split " + std::to_string(split) +
+                                     (fp8 ? " fp8" : " fp16") + (pad ? " padded" : "");
+            Problem pr = make(name, batch, kv * group, kv, dim, page, width, lens, split, 2, fp8 ? 1 : 2, 300 + i);
+            const int classes = 1 + rng.below(3);
+            for (int c = 0; c < classes; ++c) {
+                const int leader = rng.below(batch);
+                const int pages = 1 + rng.below(width);
+                for (int b = 0; b < batch; ++b) {
+                    if (b == leader || rng.below(3) == 0) continue;  // about two rows in three join
+                    const int mine = rng.below(4) == 0 ? rng.below(pages + 1) : pages;
+                    for (int e = 0; e < mine; ++e)
+                        pr.table[static_cast<size_t>(b) * width + e] = pr.table[static_cast<size_t>(leader) * width + e];
+                }
+            }
+            if (pad)
+                for (int b = 0; b < batch; ++b)
+                    for (int e = (lens[b] + page - 1) / page; e < width; ++e)
+                        pr.table[static_cast<size_t>(b) * width + e] = -1;
+            pr.unshared = false;
+            pr.ragged = kind != 0;
+            add(with_runs(pr));
+            if (i % 4 == 0) add(with_stale_runs(pr));
+        }
+    }
     // Reserved context over uniform lengths: tail rows, partly empty slots.
     add(make("xcd llama3-8b B4 L4096 reserve x4", 4, 32, 8, 128, 16, 1024, uniform(4, 4096), 256, 2, 2, 79, 4));
     add(make("xcd mqa B128 Hq16/1 D64 L1024 reserve x2", 128, 16, 1, 64, 16, 128, uniform(128, 1024), 256, 2, 2, 81,
