@@ -13,7 +13,8 @@ leave its buffer? -- is answered on the CPU:
   head layouts, a 1M-token context in a 65536-wide table, pages above 4 GiB,
   work lists and rectangular grids with tail items under exact, low and zero
   length bounds, whole-row launches, full calls over the coarser partitions
-  of large grids) through the
+  of large grids, shared-prefix items under true and stale prefix runs,
+  including seeded random sharing patterns) through the
   same ``partition_map.h`` functions the kernels call, and checks every load,
   store and LDS access against its buffer, every live token against the page
   its table entry names, and that every live state slot is written exactly
@@ -23,7 +24,8 @@ leave its buffer? -- is answered on the CPU:
   (explicit positions and the advancing variant) and the device CSR -> page
   table conversion over valid and malformed metadata. Each kernel family has
   a planted-mistake negative control (wrong reach, merge live count, append
-  capacity, missing CSR indices bound) that the walk must report. It is
+  capacity, missing CSR indices bound, shared-prefix items without their page
+  check) that the walk must report. It is
   compiled with AddressSanitizer and UndefinedBehaviorSanitizer.
 * ``oracle/cpu_decode.c`` (the FP32 restatement the bench times) runs under
   the same sanitizers on ragged, empty-row, invalid-page-id and both-format
