@@ -160,6 +160,10 @@ PREFIX = [
         ("samples B32 L2048 50% shared", (32, 32, 8, 128, 16, "uniform:2048", 256), {"shared_prefix": 0.5}),
         ("samples B32 L4096 50% shared", (32, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.5}),
         ("samples B4 L4096 50% shared", (4, 32, 8, 128, 16, "uniform:4096", 256), {"shared_prefix": 0.5}),
+        ("fp8 samples B16 L4096 50% shared", (16, 32, 8, 128, 16, "uniform:4096", 256),
+         {"shared_prefix": 0.5, "fmt": "fp8"}),
+        ("bf16 samples B8 L8192 50% shared", (8, 32, 8, 128, 16, "uniform:8192", 256),
+         {"shared_prefix": 0.5, "fmt": "bf16"}),
     ]
     for runs in (True, False)
 ]

@@ -92,17 +92,27 @@ def case(name):
         lengths = np.full(16, 4096, dtype=np.int32)
         table = shared_table(rng, 16, 256, [(0, range(1, 16), 128)])
         return Layout(16, 32, 8, 128, 16, 16 * 256), table, lengths, 256, torch.float16, None
+    if name == "samples B8 L8192 50% shared bf16 (half the coarse split)":
+        lengths = np.full(8, 8192, dtype=np.int32)
+        table = shared_table(rng, 8, 512, [(0, range(1, 8), 256)])
+        return Layout(8, 32, 8, 128, 16, 8 * 512), table, lengths, 256, torch.bfloat16, None
+    if name == "samples B16 L4096 50% shared fp8 e4m3 K/V":
+        lengths = np.full(16, 4096, dtype=np.int32)
+        table = shared_table(rng, 16, 256, [(0, range(1, 16), 128)])
+        return Layout(16, 32, 8, 128, 16, 16 * 256), table, lengths, 256, torch.float16, torch.float8_e4m3fn
     raise KeyError(name)
 
 
 # Cases whose full call runs over half the partition span it takes without
 # runs (prefix_finer_split): 512 tokens instead of 1024.
-FINER = {"samples B16 L4096 50% shared (half the coarse split)": 512}
+FINER = {"samples B16 L4096 50% shared (half the coarse split)": 512, "samples B16 L4096 50% shared fp8 e4m3 K/V": 512,
+         "samples B8 L8192 50% shared bf16 (half the coarse split)": 512}
 
 
 CASES = ["workload ragged+shared B16 GQA4 page 32", "mha B24 D64 (16 members per item)",
          "gqa8 B6 bf16 (2 members per item)", "gqa4 B16 fp8 e4m3 K/V", "two classes B16 GQA4",
-         "samples B32 L4096 50% shared (equal lengths)", "samples B16 L4096 50% shared (half the coarse split)"]
+         "samples B32 L4096 50% shared (equal lengths)", "samples B16 L4096 50% shared (half the coarse split)",
+         "samples B8 L8192 50% shared bf16 (half the coarse split)", "samples B16 L4096 50% shared fp8 e4m3 K/V"]
 
 
 @pytest.mark.parametrize("name", CASES)
