@@ -243,3 +243,43 @@ def test_captured_append_loop_grows_members_past_the_shared_prompt():
         expected = fp64.dense_attention(host_q, host_k, host_v, table, host_lengths)
         assert_parity(out.cpu().numpy(), expected, torch.float16)
     assert (host_lengths[1:] == 160 + 12 * 5).all() and host_lengths[0] == 1024
+
+
+def test_graph_captured_at_half_the_coarse_split_survives_refreshes():
+    """Equal-length samples of a 50% shared prompt run over half the coarse
+    split with shared-prefix items (512-token partitions instead of 1024). A
+    graph captured so keeps that split and its items after ``refresh``: to a
+    table with no shared pages, to ragged lengths under a shorter shared
+    prompt, and back. Every replay, with eager calls in between (whose own
+    plans follow each refresh), matches the FP64 oracle."""
+    layout, table, lengths, split, _, _ = case("samples B16 L4096 50% shared (half the coarse split)")
+    q, k, v = make_tensors(layout, seed=43)
+    host_q, host_k, host_v = (t.cpu().numpy() for t in (q, k, v))
+    plan = DecodePlan(layout, table, lengths, split_tokens=split)
+    launch = plan.launch_plan(q.dtype)
+    assert launch["kernel_split"][1] == 512 and launch["shared_prefix_items"] > 0
+    announce("shared prefix: graph at half the coarse split, refreshed")
+    plan.run(q, k, v)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = plan.run(q, k, v)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(47)
+    private = rng.permutation(layout.physical_pages)[:16 * 256].reshape(16, 256).astype(np.int32)
+    ragged = np.concatenate([[4096], rng.integers(0, 4097, 15)]).astype(np.int32)
+    shorter = shared_table(rng, 16, 256, [(3, [b for b in range(16) if b != 3], 40)])
+    for step, (t, lens) in enumerate([(table, lengths), (private, lengths), (shorter, ragged), (table, lengths)]):
+        plan.refresh(t, lens)
+        for _ in range(2):
+            graph.replay()
+            torch.cuda.synchronize()
+            announce(f"shared prefix: replay at half the coarse split after refresh {step}")
+            assert_parity(out.cpu().numpy(), fp64.dense_attention(host_q, host_k, host_v, t, lens), torch.float16)
+        eager = plan.run(q, k, v).clone()
+        torch.cuda.synchronize()
+        assert_parity(eager.cpu().numpy(), fp64.dense_attention(host_q, host_k, host_v, t, lens), torch.float16)
