@@ -283,3 +283,76 @@ def test_graph_captured_at_half_the_coarse_split_survives_refreshes():
         eager = plan.run(q, k, v).clone()
         torch.cuda.synchronize()
         assert_parity(eager.cpu().numpy(), fp64.dense_attention(host_q, host_k, host_v, t, lens), torch.float16)
+
+
+PREFIX_STRESS_CASES = 240
+
+
+def test_randomized_shared_prefixes():
+    """Randomized sharing patterns against the FP64 oracle and the same call
+    without runs: batches of 2 to 24, 1 to 8 KV heads with GQA groups 1 to 8
+    (items form) or 16 (they do not), head dims 64 / 128, pages 16 / 32,
+    splits 16 to 256, uniform, ragged or skewed lengths up to 1536 tokens,
+    FP16 / BF16 / FP8-e4m3 K/V, one to three sharing classes with random
+    leaders, members and shared page counts (some members diverging earlier),
+    rows padded past their lengths or not, alternating merges."""
+    rng = np.random.default_rng(13579)
+    worst, grouped = 0.0, 0
+    for seed in range(PREFIX_STRESS_CASES):
+        batch = int(rng.choice([2, 3, 5, 8, 12, 16, 24]))
+        kv = int(rng.choice([1, 2, 4, 8]))
+        group = int(rng.choice([1, 2, 3, 4, 8, 16]))
+        dim = int(rng.choice([64, 128]))
+        page = int(rng.choice([16, 32]))
+        split = int(rng.choice([16, 32, 64, 128, 256]))
+        longest = int(rng.integers(64, 1537))
+        width = -(-longest // page)
+        kind = int(rng.choice(3, p=[0.2, 0.4, 0.4]))  # uniform, ragged, skewed
+        lengths = np.full(batch, longest, dtype=np.int32)
+        if kind == 1:
+            lengths[1:] = rng.integers(0, longest + 1, batch - 1)
+        elif kind == 2:
+            lengths[1:] = rng.integers(0, longest // 2 + 1, batch - 1)
+        classes = []
+        for _ in range(int(rng.integers(1, 4))):
+            leader = int(rng.integers(0, batch))
+            pages = int(rng.integers(1, width + 1) if rng.random() < 0.3 else rng.integers(width // 4 + 1, width + 1))
+            members = [b for b in range(batch) if b != leader and rng.random() < 2 / 3]
+            classes.append((leader, members, pages))
+        table = shared_table(rng, batch, width, [(leader, members, pages) for leader, members, pages in classes])
+        for leader, members, pages in classes:  # a quarter of the members diverge earlier
+            for b in members:
+                if rng.random() < 0.25:
+                    cut = int(rng.integers(0, pages + 1))
+                    table[b, cut:pages] = rng.permutation(np.arange(batch * width, batch * width + width))[
+                        :pages - cut]
+        if rng.random() < 0.5:
+            table = padded(table, lengths, page)
+        layout = Layout(batch, kv * group, kv, dim, page, batch * width + width)
+        fmt = str(rng.choice(["f16", "f16", "bf16", "e4m3"]))
+        q_dtype = torch.bfloat16 if fmt == "bf16" else torch.float16
+        kv_dtype = torch.float8_e4m3fn if fmt == "e4m3" else None
+        (q, k, v), (k_scale, v_scale), exact = inputs(layout, q_dtype, kv_dtype, seed=seed + 30000)
+        merge = ("serial", "shared")[seed % 2]
+        plan = DecodePlan(layout, table, lengths, split_tokens=split, merge=merge)
+        items = plan.launch_plan(q.dtype, k.dtype)["shared_prefix_items"]
+        grouped += items > 0
+        if seed % 20 == 0:
+            announce(f"shared prefix stress case {seed}: {grouped} with items so far, worst {worst:.3e}")
+        out = plan.run(q, k, v, k_scale=k_scale, v_scale=v_scale).clone()
+        expected = fp64.dense_attention(*exact, table, lengths)
+        worst = max(worst, float(np.max(np.abs(out.cpu().numpy() - expected))))
+        ext = plan._extension
+        alone = torch.empty_like(out)
+        ext.decode(q, k, v, plan._table, plan._lengths, plan._numerator, plan._stats, alone, split,
+                   plan._merge_mode, k_scale, v_scale, plan._unshared_pages, plan._ragged_lengths,
+                   plan._length_bounds(), None)
+        try:
+            assert_parity(out.cpu().numpy(), expected, torch.float16)
+            torch.testing.assert_close(out, alone, rtol=0, atol=2e-5)
+        except AssertionError as exc:
+            raise AssertionError(f"case {seed}: {layout} split={split} {fmt} merge={merge} items={items} "
+                                 f"lengths={lengths.tolist()} classes={[(l, len(m), p) for l, m, p in classes]}"
+                                 ) from exc
+    announce(f"shared prefix stress: {PREFIX_STRESS_CASES} cases, {grouped} with items, max abs error {worst:.3e}")
+    assert grouped >= PREFIX_STRESS_CASES // 4
