@@ -634,3 +634,69 @@ def test_shared_prompt_samples_take_half_the_coarse_split(batch, context, shared
         assert grouped["shared_prefix_items"] > 0 and grouped["grid_kind"] == 2
     else:
         assert grouped["kernel_split_tokens"] == 1024 and grouped["shared_prefix_items"] == 0
+
+
+def test_launch_planner_invariants_over_random_shapes():
+    """The launch planner (`pd_decode_launch_plan`, host only) over 3000 seeded
+    random calls: formats, head layouts, pages, table widths up to 4096,
+    splits from 1 to the whole context, batches up to 2048, no / exact / low
+    / zero / excess host bounds, and prefix runs from tables with and without
+    shared prefixes. Every call is planned (or refused with ValueError for a
+    shape the checks reject), and the plan keeps the limits the launches rely
+    on: a kernel split that is the caller's times a power of two with no more
+    partitions than the caller's, grid dimensions the hardware takes,
+    workgroups of at most 1024 threads, at most 128 shared-prefix items and
+    none without runs and bounds or for FP32 inputs, and the caller's split
+    for FP32 inputs."""
+    lib = cabi.load()
+    rng = np.random.default_rng(8642)
+    formats = [(cabi.PD_DTYPE_F16, cabi.PD_DTYPE_F16), (cabi.PD_DTYPE_BF16, cabi.PD_DTYPE_BF16),
+               (cabi.PD_DTYPE_F32, cabi.PD_DTYPE_F32), (cabi.PD_DTYPE_F16, cabi.PD_DTYPE_FP8_E4M3),
+               (cabi.PD_DTYPE_BF16, cabi.PD_DTYPE_FP8_E5M2)]
+    planned = grouped = 0
+    for case in range(3000):
+        q_dtype, kv_dtype = formats[int(rng.integers(0, len(formats)))]
+        kv = int(rng.choice([1, 2, 3, 4, 5, 8, 12, 16, 32]))
+        group = int(rng.choice([1, 2, 3, 4, 8, 16, 24, 32]))
+        dim = int(rng.choice([64, 128]))
+        page = int(rng.choice([16, 32]))
+        batch = int(rng.choice([1, 2, 3, 4, 8, 16, 33, 64, 65, 128, 512, 2048]))
+        width = int(rng.choice([1, 2, 7, 16, 64, 256, 1024, 4096]))
+        if batch * width > 1 << 20:
+            width = max(1, (1 << 20) // batch)
+        capacity = width * page
+        split = int(rng.choice([16, 32, 64, 100, 128, 256, 512, 1024, 4096]))
+        splits = max(1, -(-int(rng.integers(1, capacity + 1)) // split))
+        lengths = rng.integers(0, min(capacity, splits * split) + 1, batch).astype(np.int32)
+        bounds_kind = int(rng.integers(0, 5))
+        bounds = [None, lengths, lengths // 2, np.zeros_like(lengths), lengths + 100][bounds_kind]
+        runs = None
+        if batch <= 128 and width <= 256 and rng.random() < 0.5:
+            table = rng.permutation(batch * width).reshape(batch, width).astype(np.int32)
+            if rng.random() < 0.7:
+                shared = int(rng.integers(1, width + 1))
+                table[:, :shared] = table[0, :shared]
+            runs = cabi.prefix_runs(lib, table)
+        hints = int(rng.integers(0, 4))
+        merge = int(rng.integers(0, 2))
+        args = (q_dtype, kv_dtype, batch, kv * group, kv, dim, page, width, batch * width, splits, split, merge, hints,
+                bounds, 256, runs)
+        try:
+            plan = cabi.launch_plan(lib, *args)
+        except ValueError:
+            continue  # a shape the checks reject (for example the shared merge's state limit)
+        planned += 1
+        where = f"case {case}: {args[:13]} bounds kind {bounds_kind} runs {runs is not None} -> {plan}"
+        c = plan["kernel_split_tokens"] // split
+        assert plan["kernel_split_tokens"] == c * split and c >= 1 and c & (c - 1) == 0, where
+        assert plan["kernel_splits"] == -(-splits // c) and plan["kernel_splits"] <= splits, where
+        assert plan["launches"] in (1, 2), where
+        assert 1 <= plan["grid_x"] < 1 << 32 and 1 <= plan["grid_y"] <= 65535 and 1 <= plan["grid_z"] <= 65535, where
+        assert 1 <= plan["waves_per_workgroup"] <= 16, where
+        assert 0 <= plan["shared_prefix_items"] <= 128, where
+        if runs is None or bounds is None or q_dtype == cabi.PD_DTYPE_F32:
+            assert plan["shared_prefix_items"] == 0, where
+        if q_dtype == cabi.PD_DTYPE_F32 or bounds is None:
+            assert c == 1, where
+        grouped += plan["shared_prefix_items"] > 0
+    assert planned > 2000 and grouped >= 5, (planned, grouped)
